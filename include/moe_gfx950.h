@@ -1,0 +1,132 @@
+/* moe_gfx950.h — C-ABI of libmoe_gfx950.so, the MI355X (gfx950, wave64) MoE-block library.
+ *
+ * Every data pointer is a DEVICE pointer owned by the caller (for example a torch tensor's
+ * data_ptr()); `stream` is a hipStream_t passed as void*. Every call is asynchronous on `stream`,
+ * allocates nothing, frees nothing and never synchronises the host; scratch memory comes in
+ * through (ws, ws_bytes). Routing values never travel to the host (specification/11-moe-block.md
+ * §11.7: the block is computable with zero host-visible routing values).
+ *
+ * Return value: MOE_OK (0) or a negative MOE_E_* code; moe_last_error() then returns a
+ * thread-local description. Nothing throws across the ABI. Results are deterministic: no float
+ * atomics write any returned tensor, so equal inputs give equal bits.
+ *
+ * The reference has no C-ABI: its MoE step is the Python call surface
+ *   engine/block_forward.py:614-681  moe_router / moe_shared / moe_routed / moe_block
+ *   engine/m3_forward.py:430-476     moe_block(g, E, layer)
+ *   speccheck/moe_ref.py:318-533     route / expert_gather / shared_expert / moe_block
+ * and its device work ran as separate processes (engine/device_arm.py:417-463). Each entry point
+ * below names the reference function it replaces.
+ */
+#ifndef MOE_GFX950_H
+#define MOE_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_ABI_VERSION 1
+
+enum {
+  MOE_OK = 0,
+  MOE_E_ARG = -1,          /* bad pointer, shape or enum                                     */
+  MOE_E_FORMAT = -2,       /* weight format not supported for this operand                   */
+  MOE_E_HIP = -3,          /* a HIP runtime call failed (text in moe_last_error)             */
+  MOE_E_WORKSPACE = -4,    /* ws_bytes smaller than moe_workspace_bytes() asks for            */
+  MOE_E_UNSUPPORTED = -5   /* geometry outside what the kernels are built for                */
+};
+
+/* dtypes of activations / outputs */
+enum { MOE_DT_F32 = 0, MOE_DT_BF16 = 1 };
+
+/* weight formats: ggml_type ids (tools/gguf_reader.py:10-51 block table) */
+enum { MOE_FMT_Q4_K = 12, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
+
+/* expert contraction path: GEMV = fused decode + f32 GEMV; MFMA = tiles decoded to f16 in LDS on
+ * MFMA (f32 accumulation); MFMA_BF16 = the same with bf16 operands (8 significant bits instead of
+ * 11; same MFMA rate; block outputs ~3e-3 from the f32 oracle instead of ~4e-4). */
+enum { MOE_PATH_AUTO = 0, MOE_PATH_GEMV = 1, MOE_PATH_MFMA = 2, MOE_PATH_MFMA_BF16 = 3 };
+
+int moe_abi_version(void);
+const char *moe_last_error(void);
+
+/* Scratch bytes moe_block_forward / moe_experts / moe_sort_permute / moe_router_topk need for a
+ * T-token step of this geometry (an upper bound for every path). */
+size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s);
+
+/* Bit-exact super-block decode: n_elts elements of `fmt` blocks -> f32 or bf16 (RNE of the exact
+ * f32 value). Replaces tools/gguf_reader.py:248-268 (_deq_q4_k), :299-322 (_deq_q6_k) and
+ * tools/gguf_fast_dequant.py:87-152 (dequant_np). n_elts % 256 == 0. */
+int moe_dequant(const void *blocks, int fmt, int64_t n_elts, void *out, int out_dtype,
+                void *stream);
+
+/* R1-R5 for T tokens. Replaces speccheck/moe_ref.py:318-363 (route) and
+ * engine/block_forward.py:614-636 (moe_router); engine/m3_forward.py:443-446.
+ *   R1 logits[t,e] = bf16 of the correctly rounded sum_j x[t,j]*W[e,j] (+ logit_bias[e])
+ *   R2 probs = softmax over E in f32; R3 top-K with torch CPU's tie order;
+ *   R4 w_f32 = renormalised top-K probs; R5 w_bf16 = bf16(w_f32).
+ * x: [T,H] f32 or bf16; w_router: [E,H] bf16; logit_bias: [E] f32 or NULL.
+ * logits_bf16 [T,E], probs [T,E] may be NULL; topk_ids [T,K] int32; w_f32, w_bf16 [T,K].
+ * Limits: H % 512 == 0, E <= 256, K <= 16, K * 64 > E (torch's nth_element branch). */
+int moe_router_topk(const void *x, int x_dtype, const void *w_router, const float *logit_bias,
+                    int T, int H, int E, int K, void *logits_bf16, float *probs,
+                    int32_t *topk_ids, float *w_f32, void *w_bf16, void *ws, size_t ws_bytes,
+                    void *stream);
+
+/* Stable token->expert grouping: pairs p = t*K + k sorted by expert id, ties in p order,
+ * bit-exact vs torch.argsort(ids.flatten(), stable=True). Replaces the grouping in
+ * speccheck/moe_ref.py:433-439 and engine/m3_forward.py:448-452.
+ * expert_offsets [E+1]; sorted_pairs [T*K] (value p); pair_pos [T*K] (inverse permutation);
+ * hit_list [E+1] = n_hit, then the hit expert ids ascending. */
+int moe_sort_permute(const int32_t *topk_ids, int T, int K, int E, int32_t *expert_offsets,
+                     int32_t *sorted_pairs, int32_t *pair_pos, int32_t *hit_list, void *ws,
+                     size_t ws_bytes, void *stream);
+
+/* The K routed SwiGLU experts of every token, grouped so each hit expert's weights are read once
+ * per step. Replaces speccheck/moe_ref.py:367-451 (_expert_apply, expert_gather) and
+ * engine/m3_forward.py:452-463. gate_up_q: [E][2I rows][H/256 blocks], gate rows first
+ * (spec §11.4); down_q: [E][H rows][I/256 blocks]. y [T*K, H] f32 in sorted-pair order
+ * (expert_raw before the routing weight). path: GEMV = fused dequant + f32 GEMV (decode),
+ * MFMA / MFMA_BF16 = tiles dequantised to f16 / bf16 in LDS, contracted on MFMA (prefill);
+ * AUTO picks GEMV for T <= 16 with Q4_K gate_up, MFMA otherwise. */
+int moe_experts(const void *x, int x_dtype, const void *gate_up_q, int gate_up_fmt,
+                const void *down_q, int down_fmt, const int32_t *expert_offsets,
+                const int32_t *sorted_pairs, const int32_t *hit_list, int T, int H, int I, int E,
+                int K, int path, float *y, void *ws, size_t ws_bytes, void *stream);
+
+/* Shared expert and its scalar sigmoid gate. Replaces speccheck/moe_ref.py:480-495,
+ * engine/block_forward.py:639-649 and engine/m3_forward.py:436-442.
+ * w_gate, w_up: [I_s,H] bf16; w_down: [H,I_s] bf16; w_scalar_gate: [H] bf16.
+ * shared_raw [T,H] = down(silu(gate x) * up x); gate_prob [T] = sigmoid(w_scalar_gate . x). */
+int moe_shared_expert(const void *x, int x_dtype, const void *w_gate, const void *w_up,
+                      const void *w_down, const void *w_scalar_gate, int T, int H, int I_s,
+                      int path, float *shared_raw, float *gate_prob, void *ws, size_t ws_bytes,
+                      void *stream);
+
+/* Top-K weighted combine, ascending expert id, weight reached by rank, plus the gated shared
+ * expert. Replaces speccheck/moe_ref.py:452-476, :516-518 and engine/block_forward.py:664-667,
+ * :680. y: [T*K,H] sorted order; w_bf16 [T,K]; out [T,H] f32; routed_sum, shared_out [T,H] and
+ * expert_raw [T,K,H] (slot order) are optional (NULL). */
+int moe_combine(const float *y, const int32_t *pair_pos, const int32_t *topk_ids,
+                const void *w_bf16, const float *shared_raw, const float *gate_prob, int T, int K,
+                int H, float *out, float *routed_sum, float *shared_out, float *expert_raw,
+                void *stream);
+
+/* The whole block in one stream-ordered call. Replaces speccheck/moe_ref.py:499-533 (moe_block),
+ * engine/block_forward.py:670-681 and engine/m3_forward.py:430-476. Stage outputs other than
+ * `out` may be NULL. */
+int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                      const void *w_router, const float *logit_bias, const void *gate_up_q,
+                      int gate_up_fmt, const void *down_q, int down_fmt, const void *ws_gate,
+                      const void *ws_up, const void *ws_down, const void *ws_scalar_gate,
+                      int path, float *out, void *logits_bf16, int32_t *topk_ids,
+                      void *topk_w_bf16, float *topk_w_f32, float *routed_sum,
+                      float *shared_out, float *gate_prob, float *expert_raw, void *ws,
+                      size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_GFX950_H */

@@ -1,0 +1,66 @@
+"""ctypes binding of libmoe_gfx950.so (the C-ABI declared in include/moe_gfx950.h).
+
+The library is built in-tree by build.py. There is no fallback: if the shared object is missing
+or fails to load, importing this module raises, so no code path can silently run elsewhere.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmoe_gfx950.so"
+
+MOE_OK = 0
+MOE_E_ARG = -1
+MOE_E_FORMAT = -2
+MOE_E_HIP = -3
+MOE_E_WORKSPACE = -4
+MOE_E_UNSUPPORTED = -5
+ERROR_NAMES = {MOE_E_ARG: "bad-argument", MOE_E_FORMAT: "unsupported-format",
+               MOE_E_HIP: "hip-error", MOE_E_WORKSPACE: "workspace-too-small",
+               MOE_E_UNSUPPORTED: "unsupported-geometry"}
+
+MOE_DT_F32 = 0
+MOE_DT_BF16 = 1
+MOE_FMT_Q4_K = 12
+MOE_FMT_Q6_K = 14
+MOE_FMT_BF16 = 30
+MOE_PATH_AUTO = 0
+MOE_PATH_GEMV = 1
+MOE_PATH_MFMA = 2
+MOE_PATH_MFMA_BF16 = 3
+
+# every symbol include/moe_gfx950.h declares, with its ctypes signature
+_VP, _I, _I64, _SZ, _CP = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_char_p
+SIGNATURES = {
+    "moe_abi_version": (_I, []),
+    "moe_last_error": (_CP, []),
+    "moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "moe_dequant": (_I, [_VP, _I, _I64, _VP, _I, _VP]),
+    "moe_router_topk": (_I, [_VP, _I, _VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP,
+                             _SZ, _VP]),
+    "moe_sort_permute": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_experts": (_I, [_VP, _I, _VP, _I, _VP, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP,
+                         _VP, _SZ, _VP]),
+    "moe_shared_expert": (_I, [_VP, _I, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _SZ,
+                               _VP]),
+    "moe_combine": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "moe_block_forward": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP, _I, _VP, _I, _VP,
+                               _VP, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                               _VP, _SZ, _VP]),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                          "(or python qwen3.6-35b-a3b_amd/build.py) first")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()

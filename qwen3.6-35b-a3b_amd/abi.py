@@ -1,0 +1,207 @@
+"""Python face of the C-ABI: argument validation, workspace and stream plumbing, named refusals.
+
+Every function here takes and returns torch tensors that live on one GPU and launches work on
+the current HIP stream; none of them copies routing values to the host. Errors come back as
+`Refused(tag, msg)`, the reference's error shape (engine/block_forward.py:109-114).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib as L
+
+
+class Refused(Exception):
+    """A call the library would not make. `tag` names the reason."""
+
+    def __init__(self, tag: str, msg: str):
+        super().__init__(f"{tag}: {msg}")
+        self.tag = tag
+
+
+def _check(rc: int, who: str) -> None:
+    if rc != L.MOE_OK:
+        text = L.lib.moe_last_error().decode(errors="replace")
+        raise Refused(L.ERROR_NAMES.get(rc, f"error{rc}"), f"{who}: {text}")
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, shape=None, device=None):
+    if not isinstance(t, torch.Tensor):
+        raise Refused("bad-argument", f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise Refused("bad-argument", f"{name} must live on the GPU (got {t.device})")
+    if device is not None and t.device != device:
+        raise Refused("bad-argument", f"{name} is on {t.device}, expected {device}")
+    if dtype is not None and t.dtype != dtype:
+        raise Refused("bad-argument", f"{name} has dtype {t.dtype}, expected {dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise Refused("bad-argument", f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise Refused("bad-argument", f"{name} must be contiguous")
+    return t
+
+
+def _xdt(x: torch.Tensor) -> int:
+    if x.dtype == torch.float32:
+        return L.MOE_DT_F32
+    if x.dtype == torch.bfloat16:
+        return L.MOE_DT_BF16
+    raise Refused("bad-argument", f"activations must be float32 or bfloat16, got {x.dtype}")
+
+
+_WS_CACHE: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A cached scratch buffer of at least nbytes on `device` (allocated by torch, not the library)."""
+    key = (device.index if device.index is not None else torch.cuda.current_device())
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = buf
+    return buf
+
+
+def workspace_bytes(T: int, H: int, I: int, E: int, K: int, I_s: int) -> int:
+    return int(L.lib.moe_workspace_bytes(T, H, I, E, K, I_s))
+
+
+# ---------------------------------------------------------------------------------- entry points
+def dequant(blocks: torch.Tensor, fmt: int, n_elts: int, out_dtype=torch.float32) -> torch.Tensor:
+    """Bit-exact decode of `n_elts` elements of GGUF super-blocks -> f32 / bf16 [n_elts]."""
+    _need(blocks, "blocks", torch.uint8)
+    out = torch.empty(n_elts, dtype=out_dtype, device=blocks.device)
+    odt = L.MOE_DT_F32 if out_dtype == torch.float32 else L.MOE_DT_BF16
+    _check(L.lib.moe_dequant(_p(blocks), fmt, n_elts, _p(out), odt, _stream(blocks)), "dequant")
+    return out
+
+
+def router_topk(x: torch.Tensor, w_router: torch.Tensor, top_k: int,
+                bias: torch.Tensor | None = None, want_probs: bool = False) -> dict:
+    """R1-R5 (speccheck/moe_ref.py:318-363). Returns logits (bf16), ids (int32), w_f32, w_bf16."""
+    _need(x, "x")
+    T, H = x.shape
+    E = w_router.shape[0]
+    _need(w_router, "w_router", torch.bfloat16, (E, H), x.device)
+    if bias is not None:
+        _need(bias, "logit_bias", torch.float32, (E,), x.device)
+    dev = x.device
+    logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
+    probs = torch.empty(T, E, dtype=torch.float32, device=dev) if want_probs else None
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    wf = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    wb = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
+    _check(L.lib.moe_router_topk(_p(x), _xdt(x), _p(w_router), _p(bias), T, H, E, top_k,
+                                 _p(logits), _p(probs), _p(ids), _p(wf), _p(wb), None, 0,
+                                 _stream(x)), "router_topk")
+    return {"router_logits": logits, "router_probs": probs, "topk_ids": ids,
+            "topk_weights": wb, "topk_weights_f32": wf}
+
+
+def sort_permute(ids: torch.Tensor, n_experts: int) -> dict:
+    """Stable grouping of (token, slot) pairs by expert id (torch.argsort(stable=True) order)."""
+    _need(ids, "topk_ids", torch.int32)
+    T, K = ids.shape
+    dev = ids.device
+    P = T * K
+    off = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    srt = torch.empty(P, dtype=torch.int32, device=dev)
+    pos = torch.empty(P, dtype=torch.int32, device=dev)
+    hits = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    ws = workspace(dev, ((P + 1023) // 1024) * n_experts * 4 + 256)
+    _check(L.lib.moe_sort_permute(_p(ids), T, K, n_experts, _p(off), _p(srt), _p(pos), _p(hits),
+                                  _p(ws), ws.numel(), _stream(ids)), "sort_permute")
+    return {"expert_offsets": off, "sorted_pairs": srt, "pair_pos": pos, "hit_list": hits}
+
+
+def experts(x: torch.Tensor, gate_up_q: torch.Tensor, gate_up_fmt: int, down_q: torch.Tensor,
+            down_fmt: int, grouping: dict, top_k: int, path: int = L.MOE_PATH_AUTO) -> torch.Tensor:
+    """y [T*K, H] f32 in sorted-pair order (expert_raw before the routing weight)."""
+    _need(x, "x")
+    T, H = x.shape
+    _need(gate_up_q, "gate_up_q", torch.uint8, device=x.device)
+    _need(down_q, "down_q", torch.uint8, device=x.device)
+    E, two_i = gate_up_q.shape[0], gate_up_q.shape[1]
+    I = two_i // 2
+    y = torch.empty(T * top_k, H, dtype=torch.float32, device=x.device)
+    ws = workspace(x.device, workspace_bytes(T, H, I, E, top_k, I))
+    _check(L.lib.moe_experts(_p(x), _xdt(x), _p(gate_up_q), gate_up_fmt, _p(down_q), down_fmt,
+                             _p(grouping["expert_offsets"]), _p(grouping["sorted_pairs"]),
+                             _p(grouping["hit_list"]), T, H, I, E, top_k, path, _p(y), _p(ws),
+                             ws.numel(), _stream(x)), "experts")
+    return y
+
+
+def shared_expert(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                  w_scalar_gate: torch.Tensor, path: int = L.MOE_PATH_AUTO):
+    """(shared_raw [T,H] f32, gate_prob [T] f32)."""
+    _need(x, "x")
+    T, H = x.shape
+    Is = w_gate.shape[0]
+    for n, t, shp in (("w_gate", w_gate, (Is, H)), ("w_up", w_up, (Is, H)),
+                      ("w_down", w_down, (H, Is)), ("w_scalar_gate", w_scalar_gate, (1, H))):
+        _need(t, n, torch.bfloat16, shp, x.device)
+    raw = torch.empty(T, H, dtype=torch.float32, device=x.device)
+    prob = torch.empty(T, dtype=torch.float32, device=x.device)
+    ws = workspace(x.device, T * Is * 4 + (1 << 16))
+    _check(L.lib.moe_shared_expert(_p(x), _xdt(x), _p(w_gate), _p(w_up), _p(w_down),
+                                   _p(w_scalar_gate), T, H, Is, path, _p(raw), _p(prob), _p(ws),
+                                   ws.numel(), _stream(x)), "shared_expert")
+    return raw, prob
+
+
+def combine(y: torch.Tensor, grouping: dict, ids: torch.Tensor, w_bf16: torch.Tensor,
+            shared_raw: torch.Tensor, gate_prob: torch.Tensor, stages: bool = False) -> dict:
+    """Ascending-expert-id weighted combine + gated shared expert."""
+    T, K = ids.shape
+    H = y.shape[1]
+    dev = y.device
+    out = torch.empty(T, H, dtype=torch.float32, device=dev)
+    routed = torch.empty(T, H, dtype=torch.float32, device=dev) if stages else None
+    shared_out = torch.empty(T, H, dtype=torch.float32, device=dev) if stages else None
+    raw = torch.empty(T, K, H, dtype=torch.float32, device=dev) if stages else None
+    _check(L.lib.moe_combine(_p(y), _p(grouping["pair_pos"]), _p(ids), _p(w_bf16),
+                             _p(shared_raw), _p(gate_prob), T, K, H, _p(out), _p(routed),
+                             _p(shared_out), _p(raw), _stream(y)), "combine")
+    return {"combined_out": out, "routed_sum": routed, "shared_out": shared_out, "expert_raw": raw}
+
+
+def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False,
+                  out: torch.Tensor | None = None) -> dict:
+    """The whole block in one library call (moe_block_forward). `lw` is a LayerWeights;
+    `stages` is False, True (every stage output) or a set of stage names to return."""
+    _need(x, "x")
+    T, H = x.shape
+    E, K, I, Is = lw.n_experts, lw.top_k, lw.i_e, lw.i_s
+    dev = x.device
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.float32, device=dev)
+    shapes = {"router_logits": ((T, E), torch.bfloat16), "topk_ids": ((T, K), torch.int32),
+              "topk_weights": ((T, K), torch.bfloat16),
+              "topk_weights_f32": ((T, K), torch.float32),
+              "routed_sum": ((T, H), torch.float32), "shared_out": ((T, H), torch.float32),
+              "shared_gate_prob": ((T,), torch.float32),
+              "expert_raw": ((T, K, H), torch.float32)}
+    want = set(shapes) if stages is True else (set(stages) if stages else set())
+    st = {n: torch.empty(*shapes[n][0], dtype=shapes[n][1], device=dev) for n in want}
+    ws = workspace(dev, workspace_bytes(T, H, I, E, K, Is))
+    g = st.get
+    _check(L.lib.moe_block_forward(
+        _p(x), _xdt(x), T, H, I, E, K, Is, _p(lw.router), _p(lw.router_bias), _p(lw.gate_up_q),
+        lw.gate_up_fmt, _p(lw.down_q), lw.down_fmt, _p(lw.shared_gate), _p(lw.shared_up),
+        _p(lw.shared_down), _p(lw.shared_scalar_gate), path, _p(out), _p(g("router_logits")),
+        _p(g("topk_ids")), _p(g("topk_weights")), _p(g("topk_weights_f32")), _p(g("routed_sum")),
+        _p(g("shared_out")), _p(g("shared_gate_prob")), _p(g("expert_raw")), _p(ws), ws.numel(),
+        _stream(x)), "block_forward")
+    st["combined_out"] = out
+    return st

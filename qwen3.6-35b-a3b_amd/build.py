@@ -1,0 +1,61 @@
+"""Build libmoe_gfx950.so from csrc/*.hip with hipcc for gfx950 (in-tree; no cmake, no JIT cache).
+
+`build()` always recompiles. Objects go to csrc/_build/ (git-ignored); the shared library lands
+next to this file so the package loads it from its own directory.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OUT = PKG / "libmoe_gfx950.so"
+ARCH = os.environ.get("MOE_GPU_ARCH", "gfx950")
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+# Packed-FP32 instructions are disabled for all device code; the host pass only warns about it.
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _compile(src: Path, obj: Path) -> tuple[Path, int, str]:
+    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    return src, p.returncode, (p.stdout + p.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    srcs = sorted(CSRC.glob("*.hip"))
+    bdir = CSRC / "_build"
+    bdir.mkdir(exist_ok=True)
+    objs = [bdir / (s.stem + ".o") for s in srcs]
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        results = list(ex.map(lambda so: _compile(*so), zip(srcs, objs)))
+    failed = [(s, log) for s, rc, log in results if rc != 0]
+    for s, rc, log in results:
+        if verbose or rc != 0:
+            noisy = [l for l in log.splitlines() if "packed-fp32-ops" not in l and l.strip()]
+            if noisy:
+                print(f"--- {s.name}\n" + "\n".join(noisy), file=sys.stderr)
+    if failed:
+        raise RuntimeError("hipcc failed for: " + ", ".join(s.name for s, _ in failed))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,278 @@
+// C-ABI entry points of libmoe_gfx950.so (declared in include/moe_gfx950.h): argument checks,
+// workspace carving and stream-ordered launches. No entry point allocates, frees or synchronises.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "moe_internal.h"
+
+static thread_local char g_err[512] = "";
+
+int moe_set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int moe_check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return moe_set_error(MOE_E_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MOE_OK;
+}
+
+#define MOE_TRY(expr)            \
+  do {                           \
+    const int _rc = (expr);      \
+    if (_rc != MOE_OK) return _rc; \
+  } while (0)
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+static size_t r256(size_t b) { return (b + 255) & ~size_t(255); }
+
+static int check_geom(int T, int H, int I, int E, int K, const char* who) {
+  if (T < 1 || H < 1 || I < 1 || E < 1 || K < 1)
+    return moe_set_error(MOE_E_ARG, "%s: non-positive dimension (T=%d H=%d I=%d E=%d K=%d)", who, T, H, I, E, K);
+  if (E > 256 || K > 16 || K > E || K * 64 <= E)
+    return moe_set_error(MOE_E_UNSUPPORTED, "%s: need E <= 256, K <= 16, K <= E and K*64 > E (E=%d K=%d)", who, E, K);
+  if (H % 2048 || I % 512)
+    return moe_set_error(MOE_E_UNSUPPORTED, "%s: need H %% 2048 == 0 and I %% 512 == 0 (H=%d I=%d)", who, H, I);
+  return MOE_OK;
+}
+
+static int pick_path(int path, int T, int gate_up_fmt) {
+  if (path == MOE_PATH_GEMV || path == MOE_PATH_MFMA || path == MOE_PATH_MFMA_BF16) return path;
+  if (gate_up_fmt != MOE_FMT_Q4_K) return MOE_PATH_MFMA;
+  return T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
+}
+
+struct Carve {
+  // every piece a T-token forward can need; sizes are upper bounds over both paths
+  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, flag;
+};
+
+static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
+  const size_t P = (size_t)T * K;
+  Carve c;
+  c.logits = r256((size_t)T * E * 2);
+  c.ids = r256(P * 4);
+  c.wf = r256(P * 4);
+  c.wb = r256(P * 2);
+  c.offsets = r256((size_t)(E + 1) * 4);
+  c.sorted = r256(P * 4);
+  c.pos = r256(P * 4);
+  c.hits = r256((size_t)(E + 1) * 4);
+  c.sort_ws = moe_sort_ws_bytes((int)P, E);
+  c.tiles = r256((size_t)(1 + 2 * moe_max_mtiles((int)P, E)) * 4);
+  c.S = r256(P * I * 4);
+  c.y = r256(P * H * 4);
+  c.sS = r256((size_t)T * Is * 4);
+  c.sraw = r256((size_t)T * H * 4);
+  c.gprob = r256((size_t)T * 4);
+  c.flag = 256;
+  return c;
+}
+
+extern "C" {
+
+int moe_abi_version(void) { return MOE_ABI_VERSION; }
+
+const char* moe_last_error(void) { return g_err; }
+
+size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s) {
+  if (T < 1 || E < 1 || K < 1) return 0;
+  const Carve c = carve_sizes(T, H, I, E, K, I_s);
+  return c.logits + c.ids + c.wf + c.wb + c.offsets + c.sorted + c.pos + c.hits + c.sort_ws +
+         c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.flag;
+}
+
+int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
+                void* stream) {
+  if (!blocks || !out) return moe_set_error(MOE_E_ARG, "moe_dequant: NULL pointer");
+  if (n_elts <= 0 || n_elts % 256) return moe_set_error(MOE_E_ARG, "moe_dequant: n_elts must be a positive multiple of 256");
+  if (out_dtype != MOE_DT_F32 && out_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_dequant: bad out_dtype %d", out_dtype);
+  if (fmt == MOE_FMT_Q4_K && !aligned16(blocks)) return moe_set_error(MOE_E_ARG, "moe_dequant: Q4_K blocks must be 16-byte aligned");
+  if (fmt == MOE_FMT_Q6_K && (reinterpret_cast<uintptr_t>(blocks) & 1u)) return moe_set_error(MOE_E_ARG, "moe_dequant: Q6_K blocks must be 2-byte aligned");
+  return moe_launch_dequant(blocks, fmt, n_elts, out, out_dtype, (hipStream_t)stream);
+}
+
+int moe_router_topk(const void* x, int x_dtype, const void* w_router, const float* logit_bias,
+                    int T, int H, int E, int K, void* logits_bf16, float* probs,
+                    int32_t* topk_ids, float* w_f32, void* w_bf16, void* ws, size_t ws_bytes,
+                    void* stream) {
+  if (!x || !w_router || !topk_ids || !w_f32 || !w_bf16) return moe_set_error(MOE_E_ARG, "moe_router_topk: NULL pointer");
+  if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_router_topk: bad x_dtype %d", x_dtype);
+  if (T < 1 || H < 1 || H % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_router_topk: need T >= 1 and H %% 512 == 0");
+  if (E < 1 || E > 256 || K < 1 || K > 16 || K > E || K * 64 <= E)
+    return moe_set_error(MOE_E_UNSUPPORTED, "moe_router_topk: need E <= 256, K <= 16, K*64 > E (E=%d K=%d)", E, K);
+  if (!aligned16(x) || !aligned16(w_router)) return moe_set_error(MOE_E_ARG, "moe_router_topk: x and w_router must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  uint16_t* logits = reinterpret_cast<uint16_t*>(logits_bf16);
+  if (!logits) {
+    MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+    logits = reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
+    if (!logits) return moe_set_error(MOE_E_WORKSPACE, "moe_router_topk: workspace too small for the logits");
+  }
+  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, logit_bias, T, H, E, logits, st));
+  return moe_launch_route_topk(logits, T, E, K, probs, topk_ids, w_f32,
+                               reinterpret_cast<uint16_t*>(w_bf16), nullptr, st);
+}
+
+int moe_sort_permute(const int32_t* topk_ids, int T, int K, int E, int32_t* expert_offsets,
+                     int32_t* sorted_pairs, int32_t* pair_pos, int32_t* hit_list, void* ws,
+                     size_t ws_bytes, void* stream) {
+  if (!topk_ids || !expert_offsets || !sorted_pairs || !pair_pos || !hit_list)
+    return moe_set_error(MOE_E_ARG, "moe_sort_permute: NULL pointer");
+  if (T < 1 || K < 1 || E < 1 || E > 256) return moe_set_error(MOE_E_UNSUPPORTED, "moe_sort_permute: need T, K >= 1 and 1 <= E <= 256");
+  const int P = T * K;
+  if (P > 64 && (!ws || ws_bytes < moe_sort_ws_bytes(P, E)))
+    return moe_set_error(MOE_E_WORKSPACE, "moe_sort_permute: workspace needs %zu bytes", moe_sort_ws_bytes(P, E));
+  return moe_launch_sort(topk_ids, P, E, expert_offsets, sorted_pairs, pair_pos, hit_list, ws,
+                         (hipStream_t)stream);
+}
+
+static int experts_impl(const void* x, int x_dtype, const void* gu, int gu_fmt, const void* dn,
+                        int dn_fmt, const int32_t* offsets, const int32_t* sorted_pairs,
+                        const int32_t* hit_list, int T, int H, int I, int E, int K, int path,
+                        float* y, MoeWs& w, hipStream_t st) {
+  const int P = T * K;
+  const int max_hits = P < E ? P : E;
+  path = pick_path(path, T, gu_fmt);
+  if (path == MOE_PATH_GEMV) {
+    float* S = reinterpret_cast<float*>(w.take((size_t)P * I * 4));
+    if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+    MOE_TRY(moe_launch_gemv_gateup(x, x_dtype, gu, gu_fmt, offsets, sorted_pairs, hit_list, max_hits, H, I, K, S, st));
+    return moe_launch_gemv_down(S, dn, dn_fmt, offsets, hit_list, max_hits, H, I, y, st);
+  }
+  const int max_tiles = moe_max_mtiles(P, E);
+  int32_t* tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
+  uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
+  if (!tiles || !S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+  const size_t gu_row = gu_fmt == MOE_FMT_Q4_K ? (size_t)H / 256 * 144 : gu_fmt == MOE_FMT_Q6_K ? (size_t)H / 256 * 210 : (size_t)H * 2;
+  const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
+  const uint8_t* g = reinterpret_cast<const uint8_t*>(gu);
+  MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st));
+  const int opb = path == MOE_PATH_MFMA_BF16;
+  MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
+                                 max_tiles, T, offsets, sorted_pairs, K, H, I, opb, S, st));
+  return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, opb, y, st);
+}
+
+static int check_wfmt(int gu_fmt, int dn_fmt, const void* gu, const void* dn, const char* who) {
+  if (gu_fmt != MOE_FMT_Q4_K && gu_fmt != MOE_FMT_Q6_K && gu_fmt != MOE_FMT_BF16)
+    return moe_set_error(MOE_E_FORMAT, "%s: unsupported gate_up format %d", who, gu_fmt);
+  if (dn_fmt != MOE_FMT_Q4_K && dn_fmt != MOE_FMT_Q6_K && dn_fmt != MOE_FMT_BF16)
+    return moe_set_error(MOE_E_FORMAT, "%s: unsupported down format %d", who, dn_fmt);
+  if (!aligned16(gu) || !aligned16(dn)) return moe_set_error(MOE_E_ARG, "%s: expert weights must be 16-byte aligned", who);
+  return MOE_OK;
+}
+
+int moe_experts(const void* x, int x_dtype, const void* gate_up_q, int gate_up_fmt,
+                const void* down_q, int down_fmt, const int32_t* expert_offsets,
+                const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I, int E,
+                int K, int path, float* y, void* ws, size_t ws_bytes, void* stream) {
+  if (!x || !gate_up_q || !down_q || !expert_offsets || !sorted_pairs || !hit_list || !y)
+    return moe_set_error(MOE_E_ARG, "moe_experts: NULL pointer");
+  if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_experts: bad x_dtype %d", x_dtype);
+  MOE_TRY(check_geom(T, H, I, E, K, "moe_experts"));
+  MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, down_q, "moe_experts"));
+  if (path == MOE_PATH_GEMV && gate_up_fmt != MOE_FMT_Q4_K) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K gate_up only");
+  if (path == MOE_PATH_GEMV && down_fmt == MOE_FMT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K / Q6_K down only");
+  if (!aligned16(x)) return moe_set_error(MOE_E_ARG, "moe_experts: x must be 16-byte aligned");
+  MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+  return experts_impl(x, x_dtype, gate_up_q, gate_up_fmt, down_q, down_fmt, expert_offsets,
+                      sorted_pairs, hit_list, T, H, I, E, K, path, y, w, (hipStream_t)stream);
+}
+
+static int shared_impl(const void* x, int x_dtype, const void* wg, const void* wu, const void* wd,
+                       const void* wsg, int T, int H, int Is, int path, float* shared_raw,
+                       float* gate_prob, MoeWs& w, hipStream_t st) {
+  if (path == MOE_PATH_AUTO) path = T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
+  if (path == MOE_PATH_GEMV) {
+    float* s = reinterpret_cast<float*>(w.take((size_t)T * Is * 4));
+    if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+    return moe_launch_shared_gemv(x, x_dtype, wg, wu, wd, wsg, T, H, Is, s, shared_raw, gate_prob, st);
+  }
+  uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
+  if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+  const int opb = path == MOE_PATH_MFMA_BF16;
+  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, T, H, gate_prob, st));
+  MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, wg, wu, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, opb, s, st));
+  return moe_launch_gemm_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, opb, shared_raw, st);
+}
+
+int moe_shared_expert(const void* x, int x_dtype, const void* w_gate, const void* w_up,
+                      const void* w_down, const void* w_scalar_gate, int T, int H, int I_s,
+                      int path, float* shared_raw, float* gate_prob, void* ws, size_t ws_bytes,
+                      void* stream) {
+  if (!x || !w_gate || !w_up || !w_down || !w_scalar_gate || !shared_raw || !gate_prob)
+    return moe_set_error(MOE_E_ARG, "moe_shared_expert: NULL pointer");
+  if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_shared_expert: bad x_dtype %d", x_dtype);
+  if (T < 1 || H % 2048 || I_s % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_shared_expert: need T >= 1, H %% 2048 == 0, I_s %% 512 == 0");
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) || !aligned16(w_scalar_gate))
+    return moe_set_error(MOE_E_ARG, "moe_shared_expert: pointers must be 16-byte aligned");
+  MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+  return shared_impl(x, x_dtype, w_gate, w_up, w_down, w_scalar_gate, T, H, I_s, path, shared_raw,
+                     gate_prob, w, (hipStream_t)stream);
+}
+
+int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids,
+                const void* w_bf16, const float* shared_raw, const float* gate_prob, int T, int K,
+                int H, float* out, float* routed_sum, float* shared_out, float* expert_raw,
+                void* stream) {
+  if (!y || !pair_pos || !topk_ids || !w_bf16 || !shared_raw || !gate_prob || !out)
+    return moe_set_error(MOE_E_ARG, "moe_combine: NULL pointer");
+  if (T < 1 || K < 1 || K > 16 || H < 1) return moe_set_error(MOE_E_ARG, "moe_combine: bad shape");
+  return moe_launch_combine(y, pair_pos, topk_ids, reinterpret_cast<const uint16_t*>(w_bf16),
+                            shared_raw, gate_prob, T, K, H, out, routed_sum, shared_out,
+                            expert_raw, (hipStream_t)stream);
+}
+
+int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                      const void* w_router, const float* logit_bias, const void* gate_up_q,
+                      int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
+                      const void* ws_up, const void* ws_down, const void* ws_scalar_gate,
+                      int path, float* out, void* logits_bf16, int32_t* topk_ids,
+                      void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
+                      float* shared_out, float* gate_prob, float* expert_raw, void* ws,
+                      size_t ws_bytes, void* stream) {
+  if (!x || !w_router || !gate_up_q || !down_q || !ws_gate || !ws_up || !ws_down || !ws_scalar_gate || !out)
+    return moe_set_error(MOE_E_ARG, "moe_block_forward: NULL pointer");
+  if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_block_forward: bad x_dtype %d", x_dtype);
+  MOE_TRY(check_geom(T, H, I, E, K, "moe_block_forward"));
+  MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, down_q, "moe_block_forward"));
+  if (I_s % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_block_forward: need I_s %% 512 == 0");
+  if (!aligned16(x) || !aligned16(w_router) || !aligned16(ws_gate) || !aligned16(ws_up) || !aligned16(ws_down) || !aligned16(ws_scalar_gate))
+    return moe_set_error(MOE_E_ARG, "moe_block_forward: pointers must be 16-byte aligned");
+  const size_t need = moe_workspace_bytes(T, H, I, E, K, I_s);
+  if (!ws || ws_bytes < need) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace needs %zu bytes", need);
+  hipStream_t st = (hipStream_t)stream;
+  const int P = T * K;
+  MoeWs w{reinterpret_cast<char*>(ws), ws_bytes};
+  uint16_t* logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
+  int32_t* ids = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w.take((size_t)P * 4));
+  float* wf = topk_w_f32 ? topk_w_f32 : reinterpret_cast<float*>(w.take((size_t)P * 4));
+  uint16_t* wb = topk_w_bf16 ? reinterpret_cast<uint16_t*>(topk_w_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)P * 2));
+  int32_t* offsets = reinterpret_cast<int32_t*>(w.take((size_t)(E + 1) * 4));
+  int32_t* sorted = reinterpret_cast<int32_t*>(w.take((size_t)P * 4));
+  int32_t* pos = reinterpret_cast<int32_t*>(w.take((size_t)P * 4));
+  int32_t* hits = reinterpret_cast<int32_t*>(w.take((size_t)(E + 1) * 4));
+  void* sort_ws = w.take(moe_sort_ws_bytes(P, E));
+  float* y = reinterpret_cast<float*>(w.take((size_t)P * H * 4));
+  float* sraw = reinterpret_cast<float*>(w.take((size_t)T * H * 4));
+  float* gp = gate_prob ? gate_prob : reinterpret_cast<float*>(w.take((size_t)T * 4));
+  if (!logits || !ids || !wf || !wb || !offsets || !sorted || !pos || !hits || !y || !sraw || !gp)
+    return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, logit_bias, T, H, E, logits, st));
+  MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
+  MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
+  MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
+  MOE_TRY(shared_impl(x, x_dtype, ws_gate, ws_up, ws_down, ws_scalar_gate, T, H, I_s, path, sraw, gp, w2, st));
+  MOE_TRY(experts_impl(x, x_dtype, gate_up_q, gate_up_fmt, down_q, down_fmt, offsets, sorted, hits,
+                       T, H, I, E, K, path, y, w, st));
+  return moe_launch_combine(y, pos, ids, wb, sraw, gp, T, K, H, out, routed_sum, shared_out,
+                            expert_raw, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,68 @@
+// Shared device helpers for the gfx950 MoE library: bf16/f16 bit handling, wave64 reductions,
+// and the GGUF Q4_K / Q6_K element decode (GGUF layout as read by tools/gguf_reader.py:17-51).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MOE_WAVE 64
+
+// ------------------------------------------------------------------------------ bit handling --
+__device__ __forceinline__ float bf16_to_f32(uint32_t u16) { return __uint_as_float(u16 << 16); }
+
+// f32 -> bf16 round-to-nearest-even; NaN quieted to 0x7FC0 (prototype/moe_router/
+// moe_router_kernels.h:196-205 states the same RNE rule).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu)) return 0x7FC0u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t u16) {
+  _Float16 h;
+  uint16_t v = (uint16_t)u16;
+  __builtin_memcpy(&h, &v, 2);
+  return (float)h;                      // exact for every finite f16 pattern
+}
+
+// ------------------------------------------------------------------------- wave64 reductions --
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, MOE_WAVE);
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MOE_WAVE));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, MOE_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float silu_f32(float z) { return z / (1.0f + __expf(-z)); }
+
+// ----------------------------------------------------------------------------- Q4_K element --
+// 144-byte super-block: f16 d | f16 dmin | 12 B packed 6-bit (sc, m) x 8 | 128 B nibbles.
+// get_scale_min_k4 (tools/gguf_reader.py:165-175), with the 12 scale bytes held as 3 dwords
+// s0 = bytes 0..3, s1 = 4..7, s2 = 8..11:
+//   j < 4 : sc = byte(s0, j) & 63,                          m = byte(s1, j) & 63
+//   j >= 4: sc = (byte(s2, j-4) & 15) | ((byte(s0, j-4) >> 6) << 4)
+//           m  = (byte(s2, j-4) >> 4) | ((byte(s1, j-4) >> 6) << 4)
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                              uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = (s0 >> (8 * j)) & 63u;
+    m = (s1 >> (8 * j)) & 63u;
+  } else {
+    const int b = 8 * (j - 4);
+    const uint32_t hi = (s2 >> b) & 0xFFu;
+    sc = (hi & 15u) | (((s0 >> b) >> 6 & 3u) << 4);
+    m = (hi >> 4) | (((s1 >> b) >> 6 & 3u) << 4);
+  }
+}
+
+// Q6_K (210-byte super-block): ql[128] | qh[64] | int8 sc[16] | f16 d at byte 208.
+// Element e = 128g + 32k + l: q = ((ql[64g+32(k&1)+l] >> 4(k>>1)) & 15) | (((qh[32g+l] >> 2k) & 3)
+// << 4), value = d * sc[8g + 2k + (l>>4)] * (q - 32)   (tools/gguf_reader.py:299-322).

@@ -1,0 +1,79 @@
+// Internal declarations shared by the library's translation units (not part of the C-ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/moe_gfx950.h"
+
+// thread-local error text behind moe_last_error()
+int moe_set_error(int code, const char* fmt, ...);
+// checks hipGetLastError() after a launch; returns MOE_OK or MOE_E_HIP
+int moe_check_launch(const char* what);
+
+// ---- launch helpers (each returns MOE_OK or an error code) ----------------------------------
+int moe_launch_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
+                       hipStream_t st);
+
+int moe_launch_router_logits(const void* x, int x_dtype, const void* w, const float* bias, int T,
+                             int H, int E, uint16_t* logits, hipStream_t st);
+int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
+                          float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st);
+
+// sort / permute; ws must hold moe_sort_ws_bytes(P, E) bytes
+size_t moe_sort_ws_bytes(int P, int E);
+int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t* sorted_pairs,
+                    int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st);
+
+// MFMA tile list: [count, (expert, row0) x count], rows per tile = MOE_GEMM_BM
+#define MOE_GEMM_BM 64
+int moe_max_mtiles(int P, int E);
+int moe_launch_build_tiles(const int32_t* offsets, const int32_t* hit_list, int E, int P,
+                           int32_t* tiles, hipStream_t st);
+
+// decode GEMV path: S [P, I] f32 (sorted order), then y [P, H] f32
+int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gu, int fmt,
+                           const int32_t* offsets, const int32_t* sorted_pairs,
+                           const int32_t* hit_list, int max_hits, int H, int I, int K,
+                           float* S, hipStream_t st);
+int moe_launch_gemv_down(const float* S, const void* dn, int fmt, const int32_t* offsets,
+                         const int32_t* hit_list, int max_hits, int H, int I, float* y,
+                         hipStream_t st);
+
+// MFMA path. A rows come from x (gathered through sorted_pairs / K) or, with tiles == NULL,
+// are x rows / S rows 0..T-1 (the shared expert).
+// op_bf16 = 0: f16 MFMA operands (default), 1: bf16 operands. S holds 16-bit operands.
+int moe_launch_gemm_gateup(const void* x, int x_dtype, const void* w_gate, const void* w_up,
+                           int fmt, size_t expert_stride, const int32_t* tiles, int max_tiles,
+                           int T, const int32_t* offsets, const int32_t* sorted_pairs, int K,
+                           int H, int I, int op_bf16, uint16_t* S, hipStream_t st);
+int moe_launch_gemm_down(const uint16_t* S, const void* w_down, int fmt, size_t expert_stride,
+                         const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
+                         int H, int I, int op_bf16, float* y, hipStream_t st);
+
+// shared expert
+int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const void* wu,
+                           const void* wd, const void* wsg, int T, int H, int Is, float* s_tmp,
+                           float* shared_raw, float* gate_prob, hipStream_t st);
+int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int T, int H,
+                           float* gate_prob, hipStream_t st);
+
+// combine
+int moe_launch_combine(const float* y, const int32_t* pair_pos, const int32_t* ids,
+                       const uint16_t* w_bf16, const float* shared_raw, const float* gate_prob,
+                       int T, int K, int H, float* out, float* routed_sum, float* shared_out,
+                       float* expert_raw, hipStream_t st);
+
+// workspace carving
+struct MoeWs {
+  char* p;
+  size_t left;
+  void* take(size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes > left) return nullptr;
+    void* r = p;
+    p += bytes;
+    left -= bytes;
+    return r;
+  }
+};

@@ -1,0 +1,153 @@
+// Shared expert (bf16 weights) and its scalar sigmoid gate, decode path
+// (specification/11-moe-block.md §11.6; speccheck/moe_ref.py:480-495; engine/m3_forward.py:436-442).
+//   s[t,i] = silu(gate_i . x_t) * (up_i . x_t)        (f32)
+//   shared_raw[t,h] = down_h . s[t]                   (f32)
+//   gate_prob[t] = sigmoid(wsg . x_t)                 one scalar per token
+#include "common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+template <int XDT>
+__device__ __forceinline__ void load_x8(const void* x, size_t off, float* v) {
+  if (XDT == MOE_DT_F32) {
+    const float* p = reinterpret_cast<const float*>(x) + off;
+    float4 a = *reinterpret_cast<const float4*>(p);
+    float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    uint4 a = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + off);
+    const uint32_t aa[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf16_to_f32(aa[j] & 0xFFFFu);
+      v[2 * j + 1] = bf16_to_f32(aa[j] >> 16);
+    }
+  }
+}
+
+__device__ __forceinline__ float dot8_bf16(uint4 w, const float* x) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a = fmaf(bf16_to_f32(ww[j] & 0xFFFFu), x[2 * j], a);
+    a = fmaf(bf16_to_f32(ww[j] >> 16), x[2 * j + 1], a);
+  }
+  return a;
+}
+
+// grid (Is/4 + 1); wave w of block bx < Is/4 owns intermediate row i = 4*bx + w; the last block's
+// wave 0 computes the scalar gate. Rows are H bf16; lane covers cols 512*c + 8*lane + 0..7.
+template <int XDT>
+__global__ __launch_bounds__(256) void k_shared_gateup(const void* __restrict__ x,
+                                                        const uint16_t* __restrict__ wg,
+                                                        const uint16_t* __restrict__ wu,
+                                                        const uint16_t* __restrict__ wsg, int T,
+                                                        int H, int Is, float* __restrict__ s,
+                                                        float* __restrict__ gate_prob) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nc = H / 512;
+  if (blockIdx.x == Is / 4) {
+    if (wave != 0 || gate_prob == nullptr) return;
+    for (int t = 0; t < T; ++t) {
+      float a = 0.0f;
+      for (int c = 0; c < nc; ++c) {
+        float xv[8];
+        load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
+        a += dot8_bf16(*reinterpret_cast<const uint4*>(wsg + 512 * c + 8 * lane), xv);
+      }
+      a = wave_sum_f32(a);
+      if (lane == 0) gate_prob[t] = 1.0f / (1.0f + expf(-a));
+    }
+    return;
+  }
+  const int i = blockIdx.x * 4 + wave;
+  const uint16_t* gr = wg + (size_t)i * H;
+  const uint16_t* ur = wu + (size_t)i * H;
+  for (int t = 0; t < T; ++t) {
+    float ag = 0.0f, au = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+      float xv[8];
+      load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
+      ag += dot8_bf16(*reinterpret_cast<const uint4*>(gr + 512 * c + 8 * lane), xv);
+      au += dot8_bf16(*reinterpret_cast<const uint4*>(ur + 512 * c + 8 * lane), xv);
+    }
+    ag = wave_sum_f32(ag);
+    au = wave_sum_f32(au);
+    if (lane == 0) s[(size_t)t * Is + i] = silu_f32(ag) * au;
+  }
+}
+
+// grid (H/16); wave w owns rows 16*bx + 4w + (lane>>4); 16 lanes per row of Is bf16
+__global__ __launch_bounds__(256) void k_shared_down(const float* __restrict__ s,
+                                                      const uint16_t* __restrict__ wd, int T,
+                                                      int H, int Is,
+                                                      float* __restrict__ shared_raw) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15;
+  const int row = blockIdx.x * 16 + wave * 4 + (lane >> 4);
+  const uint16_t* dr = wd + (size_t)row * Is;
+  const int nc = Is / 128;
+  for (int t = 0; t < T; ++t) {
+    float a = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+      float sv[8];
+      load_x8<MOE_DT_F32>(s, (size_t)t * Is + 128 * c + 8 * l16, sv);
+      a += dot8_bf16(*reinterpret_cast<const uint4*>(dr + 128 * c + 8 * l16), sv);
+    }
+    a += __shfl_xor(a, 8, 64);
+    a += __shfl_xor(a, 4, 64);
+    a += __shfl_xor(a, 2, 64);
+    a += __shfl_xor(a, 1, 64);
+    if (l16 == 0) shared_raw[(size_t)t * H + row] = a;
+  }
+}
+
+// scalar gate only (used beside the MFMA path): one wave per token
+template <int XDT>
+__global__ __launch_bounds__(64) void k_shared_gate(const void* __restrict__ x,
+                                                     const uint16_t* __restrict__ wsg, int T, int H,
+                                                     float* __restrict__ gate_prob) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  float a = 0.0f;
+  for (int c = 0; c < H / 512; ++c) {
+    float xv[8];
+    load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
+    a += dot8_bf16(*reinterpret_cast<const uint4*>(wsg + 512 * c + 8 * lane), xv);
+  }
+  a = wave_sum_f32(a);
+  if (lane == 0) gate_prob[t] = 1.0f / (1.0f + expf(-a));
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const void* wu,
+                           const void* wd, const void* wsg, int T, int H, int Is, float* s_tmp,
+                           float* shared_raw, float* gate_prob, hipStream_t st) {
+  if (H % 512 || Is % 128 || H % 16 || Is % 4)
+    return moe_set_error(MOE_E_UNSUPPORTED, "shared GEMV needs H %% 512 == 0, Is %% 128 == 0");
+  const uint16_t* g = reinterpret_cast<const uint16_t*>(wg);
+  const uint16_t* u = reinterpret_cast<const uint16_t*>(wu);
+  const uint16_t* d = reinterpret_cast<const uint16_t*>(wd);
+  const uint16_t* sg = reinterpret_cast<const uint16_t*>(wsg);
+  if (x_dtype == MOE_DT_F32)
+    hipLaunchKernelGGL(k_shared_gateup<MOE_DT_F32>, dim3(Is / 4 + 1), dim3(256), 0, st, x, g, u, sg, T, H, Is, s_tmp, gate_prob);
+  else
+    hipLaunchKernelGGL(k_shared_gateup<MOE_DT_BF16>, dim3(Is / 4 + 1), dim3(256), 0, st, x, g, u, sg, T, H, Is, s_tmp, gate_prob);
+  hipLaunchKernelGGL(k_shared_down, dim3(H / 16), dim3(256), 0, st, s_tmp, d, T, H, Is, shared_raw);
+  return moe_check_launch("shared_gemv");
+}
+
+int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int T, int H,
+                           float* gate_prob, hipStream_t st) {
+  const uint16_t* sg = reinterpret_cast<const uint16_t*>(wsg);
+  if (x_dtype == MOE_DT_F32)
+    hipLaunchKernelGGL(k_shared_gate<MOE_DT_F32>, dim3(T), dim3(64), 0, st, x, sg, T, H, gate_prob);
+  else
+    hipLaunchKernelGGL(k_shared_gate<MOE_DT_BF16>, dim3(T), dim3(64), 0, st, x, sg, T, H, gate_prob);
+  return moe_check_launch("shared_gate");
+}

@@ -1,0 +1,230 @@
+// Stable token->expert grouping (speccheck/moe_ref.py:433-439 grouped form; engine/m3_forward.py:
+// 448-452): pairs p = t*K + k ordered by expert id, equal ids in ascending p — the permutation
+// torch.argsort(ids.flatten(), stable=True) returns. Integer work only, so bit-exact by design.
+//
+// P <= 64 (decode): one wave ranks every pair directly.
+// Otherwise: per-chunk histograms -> one-block scan -> per-chunk stable scatter, where ranks
+// inside a 256-pair round come from wave-level id matching (8 ballots on the id bits) and a
+// per-wave count table, so no atomics decide any position.
+#include "common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+constexpr int kChunk = 1024;   // pairs per scatter block
+
+__global__ __launch_bounds__(64) void k_sort_small(const int32_t* __restrict__ ids, int P, int E,
+                                                   int32_t* __restrict__ offsets,
+                                                   int32_t* __restrict__ sorted_pairs,
+                                                   int32_t* __restrict__ pair_pos,
+                                                   int32_t* __restrict__ hit_list) {
+  __shared__ int sid[64];
+  __shared__ int sfirst[64];
+  const int lane = threadIdx.x;
+  int e = lane < P ? ids[lane] : 0x7FFFFFFF;
+  const bool valid = lane < P && e >= 0 && e < E;   // out-of-range ids are dropped, never indexed
+  if (!valid) e = 0x7FFFFFFF;
+  sid[lane] = e;
+  __syncthreads();
+  int rank = 0;
+  bool first = valid;
+  for (int q = 0; q < P; ++q) {
+    const int o = sid[q];
+    rank += (o < e) || (o == e && q < lane);
+    if (o == e && q < lane) first = false;
+  }
+  sfirst[lane] = first ? 1 : 0;
+  if (valid) {
+    sorted_pairs[rank] = lane;
+    pair_pos[lane] = rank;
+  } else if (lane < P) {
+    pair_pos[lane] = -1;
+  }
+  __syncthreads();
+  // hit list: distinct ids ascending
+  int dist_below = 0, nhit = 0;
+  for (int q = 0; q < P; ++q) {
+    if (sfirst[q]) {
+      ++nhit;
+      if (sid[q] < e) ++dist_below;
+    }
+  }
+  if (first) hit_list[1 + dist_below] = e;
+  if (lane == 0) hit_list[0] = nhit;
+  // offsets[x] = # pairs with id < x
+  for (int x = lane; x <= E; x += 64) {
+    int c = 0;
+    for (int q = 0; q < P; ++q) c += sid[q] < x;
+    offsets[x] = c;
+  }
+}
+
+// phase 1: histogram of each chunk -> hist[chunk][E]
+__global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ ids, int P, int E,
+                                                   int32_t* __restrict__ hist) {
+  __shared__ int h[256];
+  for (int i = threadIdx.x; i < E; i += 256) h[i] = 0;
+  __syncthreads();
+  const int base = blockIdx.x * kChunk;
+  for (int i = threadIdx.x; i < kChunk; i += 256) {
+    const int p = base + i;
+    if (p < P) {
+      const int e = ids[p];
+      if (e >= 0 && e < E) atomicAdd(&h[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < E; i += 256) hist[(size_t)blockIdx.x * E + i] = h[i];
+}
+
+// block-wide exclusive scan of one int per thread (256 threads)
+__device__ int block_exclusive_scan(int v, int* tmp, int* total) {
+  const int tid = threadIdx.x;
+  tmp[tid] = v;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    int add = tid >= o ? tmp[tid - o] : 0;
+    __syncthreads();
+    tmp[tid] += add;
+    __syncthreads();
+  }
+  const int incl = tmp[tid];
+  *total = tmp[255];
+  __syncthreads();
+  return incl - v;
+}
+
+// phase 2 (one block): expert totals, offsets, hit list; hist[c][e] becomes the start position of
+// chunk c's pairs of expert e.
+__global__ __launch_bounds__(256) void k_sort_scan(int32_t* __restrict__ hist, int nchunks, int P,
+                                                   int E, int32_t* __restrict__ offsets,
+                                                   int32_t* __restrict__ hit_list) {
+  __shared__ int tmp[256];
+  const int e = threadIdx.x;
+  int tot = 0;
+  if (e < E)
+    for (int c = 0; c < nchunks; ++c) tot += hist[(size_t)c * E + e];
+  int tsum;
+  const int base = block_exclusive_scan(e < E ? tot : 0, tmp, &tsum);
+  if (e < E) {
+    offsets[e] = base;
+    int run = base;
+    for (int c = 0; c < nchunks; ++c) {
+      const int v = hist[(size_t)c * E + e];
+      hist[(size_t)c * E + e] = run;
+      run += v;
+    }
+  }
+  if (e == 0) offsets[E] = tsum;   // == P unless out-of-range ids were dropped
+  int hsum;
+  const int hidx = block_exclusive_scan((e < E && tot > 0) ? 1 : 0, tmp, &hsum);
+  if (e < E && tot > 0) hit_list[1 + hidx] = e;
+  if (e == 0) hit_list[0] = hsum;
+}
+
+// phase 3: stable scatter of each chunk
+__global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int P,
+                                                      int E, const int32_t* __restrict__ start,
+                                                      int32_t* __restrict__ sorted_pairs,
+                                                      int32_t* __restrict__ pair_pos) {
+  __shared__ int run[256];
+  __shared__ int wcnt[4][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < 256; i += 256) run[i] = 0;
+  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+  const int base = blockIdx.x * kChunk;
+  for (int r = 0; r < kChunk; r += 256) {
+    for (int i = tid; i < 4 * 256; i += 256) (&wcnt[0][0])[i] = 0;
+    __syncthreads();
+    const int p = base + r + tid;
+    int e = p < P ? ids[p] : 0;
+    const bool valid = p < P && e >= 0 && e < E;
+    if (!valid) e = 0;
+    if (p < P && !valid) pair_pos[p] = -1;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank_w = __popcll(peers & lt);
+    const bool leader = valid && rank_w == 0;
+    if (leader) wcnt[wave][e] = __popcll(peers);
+    __syncthreads();
+    int dest = 0;
+    if (valid) {
+      int before = 0;
+      for (int w2 = 0; w2 < wave; ++w2) before += wcnt[w2][e];
+      dest = start[(size_t)blockIdx.x * E + e] + run[e] + before + rank_w;
+      sorted_pairs[dest] = p;
+      pair_pos[p] = dest;
+    }
+    __syncthreads();
+    if (leader) atomicAdd(&run[e], __popcll(peers));
+    __syncthreads();
+  }
+}
+
+// MFMA work list: for every hit expert (ascending) ceil(n_e / BM) tiles of BM sorted rows.
+__global__ __launch_bounds__(256) void k_build_tiles(const int32_t* __restrict__ offsets,
+                                                     const int32_t* __restrict__ hit_list,
+                                                     int32_t* __restrict__ tiles) {
+  __shared__ int tmp[256];
+  const int nhit = hit_list[0];
+  int written = 0;
+  for (int h0 = 0; h0 < nhit; h0 += 256) {
+    const int h = h0 + threadIdx.x;
+    int e = 0, n = 0;
+    if (h < nhit) {
+      e = hit_list[1 + h];
+      n = (offsets[e + 1] - offsets[e] + MOE_GEMM_BM - 1) / MOE_GEMM_BM;
+    }
+    int tot;
+    const int pre = block_exclusive_scan(n, tmp, &tot);
+    for (int i = 0; i < n; ++i) {
+      tiles[1 + 2 * (written + pre + i)] = e;
+      tiles[2 + 2 * (written + pre + i)] = offsets[e] + i * MOE_GEMM_BM;
+    }
+    written += tot;
+  }
+  if (threadIdx.x == 0) tiles[0] = written;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+size_t moe_sort_ws_bytes(int P, int E) {
+  const size_t nchunks = (size_t)(P + kChunk - 1) / kChunk;
+  return (nchunks * E * sizeof(int32_t) + 255) & ~size_t(255);
+}
+
+int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t* sorted_pairs,
+                    int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st) {
+  if (P <= 64) {
+    hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(64), 0, st, ids, P, E, offsets, sorted_pairs,
+                       pair_pos, hit_list);
+    return moe_check_launch("sort_small");
+  }
+  const int nchunks = (P + kChunk - 1) / kChunk;
+  int32_t* hist = reinterpret_cast<int32_t*>(ws);
+  hipLaunchKernelGGL(k_sort_hist, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist);
+  hipLaunchKernelGGL(k_sort_scan, dim3(1), dim3(256), 0, st, hist, nchunks, P, E, offsets, hit_list);
+  hipLaunchKernelGGL(k_sort_scatter, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, sorted_pairs,
+                     pair_pos);
+  return moe_check_launch("sort");
+}
+
+int moe_max_mtiles(int P, int E) {
+  const int hits = P < E ? P : E;
+  return (P + MOE_GEMM_BM - 1) / MOE_GEMM_BM + hits;
+}
+
+int moe_launch_build_tiles(const int32_t* offsets, const int32_t* hit_list, int E, int P,
+                           int32_t* tiles, hipStream_t st) {
+  (void)E;
+  (void)P;
+  hipLaunchKernelGGL(k_build_tiles, dim3(1), dim3(256), 0, st, offsets, hit_list, tiles);
+  return moe_check_launch("build_tiles");
+}

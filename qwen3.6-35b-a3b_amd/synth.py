@@ -1,0 +1,93 @@
+"""Seeded synthetic weights and inputs of the real architecture, for tests and the benchmark
+(N(0, 0.02) weights quantized by quant.py, N(0, 1) activations).
+
+Generation runs on whatever device is asked for (the benchmark generates its 40 x 256 Q4_K
+experts on the GPU, chunk by chunk); every draw comes from a private torch.Generator seeded from
+the config's seed, so a config is the same bytes every time on the same device type.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import quant as Q
+from .weights import LayerWeights
+
+
+def zipf_bias(n_experts: int, seed: int, s: float = 1.1, device="cpu") -> torch.Tensor:
+    """Per-expert router logit bias b_e = ln(r_e^-s / sum_r r^-s) over a seeded permutation of
+    the ranks 1..E: softmax of the bias alone is a Zipf(s) law, so routing is skewed."""
+    g = torch.Generator(device="cpu").manual_seed(seed + 7919)
+    ranks = torch.randperm(n_experts, generator=g).to(torch.float64) + 1.0
+    w = ranks.pow(-s)
+    return torch.log(w / w.sum()).to(torch.float32).to(device)
+
+
+def make_layer(seed: int, device="cuda", gate_up_fmt: int = Q.FMT_Q4_K,
+               down_fmt: int = Q.FMT_Q4_K, zipf: bool = False, n_experts: int = 256,
+               hidden: int = 2048, i_e: int = 512, i_s: int = 512, top_k: int = 8,
+               std: float = 0.02, chunk: int = 16) -> LayerWeights:
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std
+
+    router = randn(n_experts, hidden).to(torch.bfloat16)
+    gu_row = Q.row_bytes(gate_up_fmt, hidden)
+    dn_row = Q.row_bytes(down_fmt, i_e)
+    gate_up = torch.empty(n_experts, 2 * i_e, gu_row, dtype=torch.uint8, device=dev)
+    down = torch.empty(n_experts, hidden, dn_row, dtype=torch.uint8, device=dev)
+    for e0 in range(0, n_experts, chunk):
+        n = min(chunk, n_experts - e0)
+        w = randn(n, 2 * i_e, hidden)
+        gate_up[e0:e0 + n] = Q.quantize(w.reshape(-1, hidden), gate_up_fmt).view(n, 2 * i_e, gu_row)
+        del w
+        w = randn(n, hidden, i_e)
+        down[e0:e0 + n] = Q.quantize(w.reshape(-1, i_e), down_fmt).view(n, hidden, dn_row)
+        del w
+    lw = LayerWeights(
+        router=router, gate_up_q=gate_up, gate_up_fmt=gate_up_fmt, down_q=down, down_fmt=down_fmt,
+        shared_gate=randn(i_s, hidden).to(torch.bfloat16),
+        shared_up=randn(i_s, hidden).to(torch.bfloat16),
+        shared_down=randn(hidden, i_s).to(torch.bfloat16),
+        shared_scalar_gate=randn(1, hidden).to(torch.bfloat16),
+        router_bias=zipf_bias(n_experts, seed, device=dev) if zipf else None,
+        top_k=top_k)
+    lw.validate()
+    return lw
+
+
+def make_input(n_tokens: int, seed: int, device="cuda", dtype=torch.float32,
+               hidden: int = 2048) -> torch.Tensor:
+    """x ~ N(0, 1) f32 [T, H] from a private generator; cast to `dtype` (bf16 for prefill)."""
+    g = torch.Generator(device=torch.device(device)).manual_seed(seed + 104729)
+    x = torch.randn(n_tokens, hidden, generator=g, device=device, dtype=torch.float32)
+    return x.to(dtype)
+
+
+def rms_normalize(x: torch.Tensor) -> torch.Tensor:
+    """Rows rescaled to RMS 1 (the block input is a post-attention RMSNorm output; used to chain
+    layer outputs into the next layer's input in the decode benchmark)."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + 1e-6)).to(x.dtype)
+
+
+def decode_active_bytes(lw: LayerWeights) -> int:
+    """Bytes of the 8 routed + 1 shared active experts per token-layer (20,447,232)."""
+    return lw.top_k * lw.routed_bytes_per_expert() + lw.shared_bytes()
+
+
+def prefill_flops(T: int, lw: LayerWeights) -> float:
+    """Routed + shared expert FLOPs of a T-token step (2 FLOP per MAC)."""
+    per_expert = 3 * lw.i_e * lw.hidden
+    shared = 3 * lw.i_s * lw.hidden
+    return 2.0 * T * (lw.top_k * per_expert + shared)
+
+
+def router_flops(T: int, lw: LayerWeights) -> float:
+    return 2.0 * T * lw.n_experts * lw.hidden
+
+
+_ = math

@@ -1,0 +1,73 @@
+"""The C-ABI library loads, exports every symbol the header declares, and refuses bad arguments
+before touching a device (no GPU needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "moe_gfx950.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound(pkg):
+    lib = ctypes.CDLL(str(pkg._lib.LIB_PATH))
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(pkg._lib.SIGNATURES), set(names) ^ set(pkg._lib.SIGNATURES)
+
+
+def test_abi_version_and_enums_match_header(pkg):
+    text = HEADER.read_text()
+    assert pkg._lib.lib.moe_abi_version() == int(re.search(r"MOE_ABI_VERSION (\d+)", text).group(1))
+    for name in ("MOE_OK", "MOE_E_ARG", "MOE_E_FORMAT", "MOE_E_HIP", "MOE_E_WORKSPACE",
+                 "MOE_E_UNSUPPORTED", "MOE_DT_F32", "MOE_DT_BF16", "MOE_FMT_Q4_K", "MOE_FMT_Q6_K",
+                 "MOE_FMT_BF16", "MOE_PATH_AUTO", "MOE_PATH_GEMV", "MOE_PATH_MFMA",
+                 "MOE_PATH_MFMA_BF16"):
+        m = re.search(name + r"\s*=\s*(-?\d+)", text)
+        assert m and int(m.group(1)) == getattr(pkg._lib, name), name
+
+
+def test_workspace_bytes_is_monotone(pkg):
+    f = pkg._lib.lib.moe_workspace_bytes
+    a = f(1, 2048, 512, 256, 8, 512)
+    b = f(64, 2048, 512, 256, 8, 512)
+    c = f(4096, 2048, 512, 256, 8, 512)
+    assert 0 < a < b < c
+    # y [T*K, H] f32 dominates at prefill sizes
+    assert c >= 4096 * 8 * 2048 * 4
+    assert f(0, 2048, 512, 256, 8, 512) == 0
+
+
+def test_refusals_happen_on_the_host(pkg):
+    lib = pkg._lib.lib
+    # NULL pointers -> MOE_E_ARG with a message, no device call made
+    assert lib.moe_dequant(None, 12, 256, None, 0, None) == pkg._lib.MOE_E_ARG
+    assert b"NULL" in lib.moe_last_error()
+    buf = ctypes.create_string_buffer(4096)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.moe_dequant(p, 12, 100, p, 0, None) == pkg._lib.MOE_E_ARG       # not a multiple of 256
+    assert lib.moe_dequant(p, 12, 256, p, 5, None) == pkg._lib.MOE_E_ARG       # bad out dtype
+    # geometry refusals
+    rc = lib.moe_router_topk(p, 0, p, None, 1, 2048, 256, 2, p, None, p, p, p, None, 0, None)
+    assert rc == pkg._lib.MOE_E_UNSUPPORTED                                  # K*64 <= E
+    assert b"K*64 > E" in lib.moe_last_error()
+    rc = lib.moe_block_forward(p, 0, 1, 2048, 512, 256, 8, 512, p, None, p, 12, p, 12, p, p, p, p,
+                               0, p, None, None, None, None, None, None, None, None, p, 16, None)
+    assert rc == pkg._lib.MOE_E_WORKSPACE
+    rc = lib.moe_experts(p, 0, p, 99, p, 12, p, p, p, 1, 2048, 512, 256, 8, 0, p, p, 1 << 20, None)
+    assert rc == pkg._lib.MOE_E_FORMAT
+
+
+def test_product_path_never_imports_the_oracle():
+    """The package must not import, call or fall back to anything under oracle/."""
+    for f in (ROOT / "qwen3.6-35b-a3b_amd").rglob("*.py"):
+        src = f.read_text()
+        assert "oracle" not in re.sub(r'""".*?"""', "", src, flags=re.S), f

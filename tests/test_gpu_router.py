@@ -1,0 +1,96 @@
+"""R1 logits bit-exact vs the correctly rounded oracle; R3 ids bit-exact vs torch's CPU topk,
+including tie-laden rows and the heap-select branch; R4/R5 weights within f32 rounding."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from oracle import topk_model as TM
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_route(pkg, x, w_router, bias, K=8):
+    r = pkg.abi.router_topk(x, w_router, K, bias, want_probs=True)
+    torch.cuda.synchronize()
+    ref_logits, _ = O.r1_logits(x.cpu(), w_router.cpu(), None if bias is None else bias.cpu())
+    got_logits = r["router_logits"].cpu()
+    assert torch.equal(got_logits.view(torch.int16), ref_logits.view(torch.int16)), \
+        f"{(got_logits != ref_logits).sum().item()} logits differ"
+    # R2/R3 on the (identical) logits: torch CPU softmax + topk are the reference
+    probs = torch.softmax(ref_logits.float(), dim=-1)
+    vals, ids = torch.topk(probs, K, dim=-1)
+    got_ids = r["topk_ids"].cpu().long()
+    bad = (got_ids != ids).any(dim=-1)
+    assert not bad.any(), f"ids differ on {bad.sum().item()} of {len(bad)} rows; first {bad.nonzero()[:5].flatten().tolist()}"
+    # probabilities: same function, different exp implementation -> a few f32 ulps
+    assert torch.allclose(r["router_probs"].cpu(), probs, rtol=2e-6, atol=1e-9)
+    wpre = vals / vals.sum(-1, keepdim=True)
+    assert torch.allclose(r["topk_weights_f32"].cpu(), wpre, rtol=4e-6, atol=0)
+    # R5: bf16 of wpre; equal unless the f32 value sits within a few ulps of a rounding boundary
+    wb = r["topk_weights"].cpu()
+    diff = (wb.float() != wpre.to(torch.bfloat16).float())
+    if diff.any():
+        b = wpre[diff].view(torch.int32) & 0xFFFF
+        assert ((b - 0x8000).abs() < 64).all(), "bf16 weight differs away from a rounding boundary"
+    return r, got_ids
+
+
+def test_router_decode_c0(pkg, layer_c0, dev):
+    lw, _ = layer_c0
+    x = pkg.synth.make_input(1, seed=0, device=dev)
+    _check_route(pkg, x, lw.router, None)
+
+
+@pytest.mark.parametrize("T,dtype", [(8, torch.float32), (9, torch.float32), (64, torch.float32),
+                                     (300, torch.bfloat16), (4096, torch.bfloat16)])
+def test_router_batched(pkg, layer_c0, dev, T, dtype):
+    lw, _ = layer_c0
+    x = pkg.synth.make_input(T, seed=T, device=dev, dtype=dtype)
+    _check_route(pkg, x, lw.router, None)
+
+
+def test_router_zipf_bias(pkg, layer_zipf, dev):
+    lw, _ = layer_zipf
+    x = pkg.synth.make_input(64, seed=1, device=dev)
+    _check_route(pkg, x, lw.router, lw.router_bias)
+
+
+@pytest.mark.parametrize("T", [1, 64, 700])
+def test_router_tie_laden_rows(pkg, dev, T):
+    """Router rows drawn from 3 distinct rows: logits repeat exactly, so nearly every row has
+    ties inside the top 8 and across the 8/9 boundary; ids must follow torch's tie order."""
+    g = torch.Generator().manual_seed(11 + T)
+    base = (torch.randn(3, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    assign = torch.randint(0, 3, (256,), generator=g)
+    w = base[assign].contiguous().to(dev)
+    x = torch.randn(T, 2048, generator=g).to(dev)
+    _check_route(pkg, x, w, None)
+
+
+def test_router_midpoint_logits_round_to_even(pkg, dev):
+    """Logits that are exact bf16 midpoints (1 + 2^-8 -> 1.0, ties to even) and just above one
+    (-> 1 + 2^-7): the certified path must fall back and decide exactly."""
+    H = 2048
+    x = torch.zeros(2, H)
+    x[0, 0], x[0, 1] = 1.0, 2.0 ** -8
+    x[1, 0], x[1, 1], x[1, 2] = 1.0, 2.0 ** -8, 2.0 ** -40
+    w = torch.zeros(256, H)
+    w[:, 0:3] = 1.0
+    r = pkg.abi.router_topk(x.to(dev), w.to(torch.bfloat16).to(dev), 8)
+    lg = r["router_logits"].cpu().float()
+    assert (lg[0] == 1.0).all()
+    assert (lg[1] == 1.0 + 2.0 ** -7).all()
+
+
+def test_router_heap_select_branch(pkg, dev):
+    """An adversarial row drives libstdc++'s introselect into heap-select; inject it as logits
+    through the bias with a zero router matrix."""
+    vals = TM.adversarial_row(256, 8, start=-40.0)
+    ids_model, heap = TM.torch_cpu_topk(vals, 8)
+    assert heap
+    bias = torch.tensor(vals, dtype=torch.float32)
+    x = torch.randn(1, 2048)
+    w = torch.zeros(256, 2048, dtype=torch.bfloat16)
+    r, got = _check_route(pkg, x.to(dev), w.to(dev), bias.to(dev))
+    assert got[0].tolist() == ids_model

@@ -1,0 +1,112 @@
+"""Closed-form pins of the oracle's MoE block (CPU only, small synthetic geometry)."""
+import importlib.util
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from oracle import ggml_quant as GQ
+from oracle import moe_oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+_spec = importlib.util.spec_from_file_location("q_", ROOT / "qwen3.6-35b-a3b_amd" / "quant.py")
+Q = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(Q)
+
+E, H, I, K = 16, 256, 256, 8
+
+
+def _layer(seed, gu=None, dn=None, zero_scalar_gate=False):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g) * 0.05
+    gu = r(E, 2 * I, H) if gu is None else gu
+    dn = r(E, H, I) if dn is None else dn
+    return O.LayerWeights(
+        router=r(E, H).to(torch.bfloat16),
+        gate_up_q=Q.quantize(gu.reshape(-1, H), Q.FMT_Q4_K).numpy().reshape(E, 2 * I, -1),
+        gate_up_fmt=Q.FMT_Q4_K,
+        down_q=Q.quantize(dn.reshape(-1, I), Q.FMT_Q6_K).numpy().reshape(E, H, -1),
+        down_fmt=Q.FMT_Q6_K,
+        shared_gate=r(I, H).to(torch.bfloat16), shared_up=r(I, H).to(torch.bfloat16),
+        shared_down=r(H, I).to(torch.bfloat16),
+        shared_scalar_gate=torch.zeros(1, H, dtype=torch.bfloat16) if zero_scalar_gate
+        else r(1, H).to(torch.bfloat16))
+
+
+def test_identical_experts_make_routing_irrelevant():
+    """With every expert equal, routed = expert(x) whatever the routing (weights sum to 1 up to
+    the bf16 cast of each weight)."""
+    g = torch.Generator().manual_seed(1)
+    gu1 = torch.randn(1, 2 * I, H, generator=g) * 0.05
+    dn1 = torch.randn(1, H, I, generator=g) * 0.05
+    lw = _layer(2, gu=gu1.expand(E, -1, -1).contiguous(), dn=dn1.expand(E, -1, -1).contiguous())
+    x = torch.randn(5, H, generator=g)
+    out = O.moe_block(x, lw, K)
+    gu, dn = lw.expert_f32(0)
+    single = O.expert_apply(x, gu, dn)
+    wsum = out["topk_weights"].float().sum(-1, keepdim=True)
+    assert torch.allclose(out["routed_sum"], single * wsum, rtol=1e-4, atol=1e-6)
+
+
+def test_zero_experts_and_zero_shared_give_zero():
+    lw = _layer(3, gu=torch.zeros(E, 2 * I, H), dn=torch.zeros(E, H, I))
+    lw.shared_down = torch.zeros(H, I, dtype=torch.bfloat16)
+    x = torch.randn(4, H)
+    out = O.moe_block(x, lw, K)
+    assert torch.count_nonzero(out["combined_out"]) == 0
+
+
+def test_scalar_gate_zero_is_one_half():
+    lw = _layer(4, zero_scalar_gate=True)
+    x = torch.randn(3, H)
+    s = O.shared_expert(x, lw)
+    assert torch.all(s["shared_gate_prob"] == 0.5)
+    assert torch.equal(s["shared_out"], 0.5 * s["shared_raw"])
+
+
+def test_gate_first_split_is_observable():
+    """Swapping the gate and up halves changes the expert output (spec §11.4): the oracle's
+    chunk(2) order is a tested fact, not a convention that could silently flip."""
+    lw = _layer(5)
+    x = torch.randn(2, H)
+    gu, dn = lw.expert_f32(3)
+    good = O.expert_apply(x, gu, dn)
+    swapped = O.expert_apply(x, torch.cat([gu[I:], gu[:I]]), dn)
+    assert (good - swapped).abs().max() > 1e-3
+
+
+def test_expert_apply_matches_one_hot_closed_form():
+    """x = e_j: gate = W_gate[:, j], up = W_up[:, j], so y = W_down @ (silu(W_g[:,j]) * W_u[:,j])."""
+    lw = _layer(6)
+    gu, dn = lw.expert_f32(2)
+    j = 37
+    x = torch.zeros(1, H)
+    x[0, j] = 1.0
+    y = O.expert_apply(x, gu, dn)[0]
+    want = dn.double() @ (torch.nn.functional.silu(gu[:I, j].double()) * gu[I:, j].double())
+    assert torch.allclose(y.double(), want, rtol=1e-5, atol=1e-7)
+
+
+def test_all_experts_selected_when_k_equals_e():
+    """E = K: every expert is selected and the weights are the full softmax, renormalised."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(4, H, generator=g)
+    w = (torch.randn(8, H, generator=g) * 0.05).to(torch.bfloat16)
+    r = O.route(x, w, 8)
+    assert torch.equal(torch.sort(r["topk_ids"], -1).values, torch.arange(8).expand(4, 8))
+    assert torch.allclose(r["topk_weights_f32"].sum(-1), torch.ones(4), atol=1e-6)
+
+
+def test_combine_is_ascending_expert_order_with_rank_weights():
+    """routed[t] = sum over ascending expert id of w[t, rank] * raw[t, rank]; a combine that used
+    the expert id to index w would differ (weights are distinct by construction)."""
+    lw = _layer(8)
+    x = torch.randn(6, H)
+    r = O.route(x, lw.router, K)
+    e = O.experts_and_combine(x, r["topk_ids"], r["topk_weights"], lw)
+    raw, w = e["expert_raw"], r["topk_weights"].float()
+    want = (raw * w[..., None]).double().sum(1)
+    assert torch.allclose(e["routed_sum"].double(), want, rtol=1e-5, atol=1e-7)
+    w_by_id = torch.gather(w, 1, (r["topk_ids"] % K))
+    wrong = (raw * w_by_id[..., None]).double().sum(1)
+    assert (wrong - want).abs().max() > 1e-4
