@@ -82,14 +82,12 @@ def main():
     log(f"generated {L} layers ({resident / 1e9:.2f} GB routed Q4_K) in {time.time() - t0:.1f}s")
     x0 = synth.make_input(1, seed=0, device=dev)
     xbuf = x0.clone()
-    outs = [torch.empty(1, 2048, dtype=torch.float32, device=dev) for _ in range(L)]
 
     def one_token():
-        x = xbuf
-        for l, lw in enumerate(layers):
-            abi.block_forward(x, lw, out=outs[l])
-            x = x + outs[l]
-        xbuf.copy_(synth.rms_normalize(x))
+        # the residual stream through 40 layers, updated in place by the block's own residual add
+        for lw in layers:
+            abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf)
+        xbuf.copy_(synth.rms_normalize(xbuf))
 
     for _ in range(3):
         one_token()
@@ -181,7 +179,8 @@ def main():
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K, N(0,1) activations)",
         "config": {"workload": f"config 1: decode bs=1, {L} resident layer instances, "
-                               f"{args.steps} sequential tokens", "layers": L,
+                               f"{args.steps} sequential tokens (x <- x + MoE(x) per layer, "
+                               "RMS-renormalised per token)", "layers": L,
                    "tokens": args.steps, "experts": 256, "top_k": 8, "hidden": 2048,
                    "moe_intermediate": 512, "format": "Q4_K"},
         "decode_hbm_gbps": round(gbps, 1),

@@ -46,8 +46,11 @@ enum { MOE_FMT_Q4_K = 12, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
 
 /* expert contraction path: GEMV = fused decode + f32 GEMV; MFMA = tiles decoded to f16 in LDS on
  * MFMA (f32 accumulation); MFMA_BF16 = the same with bf16 operands (8 significant bits instead of
- * 11; same MFMA rate; block outputs ~3e-3 from the f32 oracle instead of ~4e-4). */
-enum { MOE_PATH_AUTO = 0, MOE_PATH_GEMV = 1, MOE_PATH_MFMA = 2, MOE_PATH_MFMA_BF16 = 3 };
+ * 11; same MFMA rate; block outputs ~3e-3 from the f32 oracle instead of ~4e-4). A single-token
+ * moe_block_forward on the GEMV path runs one persistent launch on devices with >= 256 CUs;
+ * GEMV_MULTI forces the three-launch form of the same arithmetic (any CU count). */
+enum { MOE_PATH_AUTO = 0, MOE_PATH_GEMV = 1, MOE_PATH_MFMA = 2, MOE_PATH_MFMA_BF16 = 3,
+       MOE_PATH_GEMV_MULTI = 4 };
 
 int moe_abi_version(void);
 const char *moe_last_error(void);
@@ -115,16 +118,25 @@ int moe_combine(const float *y, const int32_t *pair_pos, const int32_t *topk_ids
                 void *stream);
 
 /* The whole block in one stream-ordered call. Replaces speccheck/moe_ref.py:499-533 (moe_block),
- * engine/block_forward.py:670-681 and engine/m3_forward.py:430-476. Stage outputs other than
- * `out` may be NULL. */
+ * engine/block_forward.py:670-681 and engine/m3_forward.py:430-476. out = residual + MoE(x) when
+ * `residual` [T,H] f32 is given (the decoder layer's own residual add, engine/m3_forward.py:737;
+ * out may alias residual), else MoE(x). Stage outputs other than `out` may be NULL; expert_raw is
+ * [T,K,H] in slot order. A single token with K = 8 and Q4_K gate_up runs the fused three-launch
+ * decode path. */
 int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
                       const void *w_router, const float *logit_bias, const void *gate_up_q,
                       int gate_up_fmt, const void *down_q, int down_fmt, const void *ws_gate,
                       const void *ws_up, const void *ws_down, const void *ws_scalar_gate,
-                      int path, float *out, void *logits_bf16, int32_t *topk_ids,
-                      void *topk_w_bf16, float *topk_w_f32, float *routed_sum,
-                      float *shared_out, float *gate_prob, float *expert_raw, void *ws,
-                      size_t ws_bytes, void *stream);
+                      int path, const float *residual, float *out, void *logits_bf16,
+                      int32_t *topk_ids, void *topk_w_bf16, float *topk_w_f32,
+                      float *routed_sum, float *shared_out, float *gate_prob, float *expert_raw,
+                      void *ws, size_t ws_bytes, void *stream);
+
+/* Zero the workspace's device-side sync words (its first 64 KiB). Call once after allocating
+ * a workspace, before its first use by moe_block_forward / moe_experts / moe_shared_expert /
+ * moe_router_topk; every call leaves the words zero again. Calls sharing one workspace must be
+ * ordered on one stream. No counterpart in the reference (its device work ran in fresh processes). */
+int moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,7 @@ MOE_PATH_AUTO = 0
 MOE_PATH_GEMV = 1
 MOE_PATH_MFMA = 2
 MOE_PATH_MFMA_BF16 = 3
+MOE_PATH_GEMV_MULTI = 4
 
 # every symbol include/moe_gfx950.h declares, with its ctypes signature
 _VP, _I, _I64, _SZ, _CP = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_char_p
@@ -47,7 +48,8 @@ SIGNATURES = {
     "moe_combine": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
     "moe_block_forward": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP, _I, _VP, _I, _VP,
                                _VP, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
-                               _VP, _SZ, _VP]),
+                               _VP, _VP, _SZ, _VP]),
+    "moe_workspace_init": (_I, [_VP, _SZ, _VP]),
 }
 
 

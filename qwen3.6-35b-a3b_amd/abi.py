@@ -68,12 +68,25 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _check(L.lib.moe_workspace_init(_p(buf), buf.numel(),
+                                        ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)),
+               "workspace_init")
         _WS_CACHE[key] = buf
     return buf
 
 
 def workspace_bytes(T: int, H: int, I: int, E: int, K: int, I_s: int) -> int:
     return int(L.lib.moe_workspace_bytes(T, H, I, E, K, I_s))
+
+
+def device_error_bits(device) -> int:
+    """The workspace's device-side error word (bit 0: a bounded spin of the single-launch decode
+    layer timed out, i.e. its workgroups were not all co-resident). Reading it synchronises."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _WS_CACHE.get(key)
+    if buf is None:
+        return 0
+    return int(buf[:16].view(torch.int32)[3].item())
 
 
 # ---------------------------------------------------------------------------------- entry points
@@ -153,7 +166,7 @@ def shared_expert(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_d
         _need(t, n, torch.bfloat16, shp, x.device)
     raw = torch.empty(T, H, dtype=torch.float32, device=x.device)
     prob = torch.empty(T, dtype=torch.float32, device=x.device)
-    ws = workspace(x.device, T * Is * 4 + (1 << 16))
+    ws = workspace(x.device, workspace_bytes(T, H, Is, 256, 8, Is))
     _check(L.lib.moe_shared_expert(_p(x), _xdt(x), _p(w_gate), _p(w_up), _p(w_down),
                                    _p(w_scalar_gate), T, H, Is, path, _p(raw), _p(prob), _p(ws),
                                    ws.numel(), _stream(x)), "shared_expert")
@@ -177,15 +190,18 @@ def combine(y: torch.Tensor, grouping: dict, ids: torch.Tensor, w_bf16: torch.Te
 
 
 def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False,
-                  out: torch.Tensor | None = None) -> dict:
+                  out: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> dict:
     """The whole block in one library call (moe_block_forward). `lw` is a LayerWeights;
-    `stages` is False, True (every stage output) or a set of stage names to return."""
+    `stages` is False, True (every stage output) or a set of stage names to return;
+    out = residual + MoE(x) when `residual` (f32 [T,H], may be `out` itself) is given."""
     _need(x, "x")
     T, H = x.shape
     E, K, I, Is = lw.n_experts, lw.top_k, lw.i_e, lw.i_s
     dev = x.device
     if out is None:
         out = torch.empty(T, H, dtype=torch.float32, device=dev)
+    if residual is not None:
+        _need(residual, "residual", torch.float32, (T, H), dev)
     shapes = {"router_logits": ((T, E), torch.bfloat16), "topk_ids": ((T, K), torch.int32),
               "topk_weights": ((T, K), torch.bfloat16),
               "topk_weights_f32": ((T, K), torch.float32),
@@ -199,7 +215,8 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
     _check(L.lib.moe_block_forward(
         _p(x), _xdt(x), T, H, I, E, K, Is, _p(lw.router), _p(lw.router_bias), _p(lw.gate_up_q),
         lw.gate_up_fmt, _p(lw.down_q), lw.down_fmt, _p(lw.shared_gate), _p(lw.shared_up),
-        _p(lw.shared_down), _p(lw.shared_scalar_gate), path, _p(out), _p(g("router_logits")),
+        _p(lw.shared_down), _p(lw.shared_scalar_gate), path, _p(residual), _p(out),
+        _p(g("router_logits")),
         _p(g("topk_ids")), _p(g("topk_weights")), _p(g("topk_weights_f32")), _p(g("routed_sum")),
         _p(g("shared_out")), _p(g("shared_gate_prob")), _p(g("expert_raw")), _p(ws), ws.numel(),
         _stream(x)), "block_forward")

@@ -42,6 +42,7 @@ static int check_geom(int T, int H, int I, int E, int K, const char* who) {
 }
 
 static int pick_path(int path, int T, int gate_up_fmt) {
+  if (path == MOE_PATH_GEMV_MULTI) return MOE_PATH_GEMV;
   if (path == MOE_PATH_GEMV || path == MOE_PATH_MFMA || path == MOE_PATH_MFMA_BF16) return path;
   if (gate_up_fmt != MOE_FMT_Q4_K) return MOE_PATH_MFMA;
   return T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
@@ -83,8 +84,8 @@ const char* moe_last_error(void) { return g_err; }
 size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s) {
   if (T < 1 || E < 1 || K < 1) return 0;
   const Carve c = carve_sizes(T, H, I, E, K, I_s);
-  return c.logits + c.ids + c.wf + c.wb + c.offsets + c.sorted + c.pos + c.hits + c.sort_ws +
-         c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.flag;
+  return kSyncBytes + c.logits + c.ids + c.wf + c.wb + c.offsets + c.sorted + c.pos + c.hits +
+         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.flag;
 }
 
 int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
@@ -111,6 +112,7 @@ int moe_router_topk(const void* x, int x_dtype, const void* w_router, const floa
   uint16_t* logits = reinterpret_cast<uint16_t*>(logits_bf16);
   if (!logits) {
     MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+    w.take(kSyncBytes);
     logits = reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
     if (!logits) return moe_set_error(MOE_E_WORKSPACE, "moe_router_topk: workspace too small for the logits");
   }
@@ -181,6 +183,7 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, int gate_up_f
   if (path == MOE_PATH_GEMV && down_fmt == MOE_FMT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K / Q6_K down only");
   if (!aligned16(x)) return moe_set_error(MOE_E_ARG, "moe_experts: x must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+  w.take(kSyncBytes);
   return experts_impl(x, x_dtype, gate_up_q, gate_up_fmt, down_q, down_fmt, expert_offsets,
                       sorted_pairs, hit_list, T, H, I, E, K, path, y, w, (hipStream_t)stream);
 }
@@ -213,6 +216,7 @@ int moe_shared_expert(const void* x, int x_dtype, const void* w_gate, const void
   if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) || !aligned16(w_scalar_gate))
     return moe_set_error(MOE_E_ARG, "moe_shared_expert: pointers must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+  w.take(kSyncBytes);
   return shared_impl(x, x_dtype, w_gate, w_up, w_down, w_scalar_gate, T, H, I_s, path, shared_raw,
                      gate_prob, w, (hipStream_t)stream);
 }
@@ -225,7 +229,7 @@ int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids
     return moe_set_error(MOE_E_ARG, "moe_combine: NULL pointer");
   if (T < 1 || K < 1 || K > 16 || H < 1) return moe_set_error(MOE_E_ARG, "moe_combine: bad shape");
   return moe_launch_combine(y, pair_pos, topk_ids, reinterpret_cast<const uint16_t*>(w_bf16),
-                            shared_raw, gate_prob, T, K, H, out, routed_sum, shared_out,
+                            shared_raw, gate_prob, nullptr, T, K, H, out, routed_sum, shared_out,
                             expert_raw, (hipStream_t)stream);
 }
 
@@ -233,8 +237,8 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
                       const void* w_router, const float* logit_bias, const void* gate_up_q,
                       int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
                       const void* ws_up, const void* ws_down, const void* ws_scalar_gate,
-                      int path, float* out, void* logits_bf16, int32_t* topk_ids,
-                      void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
+                      int path, const float* residual, float* out, void* logits_bf16,
+                      int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
                       float* shared_out, float* gate_prob, float* expert_raw, void* ws,
                       size_t ws_bytes, void* stream) {
   if (!x || !w_router || !gate_up_q || !down_q || !ws_gate || !ws_up || !ws_down || !ws_scalar_gate || !out)
@@ -250,6 +254,33 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
   hipStream_t st = (hipStream_t)stream;
   const int P = T * K;
   MoeWs w{reinterpret_cast<char*>(ws), ws_bytes};
+  int* sync = reinterpret_cast<int*>(w.take(kSyncBytes));
+  const int rpath = pick_path(path, T, gate_up_fmt);
+  if (T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
+      (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q6_K) && I_s % 128 == 0 && E % 4 == 0) {
+    MoeDecodeLaunch L;
+    L.x = x; L.x_dtype = x_dtype; L.residual = residual; L.w_router = w_router; L.bias = logit_bias;
+    L.gu = gate_up_q; L.dn = down_q; L.dn_fmt = down_fmt;
+    L.sg = ws_gate; L.su = ws_up; L.sd = ws_down; L.ssg = ws_scalar_gate;
+    L.logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)E * 2));
+    L.ids = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w.take(K * 4));
+    L.w_f32 = topk_w_f32 ? topk_w_f32 : reinterpret_cast<float*>(w.take(K * 4));
+    L.w_bf16 = topk_w_bf16 ? reinterpret_cast<uint16_t*>(topk_w_bf16) : reinterpret_cast<uint16_t*>(w.take(K * 2));
+    L.s_shared = reinterpret_cast<float*>(w.take((size_t)I_s * 4));
+    L.gate_prob = gate_prob ? gate_prob : reinterpret_cast<float*>(w.take(4));
+    L.shared_raw = reinterpret_cast<float*>(w.take((size_t)H * 4));
+    L.s_routed = reinterpret_cast<float*>(w.take((size_t)K * I * 4));
+    L.out = out; L.routed_sum = routed_sum; L.shared_out = shared_out; L.expert_raw = expert_raw;
+    L.counter = sync;
+    L.H = H; L.I = I; L.E = E; L.K = K; L.Is = I_s;
+    L.ids_out_requested = (topk_ids || topk_w_bf16 || topk_w_f32) ? 1 : 0;
+    if (!L.logits || !L.ids || !L.w_f32 || !L.w_bf16 || !L.s_shared || !L.gate_prob || !L.shared_raw || !L.s_routed)
+      return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+    if (path != MOE_PATH_GEMV_MULTI &&
+        moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt))
+      return moe_launch_decode_layer(L, sync, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(sync) + 256), st);
+    return moe_launch_decode_fused(L, st);
+  }
   uint16_t* logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
   int32_t* ids = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w.take((size_t)P * 4));
   float* wf = topk_w_f32 ? topk_w_f32 : reinterpret_cast<float*>(w.take((size_t)P * 4));
@@ -271,8 +302,13 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
   MOE_TRY(shared_impl(x, x_dtype, ws_gate, ws_up, ws_down, ws_scalar_gate, T, H, I_s, path, sraw, gp, w2, st));
   MOE_TRY(experts_impl(x, x_dtype, gate_up_q, gate_up_fmt, down_q, down_fmt, offsets, sorted, hits,
                        T, H, I, E, K, path, y, w, st));
-  return moe_launch_combine(y, pos, ids, wb, sraw, gp, T, K, H, out, routed_sum, shared_out,
-                            expert_raw, st);
+  return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
+                            shared_out, expert_raw, st);
+}
+
+int moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+  if (!ws || ws_bytes < kSyncBytes) return moe_set_error(MOE_E_ARG, "moe_workspace_init: workspace smaller than %zu bytes", kSyncBytes);
+  return moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream);
 }
 
 }  // extern "C"

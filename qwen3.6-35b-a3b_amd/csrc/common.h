@@ -25,20 +25,67 @@ __device__ __forceinline__ float f16_to_f32(uint32_t u16) {
 }
 
 // ------------------------------------------------------------------------- wave64 reductions --
-__device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, MOE_WAVE);
+// DPP data movement (gfx9 encodings): quad_perm xor1 = 0xB1, xor2 = 0x4E, row_half_mirror 0x141,
+// row_mirror 0x140 (inside a 16-lane row), row_bcast15 0x142 / row_bcast31 0x143 (across rows).
+// A butterfly over them costs a few cycles per step, where a __shfl_xor goes through the LDS
+// crossbar (ds_bpermute) at LDS latency.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, true);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v)));
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = __double_as_longlong(v);
+  const uint64_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)b);
+  const uint64_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(lo | (hi << 32)));
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), l));
+}
+
+// sum over each 16-lane row, result in every lane of the row
+__device__ __forceinline__ float row16_sum_f32(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
   return v;
+}
+// sum over the wave, result in every lane
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v = row16_sum_f32(v);
+  v += dpp_f32<0x142, 0xA>(v);     // rows 1, 3 += last lane of rows 0, 2
+  v += dpp_f32<0x143, 0xC>(v);     // rows 2, 3 += lane 31
+  return readlane_f32(v, 63);
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MOE_WAVE));
-  return v;
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  // rows 0/2 keep their own value where the broadcast is masked off (the row_mask keeps `old`
+  // = 0 there, and fmaxf with a row's own max leaves it unchanged only for non-negative rows),
+  // so combine rows through readlane instead
+  const float r0 = readlane_f32(v, 15), r1 = readlane_f32(v, 31);
+  const float r2 = readlane_f32(v, 47), r3 = readlane_f32(v, 63);
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, MOE_WAVE);
-  return v;
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x141>(v);
+  v += dpp_f64<0x140>(v);
+  v += dpp_f64<0x142, 0xA>(v);
+  v += dpp_f64<0x143, 0xC>(v);
+  const uint64_t b = __double_as_longlong(v);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+  return __longlong_as_double((long long)(lo | (hi << 32)));
 }
 
 __device__ __forceinline__ float silu_f32(float z) { return z / (1.0f + __expf(-z)); }

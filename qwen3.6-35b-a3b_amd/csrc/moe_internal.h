@@ -61,8 +61,40 @@ int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int T, i
 // combine
 int moe_launch_combine(const float* y, const int32_t* pair_pos, const int32_t* ids,
                        const uint16_t* w_bf16, const float* shared_raw, const float* gate_prob,
-                       int T, int K, int H, float* out, float* routed_sum, float* shared_out,
-                       float* expert_raw, hipStream_t st);
+                       const float* residual, int T, int K, int H, float* out, float* routed_sum,
+                       float* shared_out, float* expert_raw, hipStream_t st);
+
+// fused single-token decode (three launches); requires T == 1, K == 8, Q4_K gate_up
+struct MoeDecodeLaunch {
+  const void* x;
+  int x_dtype;
+  const float* residual;
+  const void* w_router;
+  const float* bias;
+  const void* gu;
+  const void* dn;
+  int dn_fmt;
+  const void *sg, *su, *sd, *ssg;
+  uint16_t* logits;
+  int32_t* ids;
+  float* w_f32;
+  uint16_t* w_bf16;
+  float *s_shared, *gate_prob, *shared_raw, *s_routed, *out, *routed_sum, *shared_out, *expert_raw;
+  int* counter;
+  int H, I, E, K, Is;
+  int ids_out_requested;   // the caller asked for topk_ids / weights: keep torch's slot order
+};
+int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
+int moe_launch_zero_words(int* p, int n, hipStream_t st);
+
+// The first kSyncBytes of every workspace hold the library's device-side sync words (block
+// tickets, the decode layer's epoch and arrival counter, its epoch-tagged exchange words). They
+// must be zero before the first call (moe_workspace_init); calls keep them consistent.
+constexpr size_t kSyncBytes = 65536;
+// single-launch decode layer (decode_layer.hip): 256 co-resident workgroups, model geometry only
+bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, int dn_fmt);
+size_t moe_layer_exchange_bytes();
+int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint64_t* xch, hipStream_t st);
 
 // workspace carving
 struct MoeWs {

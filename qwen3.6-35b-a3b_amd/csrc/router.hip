@@ -17,78 +17,9 @@
 // and returns min(A[M], B[M-1]) for the first M where that fails. Ranks come from ballots.
 #include "common.h"
 #include "moe_internal.h"
+#include "router_dev.h"
 
 namespace moe {
-
-// ------------------------------------------------------------------------- certified rounding --
-struct DD { double hi, lo; };
-
-__device__ __forceinline__ DD two_sum(double a, double b) {
-  double s = a + b;
-  double bb = s - a;
-  double e = (a - (s - bb)) + (b - bb);
-  return {s, e};
-}
-__device__ __forceinline__ DD dd_add(DD a, DD b) {
-  DD s = two_sum(a.hi, b.hi);
-  double lo = s.lo + a.lo + b.lo;
-  return two_sum(s.hi, lo);
-}
-
-// exponent e with 2^e <= |v| < 2^(e+1), v != 0, v finite
-__device__ __forceinline__ int exp2_floor(double v) { return ilogb(v); }
-
-// Round the f64 value s (|s - exact| <= bound) to bf16. Returns false if not certified.
-__device__ __forceinline__ bool round_bf16_certified(double s, double bound, uint32_t* out) {
-  if (s == 0.0) {
-    if (bound > 0.0) {
-      // the exact value may be a tiny non-zero: certify only if every value within the bound
-      // rounds to zero, i.e. the bound is below half the smallest bf16 subnormal
-      if (bound >= ldexp(1.0, -134)) return false;
-    }
-    *out = 0u;
-    return true;
-  }
-  const double a = fabs(s);
-  const int e = exp2_floor(a);
-  const int qe = max(e - 7, -133);
-  const double r = ldexp(a, -qe);                     // exact
-  const double fl = floor(r);
-  const double dist = fabs((r - fl) - 0.5);          // in units of the quantum, exact
-  if (ldexp(dist, qe) <= bound) return false;
-  const double rounded = ldexp(rint(r), qe);          // rint: ties-to-even
-  float f = (float)rounded;                           // exact (or inf on overflow)
-  if (s < 0) f = -f;
-  *out = __float_as_uint(f) >> 16;
-  return true;
-}
-
-// Decide the bf16 rounding of hi+lo (double-double) whose error is below ddbound.
-__device__ uint32_t round_bf16_dd(DD v, double ddbound) {
-  uint32_t bits;
-  if (round_bf16_certified(v.hi, fabs(v.lo) + ddbound, &bits)) return bits;
-  // hi is within |lo| + ddbound of a midpoint: compare against that midpoint exactly.
-  const double s = v.hi;
-  if (s == 0.0 && v.lo == 0.0) return 0u;
-  const double sref = (s != 0.0) ? s : v.lo;
-  const double a = fabs(sref);
-  const int qe = max(exp2_floor(a) - 7, -133);
-  const double r = ldexp(a, -qe);
-  const double fl = floor(r);
-  const double mid_abs = ldexp(fl + 0.5, qe);
-  const double mid = (sref < 0) ? -mid_abs : mid_abs;
-  const double diff = (v.hi - mid) + v.lo;            // hi - mid is exact (close values)
-  double n;                                           // magnitude in quanta after rounding
-  if (fabs(diff) <= ddbound) {
-    n = (fmod(fl, 2.0) == 0.0) ? fl : fl + 1.0;       // tie: to even
-  } else {
-    const bool above = (sref < 0) ? (diff < 0) : (diff > 0);
-    n = above ? fl + 1.0 : fl;
-  }
-  float f = (float)ldexp(n, qe);
-  if (sref < 0) f = -f;
-  return __float_as_uint(f) >> 16;
-}
 
 // ------------------------------------------------------------------ R1, small T (T <= 8) -------
 // One wave per expert row; the row (H bf16) is read once and applied to every token.
@@ -268,203 +199,6 @@ __global__ __launch_bounds__(256) void k_router_logits_gemm(
   }
 }
 
-// ------------------------------------------------------------- R2-R5 with torch's tie order --
-// One 64-thread block (one wave) per token. Queue positions 0..E-1 live in LDS; lane l owns
-// positions l, l+64, l+128, l+192.
-struct TopkLds {
-  float v[256];
-  int i[256];
-  int pa[256];
-  int pb[256];
-  int cell[2];
-};
-
-__device__ __forceinline__ void qswap(TopkLds& s, int a, int b) {
-  float tv = s.v[a]; s.v[a] = s.v[b]; s.v[b] = tv;
-  int ti = s.i[a]; s.i[a] = s.i[b]; s.i[b] = ti;
-}
-
-// greater-than on queue positions (values only; NaN does not occur on this path)
-__device__ __forceinline__ bool qgt(const TopkLds& s, int a, int b) { return s.v[a] > s.v[b]; }
-
-// stable insertion sort, descending, of positions [lo, hi) — lane 0 only
-__device__ void q_insertion_sort(TopkLds& s, int lo, int hi) {
-  for (int i = lo + 1; i < hi; ++i) {
-    float v = s.v[i];
-    int id = s.i[i];
-    int j = i;
-    while (j > lo && v > s.v[j - 1]) {
-      s.v[j] = s.v[j - 1];
-      s.i[j] = s.i[j - 1];
-      --j;
-    }
-    s.v[j] = v;
-    s.i[j] = id;
-  }
-}
-
-// libstdc++ heap helpers, comparator "greater" — lane 0 only
-__device__ void q_push_heap(TopkLds& s, int base, int hole, int top, float v, int id) {
-  int parent = (hole - 1) / 2;
-  while (hole > top && s.v[base + parent] > v) {
-    s.v[base + hole] = s.v[base + parent];
-    s.i[base + hole] = s.i[base + parent];
-    hole = parent;
-    parent = (hole - 1) / 2;
-  }
-  s.v[base + hole] = v;
-  s.i[base + hole] = id;
-}
-__device__ void q_adjust_heap(TopkLds& s, int base, int hole, int len, float v, int id) {
-  const int top = hole;
-  int child = hole;
-  while (child < (len - 1) / 2) {
-    child = 2 * (child + 1);
-    if (s.v[base + child] > s.v[base + child - 1]) child--;
-    s.v[base + hole] = s.v[base + child];
-    s.i[base + hole] = s.i[base + child];
-    hole = child;
-  }
-  if ((len & 1) == 0 && child == (len - 2) / 2) {
-    child = 2 * (child + 1);
-    s.v[base + hole] = s.v[base + child - 1];
-    s.i[base + hole] = s.i[base + child - 1];
-    hole = child - 1;
-  }
-  q_push_heap(s, base, hole, top, v, id);
-}
-__device__ void q_heap_select(TopkLds& s, int lo, int mid, int hi) {
-  const int n = mid - lo;
-  if (n >= 2) {
-    for (int parent = (n - 2) / 2;; --parent) {
-      q_adjust_heap(s, lo, parent, n, s.v[lo + parent], s.i[lo + parent]);
-      if (parent == 0) break;
-    }
-  }
-  for (int i = mid; i < hi; ++i) {
-    if (s.v[i] > s.v[lo]) {
-      float v = s.v[i];
-      int id = s.i[i];
-      s.v[i] = s.v[lo];
-      s.i[i] = s.i[lo];
-      q_adjust_heap(s, lo, 0, n, v, id);
-    }
-  }
-}
-
-// Unguarded Hoare partition of [a, b) around the pivot at a-1, done by the whole wave.
-__device__ int wave_partition(TopkLds& s, int a, int b, int lane) {
-  const float pv = s.v[a - 1];
-  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  const uint64_t gt = (lane == 63) ? 0ull : ((~0ull) << (lane + 1));
-  bool isA[4], isB[4];
-  uint64_t mA[4], mB[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    const bool in = pos >= a && pos < b;
-    const float v = in ? s.v[pos] : 0.0f;
-    isA[j] = in && !(v > pv);
-    isB[j] = in && !(pv > v);
-    mA[j] = __ballot(isA[j]);
-    mB[j] = __ballot(isB[j]);
-  }
-  int cA[5], cB[5];
-  cA[0] = 0; cB[0] = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    cA[j + 1] = cA[j] + __popcll(mA[j]);
-    cB[j + 1] = cB[j] + __popcll(mB[j]);
-  }
-  const int totB = cB[4];
-  int rankA[4], rankB[4];
-  bool swA[4], swB[4];
-  int M = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    rankA[j] = cA[j] + __popcll(mA[j] & lt);                 // # A positions < pos
-    rankB[j] = (totB - cB[j + 1]) + __popcll(mB[j] & gt);    // # B positions > pos
-    swA[j] = isA[j] && rankB[j] > rankA[j];
-    swB[j] = isB[j] && rankA[j] > rankB[j];
-    M += __popcll(__ballot(swA[j]));
-  }
-  if (lane == 0) { s.cell[0] = 0x7FFFFFFF; s.cell[1] = 0x7FFFFFFF; }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    if (swA[j]) s.pa[rankA[j]] = pos;
-    if (swB[j]) s.pb[rankB[j]] = pos;
-    if (isA[j] && rankA[j] == M) s.cell[0] = pos;            // A[M]
-    if (isB[j] && rankB[j] == M - 1) s.cell[1] = pos;        // B[M-1]
-  }
-  __syncthreads();
-  float nv[4];
-  int ni[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int partner = -1;
-    if (swA[j]) partner = s.pb[rankA[j]];
-    if (swB[j]) partner = s.pa[rankB[j]];
-    if (partner >= 0) { nv[j] = s.v[partner]; ni[j] = s.i[partner]; }
-  }
-  // min(A[M], B[M-1]); the median-of-three guarantees A[0] exists, the clamp only keeps a broken
-  // invariant from indexing outside the range
-  const int cut = min(min(s.cell[0], s.cell[1]), b);
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (swA[j] || swB[j]) { s.v[64 * j + lane] = nv[j]; s.i[64 * j + lane] = ni[j]; }
-  }
-  __syncthreads();
-  return cut;
-}
-
-// torch CPU topk(values, k) for k*64 > n: nth_element(k-1) then sort of the first k-1.
-// Returns 1 if the heap-select branch ran (reported for tests), 0 otherwise.
-__device__ int wave_torch_topk(TopkLds& s, int n, int k, int lane) {
-  int lo = 0, hi = n;
-  const int nth = k - 1;
-  int depth = 2 * (31 - __clz(n));
-  int heap = 0;
-  while (hi - lo > 3) {
-    if (depth == 0) {
-      if (lane == 0) {
-        q_heap_select(s, lo, nth + 1, hi);
-        qswap(s, lo, nth);
-      }
-      __syncthreads();
-      heap = 1;
-      break;
-    }
-    --depth;
-    const int mid = lo + (hi - lo) / 2;
-    if (lane == 0) {
-      // move_median_to_first(lo, lo+1, mid, hi-1)
-      const int a = lo + 1, b = mid, c = hi - 1;
-      int pick;
-      if (qgt(s, a, b)) {
-        if (qgt(s, b, c)) pick = b;
-        else if (qgt(s, a, c)) pick = c;
-        else pick = a;
-      } else if (qgt(s, a, c)) pick = a;
-      else if (qgt(s, b, c)) pick = c;
-      else pick = b;
-      qswap(s, lo, pick);
-    }
-    __syncthreads();
-    const int cut = wave_partition(s, lo + 1, hi, lane);
-    if (cut <= nth) lo = cut;
-    else hi = cut;
-  }
-  if (lane == 0) {
-    if (!heap) q_insertion_sort(s, lo, hi);
-    q_insertion_sort(s, 0, k - 1);
-  }
-  __syncthreads();
-  return heap;
-}
-
 __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ logits, int T,
                                                    int E, int K, float* __restrict__ probs,
                                                    int32_t* __restrict__ ids,
@@ -475,47 +209,15 @@ __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ 
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   if (t >= T) return;
-  float lv[4];
-  float m = -INFINITY;
+  float p[4];
+  route_softmax(logits + (size_t)t * E, E, lane, p);
+  if (probs) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    lv[j] = pos < E ? bf16_to_f32(logits[(size_t)t * E + pos]) : -INFINITY;
-    m = fmaxf(m, lv[j]);
+    for (int j = 0; j < 4; ++j)
+      if (64 * j + lane < E) probs[(size_t)t * E + 64 * j + lane] = p[j];
   }
-  m = wave_max_f32(m);
-  float ex[4], sum = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    ex[j] = pos < E ? expf(lv[j] - m) : 0.0f;
-    sum += ex[j];
-  }
-  sum = wave_sum_f32(sum);
-  const float rs = 1.0f / sum;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    if (pos < E) {
-      const float p = ex[j] * rs;
-      s.v[pos] = p;
-      s.i[pos] = pos;
-      if (probs) probs[(size_t)t * E + pos] = p;
-    }
-  }
-  __syncthreads();
-  const int heap = wave_torch_topk(s, E, K, lane);
-  if (lane == 0) {
-    float tot = 0.0f;
-    for (int k = 0; k < K; ++k) tot += s.v[k];
-    for (int k = 0; k < K; ++k) {
-      const float wv = s.v[k] / tot;
-      ids[(size_t)t * K + k] = s.i[k];
-      w_f32[(size_t)t * K + k] = wv;
-      w_bf16[(size_t)t * K + k] = (uint16_t)f32_to_bf16(wv);
-    }
-    if (heap && heap_flag) atomicAdd(heap_flag, 1);
-  }
+  route_select_and_write(s, p, E, K, lane, ids + (size_t)t * K, w_f32 + (size_t)t * K,
+                         w_bf16 + (size_t)t * K, heap_flag);
 }
 
 }  // namespace moe

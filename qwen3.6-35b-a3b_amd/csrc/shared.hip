@@ -5,38 +5,9 @@
 //   gate_prob[t] = sigmoid(wsg . x_t)                 one scalar per token
 #include "common.h"
 #include "moe_internal.h"
+#include "gemv_dev.h"
 
 namespace moe {
-
-template <int XDT>
-__device__ __forceinline__ void load_x8(const void* x, size_t off, float* v) {
-  if (XDT == MOE_DT_F32) {
-    const float* p = reinterpret_cast<const float*>(x) + off;
-    float4 a = *reinterpret_cast<const float4*>(p);
-    float4 b = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    uint4 a = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + off);
-    const uint32_t aa[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[2 * j] = bf16_to_f32(aa[j] & 0xFFFFu);
-      v[2 * j + 1] = bf16_to_f32(aa[j] >> 16);
-    }
-  }
-}
-
-__device__ __forceinline__ float dot8_bf16(uint4 w, const float* x) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-  float a = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    a = fmaf(bf16_to_f32(ww[j] & 0xFFFFu), x[2 * j], a);
-    a = fmaf(bf16_to_f32(ww[j] >> 16), x[2 * j + 1], a);
-  }
-  return a;
-}
 
 // grid (Is/4 + 1); wave w of block bx < Is/4 owns intermediate row i = 4*bx + w; the last block's
 // wave 0 computes the scalar gate. Rows are H bf16; lane covers cols 512*c + 8*lane + 0..7.
@@ -97,10 +68,7 @@ __global__ __launch_bounds__(256) void k_shared_down(const float* __restrict__ s
       load_x8<MOE_DT_F32>(s, (size_t)t * Is + 128 * c + 8 * l16, sv);
       a += dot8_bf16(*reinterpret_cast<const uint4*>(dr + 128 * c + 8 * l16), sv);
     }
-    a += __shfl_xor(a, 8, 64);
-    a += __shfl_xor(a, 4, 64);
-    a += __shfl_xor(a, 2, 64);
-    a += __shfl_xor(a, 1, 64);
+    a = row16_sum_f32(a);
     if (l16 == 0) shared_raw[(size_t)t * H + row] = a;
   }
 }

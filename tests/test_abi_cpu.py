@@ -30,7 +30,7 @@ def test_abi_version_and_enums_match_header(pkg):
     for name in ("MOE_OK", "MOE_E_ARG", "MOE_E_FORMAT", "MOE_E_HIP", "MOE_E_WORKSPACE",
                  "MOE_E_UNSUPPORTED", "MOE_DT_F32", "MOE_DT_BF16", "MOE_FMT_Q4_K", "MOE_FMT_Q6_K",
                  "MOE_FMT_BF16", "MOE_PATH_AUTO", "MOE_PATH_GEMV", "MOE_PATH_MFMA",
-                 "MOE_PATH_MFMA_BF16"):
+                 "MOE_PATH_MFMA_BF16", "MOE_PATH_GEMV_MULTI"):
         m = re.search(name + r"\s*=\s*(-?\d+)", text)
         assert m and int(m.group(1)) == getattr(pkg._lib, name), name
 
@@ -60,10 +60,12 @@ def test_refusals_happen_on_the_host(pkg):
     assert rc == pkg._lib.MOE_E_UNSUPPORTED                                  # K*64 <= E
     assert b"K*64 > E" in lib.moe_last_error()
     rc = lib.moe_block_forward(p, 0, 1, 2048, 512, 256, 8, 512, p, None, p, 12, p, 12, p, p, p, p,
-                               0, p, None, None, None, None, None, None, None, None, p, 16, None)
+                               0, None, p, None, None, None, None, None, None, None, None, p, 16,
+                               None)
     assert rc == pkg._lib.MOE_E_WORKSPACE
     rc = lib.moe_experts(p, 0, p, 99, p, 12, p, p, p, 1, 2048, 512, 256, 8, 0, p, p, 1 << 20, None)
     assert rc == pkg._lib.MOE_E_FORMAT
+    assert lib.moe_workspace_init(p, 16, None) == pkg._lib.MOE_E_ARG
 
 
 def test_product_path_never_imports_the_oracle():

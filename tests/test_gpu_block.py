@@ -86,3 +86,83 @@ def test_deterministic_repeat(pkg, layer_c0, dev):
     a = pkg.abi.block_forward(x, lw)["combined_out"].clone()
     b = pkg.abi.block_forward(x, lw)["combined_out"]
     assert torch.equal(a, b)
+
+
+def test_decode_fused_residual_in_place(pkg, layer_c0, dev):
+    """The fused single-token path with the residual add done in place (out aliases residual):
+    out = x + MoE(x)."""
+    lw, ow = layer_c0
+    x = pkg.synth.make_input(1, seed=21, device=dev)
+    ref = O.moe_block(x.cpu(), ow)
+    buf = x.clone()
+    pkg.abi.block_forward(buf, lw, out=buf, residual=buf)
+    torch.cuda.synchronize()
+    assert_close(buf.cpu() - x.cpu(), ref["combined_out"], "fused residual")
+
+
+def test_decode_fused_q6k_down(pkg, layer_q6k, dev):
+    lw, ow = layer_q6k
+    for seed in (1, 2, 3):
+        x = pkg.synth.make_input(1, seed=40 + seed, device=dev)
+        st = pkg.block.moe_block(x, lw, pkg.load_geometry())
+        _compare(st, O.moe_block(x.cpu(), ow), tag=f"fused q6k seed={seed}")
+
+
+def test_decode_fused_many_tokens_sequential(pkg, layer_zipf, dev):
+    """64 sequential single-token calls (Zipf-skewed routing) through the fused path: every one
+    matches the oracle bit for bit on routing; exercises the device ticket reset between calls."""
+    lw, ow = layer_zipf
+    xs = pkg.synth.make_input(64, seed=77, device=dev)
+    outs = [pkg.block.moe_block(xs[i:i + 1], lw, pkg.load_geometry()) for i in range(64)]
+    ref = O.moe_block(xs.cpu(), ow)
+    ids = torch.cat([o["topk_ids"] for o in outs]).cpu()
+    assert torch.equal(ids, ref["topk_ids"])
+    out = torch.cat([o["combined_out"] for o in outs]).cpu()
+    assert_close(out, ref["combined_out"], "fused x64")
+
+
+def test_decode_single_launch_and_three_launch_paths_agree(pkg, layer_c0, dev):
+    """The persistent single-launch layer and the three-launch form of the same arithmetic both
+    match the oracle on 32 tokens, and no bounded spin timed out."""
+    lw, ow = layer_c0
+    xs = pkg.synth.make_input(32, seed=5, device=dev)
+    ref = O.moe_block(xs.cpu(), ow)
+    for path in (pkg._lib.MOE_PATH_GEMV, pkg._lib.MOE_PATH_GEMV_MULTI):
+        outs, ids = [], []
+        for i in range(32):
+            st = pkg.abi.block_forward(xs[i:i + 1].contiguous(), lw, path=path, stages={"topk_ids"})
+            outs.append(st["combined_out"])
+            ids.append(st["topk_ids"])
+        torch.cuda.synchronize()
+        assert torch.equal(torch.cat(ids).cpu().long(), ref["topk_ids"]), path
+        assert_close(torch.cat(outs), ref["combined_out"], f"decode path {path}")
+    assert pkg.abi.device_error_bits(dev) == 0
+
+
+def test_decode_graph_replay_matches_eager(pkg, layer_c0, dev):
+    """The single-launch layer inside a captured HIP graph, replayed several times with eager work
+    between replays: every replay equals the eager result bit for bit (the epoch-tagged exchange
+    words must advance correctly across replays)."""
+    lw, _ = layer_c0
+    x0 = pkg.synth.make_input(1, seed=99, device=dev)
+    xin = x0.clone()
+    out = torch.empty_like(x0)
+    pkg.abi.block_forward(xin, lw, out=out)        # eager, also allocates the workspace
+    torch.cuda.synchronize()
+    want = out.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            pkg.abi.block_forward(xin, lw, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(5):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+        pkg.abi.block_forward(xin, lw, out=out)    # eager call between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+    assert pkg.abi.device_error_bits(dev) == 0
