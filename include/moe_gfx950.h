@@ -132,10 +132,12 @@ int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, in
                       float *routed_sum, float *shared_out, float *gate_prob, float *expert_raw,
                       void *ws, size_t ws_bytes, void *stream);
 
-/* Zero the workspace's device-side sync words (its first 64 KiB). Call once after allocating
- * a workspace, before its first use by moe_block_forward / moe_experts / moe_shared_expert /
- * moe_router_topk; every call leaves the words zero again. Calls sharing one workspace must be
- * ordered on one stream. No counterpart in the reference (its device work ran in fresh processes). */
+/* Zero the workspace's device-side sync words (its first 256 KiB: counters, the single-launch
+ * decode layer's epoch and its two exchange buffers). Call once after allocating a workspace,
+ * before its first use by moe_block_forward / moe_experts / moe_shared_expert / moe_router_topk
+ * (a workspace that starts zeroed needs no call); every call leaves the words valid for the next.
+ * Calls sharing one workspace must be ordered on one stream. No counterpart in the reference (its
+ * device work ran in fresh processes). */
 int moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus

@@ -278,7 +278,7 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
       return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
     if (path != MOE_PATH_GEMV_MULTI &&
         moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt))
-      return moe_launch_decode_layer(L, sync, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(sync) + 256), st);
+      return moe_launch_decode_layer(L, sync, reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sync) + 256), st);
     return moe_launch_decode_fused(L, st);
   }
   uint16_t* logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));

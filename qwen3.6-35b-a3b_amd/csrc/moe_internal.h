@@ -88,13 +88,13 @@ int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
 int moe_launch_zero_words(int* p, int n, hipStream_t st);
 
 // The first kSyncBytes of every workspace hold the library's device-side sync words (block
-// tickets, the decode layer's epoch and arrival counter, its epoch-tagged exchange words). They
+// tickets, the decode layer's epoch and arrival counter, its two exchange buffers). They
 // must be zero before the first call (moe_workspace_init); calls keep them consistent.
-constexpr size_t kSyncBytes = 65536;
+constexpr size_t kSyncBytes = 262144;
 // single-launch decode layer (decode_layer.hip): 256 co-resident workgroups, model geometry only
 bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, int dn_fmt);
 size_t moe_layer_exchange_bytes();
-int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint64_t* xch, hipStream_t st);
+int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st);
 
 // workspace carving
 struct MoeWs {

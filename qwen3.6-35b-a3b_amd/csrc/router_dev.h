@@ -376,6 +376,33 @@ __device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lan
   for (int j = 0; j < 4; ++j) p[j] *= rs;
 }
 
+// R3-R5 by the exact replay of torch's CPU topk (for ties that the fast paths cannot settle),
+// then w = p_k / sum_k p_k (rank order) and its bf16 cast. Writes ids/w_f32/w_bf16[0..K) from
+// lane 0. p: lane's probabilities at positions lane + 64j.
+__device__ __forceinline__ void route_replay_and_write(TopkLds& s, const float* p, int E, int K,
+                                                       int lane, int32_t* ids, float* w_f32,
+                                                       uint16_t* w_bf16, int32_t* heap_flag) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int pos = 64 * j + lane;
+    if (pos < E) { s.v[pos] = p[j]; s.i[pos] = pos; }
+  }
+  wave_sync();
+  const int heap = wave_torch_topk(s, E, K, lane);
+  if (lane == 0) {
+    float tot = 0.0f;
+    for (int k = 0; k < K; ++k) tot += s.v[k];
+    for (int k = 0; k < K; ++k) {
+      const float wv = s.v[k] / tot;
+      ids[k] = s.i[k];
+      w_f32[k] = wv;
+      w_bf16[k] = (uint16_t)f32_to_bf16(wv);
+    }
+    if (heap && heap_flag) atomicAdd(heap_flag, 1);
+  }
+  wave_sync();
+}
+
 // R3-R5 for one token by one wave: fast path, else the exact replay of torch's CPU topk; then
 // w = p_k / sum_k p_k (rank order) and its bf16 cast. Writes ids/w_f32/w_bf16[0..K) from lane 0.
 // exact_order = false accepts the fast path's slot order when ties sit only inside the top K
@@ -405,25 +432,66 @@ __device__ __forceinline__ void route_select_and_write(TopkLds& s, const float* 
     }
     return;
   }
+  route_replay_and_write(s, p, E, K, lane, ids, w_f32, w_bf16, heap_flag);
+}
+
+// Fast top-K over E = 256 probabilities (lane holds positions lane + 64j) with 32-bit keys: the
+// lane sorts its four values, then K + 1 rounds each take the wave maximum (DPP row maxima + four
+// readlanes) and pop it from the lowest lane that holds it. p >= 0, so the f32 bit patterns order
+// like the values. Lane r < K ends with the rank-r id and value; *tot gets sum_k p_k in rank order.
+// Returns 0 (no equal values among the first K + 1: torch's answer), 1 (equal values only inside
+// the top K: same set and weights, slot order among equals may differ), 2 (the K-th and (K+1)-th
+// are equal: the set depends on torch's tie order).
+template <int K>
+__device__ __forceinline__ int wave_topk32(const float* p, int lane, int& my_id, float& my_val,
+                                           float& tot) {
+  uint32_t k0 = __float_as_uint(p[0]), k1 = __float_as_uint(p[1]);
+  uint32_t k2 = __float_as_uint(p[2]), k3 = __float_as_uint(p[3]);
+  int p0 = lane, p1 = lane + 64, p2 = lane + 128, p3 = lane + 192;
+#define MOE_CX32(a, b)                                     \
+  {                                                        \
+    const bool sw_ = k##a < k##b;                          \
+    const uint32_t tk_ = sw_ ? k##b : k##a;                \
+    k##b = sw_ ? k##a : k##b; k##a = tk_;                  \
+    const int tp_ = sw_ ? p##b : p##a;                     \
+    p##b = sw_ ? p##a : p##b; p##a = tp_;                  \
+  }
+  MOE_CX32(0, 1) MOE_CX32(2, 3) MOE_CX32(0, 2) MOE_CX32(1, 3) MOE_CX32(1, 2)
+#undef MOE_CX32
+  int code = 0;
+  uint32_t prev = 0;
+  float sum = 0.0f;
+  my_id = 0;
+  my_val = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    if (pos < E) { s.v[pos] = p[j]; s.i[pos] = pos; }
-  }
-  wave_sync();
-  const int heap = wave_torch_topk(s, E, K, lane);
-  if (lane == 0) {
-    float tot = 0.0f;
-    for (int k = 0; k < K; ++k) tot += s.v[k];
-    for (int k = 0; k < K; ++k) {
-      const float wv = s.v[k] / tot;
-      ids[k] = s.i[k];
-      w_f32[k] = wv;
-      w_bf16[k] = (uint16_t)f32_to_bf16(wv);
+  for (int r = 0; r <= K; ++r) {
+    uint32_t m = k0;
+    m = max(m, dpp_u32<0xB1>(m));
+    m = max(m, dpp_u32<0x4E>(m));
+    m = max(m, dpp_u32<0x141>(m));
+    m = max(m, dpp_u32<0x140>(m));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)m, 15);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)m, 31);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)m, 47);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
+    m = max(max(r0, r1), max(r2, r3));
+    const uint64_t own = __ballot(k0 == m);
+    const int owner = __builtin_ctzll(own);
+    if (r > 0 && m == prev) code = (r == K) ? 2 : max(code, 1);
+    prev = m;
+    if (r < K) {
+      const int id = __builtin_amdgcn_readlane(p0, owner);
+      const float v = __uint_as_float(m);
+      sum += v;
+      if (lane == r) { my_id = id; my_val = v; }
+      if (lane == owner) {
+        k0 = k1; k1 = k2; k2 = k3; k3 = 0u;
+        p0 = p1; p1 = p2; p2 = p3;
+      }
     }
-    if (heap && heap_flag) atomicAdd(heap_flag, 1);
   }
-  wave_sync();
+  tot = sum;
+  return code;
 }
 
 }  // namespace moe

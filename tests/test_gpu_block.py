@@ -166,3 +166,46 @@ def test_decode_graph_replay_matches_eager(pkg, layer_c0, dev):
         torch.cuda.synchronize()
         assert torch.equal(out, want), rep
     assert pkg.abi.device_error_bits(dev) == 0
+
+
+def _tied_router(lw, ow, groups, dev):
+    """Copies of the layer whose router gives tied logits: every expert of a group gets the first
+    member's router row and the group's bias, so their logits (and probabilities) are equal."""
+    import dataclasses
+    router = lw.router.clone()
+    bias = torch.zeros(lw.n_experts, dtype=torch.float32, device=dev)
+    for members, b in groups:
+        for e in members:
+            router[e] = router[members[0]]
+            bias[e] = b
+    lw2 = dataclasses.replace(lw, router=router, router_bias=bias)
+    ow2 = dataclasses.replace(ow, router=router.cpu(), router_bias=bias.cpu())
+    return lw2, ow2
+
+
+@pytest.mark.parametrize("case", ["inner", "boundary"])
+def test_decode_single_launch_ties(pkg, layer_c0, dev, case):
+    """Tied probabilities through the single-launch layer. 'inner': two equal experts inside the
+    top 8 (the fast selection is exact up to slot order); 'boundary': the 8th and 9th are equal
+    (which one torch keeps depends on its partition order, so the exact replay must run). With
+    routing outputs requested the ids match torch's order exactly; without them the block output
+    is the same bits (the combine runs in ascending expert id, independent of slot order)."""
+    lw, ow = layer_c0
+    if case == "inner":
+        groups = [([10, 11], 8.0), ([20], 8.0), ([21], 8.0), ([22], 8.0), ([23], 8.0),
+                  ([24], 8.0), ([25], 8.0)]
+    else:
+        groups = [([30], 12.0), ([31], 12.0), ([32], 12.0), ([33], 12.0), ([34], 12.0),
+                  ([35], 12.0), ([36], 12.0), ([40, 41], 6.0)]
+    lw2, ow2 = _tied_router(lw, ow, groups, dev)
+    xs = pkg.synth.make_input(6, seed=17, device=dev)
+    ref = O.moe_block(xs.cpu(), ow2)
+    for i in range(xs.shape[0]):
+        x = xs[i:i + 1].contiguous()
+        st = pkg.abi.block_forward(x, lw2, stages={"topk_ids", "topk_weights"})
+        plain = pkg.abi.block_forward(x, lw2)
+        torch.cuda.synchronize()
+        assert torch.equal(st["topk_ids"].cpu().long(), ref["topk_ids"][i:i + 1]), (case, i)
+        assert_close(st["combined_out"].cpu(), ref["combined_out"][i:i + 1], f"{case} token {i}")
+        assert torch.equal(plain["combined_out"], st["combined_out"]), (case, i)
+    assert pkg.abi.device_error_bits(dev) == 0
