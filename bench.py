@@ -2,23 +2,37 @@
 
 Headline (`value`): Q4_K MoE-layer decode at bs=1, config 1 — 40 independent resident layer
 instances (~18.1 GB of Q4_K experts, so every expert byte comes from HBM), one token at a time
-through all 40 layers, the next layer's input being the previous layer's residual stream
-(x <- x + MoE(x), the decoder layer's own residual add), 1024 sequential tokens by default.
-A step is one token through the 40 layers; it is captured once as a HIP graph and replayed.
-Reported as us per token per layer, with the HBM rate over the 8 routed + 1 shared active
-experts' bytes (20,447,232 B per token-layer).
+through all 40 layers as the decoder's MoE half runs them (engine/m3_forward.py:732-737):
+h <- h + MoE(rmsnorm(h)) per layer, the post-attention RMSNorm and the residual add fused into the
+single-launch layer, each layer's input the previous layer's output; h is rescaled to RMS 1
+between tokens. 1024 sequential tokens by default. A step is one token through the 40 layers; it is captured once as a
+HIP graph and replayed. Reported as us per token per layer, with the HBM rate over the 8 routed +
+1 shared active experts' bytes (20,447,232 B per token-layer).
 
-Also on the line: prefill tokens/s at T = 4096 (config 3) with MFMA utilisation against the bf16
-dense peak, the roofline of the dominant decode kernel, and the CPU baseline (this repo's CPU
-oracle of the same block, timed on the host on a bounded sample).
+`roofline`: the dominant kernel of that path, the single-launch decode layer (k_dec_layer), timed
+alone with HIP events on the stream it is launched on: a graph of 40 back-to-back launches over
+the 40 layers (independent inputs), replayed; average launch period = elapsed / launches.
+`traffic` comes from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same kernel
+(`--pmc` workload, calibrated against a copy kernel of known size).
 
-Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 16] [--layers 40] [--no-cpu]
+Also on the line: batched decode at T = 64 with Zipf routing (config 2), prefill tokens/s at
+T = 4096 (config 3) with MFMA utilisation against the bf16 dense peak, and the CPU baseline (this
+repo's CPU oracle of the same block, timed on the host on a bounded sample).
+
+Usage:
+  python bench.py [--gpus 1] [--steps 1024] [--warmup 16] [--layers 40] [--no-cpu] [--no-prefill]
+  python bench.py --pmc                      short decode workload + copy calibration (for rocprofv3 --pmc)
+  python bench.py --pmc-summary DIR_FETCH DIR_WRITE   traffic summary (markdown) from two --pmc runs
+  python bench.py --stats-summary DIR [CMD]   kernel table (markdown) from rocprofv3 --kernel-trace --stats
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -28,6 +42,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_SUMMARY = ROOT / "profiles" / "k_dec_layer_c1_traffic.md"
+DECODE_KERNEL = "k_dec_layer"
+COPY_MIB = 512                      # calibration copy: reads and writes this many MiB
+PMC_REGEX = "k_dec_layer|MulFunctor"
 
 
 def log(msg: str) -> None:
@@ -40,16 +58,23 @@ def parse():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--kernel-reps", type=int, default=64)
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-c2", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant-kernel timing (what the kernel-trace profile covers)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--pmc", action="store_true")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("DIR_FETCH", "DIR_WRITE"))
+    ap.add_argument("--stats-summary", nargs="+", metavar="DIR [CMD]")
     return ap.parse_args()
 
 
-def time_stream(fn, n: int, torch) -> float:
-    """Average ms of fn() over n calls, HIP events on the current stream."""
-    st = torch.cuda.current_stream()
+def time_stream(fn, n: int, torch, stream=None) -> float:
+    """Average ms of fn() over n calls, HIP events on `stream` (default: the current stream)."""
+    st = stream or torch.cuda.current_stream()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(st)
     for _ in range(n):
@@ -59,11 +84,183 @@ def time_stream(fn, n: int, torch) -> float:
     return a.elapsed_time(b) / n
 
 
+def capture(torch, fn):
+    """fn's launches captured into a HIP graph on a side stream."""
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            fn()
+    torch.cuda.current_stream().wait_stream(cap)
+    torch.cuda.synchronize()
+    return g
+
+
+# ------------------------------------------------------------------------------ rocprof helpers --
+def _counter_rows(d: str):
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    for f in files:
+        with open(f) as fh:
+            yield from csv.DictReader(fh)
+
+
+def _per_dispatch(d: str, counter: str):
+    """{kernel name: [per-dispatch value]} for one counter (summed over its dimension rows)."""
+    acc: dict[tuple, float] = {}
+    names: dict[tuple, str] = {}
+    for r in _counter_rows(d):
+        if r.get("Counter_Name") != counter:
+            continue
+        key = (r.get("Dispatch_Id"), r.get("Agent_Id"))
+        acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+        names[key] = r.get("Kernel_Name", "")
+    out: dict[str, list] = {}
+    for k, v in acc.items():
+        out.setdefault(names[k], []).append(v)
+    return out
+
+
+def pmc_summary(dir_fetch: str, dir_write: str) -> str:
+    """Markdown summary of two rocprofv3 --pmc runs of `bench.py --pmc`: FETCH_SIZE / WRITE_SIZE
+    (KiB per dispatch) of the decode layer kernel, scaled by what the same counters read for a
+    plain copy of COPY_MIB MiB (known bytes each way)."""
+    import statistics
+    f, w = _per_dispatch(dir_fetch, "FETCH_SIZE"), _per_dispatch(dir_write, "WRITE_SIZE")
+
+    def pick(d, pat):
+        ks = [k for k in d if re.search(pat, k)]
+        if not ks:
+            raise SystemExit(f"no kernel matching {pat!r} in {sorted(d)[:8]}")
+        return max(ks, key=lambda k: len(d[k]))
+
+    kf, kw = pick(f, DECODE_KERNEL), pick(w, DECODE_KERNEL)
+    def largest(d, pat):
+        vals = [(v, k) for k in d if re.search(pat, k) for v in d[k]]
+        if not vals:
+            raise SystemExit(f"no kernel matching {pat!r}")
+        return max(vals)
+
+    # the calibration multiply is the largest elementwise dispatch of the run
+    copy_f, cf = largest(f, r"elementwise")
+    copy_w, cw = largest(w, r"elementwise")
+    copy_kib = COPY_MIB * 1024.0
+    sf, sw = copy_kib / copy_f, copy_kib / copy_w
+    fetch = statistics.median(f[kf]) * sf * 1024.0
+    write = statistics.median(w[kw]) * sw * 1024.0
+    lines = [
+        "# k_dec_layer (config 1 decode layer): HBM traffic per launch from rocprofv3 PMC",
+        "",
+        "Commands (GPU box, repo root):",
+        "",
+        f"    rocprofv3 --pmc FETCH_SIZE --kernel-include-regex '{PMC_REGEX}' --output-format csv -d /tmp/pmc_f -o f -- python3 bench.py --pmc",
+        f"    rocprofv3 --pmc WRITE_SIZE --kernel-include-regex '{PMC_REGEX}' --output-format csv -d /tmp/pmc_w -o w -- python3 bench.py --pmc",
+        "    python3 bench.py --pmc-summary /tmp/pmc_f /tmp/pmc_w",
+        "",
+        f"Calibration: a {COPY_MIB} MiB elementwise multiply ({cf[:60]}) reads {copy_f:.0f} KiB (FETCH_SIZE)",
+        f"and writes {copy_w:.0f} KiB (WRITE_SIZE) for {copy_kib:.0f} KiB each way:",
+        f"scale factors fetch {sf:.4f}, write {sw:.4f}.",
+        "",
+        "| kernel | dispatches | FETCH_SIZE KiB (median) | WRITE_SIZE KiB (median) | scaled fetch B | scaled write B |",
+        "|---|---|---|---|---|---|",
+        f"| {kf[:60]} | {len(f[kf])} | {statistics.median(f[kf]):.1f} | {statistics.median(w[kw]):.1f} "
+        f"| {fetch:.0f} | {write:.0f} |",
+        "",
+        f"traffic_bytes_per_launch: {fetch + write:.0f}",
+        "",
+        "Algorithmic bytes per launch: 20,447,232 (8 routed Q4_K experts + bf16 shared expert) plus",
+        "1,052,672 router + shared-gate bytes = 21,499,904.",
+    ]
+    return "\n".join(lines) + "\n"
+
+
+def stats_summary(d: str, cmd: str) -> str:
+    """Markdown table of the kernels in a rocprofv3 --kernel-trace --stats run, by total time."""
+    files = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_stats.csv under {d}")
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    rows.sort(key=lambda r: -float(r.get("TotalDurationNs", 0) or 0))
+    ours = [r for r in rows if "moe::" in r["Name"]]
+    rest = [r for r in rows if "moe::" not in r["Name"]][:10]
+    out = ["# rocprofv3 kernel statistics", "", "Command (GPU box, repo root):", "", f"    {cmd}", "",
+           "This library's kernels (moe::) first, then the ten largest others (input generation).", "",
+           "| kernel | calls | avg us | min us | max us | total ms | % |", "|---|---|---|---|---|---|---|"]
+    for r in ours + rest:
+        name = re.sub(r"\s+", " ", r["Name"])[:90]
+        out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                   f"{float(r['TotalDurationNs']) / 1e6:.3f} | {float(r.get('Percentage', 0) or 0):.1f} |")
+    return "\n".join(out) + "\n"
+
+
+def committed_traffic():
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", TRAFFIC_SUMMARY.read_text())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+# ------------------------------------------------------------------------------------ workloads --
+def pmc_workload(pkg, torch, dev, L: int) -> None:
+    """What the PMC passes profile: 4 tokens through L decode layers (eager), then the copy."""
+    synth, abi = pkg.synth, pkg.abi
+    layers = [synth.make_layer(seed=1000 + l, device=dev) for l in range(L)]
+    norms = [synth.make_norm_weight(seed=5000 + l, device=dev) for l in range(L)]
+    x = synth.make_input(1, seed=0, device=dev)
+    for _ in range(4):
+        for lw, nw in zip(layers, norms):
+            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw)
+        x.copy_(synth.rms_normalize(x))
+    torch.cuda.synchronize()
+    del layers
+    src = torch.ones(COPY_MIB * 2 ** 20 // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.mul(src, 2.0, out=dst)         # an elementwise kernel: reads and writes COPY_MIB MiB
+    torch.cuda.synchronize()
+    log(f"pmc workload done: {4 * L} decode-layer launches, one {COPY_MIB} MiB elementwise copy")
+
+
+def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> float:
+    """Average launch period of the single-launch decode layer (norm fused, as in the decode
+    chain): a graph of len(layers) back-to-back launches on independent inputs, replayed `reps`
+    times, HIP events on the stream the graph runs on."""
+    L = len(layers)
+    xs = synth.make_input(L, seed=7, device=dev)
+    ys = torch.empty_like(xs)
+
+    def layer_launches():
+        for l, lw in enumerate(layers):
+            abi.block_forward(xs[l:l + 1], lw, out=ys[l:l + 1], residual=xs[l:l + 1],
+                              norm_w=norms[l])
+
+    layer_launches()
+    torch.cuda.synchronize()
+    gk = capture(torch, layer_launches)
+    for _ in range(4):
+        gk.replay()
+    torch.cuda.synchronize()
+    return time_stream(gk.replay, reps, torch) / L
+
+
 def main():
     args = parse()
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary), end="")
+        return
+    if args.stats_summary:
+        d = args.stats_summary[0]
+        print(stats_summary(d, " ".join(args.stats_summary[1:]) or "(not given)"), end="")
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU "
-                          "sharding is design-only, see DESIGN.md)"}))
+                          "sharding is design-only, described in DESIGN.md)"}))
         sys.exit(2)
     import torch
     import __graft_entry__ as ge
@@ -73,6 +270,9 @@ def main():
     torch.cuda.set_device(dev)
     synth, abi = pkg.synth, pkg.abi
     L = args.layers
+    if args.pmc:
+        pmc_workload(pkg, torch, dev, L)
+        return
 
     # ---------------------------------------------------------------- decode, config 1
     t0 = time.time()
@@ -80,59 +280,64 @@ def main():
     torch.cuda.synchronize()
     resident = sum(lw.gate_up_q.numel() + lw.down_q.numel() for lw in layers)
     log(f"generated {L} layers ({resident / 1e9:.2f} GB routed Q4_K) in {time.time() - t0:.1f}s")
+    active = synth.decode_active_bytes(layers[0])
+    if args.kernel_only:
+        norms = [synth.make_norm_weight(seed=5000 + l, device=dev) for l in range(L)]
+        ms_k = dominant_kernel_ms(torch, synth, abi, layers, norms, dev, args.kernel_reps)
+        log(f"{DECODE_KERNEL}: {ms_k * 1000:.2f} us per launch (graph of {L} launches), "
+            f"{active / (ms_k * 1e-3) / 1e9:.0f} GB/s on {active} B")
+        return
     x0 = synth.make_input(1, seed=0, device=dev)
     xbuf = x0.clone()
+    norms = [synth.make_norm_weight(seed=5000 + l, device=dev) for l in range(L)]
 
     def one_token():
-        # the residual stream through 40 layers, updated in place by the block's own residual add
-        for lw in layers:
-            abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf)
+        # the residual stream through L layers: h <- h + MoE(rmsnorm(h)), in place
+        for lw, nw in zip(layers, norms):
+            abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw)
         xbuf.copy_(synth.rms_normalize(xbuf))
 
     for _ in range(3):
         one_token()
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(g, stream=cap):
-            one_token()
-    torch.cuda.current_stream().wait_stream(cap)
-    torch.cuda.synchronize()
+    g = capture(torch, one_token)
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
     ms = time_stream(g.replay, args.steps, torch)
     us_tok_layer = ms * 1000.0 / L
-    active = synth.decode_active_bytes(layers[0])
     gbps = active / (us_tok_layer * 1e-6) / 1e9
     log(f"decode: {ms:.3f} ms/token over {L} layers = {us_tok_layer:.2f} us/token/layer, "
         f"{gbps:.0f} GB/s on {active} active B/token-layer")
 
-    # dominant kernel: the routed-expert contraction of one decode token (GEMV path), alone
-    lw = layers[0]
-    r = abi.router_topk(x0, lw.router, 8)
-    gr = abi.sort_permute(r["topk_ids"], lw.n_experts)
-    routed_bytes = 8 * lw.routed_bytes_per_expert()
-    y = torch.empty(8, 2048, dtype=torch.float32, device=dev)
+    ms_k = dominant_kernel_ms(torch, synth, abi, layers, norms, dev, args.kernel_reps)
+    kern_gbps = active / (ms_k * 1e-3) / 1e9
+    traffic = committed_traffic()
+    log(f"{DECODE_KERNEL}: {ms_k * 1000:.2f} us per launch (graph of {L} launches), "
+        f"{kern_gbps:.0f} GB/s on {active} B; traffic/launch {traffic}")
+    err_bits = abi.device_error_bits(dev)
+    if err_bits:
+        log(f"WARNING: device error bits {err_bits:#x} (a bounded spin timed out)")
 
-    def experts_call():
-        abi.experts(x0, lw.gate_up_q, lw.gate_up_fmt, lw.down_q, lw.down_fmt, gr, 8, path=1)
-
-    for _ in range(20):
-        experts_call()
-    # rotate over layers so the bytes come from HBM, not the 256 MB MALL
-    lws = layers
-
-    def experts_rot():
-        for lw2 in lws:
-            abi.experts(x0, lw2.gate_up_q, lw2.gate_up_fmt, lw2.down_q, lw2.down_fmt, gr, 8, path=1)
-
-    ms_exp = time_stream(experts_rot, 20, torch) / len(lws)
-    exp_gbps = routed_bytes / (ms_exp * 1e-3) / 1e9
-    log(f"routed experts (gate_up + down GEMV, 8 experts): {ms_exp * 1000:.2f} us, {exp_gbps:.0f} GB/s")
-    del y
+    # ---------------------------------------------------------------- batched decode, config 2
+    c2 = {}
+    if not args.no_c2:
+        lz = synth.make_layer(seed=1, device=dev, zipf=True)
+        xz = synth.make_input(64, seed=1, device=dev)
+        oz = torch.empty_like(xz)
+        r = abi.router_topk(xz, lz.router, lz.top_k, bias=lz.router_bias)
+        uniq = int(torch.unique(r["topk_ids"]).numel())
+        for _ in range(3):
+            abi.block_forward(xz, lz, out=oz)
+        torch.cuda.synchronize()
+        gz = capture(torch, lambda: abi.block_forward(xz, lz, out=oz))
+        ms_z = time_stream(gz.replay, 50, torch)
+        bytes_z = uniq * lz.routed_bytes_per_expert() + lz.shared_bytes()
+        c2 = {"c2_us_per_step": round(ms_z * 1000, 2), "c2_unique_experts": uniq,
+              "c2_gbps": round(bytes_z / (ms_z * 1e-3) / 1e9, 1)}
+        log(f"c2 T=64 zipf: {ms_z * 1000:.1f} us/step, {uniq} unique experts, "
+            f"{c2['c2_gbps']:.0f} GB/s")
+        del lz
 
     # ---------------------------------------------------------------- prefill, config 3
     prefill = {}
@@ -166,10 +371,11 @@ def main():
             t_cpu += time.perf_counter() - t1
             xc = synth.rms_normalize(xc + res["combined_out"])
             n += 1
-        cpu = {"value": t_cpu / n * 1e6, "unit": "us/token/layer", "cores": torch.get_num_threads(),
-               "kind": "port",
-               "sample": f"{n} sequential decode tokens through one layer (config 0/1 shapes): "
-                         "oracle dequant of the 8 selected Q4_K experts + f32 F.linear + shared"}
+        cpu = {"value": round(t_cpu / n * 1e6, 1), "unit": "us/token/layer",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{n} sequential decode tokens through one config-1 layer: oracle "
+                         "dequant of the 8 selected Q4_K experts + f32 F.linear + shared expert "
+                         f"(os.cpu_count()={os.cpu_count()})"}
         log(f"cpu baseline: {cpu['value']:.0f} us/token/layer over {n} tokens, {cpu['cores']} threads")
 
     result = {
@@ -179,18 +385,20 @@ def main():
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K, N(0,1) activations)",
         "config": {"workload": f"config 1: decode bs=1, {L} resident layer instances, "
-                               f"{args.steps} sequential tokens (x <- x + MoE(x) per layer, "
-                               "RMS-renormalised per token)", "layers": L,
+                               f"{args.steps} sequential tokens (h <- h + MoE(rmsnorm(h)) per "
+                               "layer, norm and residual fused; h RMS-renormalised per token)",
+                   "layers": L,
                    "tokens": args.steps, "experts": 256, "top_k": 8, "hidden": 2048,
                    "moe_intermediate": 512, "format": "Q4_K"},
         "decode_hbm_gbps": round(gbps, 1),
         "decode_hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(exp_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(exp_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "routed experts GEMV (k_gemv_gateup_q4k + k_gemv_down_q4k)",
-                     "bytes_per_launch": routed_bytes, "avg_us": round(ms_exp * 1000, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "kernel": DECODE_KERNEL,
+                     "bytes_per_launch": active, "avg_us": round(ms_k * 1000, 3)},
         "cpu_baseline": cpu,
     }
+    result.update(c2)
     result.update({k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()})
     print(json.dumps(result), flush=True)
 

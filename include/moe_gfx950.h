@@ -118,13 +118,17 @@ int moe_combine(const float *y, const int32_t *pair_pos, const int32_t *topk_ids
                 void *stream);
 
 /* The whole block in one stream-ordered call. Replaces speccheck/moe_ref.py:499-533 (moe_block),
- * engine/block_forward.py:670-681 and engine/m3_forward.py:430-476. out = residual + MoE(x) when
- * `residual` [T,H] f32 is given (the decoder layer's own residual add, engine/m3_forward.py:737;
- * out may alias residual), else MoE(x). Stage outputs other than `out` may be NULL; expert_raw is
- * [T,K,H] in slot order. A single token with K = 8 and Q4_K gate_up runs the fused three-launch
- * decode path. */
+ * engine/block_forward.py:670-681 and engine/m3_forward.py:430-476.
+ * norm_w [H] f32 (optional): the block input is then the post-attention RMSNorm of x, Form A with
+ * the artifact's (1+w) already in norm_w (engine/m3_forward.py:303-307, :732-733):
+ * (x * f32(1/sqrt(mean(x^2) + norm_eps))) * norm_w, the scale evaluated in f64 and rounded once;
+ * NULL: x is the block input as given. out = residual + MoE(input) when `residual` [T,H] f32 is
+ * given (the decoder layer's own residual add, engine/m3_forward.py:737; out may alias residual
+ * and x), else MoE(input). Stage outputs other than `out` may be NULL; expert_raw is [T,K,H] in
+ * slot order. A single token with K = 8 and Q4_K gate_up runs the single-launch decode layer
+ * (the norm fused into it) on devices with >= 256 CUs, else the three-launch decode path. */
 int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
-                      const void *w_router, const float *logit_bias, const void *gate_up_q,
+                      const float *norm_w, float norm_eps, const void *w_router, const float *logit_bias, const void *gate_up_q,
                       int gate_up_fmt, const void *down_q, int down_fmt, const void *ws_gate,
                       const void *ws_up, const void *ws_down, const void *ws_scalar_gate,
                       int path, const float *residual, float *out, void *logits_bf16,

@@ -29,4 +29,7 @@ Pinning status (what checks each function; details in the test files):
   r1_logits             f64 brute force plus exact rational recompute at rounding midpoints.
   route / moe_block     invariants (weights sum to 1, descending order), closed forms
                         (one-hot x, W=0, E=K), brute-force f64 on tiny shapes.
+  rmsnorm_a             closed form on constant rows, exact invariance under power-of-two
+                        scaling (eps = 0), exact-rational scale on random rows, within 2 ulp of
+                        torch's own f32 formula (the reference's arithmetic).
 """

@@ -15,6 +15,11 @@ engine/block_forward.py:614-681, specification/11-moe-block.md §11.2-§11.6):
   shared[t] = sigmoid(wsg . x) * down_s @ (silu(gate_s x) * up_s x)                 (f32)
   out = routed + shared
 
+With a post-attention norm weight (the decoder layer's MoE half, engine/m3_forward.py:732-737):
+
+  xn  = rmsnorm_a(x1, w) = (x1 * r) * w,  r = f32(1 / sqrt(mean(x1^2) + eps))  (f64, one rounding)
+  x   = x1 + moe_block(xn)["combined_out"]
+
 R1 is the one deliberate departure from the reference's own arithmetic: torch's bf16 F.linear sums
 in a blocked, thread-dependent order (prototype/moe_router/results.md:36), so this oracle defines
 R1 as the correctly rounded dot — f64 accumulation with a certified error bound, and an exact
@@ -218,6 +223,28 @@ def moe_block(x: torch.Tensor, lw: LayerWeights, top_k: int = 8) -> dict:
 
 
 # --------------------------------------------------------------------------------- comparators
+def rmsnorm_a(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """Post-attention RMSNorm, Form A with the artifact's (1 + w) already in w
+    (engine/m3_forward.py:303-307): (x * r) * w in f32. This oracle evaluates the scale
+    r = 1/sqrt(mean(x^2) + eps) in f64 (every square of an f32 is exact there) and rounds it once
+    to f32; torch's f32 mean sums in a vectorized, unpinnable order and differs from it by at most
+    a couple of f32 ulps of r."""
+    xf = x.float()
+    x64 = xf.double()
+    ms = (x64 * x64).sum(-1, keepdim=True) / x.shape[-1]
+    r = (1.0 / torch.sqrt(ms + float(eps))).float()
+    return (xf * r) * w.float()
+
+
+def residual_step(x1: torch.Tensor, lw: LayerWeights, norm_w: torch.Tensor, eps: float,
+                  top_k: int = 8) -> dict:
+    """The decoder layer's MoE half (engine/m3_forward.py:732-737): h = rmsnorm_a(x1, w);
+    x = x1 + moe_block(h). Returns moe_block's stages (on h) plus "x_out"."""
+    st = moe_block(rmsnorm_a(x1, norm_w, eps), lw, top_k)
+    st["x_out"] = x1.float() + st["combined_out"]
+    return st
+
+
 def metrics(a: torch.Tensor, b: torch.Tensor, name: str = "") -> dict:
     """speccheck/moe_ref.py:578-630 comparator fields (max_abs, max_abs_over_scale, 1-cos, ndiff);
     refuses non-finite input and an all-zero reference."""

@@ -46,7 +46,8 @@ SIGNATURES = {
     "moe_shared_expert": (_I, [_VP, _I, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _SZ,
                                _VP]),
     "moe_combine": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
-    "moe_block_forward": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP, _I, _VP, _I, _VP,
+    "moe_block_forward": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, _VP, ctypes.c_float,
+                               _VP, _VP, _VP, _I, _VP, _I, _VP,
                                _VP, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                _VP, _VP, _SZ, _VP]),
     "moe_workspace_init": (_I, [_VP, _SZ, _VP]),

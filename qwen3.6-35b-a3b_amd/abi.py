@@ -190,12 +190,17 @@ def combine(y: torch.Tensor, grouping: dict, ids: torch.Tensor, w_bf16: torch.Te
 
 
 def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False,
-                  out: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> dict:
+                  out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+                  norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6) -> dict:
     """The whole block in one library call (moe_block_forward). `lw` is a LayerWeights;
     `stages` is False, True (every stage output) or a set of stage names to return;
-    out = residual + MoE(x) when `residual` (f32 [T,H], may be `out` itself) is given."""
+    out = residual + MoE(input) when `residual` (f32 [T,H], may be `out` or `x` itself) is given.
+    input = x, or the post-attention RMSNorm of x when `norm_w` (f32 [H], the artifact's 1+w) is
+    given: engine/m3_forward.py:732-737 is then block_forward(x1, lw, norm_w=w, residual=x1)."""
     _need(x, "x")
     T, H = x.shape
+    if norm_w is not None:
+        _need(norm_w, "norm_w", torch.float32, (H,), x.device)
     E, K, I, Is = lw.n_experts, lw.top_k, lw.i_e, lw.i_s
     dev = x.device
     if out is None:
@@ -213,7 +218,7 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
     ws = workspace(dev, workspace_bytes(T, H, I, E, K, Is))
     g = st.get
     _check(L.lib.moe_block_forward(
-        _p(x), _xdt(x), T, H, I, E, K, Is, _p(lw.router), _p(lw.router_bias), _p(lw.gate_up_q),
+        _p(x), _xdt(x), T, H, I, E, K, Is, _p(norm_w), float(norm_eps), _p(lw.router), _p(lw.router_bias), _p(lw.gate_up_q),
         lw.gate_up_fmt, _p(lw.down_q), lw.down_fmt, _p(lw.shared_gate), _p(lw.shared_up),
         _p(lw.shared_down), _p(lw.shared_scalar_gate), path, _p(residual), _p(out),
         _p(g("router_logits")),

@@ -50,7 +50,7 @@ static int pick_path(int path, int T, int gate_up_fmt) {
 
 struct Carve {
   // every piece a T-token forward can need; sizes are upper bounds over both paths
-  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, flag;
+  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, xn, flag;
 };
 
 static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
@@ -71,6 +71,7 @@ static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
   c.sS = r256((size_t)T * Is * 4);
   c.sraw = r256((size_t)T * H * 4);
   c.gprob = r256((size_t)T * 4);
+  c.xn = r256((size_t)T * H * 4);
   c.flag = 256;
   return c;
 }
@@ -85,7 +86,7 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s) {
   if (T < 1 || E < 1 || K < 1) return 0;
   const Carve c = carve_sizes(T, H, I, E, K, I_s);
   return kSyncBytes + c.logits + c.ids + c.wf + c.wb + c.offsets + c.sorted + c.pos + c.hits +
-         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.flag;
+         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.xn + c.flag;
 }
 
 int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
@@ -234,6 +235,7 @@ int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids
 }
 
 int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                      const float* norm_w, float norm_eps,
                       const void* w_router, const float* logit_bias, const void* gate_up_q,
                       int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
                       const void* ws_up, const void* ws_down, const void* ws_scalar_gate,
@@ -249,6 +251,8 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
   if (I_s % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_block_forward: need I_s %% 512 == 0");
   if (!aligned16(x) || !aligned16(w_router) || !aligned16(ws_gate) || !aligned16(ws_up) || !aligned16(ws_down) || !aligned16(ws_scalar_gate))
     return moe_set_error(MOE_E_ARG, "moe_block_forward: pointers must be 16-byte aligned");
+  if (norm_w && (!aligned16(norm_w) || !(norm_eps >= 0.0f) || norm_eps > 1.0f))
+    return moe_set_error(MOE_E_ARG, "moe_block_forward: norm_w must be 16-byte aligned and 0 <= norm_eps <= 1");
   const size_t need = moe_workspace_bytes(T, H, I, E, K, I_s);
   if (!ws || ws_bytes < need) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace needs %zu bytes", need);
   hipStream_t st = (hipStream_t)stream;
@@ -256,8 +260,19 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
   MoeWs w{reinterpret_cast<char*>(ws), ws_bytes};
   int* sync = reinterpret_cast<int*>(w.take(kSyncBytes));
   const int rpath = pick_path(path, T, gate_up_fmt);
-  if (T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
-      (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q6_K) && I_s % 128 == 0 && E % 4 == 0) {
+  const bool decode = T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
+                      (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q6_K) && I_s % 128 == 0 && E % 4 == 0;
+  const bool one_launch = decode && path != MOE_PATH_GEMV_MULTI &&
+                          moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt);
+  if (norm_w && !one_launch) {
+    // every other path reads the normalized rows from the workspace (f32)
+    float* xn = reinterpret_cast<float*>(w.take((size_t)T * H * 4));
+    if (!xn) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+    MOE_TRY(moe_launch_rmsnorm(x, x_dtype, T, H, norm_w, norm_eps, xn, st));
+    x = xn;
+    x_dtype = MOE_DT_F32;
+  }
+  if (decode) {
     MoeDecodeLaunch L;
     L.x = x; L.x_dtype = x_dtype; L.residual = residual; L.w_router = w_router; L.bias = logit_bias;
     L.gu = gate_up_q; L.dn = down_q; L.dn_fmt = down_fmt;
@@ -274,10 +289,11 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
     L.counter = sync;
     L.H = H; L.I = I; L.E = E; L.K = K; L.Is = I_s;
     L.ids_out_requested = (topk_ids || topk_w_bf16 || topk_w_f32) ? 1 : 0;
+    L.norm_w = one_launch ? norm_w : nullptr;
+    L.norm_eps = norm_eps;
     if (!L.logits || !L.ids || !L.w_f32 || !L.w_bf16 || !L.s_shared || !L.gate_prob || !L.shared_raw || !L.s_routed)
       return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
-    if (path != MOE_PATH_GEMV_MULTI &&
-        moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt))
+    if (one_launch)
       return moe_launch_decode_layer(L, sync, reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sync) + 256), st);
     return moe_launch_decode_fused(L, st);
   }

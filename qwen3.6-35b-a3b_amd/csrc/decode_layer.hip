@@ -3,6 +3,8 @@
 // between them through self-validating exchange words instead of kernel boundaries or
 // device-wide fences.
 //
+//   start    every wg stages x in LDS, RMS-normalized when a post-attention norm weight is given
+//            (Form A, engine/m3_forward.py:303-307; the f64 sum of squares is a block reduction)
 //   phase 1  wg g: router logit e = g (f64, certified bf16) | shared gate/up rows i = 2g, 2g+1 |
 //            (wg 0) the scalar shared gate                 -> logits[E], s_shared[I_s], gate
 //   phase 2  every wg waits for the 256 logits and runs R2-R5 itself (same answer everywhere; the
@@ -62,6 +64,8 @@ struct LayerArgs {
   float* shared_out;
   float* expert_raw;
   int exact_order;                      // stage outputs requested: keep torch's slot order
+  const float* norm_w;                  // post-attention RMSNorm weight [H] f32, or NULL
+  float norm_eps;
 };
 
 // exchange buffer layout (uint32 words; every region starts 16-byte aligned)
@@ -143,6 +147,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ float sh_raw[8];
   __shared__ float ys[K][8];
   __shared__ float s_gate;
+  __shared__ double s_red[kThreads / 64];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int l16 = lane & 15;
@@ -156,7 +161,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(xb, 0, XW_BUF * 4, 0x00020000);
 
-  // x into LDS as f32; the residual of this workgroup's 8 output rows; the next buffer's slice
+  // x into LDS as f32 (RMS-normalized first when norm_w is given); the residual of this
+  // workgroup's 8 output rows; the next buffer's slice
   {
     float4 v;
     if (XDT == MOE_DT_F32) {
@@ -165,6 +171,19 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       const uint2 u = reinterpret_cast<const uint2*>(a.x)[t];
       v = make_float4(bf16_to_f32(u.x & 0xFFFFu), bf16_to_f32(u.x >> 16),
                       bf16_to_f32(u.y & 0xFFFFu), bf16_to_f32(u.y >> 16));
+    }
+    if (a.norm_w) {
+      // r = f32(1 / sqrt(mean(x^2) + eps)) in f64: every square is exact, one final rounding
+      const float4 nw = reinterpret_cast<const float4*>(a.norm_w)[t];
+      double ss = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+      ss = wave_sum_f64(ss);
+      if (lane == 0) s_red[wave] = ss;
+      __syncthreads();
+      double tot = 0.0;
+#pragma unroll
+      for (int j = 0; j < kThreads / 64; ++j) tot += s_red[j];
+      const float r = (float)(1.0 / sqrt(tot / (double)H + (double)a.norm_eps));
+      v = make_float4((v.x * r) * nw.x, (v.y * r) * nw.y, (v.z * r) * nw.z, (v.w * r) * nw.w);
     }
     reinterpret_cast<float4*>(s_x)[t] = v;
   }
@@ -492,6 +511,8 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   a.gate_prob_out = L.gate_prob; a.out = L.out; a.routed_sum = L.routed_sum;
   a.shared_out = L.shared_out; a.expert_raw = L.expert_raw;
   a.exact_order = (L.ids_out_requested || L.expert_raw) ? 1 : 0;
+  a.norm_w = L.norm_w;
+  a.norm_eps = L.norm_eps;
   if (L.x_dtype == MOE_DT_F32)
     hipLaunchKernelGGL(k_dec_layer<MOE_DT_F32>, dim3(kG), dim3(kThreads), 0, st, a);
   else

@@ -83,8 +83,13 @@ struct MoeDecodeLaunch {
   int* counter;
   int H, I, E, K, Is;
   int ids_out_requested;   // the caller asked for topk_ids / weights: keep torch's slot order
+  const float* norm_w;     // post-attention RMSNorm weight [H] f32, or NULL (x is the input)
+  float norm_eps;
 };
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
+// xn[T,H] f32 = (x * f32(1/sqrt(mean_f64(x^2) + eps))) * w   (norm.hip)
+int moe_launch_rmsnorm(const void* x, int x_dtype, int T, int H, const float* w, float eps,
+                       float* out, hipStream_t st);
 int moe_launch_zero_words(int* p, int n, hipStream_t st);
 
 // The first kSyncBytes of every workspace hold the library's device-side sync words (block

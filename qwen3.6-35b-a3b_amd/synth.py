@@ -74,6 +74,12 @@ def rms_normalize(x: torch.Tensor) -> torch.Tensor:
     return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + 1e-6)).to(x.dtype)
 
 
+def make_norm_weight(seed: int, device="cuda", hidden: int = 2048, std: float = 0.1) -> torch.Tensor:
+    """A post-attention RMSNorm weight as the artifact stores it (1 + w folded in): 1 + N(0, std)."""
+    g = torch.Generator(device="cpu").manual_seed(seed + 15485863)
+    return (1.0 + std * torch.randn(hidden, generator=g)).to(device)
+
+
 def decode_active_bytes(lw: LayerWeights) -> int:
     """Bytes of the 8 routed + 1 shared active experts per token-layer (20,447,232)."""
     return lw.top_k * lw.routed_bytes_per_expert() + lw.shared_bytes()

@@ -59,10 +59,15 @@ def test_refusals_happen_on_the_host(pkg):
     rc = lib.moe_router_topk(p, 0, p, None, 1, 2048, 256, 2, p, None, p, p, p, None, 0, None)
     assert rc == pkg._lib.MOE_E_UNSUPPORTED                                  # K*64 <= E
     assert b"K*64 > E" in lib.moe_last_error()
-    rc = lib.moe_block_forward(p, 0, 1, 2048, 512, 256, 8, 512, p, None, p, 12, p, 12, p, p, p, p,
-                               0, None, p, None, None, None, None, None, None, None, None, p, 16,
-                               None)
+    rc = lib.moe_block_forward(p, 0, 1, 2048, 512, 256, 8, 512, None, 1e-6, p, None, p, 12, p, 12,
+                               p, p, p, p, 0, None, p, None, None, None, None, None, None, None,
+                               None, p, 16, None)
     assert rc == pkg._lib.MOE_E_WORKSPACE
+    # a negative norm eps is refused before anything else is looked at
+    rc = lib.moe_block_forward(p, 0, 1, 2048, 512, 256, 8, 512, p, -1.0, p, None, p, 12, p, 12,
+                               p, p, p, p, 0, None, p, None, None, None, None, None, None, None,
+                               None, p, 1 << 30, None)
+    assert rc == pkg._lib.MOE_E_ARG
     rc = lib.moe_experts(p, 0, p, 99, p, 12, p, p, p, 1, 2048, 512, 256, 8, 0, p, p, 1 << 20, None)
     assert rc == pkg._lib.MOE_E_FORMAT
     assert lib.moe_workspace_init(p, 16, None) == pkg._lib.MOE_E_ARG

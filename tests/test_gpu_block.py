@@ -209,3 +209,40 @@ def test_decode_single_launch_ties(pkg, layer_c0, dev, case):
         assert_close(st["combined_out"].cpu(), ref["combined_out"][i:i + 1], f"{case} token {i}")
         assert torch.equal(plain["combined_out"], st["combined_out"]), (case, i)
     assert pkg.abi.device_error_bits(dev) == 0
+
+
+def _norm_weight(seed, H, dev):
+    g = torch.Generator().manual_seed(seed)
+    return (1.0 + 0.1 * torch.randn(H, generator=g)).to(dev)
+
+
+@pytest.mark.parametrize("path", ["single_launch", "three_launch"])
+def test_decode_with_post_attention_norm(pkg, layer_c0, dev, path):
+    """engine/m3_forward.py:732-737 in one call: x = x1 + MoE(rmsnorm_a(x1, w)) with the norm fused
+    into the single-launch layer (or a norm kernel in front of the three-launch form). Routing
+    bit-exact against the oracle, x_out within the block tolerance, residual updated in place."""
+    lw, ow = layer_c0
+    w = _norm_weight(31, 2048, dev)
+    scales = torch.tensor([0.25, 1.0, 3.0, 17.0, 0.5, 8.0], device=dev).view(-1, 1)
+    x1 = pkg.synth.make_input(6, seed=31, device=dev) * scales
+    ref = O.residual_step(x1.cpu(), ow, w.cpu(), 1e-6)
+    p = pkg._lib.MOE_PATH_GEMV if path == "single_launch" else pkg._lib.MOE_PATH_GEMV_MULTI
+    for i in range(x1.shape[0]):
+        h = x1[i:i + 1].clone()
+        st = pkg.abi.block_forward(h, lw, path=p, stages={"topk_ids"}, out=h, residual=h, norm_w=w)
+        torch.cuda.synchronize()
+        assert torch.equal(st["topk_ids"].cpu().long(), ref["topk_ids"][i:i + 1]), (path, i)
+        assert_close(h.cpu() - x1[i:i + 1].cpu(), ref["combined_out"][i:i + 1], f"{path} token {i}")
+    assert pkg.abi.device_error_bits(dev) == 0
+
+
+@pytest.mark.parametrize("path", [1, 2])
+def test_batched_with_post_attention_norm(pkg, layer_zipf, dev, path):
+    """The norm kernel in front of the multi-token paths (GEMV and MFMA), c2 shapes."""
+    lw, ow = layer_zipf
+    w = _norm_weight(32, 2048, dev)
+    x1 = pkg.synth.make_input(64, seed=32, device=dev) * 4.0
+    ref = O.residual_step(x1.cpu(), ow, w.cpu(), 1e-6)
+    st = pkg.abi.block_forward(x1, lw, path=path, stages={"topk_ids"}, residual=x1, norm_w=w)
+    assert torch.equal(st["topk_ids"].cpu().long(), ref["topk_ids"]), path
+    assert_close(st["combined_out"].cpu() - x1.cpu(), ref["combined_out"], f"norm path {path}")
