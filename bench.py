@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-c2", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config-3 prefill timing (what the prefill profile covers)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing (what the kernel-trace profile covers)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -249,6 +251,22 @@ def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> floa
     return time_stream(gk.replay, reps, torch) / L
 
 
+def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
+    """Config 3: one block over T = 4096 bf16 tokens (uniform routing), HIP events."""
+    xp = synth.make_input(4096, seed=2, device=dev, dtype=torch.bfloat16)
+    outp = torch.empty(4096, 2048, dtype=torch.float32, device=dev)
+    for _ in range(2):
+        abi.block_forward(xp, lwp, out=outp)
+    torch.cuda.synchronize()
+    ms_p = time_stream(lambda: abi.block_forward(xp, lwp, out=outp), steps, torch)
+    flops = synth.prefill_flops(4096, lwp)
+    tflops = flops / (ms_p * 1e-3) / 1e12
+    log(f"prefill T=4096: {ms_p:.3f} ms, {4096 / (ms_p * 1e-3):.0f} tok/s, "
+        f"{tflops:.1f} TFLOP/s ({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+    return {"prefill_tok_s": 4096 / (ms_p * 1e-3), "prefill_ms": ms_p,
+            "prefill_tflops": tflops, "prefill_mfma_util": tflops / BF16_PEAK_TFLOPS}
+
+
 def main():
     args = parse()
     if args.pmc_summary:
@@ -272,6 +290,12 @@ def main():
     L = args.layers
     if args.pmc:
         pmc_workload(pkg, torch, dev, L)
+        return
+
+    if args.prefill_only:
+        lwp = synth.make_layer(seed=2, device=dev)
+        r = prefill_c3(torch, synth, abi, lwp, dev, args.prefill_steps)
+        print(json.dumps({k: round(v, 4) for k, v in r.items()}), flush=True)
         return
 
     # ---------------------------------------------------------------- decode, config 1
@@ -342,19 +366,7 @@ def main():
     # ---------------------------------------------------------------- prefill, config 3
     prefill = {}
     if not args.no_prefill:
-        lwp = layers[0]
-        xp = synth.make_input(4096, seed=2, device=dev, dtype=torch.bfloat16)
-        outp = torch.empty(4096, 2048, dtype=torch.float32, device=dev)
-        for _ in range(2):
-            abi.block_forward(xp, lwp, out=outp)
-        torch.cuda.synchronize()
-        ms_p = time_stream(lambda: abi.block_forward(xp, lwp, out=outp), args.prefill_steps, torch)
-        flops = synth.prefill_flops(4096, lwp)
-        tflops = flops / (ms_p * 1e-3) / 1e12
-        prefill = {"prefill_tok_s": 4096 / (ms_p * 1e-3), "prefill_ms": ms_p,
-                   "prefill_tflops": tflops, "prefill_mfma_util": tflops / BF16_PEAK_TFLOPS}
-        log(f"prefill T=4096: {ms_p:.2f} ms, {prefill['prefill_tok_s']:.0f} tok/s, "
-            f"{tflops:.1f} TFLOP/s ({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+        prefill = prefill_c3(torch, synth, abi, layers[0], dev, args.prefill_steps)
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None

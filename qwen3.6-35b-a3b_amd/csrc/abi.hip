@@ -50,7 +50,7 @@ static int pick_path(int path, int T, int gate_up_fmt) {
 
 struct Carve {
   // every piece a T-token forward can need; sizes are upper bounds over both paths
-  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, xn, flag;
+  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, xn, x16, flag;
 };
 
 static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
@@ -65,13 +65,14 @@ static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
   c.pos = r256(P * 4);
   c.hits = r256((size_t)(E + 1) * 4);
   c.sort_ws = moe_sort_ws_bytes((int)P, E);
-  c.tiles = r256((size_t)(1 + 2 * moe_max_mtiles((int)P, E)) * 4);
+  c.tiles = r256((size_t)(1 + 2 * moe_max_mtiles((int)P, E, MOE_GEMM_BM)) * 4);
   c.S = r256(P * I * 4);
   c.y = r256(P * H * 4);
   c.sS = r256((size_t)T * Is * 4);
   c.sraw = r256((size_t)T * H * 4);
   c.gprob = r256((size_t)T * 4);
   c.xn = r256((size_t)T * H * 4);
+  c.x16 = r256((size_t)T * H * 2);
   c.flag = 256;
   return c;
 }
@@ -86,7 +87,7 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s) {
   if (T < 1 || E < 1 || K < 1) return 0;
   const Carve c = carve_sizes(T, H, I, E, K, I_s);
   return kSyncBytes + c.logits + c.ids + c.wf + c.wb + c.offsets + c.sorted + c.pos + c.hits +
-         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.xn + c.flag;
+         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.xn + c.x16 + c.flag;
 }
 
 int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
@@ -135,10 +136,11 @@ int moe_sort_permute(const int32_t* topk_ids, int T, int K, int E, int32_t* expe
                          (hipStream_t)stream);
 }
 
-static int experts_impl(const void* x, int x_dtype, const void* gu, int gu_fmt, const void* dn,
-                        int dn_fmt, const int32_t* offsets, const int32_t* sorted_pairs,
-                        const int32_t* hit_list, int T, int H, int I, int E, int K, int path,
-                        float* y, MoeWs& w, hipStream_t st) {
+// x16: the rows already in f16 (the MFMA paths' activation operand), or NULL to convert here
+static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const void* gu, int gu_fmt,
+                        const void* dn, int dn_fmt, const int32_t* offsets,
+                        const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
+                        int E, int K, int path, float* y, MoeWs& w, hipStream_t st) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
   path = pick_path(path, T, gu_fmt);
@@ -148,14 +150,28 @@ static int experts_impl(const void* x, int x_dtype, const void* gu, int gu_fmt, 
     MOE_TRY(moe_launch_gemv_gateup(x, x_dtype, gu, gu_fmt, offsets, sorted_pairs, hit_list, max_hits, H, I, K, S, st));
     return moe_launch_gemv_down(S, dn, dn_fmt, offsets, hit_list, max_hits, H, I, y, st);
   }
-  const int max_tiles = moe_max_mtiles(P, E);
-  int32_t* tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
-  uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
-  if (!tiles || !S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
   const size_t gu_row = gu_fmt == MOE_FMT_Q4_K ? (size_t)H / 256 * 144 : gu_fmt == MOE_FMT_Q6_K ? (size_t)H / 256 * 210 : (size_t)H * 2;
   const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
   const uint8_t* g = reinterpret_cast<const uint8_t*>(gu);
-  MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st));
+  const bool v2 = path == MOE_PATH_MFMA && moe_gemm2_supports(gu_fmt) && moe_gemm2_supports(dn_fmt) &&
+                  H % 256 == 0 && I % 256 == 0;
+  const int bm = v2 ? MOE_GEMM2_BM : MOE_GEMM_BM;
+  const int max_tiles = moe_max_mtiles(P, E, bm);
+  int32_t* tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
+  uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
+  if (!tiles || !S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+  MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, bm));
+  if (v2) {
+    if (!x16) {
+      uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+      if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+      MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+      x16 = c;
+    }
+    MOE_TRY(moe_launch_gemm3_gateup(x16, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
+                                    max_tiles, T, offsets, sorted_pairs, K, H, I, S, st));
+    return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, st);
+  }
   const int opb = path == MOE_PATH_MFMA_BF16;
   MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
                                  max_tiles, T, offsets, sorted_pairs, K, H, I, opb, S, st));
@@ -185,23 +201,33 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, int gate_up_f
   if (!aligned16(x)) return moe_set_error(MOE_E_ARG, "moe_experts: x must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
-  return experts_impl(x, x_dtype, gate_up_q, gate_up_fmt, down_q, down_fmt, expert_offsets,
+  return experts_impl(x, x_dtype, nullptr, gate_up_q, gate_up_fmt, down_q, down_fmt, expert_offsets,
                       sorted_pairs, hit_list, T, H, I, E, K, path, y, w, (hipStream_t)stream);
 }
 
-static int shared_impl(const void* x, int x_dtype, const void* wg, const void* wu, const void* wd,
-                       const void* wsg, int T, int H, int Is, int path, float* shared_raw,
-                       float* gate_prob, MoeWs& w, hipStream_t st) {
+static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const void* wg,
+                       const void* wu, const void* wd, const void* wsg, int T, int H, int Is,
+                       int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st) {
   if (path == MOE_PATH_AUTO) path = T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
-  if (path == MOE_PATH_GEMV) {
+  if (path == MOE_PATH_GEMV || path == MOE_PATH_GEMV_MULTI) {
     float* s = reinterpret_cast<float*>(w.take((size_t)T * Is * 4));
     if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
     return moe_launch_shared_gemv(x, x_dtype, wg, wu, wd, wsg, T, H, Is, s, shared_raw, gate_prob, st);
   }
   uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
   if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
-  const int opb = path == MOE_PATH_MFMA_BF16;
   MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, T, H, gate_prob, st));
+  if (path == MOE_PATH_MFMA && H % 256 == 0 && Is % 256 == 0) {
+    if (!x16) {
+      uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+      if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+      MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+      x16 = c;
+    }
+    MOE_TRY(moe_launch_gemm3_gateup(x16, wg, wu, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, s, st));
+    return moe_launch_gemm3_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, shared_raw, st);
+  }
+  const int opb = path == MOE_PATH_MFMA_BF16;
   MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, wg, wu, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, opb, s, st));
   return moe_launch_gemm_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, opb, shared_raw, st);
 }
@@ -218,8 +244,8 @@ int moe_shared_expert(const void* x, int x_dtype, const void* w_gate, const void
     return moe_set_error(MOE_E_ARG, "moe_shared_expert: pointers must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
-  return shared_impl(x, x_dtype, w_gate, w_up, w_down, w_scalar_gate, T, H, I_s, path, shared_raw,
-                     gate_prob, w, (hipStream_t)stream);
+  return shared_impl(x, x_dtype, nullptr, w_gate, w_up, w_down, w_scalar_gate, T, H, I_s, path,
+                     shared_raw, gate_prob, w, (hipStream_t)stream);
 }
 
 int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids,
@@ -311,12 +337,19 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
   float* gp = gate_prob ? gate_prob : reinterpret_cast<float*>(w.take((size_t)T * 4));
   if (!logits || !ids || !wf || !wb || !offsets || !sorted || !pos || !hits || !y || !sraw || !gp)
     return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+  // the MFMA path's f16 activation operand, converted once for the shared and routed GEMMs
+  uint16_t* x16 = nullptr;
+  if (rpath == MOE_PATH_MFMA) {
+    x16 = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+    if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+    MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
+  }
   MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, logit_bias, T, H, E, logits, st));
   MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
   MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
   MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
-  MOE_TRY(shared_impl(x, x_dtype, ws_gate, ws_up, ws_down, ws_scalar_gate, T, H, I_s, path, sraw, gp, w2, st));
-  MOE_TRY(experts_impl(x, x_dtype, gate_up_q, gate_up_fmt, down_q, down_fmt, offsets, sorted, hits,
+  MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate, T, H, I_s, path, sraw, gp, w2, st));
+  MOE_TRY(experts_impl(x, x_dtype, x16, gate_up_q, gate_up_fmt, down_q, down_fmt, offsets, sorted, hits,
                        T, H, I, E, K, path, y, w, st));
   return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                             shared_out, expert_raw, st);

@@ -1,0 +1,372 @@
+// Prefill-path grouped GEMM, warp-specialized form (gfx950, v_mfma_f32_32x32x16_f16, f32 acc).
+//
+// Work: one tile of up to 128 sorted (token, slot) rows of one expert (k_build_tiles, 128-row
+// tiles) times one output slab per block, in the XCD-aware order of gemm2.hip. Block = 8 waves,
+// one producer and one consumer per SIMD:
+//   producers (waves 4..7): per 64-wide K step, load the activation rows (f16) and the raw Q4_K /
+//     bf16 bytes of the slab's weight rows, decode the weights to f16 once, and store both tiles
+//     into LDS (double buffered);
+//   consumers (waves 0..3): read A and B fragments from LDS and issue the MFMAs; each owns all 128
+//     rows x (32 gate + 32 up) columns (gate_up) or 64 down columns (down).
+// A producer's VALU decode and a consumer's MFMAs on the same SIMD run concurrently, and every
+// weight element is decoded exactly once per block. One barrier per step hands the buffers over.
+//
+// Decode arithmetic (mantissa trick, as in gemm2.hip): low nibble q under the f16 0x6400 (1024)
+// gives 1024 + q, a high nibble left at bits 4-7 under 0x5400 (64, ulp 1/16) gives 64 + q; one
+// packed subtract leaves q exactly and one packed FMA gives q * f16(d * sc) - f16(dmin * m).
+#include "common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+namespace g3 {
+
+constexpr int kBM = MOE_GEMM2_BM;       // 128 rows per tile
+constexpr int kBK = 64;                 // K per step
+constexpr int kS = 72;                  // LDS row stride in f16 (144 B)
+constexpr int kXcd = 8;
+constexpr int kBN = 256;                // weight rows per block (gate_up: 128 gate + 128 up)
+
+__device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                               __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t and_or_s(uint32_t p, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(p), "s"(mask), "v"(magic));
+  return r;
+}
+
+// 4 nibbles (bytes of w at positions sel) -> f16x2 pairs, scale applied
+template <bool HIGH>
+__device__ __forceinline__ uint32_t q4_pair(uint32_t w, uint32_t sel, f16x2_t ds, f16x2_t ndm) {
+  const uint32_t p = __builtin_amdgcn_perm(0u, w, sel);
+  const uint32_t magic = HIGH ? and_or_s(p, 0x00F000F0u, 0x54005400u)
+                              : and_or_s(p, 0x000F000Fu, 0x64006400u);
+  const _Float16 off = HIGH ? (_Float16)64.0f : (_Float16)1024.0f;
+  const f16x2_t q = __builtin_bit_cast(f16x2_t, magic) - (f16x2_t){off, off};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, ds, ndm));
+}
+
+// 16 bytes of nibbles -> 16 f16 (low or high nibbles), as two uint4 in k order
+template <bool HIGH>
+__device__ __forceinline__ void q4_16(uint4 w, f16x2_t ds, f16x2_t ndm, uint4& o0, uint4& o1) {
+  o0.x = q4_pair<HIGH>(w.x, 0x0C010C00u, ds, ndm);
+  o0.y = q4_pair<HIGH>(w.x, 0x0C030C02u, ds, ndm);
+  o0.z = q4_pair<HIGH>(w.y, 0x0C010C00u, ds, ndm);
+  o0.w = q4_pair<HIGH>(w.y, 0x0C030C02u, ds, ndm);
+  o1.x = q4_pair<HIGH>(w.z, 0x0C010C00u, ds, ndm);
+  o1.y = q4_pair<HIGH>(w.z, 0x0C030C02u, ds, ndm);
+  o1.z = q4_pair<HIGH>(w.w, 0x0C010C00u, ds, ndm);
+  o1.w = q4_pair<HIGH>(w.w, 0x0C030C02u, ds, ndm);
+}
+
+__device__ __forceinline__ void q4_scales(uint4 hdr, int j, f16x2_t& ds, f16x2_t& ndm) {
+  uint32_t sc, m;
+  q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
+  const _Float16 d = (_Float16)(f16_to_f32(hdr.x & 0xFFFFu) * (float)sc);
+  const _Float16 n = (_Float16)(-(f16_to_f32(hdr.x >> 16) * (float)m));
+  ds = (f16x2_t){d, d};
+  ndm = (f16x2_t){n, n};
+}
+
+__device__ __forceinline__ uint32_t bf2_to_f16x2(uint32_t w) {
+  const f16x2_t v = {(_Float16)__uint_as_float(w << 16), (_Float16)__uint_as_float(w & 0xFFFF0000u)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// One producer thread's share of a step: weight row `row` (a 64-wide K step = 64 elements) and
+// activation row `arow` (64 elements = 128 B, as 2 threads x 64 B... see Producer).
+template <int WFMT>
+struct WRaw;
+template <>
+struct WRaw<MOE_FMT_Q4_K> {
+  uint4 hdr, lo, hi;                    // header, nibble bytes [0,16) and [16,32) of the step's group
+  __device__ __forceinline__ void load(const uint8_t* row, int k0) {
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 144;
+    const int g = (k0 >> 6) & 3;
+    hdr = *reinterpret_cast<const uint4*>(b);
+    lo = *reinterpret_cast<const uint4*>(b + 16 + 32 * g);
+    hi = *reinterpret_cast<const uint4*>(b + 16 + 32 * g + 16);
+  }
+  // 64 f16 in k order into dst (LDS row, 128 B)
+  __device__ __forceinline__ void decode(int k0, uint16_t* dst) const {
+    const int g = (k0 >> 6) & 3;
+    f16x2_t ds0, nd0, ds1, nd1;
+    q4_scales(hdr, 2 * g, ds0, nd0);
+    q4_scales(hdr, 2 * g + 1, ds1, nd1);
+    uint4 a, b;
+    uint4* d = reinterpret_cast<uint4*>(dst);
+    q4_16<false>(lo, ds0, nd0, a, b);     // elements 0..15
+    d[0] = a; d[1] = b;
+    q4_16<false>(hi, ds0, nd0, a, b);     // 16..31
+    d[2] = a; d[3] = b;
+    q4_16<true>(lo, ds1, nd1, a, b);      // 32..47
+    d[4] = a; d[5] = b;
+    q4_16<true>(hi, ds1, nd1, a, b);      // 48..63
+    d[6] = a; d[7] = b;
+  }
+};
+template <>
+struct WRaw<MOE_FMT_BF16> {
+  uint4 q[8];
+  __device__ __forceinline__ void load(const uint8_t* row, int k0) {
+    const uint4* r = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(row) + k0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = r[i];
+  }
+  __device__ __forceinline__ void decode(int, uint16_t* dst) const {
+    uint4* d = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      d[i] = make_uint4(bf2_to_f16x2(q[i].x), bf2_to_f16x2(q[i].y), bf2_to_f16x2(q[i].z), bf2_to_f16x2(q[i].w));
+  }
+};
+
+__device__ __forceinline__ size_t row_bytes(int fmt, int cols) {
+  return fmt == MOE_FMT_Q4_K ? (size_t)(cols / 256) * 144 : (size_t)cols * 2;
+}
+
+__device__ __forceinline__ int tile_rows(const int32_t* tiles, const int32_t* offsets, int T,
+                                         int ncol, int& e, int& m0, int& mend, int& col) {
+  const int count = tiles ? tiles[0] : (T + kBM - 1) / kBM;
+  const int per = (count + kXcd - 1) / kXcd;
+  const int xcd = blockIdx.x % kXcd, slot = blockIdx.x / kXcd;
+  const int tl = slot / ncol;
+  col = slot % ncol;
+  const int tile = xcd * per + tl;
+  if (tl >= per || tile >= count) return 0;
+  if (tiles) {
+    e = tiles[1 + 2 * tile];
+    m0 = tiles[2 + 2 * tile];
+    mend = min(m0 + kBM, offsets[e + 1]);
+  } else {
+    e = 0;
+    m0 = tile * kBM;
+    mend = min(m0 + kBM, T);
+  }
+  return 1;
+}
+
+struct Smem {
+  uint16_t A[2][kBM * kS];              // 2 x 18 KB
+  uint16_t B[2][kBN * kS];              // 2 x 36 KB
+};
+
+// Producer thread p (0..255): weight row p of the slab (one 64-wide K step = 64 elements) and
+// half an activation row: row p >> 1, elements [32 (p & 1), +32) (4 x 16 B). Two named sets of
+// raw registers alternate by step parity (compile time, so nothing is indexed at run time).
+template <int WFMT>
+struct PSet {
+  WRaw<WFMT> w;
+  uint4 a[4];
+  __device__ __forceinline__ void load(const uint8_t* wrow, const uint16_t* asrc, int k0, int p) {
+    w.load(wrow, k0);
+    const uint4* s = reinterpret_cast<const uint4*>(asrc + k0 + 32 * (p & 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = s[j];
+  }
+  __device__ __forceinline__ void store(int k0, int p, uint16_t* As, uint16_t* Bs) const {
+    w.decode(k0, Bs + p * kS);
+    uint4* d = reinterpret_cast<uint4*>(As + (p >> 1) * kS + 32 * (p & 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] = a[j];
+  }
+};
+
+// consumers read buffer J for step ks; fill buffer J ^ 1 with step ks + 1 (set `nxt`) and request
+// step ks + 2's bytes into set `cur` (consumed a step ago)
+template <int WFMT, int J>
+__device__ __forceinline__ void pstep(PSet<WFMT>& cur, PSet<WFMT>& nxt, int ks, int nk,
+                                      const uint16_t* asrc, const uint8_t* wrow, int p, Smem& sm) {
+  nxt.store(min(ks + 1, nk - 1) * kBK, p, sm.A[J ^ 1], sm.B[J ^ 1]);
+  cur.load(wrow, asrc, min(ks + 2, nk - 1) * kBK, p);
+  __syncthreads();
+}
+
+template <int WFMT>
+__device__ __forceinline__ void produce(int nk, const uint16_t* asrc, const uint8_t* wrow, int p,
+                                        Smem& sm) {
+  PSet<WFMT> s0, s1;
+  s0.load(wrow, asrc, 0, p);
+  s1.load(wrow, asrc, min(1, nk - 1) * kBK, p);
+  s0.store(0, p, sm.A[0], sm.B[0]);
+  __syncthreads();
+  for (int k2 = 0; k2 < nk; k2 += 2) {
+    // step k2: buffer 0 is read; s1 (step k2 + 1) is stored, s0 reloads step k2 + 2
+    pstep<WFMT, 0>(s0, s1, k2, nk, asrc, wrow, p, sm);
+    // step k2 + 1: buffer 1 is read; s0 (step k2 + 2) is stored, s1 reloads step k2 + 3
+    pstep<WFMT, 1>(s1, s0, k2 + 1, nk, asrc, wrow, p, sm);
+  }
+}
+
+__device__ __forceinline__ uint4 frag(const uint16_t* S, int row, int s, int lane) {
+  return *reinterpret_cast<const uint4*>(S + row * kS + 16 * s + 8 * (lane >> 5));
+}
+
+// Consumer wave c (0..3): all 128 rows (NG active 32-row groups) x B rows {b0 + lane%32} and
+// {b1 + lane%32} of the slab.
+template <int NG>
+__device__ __forceinline__ void consume(int nk, int b0, int b1, Smem& sm, f32x16_t (&acc)[4][2]) {
+  const int lane = threadIdx.x & 63;
+  __syncthreads();
+  for (int k2 = 0; k2 < nk; k2 += 2) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint16_t* As = sm.A[j];
+      const uint16_t* Bs = sm.B[j];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 bg = frag(Bs, b0 + (lane & 31), s, lane);
+        const uint4 bu = frag(Bs, b1 + (lane & 31), s, lane);
+#pragma unroll
+        for (int mg = 0; mg < NG; ++mg) {
+          const uint4 a = frag(As, 32 * mg + (lane & 31), s, lane);
+          acc[mg][0] = mfma(a, bg, acc[mg][0]);
+          acc[mg][1] = mfma(a, bu, acc[mg][1]);
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int NG>
+__device__ __forceinline__ void consume_n(int ng, int nk, int b0, int b1, Smem& sm,
+                                          f32x16_t (&acc)[4][2]) {
+  (void)NG;
+  if (ng >= 4) consume<4>(nk, b0, b1, sm, acc);
+  else if (ng == 3) consume<3>(nk, b0, b1, sm, acc);
+  else if (ng == 2) consume<2>(nk, b0, b1, sm, acc);
+  else consume<1>(nk, b0, b1, sm, acc);
+}
+
+}  // namespace g3
+
+// ----------------------------------------------------------------------------------- gate/up --
+template <int WFMT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3_gateup(
+    const uint16_t* __restrict__ x16, const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
+    size_t estride, const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ sorted_pairs, int K, int H, int I, int T,
+    uint16_t* __restrict__ S) {
+  using namespace g3;
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  int e, m0, mend, col;
+  if (!tile_rows(tiles, offsets, T, I / 128, e, m0, mend, col)) return;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int nk = H / kBK;
+  if (wave >= 4) {
+    const int p = t - 256;
+    const int m = min(m0 + (p >> 1), mend - 1);
+    const uint16_t* asrc = x16 + (size_t)(tiles ? sorted_pairs[m] / K : m) * H;
+    const int r = p & 127;
+    const uint8_t* wrow = (p < 128 ? wg : wu) + (size_t)e * estride +
+                          (size_t)(col * 128 + r) * row_bytes(WFMT, H);
+    produce<WFMT>(nk, asrc, wrow, p, sm);
+    return;
+  }
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int mg = 0; mg < 4; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
+  const int ng = __builtin_amdgcn_readfirstlane((mend - m0 + 31) >> 5);
+  consume_n<0>(ng, nk, 32 * wave, 128 + 32 * wave, sm, acc);
+  const int n = col * 128 + 32 * wave + (lane & 31), h = lane >> 5;
+#pragma unroll
+  for (int mg = 0; mg < 4; ++mg) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (mm < mend) {
+        float v = silu_f32(acc[mg][0][r]) * acc[mg][1][r];
+        v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+        S[(size_t)mm * I + n] = __builtin_bit_cast(uint16_t, (_Float16)v);
+      }
+    }
+  }
+}
+
+// -------------------------------------------------------------------------------------- down --
+template <int WFMT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3_down(
+    const uint16_t* __restrict__ S, const uint8_t* __restrict__ wd, size_t estride,
+    const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets, int H, int I, int T,
+    float* __restrict__ y) {
+  using namespace g3;
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  int e, m0, mend, col;
+  if (!tile_rows(tiles, offsets, T, H / kBN, e, m0, mend, col)) return;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int nk = I / kBK;
+  if (wave >= 4) {
+    const int p = t - 256;
+    const uint16_t* asrc = S + (size_t)min(m0 + (p >> 1), mend - 1) * I;
+    const uint8_t* wrow = wd + (size_t)e * estride + (size_t)(col * kBN + p) * row_bytes(WFMT, I);
+    produce<WFMT>(nk, asrc, wrow, p, sm);
+    return;
+  }
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int mg = 0; mg < 4; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
+  const int ng = __builtin_amdgcn_readfirstlane((mend - m0 + 31) >> 5);
+  consume_n<0>(ng, nk, 64 * wave, 64 * wave + 32, sm, acc);
+  const int nb = col * kBN + 64 * wave + (lane & 31), h = lane >> 5;
+#pragma unroll
+  for (int mg = 0; mg < 4; ++mg) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (mm < mend) {
+        y[(size_t)mm * H + nb] = acc[mg][0][r];
+        y[(size_t)mm * H + nb + 32] = acc[mg][1][r];
+      }
+    }
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int fmt,
+                            size_t expert_stride, const int32_t* tiles, int max_tiles, int T,
+                            const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
+                            int I, uint16_t* S, hipStream_t st) {
+  if (H % 256 || I % 128)
+    return moe_set_error(MOE_E_UNSUPPORTED, "gemm3 gate_up needs H %% 256 == 0, I %% 128 == 0");
+  const uint8_t* g = reinterpret_cast<const uint8_t*>(w_gate);
+  const uint8_t* u = reinterpret_cast<const uint8_t*>(w_up);
+  const int ntile = tiles ? max_tiles : (T + g3::kBM - 1) / g3::kBM;
+  const dim3 grid(g3::kXcd * ((ntile + g3::kXcd - 1) / g3::kXcd) * (I / 128));
+  if (fmt == MOE_FMT_Q4_K)
+    hipLaunchKernelGGL(k_gemm3_gateup<MOE_FMT_Q4_K>, grid, dim3(512), 0, st, x16, g, u, expert_stride, tiles, offsets, sorted_pairs, K, H, I, T, S);
+  else if (fmt == MOE_FMT_BF16)
+    hipLaunchKernelGGL(k_gemm3_gateup<MOE_FMT_BF16>, grid, dim3(512), 0, st, x16, g, u, expert_stride, tiles, offsets, sorted_pairs, K, H, I, T, S);
+  else
+    return moe_set_error(MOE_E_FORMAT, "gemm3 gate_up: unsupported format %d", fmt);
+  return moe_check_launch("gemm3_gateup");
+}
+
+int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t expert_stride,
+                          const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
+                          int H, int I, float* y, hipStream_t st) {
+  if (H % g3::kBN || I % 256)
+    return moe_set_error(MOE_E_UNSUPPORTED, "gemm3 down needs H %% 256 == 0, I %% 256 == 0");
+  const uint8_t* w = reinterpret_cast<const uint8_t*>(w_down);
+  const int ntile = tiles ? max_tiles : (T + g3::kBM - 1) / g3::kBM;
+  const dim3 grid(g3::kXcd * ((ntile + g3::kXcd - 1) / g3::kXcd) * (H / g3::kBN));
+  if (fmt == MOE_FMT_Q4_K)
+    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q4_K>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
+  else if (fmt == MOE_FMT_BF16)
+    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_BF16>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
+  else
+    return moe_set_error(MOE_E_FORMAT, "gemm3 down: unsupported format %d", fmt);
+  return moe_check_launch("gemm3_down");
+}

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict_
 // MFMA work list: for every hit expert (ascending) ceil(n_e / BM) tiles of BM sorted rows.
 __global__ __launch_bounds__(256) void k_build_tiles(const int32_t* __restrict__ offsets,
                                                      const int32_t* __restrict__ hit_list,
-                                                     int32_t* __restrict__ tiles) {
+                                                     int32_t* __restrict__ tiles, int bm) {
   __shared__ int tmp[256];
   const int nhit = hit_list[0];
   int written = 0;
@@ -178,13 +178,13 @@ __global__ __launch_bounds__(256) void k_build_tiles(const int32_t* __restrict__
     int e = 0, n = 0;
     if (h < nhit) {
       e = hit_list[1 + h];
-      n = (offsets[e + 1] - offsets[e] + MOE_GEMM_BM - 1) / MOE_GEMM_BM;
+      n = (offsets[e + 1] - offsets[e] + bm - 1) / bm;
     }
     int tot;
     const int pre = block_exclusive_scan(n, tmp, &tot);
     for (int i = 0; i < n; ++i) {
       tiles[1 + 2 * (written + pre + i)] = e;
-      tiles[2 + 2 * (written + pre + i)] = offsets[e] + i * MOE_GEMM_BM;
+      tiles[2 + 2 * (written + pre + i)] = offsets[e] + i * bm;
     }
     written += tot;
   }
@@ -216,15 +216,15 @@ int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t*
   return moe_check_launch("sort");
 }
 
-int moe_max_mtiles(int P, int E) {
+int moe_max_mtiles(int P, int E, int bm) {
   const int hits = P < E ? P : E;
-  return (P + MOE_GEMM_BM - 1) / MOE_GEMM_BM + hits;
+  return (P + bm - 1) / bm + hits;
 }
 
 int moe_launch_build_tiles(const int32_t* offsets, const int32_t* hit_list, int E, int P,
-                           int32_t* tiles, hipStream_t st) {
+                           int32_t* tiles, hipStream_t st, int bm) {
   (void)E;
   (void)P;
-  hipLaunchKernelGGL(k_build_tiles, dim3(1), dim3(256), 0, st, offsets, hit_list, tiles);
+  hipLaunchKernelGGL(k_build_tiles, dim3(1), dim3(256), 0, st, offsets, hit_list, tiles, bm);
   return moe_check_launch("build_tiles");
 }
