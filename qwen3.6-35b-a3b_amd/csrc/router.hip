@@ -15,6 +15,8 @@
 // ascending order and B = positions whose value is not less than it (right-scan stops) in
 // descending order, the sequential partition swaps A[m] <-> B[m] for every m with A[m] < B[m]
 // and returns min(A[M], B[M-1]) for the first M where that fails. Ranks come from ballots.
+#include <type_traits>
+
 #include "common.h"
 #include "moe_internal.h"
 #include "router_dev.h"
@@ -113,12 +115,148 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
   }
 }
 
+// Rare path of the certificate: one logit recomputed sequentially in double-double (each
+// product is exact in f64, TwoSum accumulation), then rounded to bf16.
+template <int XDT>
+__device__ __noinline__ uint32_t logit_dd_recompute(const void* __restrict__ xv,
+                                                    const uint16_t* __restrict__ w, int t, int e,
+                                                    int H, double bval, double xsq, double wsq) {
+  DD d = {0.0, 0.0};
+  for (int k = 0; k < H; ++k) {
+    const double xk = (XDT == MOE_DT_F32)
+                          ? (double)reinterpret_cast<const float*>(xv)[(size_t)t * H + k]
+                          : (double)bf16_to_f32(reinterpret_cast<const uint16_t*>(xv)[(size_t)t * H + k]);
+    d = dd_add(d, DD{xk * (double)bf16_to_f32(w[(size_t)e * H + k]), 0.0});
+  }
+  d = dd_add(d, DD{bval, 0.0});
+  const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
+  return round_bf16_dd(d, ddb);
+}
+
+// ------------------------------------------------------- R1, large T: f64 MFMA tile GEMM -----
+// v_mfma_f64_16x16x4f64 (A 16x4: lane l holds A[l%16][l/16]; B 4x16: lane l holds B[l/16][l%16];
+// D 16x16 in 4 f64 registers: lane l, register j holds D[4j + l/16][l%16]). The contraction
+// index is free to permute as long as A and B agree, so in a 16-wide k step lane group g = l/16
+// owns k = 4g..4g+3 and feeds one of them to each of the step's 4 MFMAs: one 16-byte (f32 x)
+// or 8-byte (bf16 x / W) load per operand row per step.
+// Block = 4 waves = 32 tokens x 128 experts; wave w owns experts 32w..32w+31 as 2 x 2 tiles.
+// Operands come straight from global memory through a 4-step register ring (x rows are shared by
+// the block's waves in L1; W, 1 MB at E=256, stays in L2). Each logit gets the same certificate
+// as every R1 kernel here: f64 summation in any order stays within 4 (H+3) 2^-53 ||x|| ||W_e||
+// of the exact sum.
+template <int XDT>
+struct RouterRaw {
+  using XT = typename std::conditional<XDT == MOE_DT_F32, float4, uint2>::type;
+  XT a0, a1;
+  uint2 b0, b1;
+};
+
+template <int XDT>
+__device__ __forceinline__ void router_cvt_x(const typename RouterRaw<XDT>::XT& v, double* o) {
+  if constexpr (XDT == MOE_DT_F32) {
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else {
+    o[0] = bf16_to_f32(v.x & 0xFFFFu); o[1] = bf16_to_f32(v.x >> 16);
+    o[2] = bf16_to_f32(v.y & 0xFFFFu); o[3] = bf16_to_f32(v.y >> 16);
+  }
+}
+__device__ __forceinline__ void router_cvt_w(uint2 v, double* o) {
+  o[0] = bf16_to_f32(v.x & 0xFFFFu); o[1] = bf16_to_f32(v.x >> 16);
+  o[2] = bf16_to_f32(v.y & 0xFFFFu); o[3] = bf16_to_f32(v.y >> 16);
+}
+
+template <int XDT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+k_router_logits_mfma(const void* __restrict__ xv, const uint16_t* __restrict__ w,
+                     const float* __restrict__ bias, int T, int H, int E,
+                     uint16_t* __restrict__ logits) {
+  using XT = typename RouterRaw<XDT>::XT;
+  using d4 = double __attribute__((ext_vector_type(4)));
+  constexpr int D = 4;                                  // ring depth in 16-wide k steps
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int t0 = blockIdx.x * 32;
+  const int e0 = blockIdx.y * 128 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 32;
+  if (e0 >= E) return;
+  // operand rows (clamped into range; results of clamped rows are never stored)
+  const XT* xa = reinterpret_cast<const XT*>(
+      reinterpret_cast<const char*>(xv) + ((size_t)min(t0 + r, T - 1) * H + 4 * g) * sizeof(XT) / 4);
+  const XT* xb = reinterpret_cast<const XT*>(
+      reinterpret_cast<const char*>(xv) + ((size_t)min(t0 + 16 + r, T - 1) * H + 4 * g) * sizeof(XT) / 4);
+  const uint2* wa = reinterpret_cast<const uint2*>(w + (size_t)min(e0 + r, E - 1) * H + 4 * g);
+  const uint2* wb = reinterpret_cast<const uint2*>(w + (size_t)min(e0 + 16 + r, E - 1) * H + 4 * g);
+  // one 16-wide k step is 4 XT / 4 uint2 further along each row
+  auto load = [&](RouterRaw<XDT>& q, int step) {
+    q.a0 = xa[4 * step]; q.a1 = xb[4 * step];
+    q.b0 = wa[4 * step]; q.b1 = wb[4 * step];
+  };
+  d4 c00 = {0, 0, 0, 0}, c01 = c00, c10 = c00, c11 = c00;  // [token half][expert half]
+  double xsa = 0, xsb = 0, wsa = 0, wsb = 0;
+  const int nst = H / 16;
+  RouterRaw<XDT> q[D];
+#pragma unroll
+  for (int s = 0; s < D; ++s) load(q[s], s);
+  for (int it = 0; it < nst; it += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      double a0[4], a1[4], b0[4], b1[4];
+      router_cvt_x<XDT>(q[s].a0, a0);
+      router_cvt_x<XDT>(q[s].a1, a1);
+      router_cvt_w(q[s].b0, b0);
+      router_cvt_w(q[s].b1, b1);
+      if (it + s + D < nst) load(q[s], it + s + D);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c00 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0[i], b0[i], c00, 0, 0, 0);
+        c01 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0[i], b1[i], c01, 0, 0, 0);
+        c10 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1[i], b0[i], c10, 0, 0, 0);
+        c11 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1[i], b1[i], c11, 0, 0, 0);
+        xsa = fma(a0[i], a0[i], xsa);
+        xsb = fma(a1[i], a1[i], xsb);
+        wsa = fma(b0[i], b0[i], wsa);
+        wsb = fma(b1[i], b1[i], wsb);
+      }
+    }
+  }
+  // squared norms: sum the four lane groups; lane r then holds row r's (and column r's) norm
+#pragma unroll
+  for (int o = 16; o <= 32; o <<= 1) {
+    xsa += __shfl_xor(xsa, o, 64);
+    xsb += __shfl_xor(xsb, o, 64);
+    wsa += __shfl_xor(wsa, o, 64);
+    wsb += __shfl_xor(wsb, o, 64);
+  }
+  const d4* acc[4] = {&c00, &c01, &c10, &c11};
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const int th = q4 >> 1, eh = q4 & 1;
+    const int e = e0 + 16 * eh + r;
+    const double wsq = eh ? wsb : wsa;
+    const double bval = (bias && e < E) ? (double)bias[e] : 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 4 * j + g;                       // token row within the 16-row half
+      const double xsq = __shfl(th ? xsb : xsa, row, 64);
+      const int t = t0 + 16 * th + row;
+      if (t >= T || e >= E) continue;
+      const double s = (*acc[q4])[j] + bval;
+      const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
+      uint32_t bits;
+      if (!round_bf16_certified(s, bound, &bits))
+        bits = logit_dd_recompute<XDT>(xv, w, t, e, H, bval, xsq, wsq);
+      logits[(size_t)t * E + e] = (uint16_t)bits;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- R1, large T: f64 tile GEMM --
-// 64 tokens x 64 experts per block of 256 threads; each thread owns a 4x4 patch.
+// Shapes the MFMA kernel does not take (H % 64 != 0): 64 tokens x 64 experts per block of 256
+// threads; each thread owns a 4x4 patch.
 template <int XDT>
 __global__ __launch_bounds__(256) void k_router_logits_gemm(
     const void* __restrict__ xv, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     int T, int H, int E, uint16_t* __restrict__ logits) {
+
   __shared__ double xs[16][64 + 2];
   __shared__ double wsm[16][64 + 2];
   const int tid = threadIdx.x;
@@ -181,19 +319,8 @@ __global__ __launch_bounds__(256) void k_router_logits_gemm(
       const double s = acc[i][j] + bval;
       const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xsq[i]) * sqrt(wsq[j]) + fabs(bval));
       uint32_t bits;
-      if (!round_bf16_certified(s, bound, &bits)) {
-        // rare: sequential double-double recompute of this one logit
-        DD d = {0.0, 0.0};
-        for (int k = 0; k < H; ++k) {
-          double xk = (XDT == MOE_DT_F32)
-                          ? (double)reinterpret_cast<const float*>(xv)[(size_t)t * H + k]
-                          : (double)bf16_to_f32(reinterpret_cast<const uint16_t*>(xv)[(size_t)t * H + k]);
-          d = dd_add(d, DD{xk * (double)bf16_to_f32(w[(size_t)e * H + k]), 0.0});
-        }
-        d = dd_add(d, DD{bval, 0.0});
-        const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq[i]) * sqrt(wsq[j]) + fabs(bval));
-        bits = round_bf16_dd(d, ddb);
-      }
+      if (!round_bf16_certified(s, bound, &bits))
+        bits = logit_dd_recompute<XDT>(xv, w, t, e, H, bval, xsq[i], wsq[j]);
       logits[(size_t)t * E + e] = (uint16_t)bits;
     }
   }
@@ -233,6 +360,12 @@ int moe_launch_router_logits(const void* x, int x_dtype, const void* w, const fl
       hipLaunchKernelGGL(k_router_logits_gemv<MOE_DT_F32>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
     else
       hipLaunchKernelGGL(k_router_logits_gemv<MOE_DT_BF16>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
+  } else if (H % 64 == 0) {
+    dim3 grid((T + 31) / 32, (E + 127) / 128);
+    if (x_dtype == MOE_DT_F32)
+      hipLaunchKernelGGL(k_router_logits_mfma<MOE_DT_F32>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
+    else
+      hipLaunchKernelGGL(k_router_logits_mfma<MOE_DT_BF16>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
   } else {
     dim3 grid((E + 63) / 64, (T + 63) / 64);
     if (x_dtype == MOE_DT_F32)

@@ -68,19 +68,31 @@ def test_router_tie_laden_rows(pkg, dev, T):
     _check_route(pkg, x, w, None)
 
 
-def test_router_midpoint_logits_round_to_even(pkg, dev):
+@pytest.mark.parametrize("T", [2, 40])
+def test_router_midpoint_logits_round_to_even(pkg, dev, T):
     """Logits that are exact bf16 midpoints (1 + 2^-8 -> 1.0, ties to even) and just above one
-    (-> 1 + 2^-7): the certified path must fall back and decide exactly."""
+    (-> 1 + 2^-7): the certified path must fall back and decide exactly. T = 2 runs the
+    small-T kernel, T = 40 the MFMA tile kernel (rows alternate the two patterns)."""
     H = 2048
-    x = torch.zeros(2, H)
-    x[0, 0], x[0, 1] = 1.0, 2.0 ** -8
-    x[1, 0], x[1, 1], x[1, 2] = 1.0, 2.0 ** -8, 2.0 ** -40
+    x = torch.zeros(T, H)
+    x[0::2, 0], x[0::2, 1] = 1.0, 2.0 ** -8
+    x[1::2, 0], x[1::2, 1], x[1::2, 2] = 1.0, 2.0 ** -8, 2.0 ** -40
     w = torch.zeros(256, H)
     w[:, 0:3] = 1.0
     r = pkg.abi.router_topk(x.to(dev), w.to(torch.bfloat16).to(dev), 8)
     lg = r["router_logits"].cpu().float()
-    assert (lg[0] == 1.0).all()
-    assert (lg[1] == 1.0 + 2.0 ** -7).all()
+    assert (lg[0::2] == 1.0).all()
+    assert (lg[1::2] == 1.0 + 2.0 ** -7).all()
+
+
+@pytest.mark.parametrize("T,E,dtype", [(45, 200, torch.float32), (33, 24, torch.bfloat16)])
+def test_router_ragged_tiles(pkg, dev, T, E, dtype):
+    """T and E that leave partial 32-token / 128-expert / 16-expert tiles, with a bias."""
+    g = torch.Generator().manual_seed(T * 1000 + E)
+    w = (torch.randn(E, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(E, generator=g) * 0.1
+    x = torch.randn(T, 2048, generator=g).to(dtype)
+    _check_route(pkg, x.to(dev), w.to(dev), bias.to(dev))
 
 
 def test_router_heap_select_branch(pkg, dev):
