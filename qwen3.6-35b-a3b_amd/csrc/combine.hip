@@ -60,6 +60,71 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
   out[(size_t)t * H + h] = (residual ? residual[(size_t)t * H + h] : 0.0f) + acc + sh;
 }
 
+// Same sums, four columns per thread (H % 4 == 0) and a compile-time K: the K expert rows are
+// all in flight before the first add, and the ascending-id order comes from per-slot ranks
+// (ids within a token are distinct; equal ids would keep slot order) instead of a serial sort.
+// grid = (T, ceil(H / 1024)), block = 256.
+template <int KK>
+__global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ y,
+                                                  const int32_t* __restrict__ pair_pos,
+                                                  const int32_t* __restrict__ ids,
+                                                  const uint16_t* __restrict__ w_bf16,
+                                                  const float* __restrict__ shared_raw,
+                                                  const float* __restrict__ gate_prob,
+                                                  const float* __restrict__ residual, int T,
+                                                  int H, float* __restrict__ out,
+                                                  float* __restrict__ routed_sum,
+                                                  float* __restrict__ shared_out,
+                                                  float* __restrict__ expert_raw) {
+  __shared__ int s_pos[KK], s_slot[KK];
+  __shared__ float s_w[KK];
+  const int t = blockIdx.x;
+  if (threadIdx.x < KK) {
+    const int k = threadIdx.x;
+    const int32_t* tid = ids + (size_t)t * KK;
+    const int id = tid[k];
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < KK; ++j) {
+      const int o = tid[j];
+      rank += (o < id) || (o == id && j < k);
+    }
+    s_pos[rank] = pair_pos[(size_t)t * KK + k];
+    s_slot[rank] = k;
+    s_w[rank] = bf16_to_f32(w_bf16[(size_t)t * KK + k]);
+  }
+  __syncthreads();
+  const int h = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (h >= H) return;
+  float4 v[KK];
+#pragma unroll
+  for (int j = 0; j < KK; ++j) {
+    const int pos = s_pos[j];
+    v[j] = pos >= 0 ? *reinterpret_cast<const float4*>(y + (size_t)pos * H + h)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);       // dropped (out-of-range) id
+  }
+  const size_t o = (size_t)t * H + h;
+  const float4 sr = *reinterpret_cast<const float4*>(shared_raw + o);
+  const float4 rs = residual ? *reinterpret_cast<const float4*>(residual + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float gp = gate_prob[t];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < KK; ++j) {
+    const float w = s_w[j];
+    acc.x += w * v[j].x;
+    acc.y += w * v[j].y;
+    acc.z += w * v[j].z;
+    acc.w += w * v[j].w;
+    if (expert_raw)
+      *reinterpret_cast<float4*>(expert_raw + ((size_t)t * KK + s_slot[j]) * H + h) = v[j];
+  }
+  const float4 sh = make_float4(gp * sr.x, gp * sr.y, gp * sr.z, gp * sr.w);
+  if (routed_sum) *reinterpret_cast<float4*>(routed_sum + o) = acc;
+  if (shared_out) *reinterpret_cast<float4*>(shared_out + o) = sh;
+  *reinterpret_cast<float4*>(out + o) =
+      make_float4(rs.x + acc.x + sh.x, rs.y + acc.y + sh.y, rs.z + acc.z + sh.z, rs.w + acc.w + sh.w);
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -68,6 +133,14 @@ int moe_launch_combine(const float* y, const int32_t* pair_pos, const int32_t* i
                        const uint16_t* w_bf16, const float* shared_raw, const float* gate_prob,
                        const float* residual, int T, int K, int H, float* out, float* routed_sum,
                        float* shared_out, float* expert_raw, hipStream_t st) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (K == 8 && H % 4 == 0 && a16(y) && a16(shared_raw) && a16(residual) && a16(out) &&
+      a16(routed_sum) && a16(shared_out) && a16(expert_raw)) {
+    dim3 grid(T, (H + 1023) / 1024);
+    hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16, shared_raw,
+                       gate_prob, residual, T, H, out, routed_sum, shared_out, expert_raw);
+    return moe_check_launch("combine");
+  }
   dim3 grid(T, (H + 255) / 256);
   hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16, shared_raw,
                      gate_prob, residual, T, K, H, out, routed_sum, shared_out, expert_raw);
