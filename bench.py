@@ -217,8 +217,8 @@ def pmc_workload(pkg, torch, dev, L: int) -> None:
     norms = [synth.make_norm_weight(seed=5000 + l, device=dev) for l in range(L)]
     x = synth.make_input(1, seed=0, device=dev)
     for _ in range(4):
-        for lw, nw in zip(layers, norms):
-            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw)
+        for l, (lw, nw) in enumerate(zip(layers, norms)):
+            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw, next_layer=layers[(l + 1) % L])
         x.copy_(synth.rms_normalize(x))
     torch.cuda.synchronize()
     del layers
@@ -240,7 +240,7 @@ def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> floa
     def layer_launches():
         for l, lw in enumerate(layers):
             abi.block_forward(xs[l:l + 1], lw, out=ys[l:l + 1], residual=xs[l:l + 1],
-                              norm_w=norms[l])
+                              norm_w=norms[l], next_layer=layers[(l + 1) % L])
 
     layer_launches()
     torch.cuda.synchronize()
@@ -316,9 +316,11 @@ def main():
     norms = [synth.make_norm_weight(seed=5000 + l, device=dev) for l in range(L)]
 
     def one_token():
-        # the residual stream through L layers: h <- h + MoE(rmsnorm(h)), in place
-        for lw, nw in zip(layers, norms):
-            abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw)
+        # the residual stream through L layers: h <- h + MoE(rmsnorm(h)), in place; each call
+        # names the next layer so its routing-independent weights are warmed into L2
+        for l, (lw, nw) in enumerate(zip(layers, norms)):
+            abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw,
+                              next_layer=layers[(l + 1) % L])
         xbuf.copy_(synth.rms_normalize(xbuf))
 
     for _ in range(3):

@@ -136,10 +136,40 @@ int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, in
                       float *routed_sum, float *shared_out, float *gate_prob, float *expert_raw,
                       void *ws, size_t ws_bytes, void *stream);
 
-/* Zero the workspace's device-side sync words (its first 256 KiB: counters, the single-launch
- * decode layer's epoch and its two exchange buffers). Call once after allocating a workspace,
- * before its first use by moe_block_forward / moe_experts / moe_shared_expert / moe_router_topk
- * (a workspace that starts zeroed needs no call); every call leaves the words valid for the next.
+/* The routing-independent weights of the layer that the same stream runs next (its router, its
+ * shared expert and the shared expert's scalar gate; shapes as in moe_block_forward). */
+typedef struct moe_next_layer {
+  const void *w_router;         /* [E,H] bf16 */
+  const void *ws_gate, *ws_up;  /* [I_s,H] bf16 */
+  const void *ws_down;          /* [H,I_s] bf16 */
+  const void *ws_scalar_gate;   /* [H] bf16 */
+} moe_next_layer;
+
+/* moe_block_forward with a hint: `next` (may be NULL) names the next layer's routing-independent
+ * weights. The single-launch decode layer then reads, at the end of its run, the parts of them
+ * that each workgroup reads first in the next layer, so that they come from the L2 of the same
+ * XCD instead of HBM; other paths ignore the hint. Results are identical with or without it.
+ * Same arguments, limits and errors as moe_block_forward otherwise. Replaces, like
+ * moe_block_forward, engine/m3_forward.py:430-476 in its layer loop (engine/m3_forward.py:714-737),
+ * where the next layer's weights are known ahead of its input. */
+int moe_block_forward_prefetch(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                               const float *norm_w, float norm_eps, const void *w_router,
+                               const float *logit_bias, const void *gate_up_q, int gate_up_fmt,
+                               const void *down_q, int down_fmt, const void *ws_gate,
+                               const void *ws_up, const void *ws_down, const void *ws_scalar_gate,
+                               int path, const float *residual, float *out, void *logits_bf16,
+                               int32_t *topk_ids, void *topk_w_bf16, float *topk_w_f32,
+                               float *routed_sum, float *shared_out, float *gate_prob,
+                               float *expert_raw, void *ws, size_t ws_bytes, void *stream,
+                               const moe_next_layer *next);
+
+/* Zero the workspace's device-side sync words (its first 512 KiB: counters, the single-launch
+ * decode layer's per-CU launch counts and its two exchange buffers) and record this device's CU
+ * layout there (one short launch: the rank of each CU inside its XCD, which the single-launch
+ * decode layer reads to take its role with one load). Call once after allocating a workspace,
+ * before its first use by moe_block_forward / moe_experts / moe_shared_expert / moe_router_topk.
+ * A workspace zeroed by other means also works (the decode layer then takes its roles by atomic
+ * tickets: same results, a slower start). Every call leaves the words valid for the next.
  * Calls sharing one workspace must be ordered on one stream. No counterpart in the reference (its
  * device work ran in fresh processes). */
 int moe_workspace_init(void *ws, size_t ws_bytes, void *stream);

@@ -31,6 +31,15 @@ MOE_PATH_MFMA = 2
 MOE_PATH_MFMA_BF16 = 3
 MOE_PATH_GEMV_MULTI = 4
 
+
+
+class NextLayer(ctypes.Structure):
+    """moe_next_layer: the routing-independent weights of the layer the stream runs next."""
+    _fields_ = [("w_router", ctypes.c_void_p), ("ws_gate", ctypes.c_void_p),
+                ("ws_up", ctypes.c_void_p), ("ws_down", ctypes.c_void_p),
+                ("ws_scalar_gate", ctypes.c_void_p)]
+
+
 # every symbol include/moe_gfx950.h declares, with its ctypes signature
 _VP, _I, _I64, _SZ, _CP = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_char_p
 SIGNATURES = {
@@ -50,6 +59,11 @@ SIGNATURES = {
                                _VP, _VP, _VP, _I, _VP, _I, _VP,
                                _VP, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                _VP, _VP, _SZ, _VP]),
+    "moe_block_forward_prefetch": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, _VP, ctypes.c_float,
+                                        _VP, _VP, _VP, _I, _VP, _I, _VP,
+                                        _VP, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                                        _VP, _VP, _VP, _VP, _SZ, _VP,
+                                        ctypes.POINTER(NextLayer)]),
     "moe_workspace_init": (_I, [_VP, _SZ, _VP]),
 }
 

@@ -80,8 +80,10 @@ def workspace_bytes(T: int, H: int, I: int, E: int, K: int, I_s: int) -> int:
 
 
 def device_error_bits(device) -> int:
-    """The workspace's device-side error word (bit 0: a bounded spin of the single-launch decode
-    layer timed out, i.e. its workgroups were not all co-resident). Reading it synchronises."""
+    """The workspace's device-side error word of the single-launch decode layer: bit 0, a bounded
+    spin timed out (its workgroups were not all co-resident); bit 1, an XCD received more
+    workgroups than it has CUs (no role for some). Zero when every launch ran as designed.
+    Reading it synchronises."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WS_CACHE.get(key)
     if buf is None:
@@ -191,12 +193,16 @@ def combine(y: torch.Tensor, grouping: dict, ids: torch.Tensor, w_bf16: torch.Te
 
 def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False,
                   out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
-                  norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6) -> dict:
+                  norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                  next_layer=None) -> dict:
     """The whole block in one library call (moe_block_forward). `lw` is a LayerWeights;
     `stages` is False, True (every stage output) or a set of stage names to return;
     out = residual + MoE(input) when `residual` (f32 [T,H], may be `out` or `x` itself) is given.
     input = x, or the post-attention RMSNorm of x when `norm_w` (f32 [H], the artifact's 1+w) is
-    given: engine/m3_forward.py:732-737 is then block_forward(x1, lw, norm_w=w, residual=x1)."""
+    given: engine/m3_forward.py:732-737 is then block_forward(x1, lw, norm_w=w, residual=x1).
+    `next_layer` (a LayerWeights, optional) is the layer this stream runs next: its
+    routing-independent weights are warmed into L2 by the single-launch decode layer
+    (moe_block_forward_prefetch); results do not depend on it."""
     _need(x, "x")
     T, H = x.shape
     if norm_w is not None:
@@ -217,13 +223,24 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
     st = {n: torch.empty(*shapes[n][0], dtype=shapes[n][1], device=dev) for n in want}
     ws = workspace(dev, workspace_bytes(T, H, I, E, K, Is))
     g = st.get
-    _check(L.lib.moe_block_forward(
+    args = (
         _p(x), _xdt(x), T, H, I, E, K, Is, _p(norm_w), float(norm_eps), _p(lw.router), _p(lw.router_bias), _p(lw.gate_up_q),
         lw.gate_up_fmt, _p(lw.down_q), lw.down_fmt, _p(lw.shared_gate), _p(lw.shared_up),
         _p(lw.shared_down), _p(lw.shared_scalar_gate), path, _p(residual), _p(out),
         _p(g("router_logits")),
         _p(g("topk_ids")), _p(g("topk_weights")), _p(g("topk_weights_f32")), _p(g("routed_sum")),
         _p(g("shared_out")), _p(g("shared_gate_prob")), _p(g("expert_raw")), _p(ws), ws.numel(),
-        _stream(x)), "block_forward")
+        _stream(x))
+    if next_layer is None:
+        _check(L.lib.moe_block_forward(*args), "block_forward")
+    else:
+        nl = next_layer
+        for name, t in (("next router", nl.router), ("next shared_gate", nl.shared_gate),
+                        ("next shared_up", nl.shared_up), ("next shared_down", nl.shared_down),
+                        ("next shared_scalar_gate", nl.shared_scalar_gate)):
+            _need(t, name, device=dev)
+        hint = L.NextLayer(nl.router.data_ptr(), nl.shared_gate.data_ptr(), nl.shared_up.data_ptr(),
+                           nl.shared_down.data_ptr(), nl.shared_scalar_gate.data_ptr())
+        _check(L.lib.moe_block_forward_prefetch(*args, ctypes.byref(hint)), "block_forward")
     st["combined_out"] = out
     return st

@@ -260,7 +260,7 @@ int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids
                             expert_raw, (hipStream_t)stream);
 }
 
-int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
                       const float* norm_w, float norm_eps,
                       const void* w_router, const float* logit_bias, const void* gate_up_q,
                       int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
@@ -268,7 +268,8 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
                       int path, const float* residual, float* out, void* logits_bf16,
                       int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
                       float* shared_out, float* gate_prob, float* expert_raw, void* ws,
-                      size_t ws_bytes, void* stream) {
+                      size_t ws_bytes, void* stream,
+                              const moe_next_layer* next) {
   if (!x || !w_router || !gate_up_q || !down_q || !ws_gate || !ws_up || !ws_down || !ws_scalar_gate || !out)
     return moe_set_error(MOE_E_ARG, "moe_block_forward: NULL pointer");
   if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_block_forward: bad x_dtype %d", x_dtype);
@@ -317,6 +318,10 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
     L.ids_out_requested = (topk_ids || topk_w_bf16 || topk_w_f32) ? 1 : 0;
     L.norm_w = one_launch ? norm_w : nullptr;
     L.norm_eps = norm_eps;
+    if (next) {
+      L.nx_router = next->w_router; L.nx_sg = next->ws_gate; L.nx_su = next->ws_up;
+      L.nx_sd = next->ws_down; L.nx_ssg = next->ws_scalar_gate;
+    }
     if (!L.logits || !L.ids || !L.w_f32 || !L.w_bf16 || !L.s_shared || !L.gate_prob || !L.shared_raw || !L.s_routed)
       return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
     if (one_launch)
@@ -355,9 +360,35 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
                             shared_out, expert_raw, st);
 }
 
+int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                      const float* norm_w, float norm_eps,
+                      const void* w_router, const float* logit_bias, const void* gate_up_q,
+                      int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
+                      const void* ws_up, const void* ws_down, const void* ws_scalar_gate,
+                      int path, const float* residual, float* out, void* logits_bf16,
+                      int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
+                      float* shared_out, float* gate_prob, float* expert_raw, void* ws,
+                      size_t ws_bytes, void* stream) {
+  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, norm_w, norm_eps, w_router, logit_bias, gate_up_q, gate_up_fmt, down_q, down_fmt, ws_gate, ws_up, ws_down, ws_scalar_gate, path, residual, out, logits_bf16, topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob, expert_raw, ws, ws_bytes, stream, nullptr);
+}
+
+int moe_block_forward_prefetch(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                      const float* norm_w, float norm_eps,
+                      const void* w_router, const float* logit_bias, const void* gate_up_q,
+                      int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
+                      const void* ws_up, const void* ws_down, const void* ws_scalar_gate,
+                      int path, const float* residual, float* out, void* logits_bf16,
+                      int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
+                      float* shared_out, float* gate_prob, float* expert_raw, void* ws,
+                      size_t ws_bytes, void* stream,
+                               const moe_next_layer* next) {
+  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, norm_w, norm_eps, w_router, logit_bias, gate_up_q, gate_up_fmt, down_q, down_fmt, ws_gate, ws_up, ws_down, ws_scalar_gate, path, residual, out, logits_bf16, topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob, expert_raw, ws, ws_bytes, stream, next);
+}
+
 int moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {
   if (!ws || ws_bytes < kSyncBytes) return moe_set_error(MOE_E_ARG, "moe_workspace_init: workspace smaller than %zu bytes", kSyncBytes);
-  return moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream);
+  MOE_TRY(moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream));
+  return moe_launch_cu_probe(reinterpret_cast<int*>(ws), (hipStream_t)stream);
 }
 
 }  // extern "C"

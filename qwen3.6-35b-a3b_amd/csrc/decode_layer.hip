@@ -1,35 +1,40 @@
-// Single-token decode of one MoE block in ONE launch: a persistent grid of 256 workgroups of 8
-// waves (one per CU on MI355X, all co-resident) runs the block's dependent phases and hands data
-// between them through self-validating exchange words instead of kernel boundaries or
-// device-wide fences.
+// Single-token decode of one MoE block in ONE launch, laid out over the 8 XCDs of an MI355X.
 //
-//   start    every wg stages x in LDS, RMS-normalized when a post-attention norm weight is given
-//            (Form A, engine/m3_forward.py:303-307; the f64 sum of squares is a block reduction)
-//   phase 1  wg g: router logit e = g (f64, certified bf16) | shared gate/up rows i = 2g, 2g+1 |
-//            (wg 0) the scalar shared gate                 -> logits[E], s_shared[I_s], gate
-//   phase 2  every wg waits for the 256 logits and runs R2-R5 itself (same answer everywhere; the
-//            fast top-k's slot order stands in for torch's when ties sit inside the top 8 and no
-//            stage output is asked for: same experts, same weights);
-//            wg g: routed gate/up rows of slot k = g/32, i in [16(g%32), +16) -> s_routed[k];
-//            its down-projection weights are requested here, ahead of their use;
-//            shared down rows 8g..8g+7 (one wave; waits for s_shared)
-//   phase 3  wg g: down rows h in [64(g%32), +64) of slot k's expert (waits for the 512 words of
-//            s_routed[k] only)                             -> y[k][h]
-//   phase 4  wg g: ascending-expert-id combine of y[0..7][8g..8g+7], gated shared expert,
-//            residual -> out[8g..8g+7]
-// Each workgroup reads at most 2 KB of exchange words per phase: the words are hot (every
-// workgroup polls the same few KB while the weights stream), so their volume sets the latency.
+// A persistent grid of 256 workgroups of 8 waves (one per CU; the LDS footprint keeps it at one,
+// so every XCD holds exactly 32) runs the block's dependent phases and hands data between them
+// through self-validating exchange words. A workgroup's role is (x, r): x = the XCD it runs on
+// (hardware register XCC_ID), r = the rank of its CU among that XCD's 32, read from a table that
+// moe_workspace_init's probe launch records (one load; a per-XCD atomic ticket instead, when no
+// table was recorded, costs 1.5-3 us of contention at the start).
+// XCD x owns routed slot k = x and the 64-wide slice [64x, 64x+64) of the shared expert's
+// intermediate axis, so two of the three exchanges stay among the 32 workgroups of one XCD:
+//
+//   start    stage x in LDS, RMS-normalized when a post-attention norm weight is given (Form A,
+//            engine/m3_forward.py:303-307; f64 sum of squares, one rounding)
+//   phase 1  wg (x, r): router logits e in [8r, 8r+8) (one wave each; f64, certified bf16), so
+//            each XCD computes all 256 logits itself | shared gate/up rows i = 64x + 2r (+1) |
+//            the scalar shared gate p (every workgroup, for its own combine rows)
+//   phase 2  wait for the XCD's 256 logits; R2-R5 (same answer everywhere); routed gate/up rows of
+//            slot x, i in [16r, 16r+16), its down rows requested ahead of use;
+//            shared-down partial over the XCD's 64 i-values for rows h in [64r, 64r+64)
+//   phase 3  wait for slot x's 512 activations (XCD-local); down rows h in [64r, 64r+64)
+//   phase 4  wg (x, r) combines rows [8j, 8j+8), j = 32x + r: the 8 slots' outputs in ascending
+//            expert id, the 8 shared-down partials in ascending x, gate, residual
+//   (hint)   with the next layer's routing-independent weights given, waves 4-7 read the parts
+//            that role (x, r) will need into XCD x's L2 while phase 4 waits
 //
 // Exchange words are 32-bit: a value is stored as the complement of its bit pattern (NaNs made
 // canonical first), so 0 never encodes a value and means "not written yet". Each word is written
 // once per launch by one dword store that bypasses the non-coherent L2 (agent-scope relaxed atomic
-// store, sc1) and read the same way (sc1 loads, up to 16 bytes at a time); a reader re-polls, all
-// of its missing words in parallel, until every word it needs is non-zero. Two buffers alternate
-// by the launch's epoch parity, and each launch zeroes the buffer the next launch will use, so a
-// zeroed workspace is a valid starting state and graph replays work. The epoch lives in the
-// workspace's sync words: every workgroup reads it at the start, the last workgroup to finish
-// (arrival counter) advances it. Every spin is bounded: on a timeout the workgroup records an
-// error bit and carries on (no hang).
+// store, sc1) and read the same way (sc1 loads, 16 bytes at a time); a reader re-polls all of its
+// missing words in parallel until every word it needs is non-zero. Exchange latency grows with the
+// number of workgroups reading the same lines, which is why no region here has more than 32
+// readers. Two buffers alternate by the launch's epoch parity, and each launch zeroes the buffer
+// the next launch will use, so a zeroed workspace is a valid starting state and graph replays
+// work. The launch count (epoch) is kept per CU, in the CU's table word next to its rank: the one
+// workgroup a launch places on that CU reads it at the start and writes it back incremented at
+// the end, so no launch ends on a contended atomic. Every spin is bounded: on a timeout the
+// workgroup records an error bit and carries on (no hang).
 #include "common.h"
 #include "moe_internal.h"
 #include "router_dev.h"
@@ -37,9 +42,25 @@
 
 namespace moe {
 
-constexpr int kG = 256;                 // workgroups (one per CU)
+constexpr int kXcd = 8;                 // XCDs on MI355X
+constexpr int kPer = 32;                // workgroups (CUs) per XCD
+constexpr int kG = kXcd * kPer;         // 256 workgroups
 constexpr int kThreads = 512;           // 8 waves
 constexpr int kSpinLimit = 1 << 20;     // polls (each a memory round trip) before giving up
+constexpr int kOccPad = 5120;           // uint4s of LDS that keep the grid at one workgroup per CU
+// sync words (int32 index into the workspace's first kSyncBytes)
+constexpr int kErrWord = 3;             // error bits
+constexpr int kTableValid = 4;          // 1: the CU table below is complete; 2: the probe failed
+constexpr int kProbeArrive = 5;         // probe launch: arrival counter
+constexpr int kProbeBad = 6;            // probe launch: nonzero when a CU was seen twice
+constexpr int kTicket = 32;             // fallback per-XCD tickets (32..39), taken modulo kPer
+constexpr int kProbeCount = 40;         // probe launch: workgroups seen per XCD (40..47)
+constexpr int kCuTable = 114688;        // [xcd][64]: (epoch << 8) | (rank + 1), slot = se*16 + cu
+constexpr int kRoleEpoch = kCuTable + kXcd * 64;   // fallback: epoch per role [256]
+
+// error bits (sync word 3)
+constexpr int kErrSpin = 1;             // a bounded wait timed out
+constexpr int kErrRole = 2;             // an XCD received more than kPer workgroups
 
 struct LayerArgs {
   const void* x;
@@ -52,7 +73,7 @@ struct LayerArgs {
   const uint16_t* su;
   const uint16_t* sd;
   const uint16_t* ssg;
-  int* sync;                            // [0] ticket, [1] epoch, [2] arrivals, [3] error bits
+  int* sync;                            // sync words (see kErrWord .. kRoleEpoch)
   uint32_t* xch;                        // two exchange buffers of XW_BUF words
   uint16_t* logits_out;
   int32_t* ids_out;
@@ -66,16 +87,67 @@ struct LayerArgs {
   int exact_order;                      // stage outputs requested: keep torch's slot order
   const float* norm_w;                  // post-attention RMSNorm weight [H] f32, or NULL
   float norm_eps;
+  // the next layer's routing-independent weights (L2 warm-up hint), or NULL
+  const uint16_t* nx_router;
+  const uint16_t* nx_sg;
+  const uint16_t* nx_su;
+  const uint16_t* nx_sd;
+  const uint16_t* nx_ssg;
 };
 
 // exchange buffer layout (uint32 words; every region starts 16-byte aligned)
-constexpr int XW_LOGITS = 0;            // 256 logits (bf16 bits)
-constexpr int XW_GATE = 256;            // 4 copies of the sigmoid of the shared expert's gate
-constexpr int XW_SSH = 260;             // 512 shared-expert activations
-constexpr int XW_SR = 772;              // 8 x 512 routed activations, slot-major
-constexpr int XW_Y = 772 + 4096;        // 8 x 2048 routed expert outputs, slot-major
-constexpr int XW_BUF = XW_Y + 8 * 2048; // words per buffer
+constexpr int XW_LOG = 0;                       // [xcd][256] router logits (bf16 bits)
+constexpr int XW_SSH = XW_LOG + kXcd * 256;     // [xcd][64] shared activations of the xcd's slice
+constexpr int XW_SR = XW_SSH + kXcd * 64;       // [slot][512] routed activations
+constexpr int XW_Y = XW_SR + kXcd * 512;        // [slot][2048] routed expert outputs
+constexpr int XW_SHP = XW_Y + kXcd * 2048;      // [xcd][2048] shared-down partial sums
+constexpr int XW_BUF = XW_SHP + kXcd * 2048;    // words per buffer
 constexpr int kClearPerWg = (XW_BUF + kG - 1) / kG;
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 15u;
+}
+// the CU's slot inside its XCD: shader engine (HW_ID bits 13-15) x 16 + CU (bits 8-11)
+__device__ __forceinline__ int cu_slot() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(v));
+  return (int)(((v >> 13) & 3u) * 16u + ((v >> 8) & 15u));
+}
+__device__ __forceinline__ int aload(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void astore(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Probe launch (moe_workspace_init): one workgroup per CU (same LDS footprint as the layer), each
+// records its CU's rank within the XCD; the table is valid when every XCD saw exactly kPer
+// distinct CUs.
+__global__ __launch_bounds__(64) void k_cu_probe(int* sync) {
+  __shared__ uint4 s_occ[kOccPad + 1024];
+  // the LDS footprint is the point (one workgroup per CU); this never-true branch keeps it
+  const bool never = sync[kErrWord] == 0x7FFFFFFF;
+  if (never) s_occ[threadIdx.x] = make_uint4(1, 2, 3, 4);
+  __syncthreads();
+  if (never) sync[kProbeBad] += (int)s_occ[threadIdx.x ^ 1].x;
+  if (threadIdx.x != 0) return;
+  const int xcd = (int)xcc_id() & (kXcd - 1);
+  const int slot = cu_slot();
+  const int rank = __hip_atomic_fetch_add(sync + kProbeCount + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int expected = 0;
+  const bool fresh = __hip_atomic_compare_exchange_strong(
+      sync + kCuTable + 64 * xcd + slot, &expected, rank + 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+      __HIP_MEMORY_SCOPE_AGENT);
+  if (!fresh || rank >= kPer) __hip_atomic_fetch_add(sync + kProbeBad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int arrived = __hip_atomic_fetch_add(sync + kProbeArrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (arrived == kG - 1) {
+    bool ok = aload(sync + kProbeBad) == 0;
+    for (int q = 0; q < kXcd; ++q) ok = ok && aload(sync + kProbeCount + q) == kPer;
+    astore(sync + kTableValid, ok ? 1 : 2);
+  }
+}
 
 __device__ __forceinline__ uint32_t xenc(float v) {
   const uint32_t b = (v != v) ? 0x7FC00000u : __float_as_uint(v);
@@ -106,100 +178,293 @@ __device__ __forceinline__ void xwait(uint32_t* p, int stride, int* err, uint32_
 #pragma unroll
     for (int j = 0; j < N; ++j) ok = ok && v[j] != 0u;
     if (ok) return;
-    if (spins >= kSpinLimit) { atomicOr(err, 1); return; }
+    if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); return; }
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int j = 0; j < N; ++j)
       if (v[j] == 0u) v[j] = xload(p + j * stride);
   }
 }
-// N 16-byte groups at byte offsets off[j] of the buffer, same protocol
-template <int N>
-__device__ __forceinline__ void xwait4(__amdgpu_buffer_rsrc_t r, const int* off, int* err,
-                                       uint4* v) {
-#pragma unroll
-  for (int j = 0; j < N; ++j) v[j] = xload4(r, off[j]);
-  for (int spins = 0;; ++spins) {
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < N; ++j) ok = ok && xfull(v[j]);
-    if (ok) return;
-    if (spins >= kSpinLimit) { atomicOr(err, 1); return; }
+// one 16-byte group at byte offset `off` of the buffer, same protocol
+__device__ __forceinline__ uint4 xwait4(__amdgpu_buffer_rsrc_t r, int off, int* err) {
+  uint4 v = xload4(r, off);
+  for (int spins = 0; !xfull(v); ++spins) {
+    if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); break; }
     __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-    for (int j = 0; j < N; ++j)
-      if (!xfull(v[j])) v[j] = xload4(r, off[j]);
+    v = xload4(r, off);
   }
+  return v;
+}
+
+// R1 for one router row held by a wave: w[c] = W[e, 512c + 8 lane .. +8), xv[c] = the matching x.
+// The correctly rounded bf16 of sum + bias: f64 sum (every product x_j w_j is exact in f64) with
+// the certified error bound 4(H+3) 2^-53 (|x|_1 max|w| + |b|), which bounds sum |x_j w_j| + |b|
+// times the summation's error factor; a double-double recompute settles what that does not.
+// xl1 >= |x|_1 is the workgroup's bound on the input's 1-norm.
+__device__ __forceinline__ uint32_t router_row_bits(const uint4* w, const float (*xv)[8],
+                                                   double bval, double xl1) {
+  constexpr int H = 2048;
+  double acc = 0.0;
+  uint32_t wm = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = fma((double)xv[c][2 * i], (double)bf16_to_f32(ww[i] & 0xFFFFu), acc);
+      acc = fma((double)xv[c][2 * i + 1], (double)bf16_to_f32(ww[i] >> 16), acc);
+      wm = max(wm, max(ww[i] & 0x7FFFu, (ww[i] >> 16) & 0x7FFFu));
+    }
+  }
+  acc = wave_sum_f64(acc);
+  wm = max(wm, dpp_u32<0xB1>(wm));
+  wm = max(wm, dpp_u32<0x4E>(wm));
+  wm = max(wm, dpp_u32<0x141>(wm));
+  wm = max(wm, dpp_u32<0x140>(wm));
+  wm = max(max((uint32_t)__builtin_amdgcn_readlane((int)wm, 15), (uint32_t)__builtin_amdgcn_readlane((int)wm, 31)),
+           max((uint32_t)__builtin_amdgcn_readlane((int)wm, 47), (uint32_t)__builtin_amdgcn_readlane((int)wm, 63)));
+  const double nrm = xl1 * (double)bf16_to_f32(wm) + fabs(bval);
+  uint32_t bits;
+  if (!round_bf16_certified(acc + bval, 4.0 * (double)(H + 3) * 0x1p-53 * nrm, &bits)) {
+    DD d = {0.0, 0.0};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const double w_ = bf16_to_f32((i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu));
+        d = dd_add(d, DD{(double)xv[c][i] * w_, 0.0});
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      DD other = {__shfl_xor(d.hi, o, 64), __shfl_xor(d.lo, o, 64)};
+      d = dd_add(d, other);
+    }
+    d = dd_add(d, DD{bval, 0.0});
+    bits = round_bf16_dd(d, (double)(H + 64) * 0x1p-104 * 16.0 * nrm);
+  }
+  return bits;
+}
+
+__device__ __forceinline__ uint32_t xor4(uint4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
+
+// XCD-local exchange words: written and read only by the workgroups of one XCD, through that
+// XCD's L2 (non-temporal stores and loads: the L2 is coherent among its CUs, and the CU's own L1
+// is not consulted), which halves the round trip of the agent-scope (MALL) words.
+__device__ __forceinline__ void lstore(__amdgpu_buffer_rsrc_t r, int off, uint32_t w) {
+  __builtin_amdgcn_raw_buffer_store_b32(w, r, off, 0, 2);
+}
+__device__ __forceinline__ uint32_t lload(__amdgpu_buffer_rsrc_t r, int off) {
+  asm volatile("" ::: "memory");
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 2);
+}
+__device__ __forceinline__ uint4 lload4(__amdgpu_buffer_rsrc_t r, int off) {
+  asm volatile("" ::: "memory");
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint4 lwait4(__amdgpu_buffer_rsrc_t r, int off, int* err) {
+  uint4 v = lload4(r, off);
+  for (int spins = 0; !xfull(v); ++spins) {
+    if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); break; }
+    __builtin_amdgcn_s_sleep(1);
+    v = lload4(r, off);
+  }
+  return v;
+}
+
+// maximum over the wave, in every lane (DPP maxima inside each 16-lane row, then the four rows)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 15), (uint32_t)__builtin_amdgcn_readlane((int)v, 31)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)v, 47), (uint32_t)__builtin_amdgcn_readlane((int)v, 63)));
+}
+// bf16 bits <-> a 16-bit key with the same order as the values (no NaNs on this path)
+__device__ __forceinline__ uint32_t bf16_key(uint32_t b) { return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u); }
+__device__ __forceinline__ uint32_t bf16_unkey(uint32_t k) { return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu); }
+
+// R2-R5 for one token, by one wave holding the 256 logits' bf16 bits lb[q] of experts lane + 64q.
+// The 9 largest logits are found on 24-bit keys (value key << 8 | 255 - id: distinct, and the
+// logit order is the probability order, since p = exp(l - max) / sum is monotone); their
+// probabilities p_r = f32(exp(l_r - max)) * (1 / sum) are the softmax's own values (R2: the full
+// sum of 256 exps, as route_softmax). Without two equal probabilities among the first 9 the
+// selection is torch's; with equal ones only inside the first 8 it is torch's up to slot order
+// (same experts, same weights), accepted when exact_order is false. Otherwise returns false and
+// leaves the full probabilities in p for the exact replay. On success lanes < K write ids, w_f32
+// (p_r / sum of the 8 in rank order) and w_bf16.
+template <int K>
+__device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bool exact_order,
+                                                float* p, int* ids, float* wf, uint16_t* wb) {
+  uint32_t k0 = (bf16_key(lb[0]) << 8) | (uint32_t)(255 - lane);
+  uint32_t k1 = (bf16_key(lb[1]) << 8) | (uint32_t)(191 - lane);
+  uint32_t k2 = (bf16_key(lb[2]) << 8) | (uint32_t)(127 - lane);
+  uint32_t k3 = (bf16_key(lb[3]) << 8) | (uint32_t)(63 - lane);
+  {
+    // each lane's four keys, descending
+    uint32_t a = max(k0, k1), b = min(k0, k1), c = max(k2, k3), d = min(k2, k3);
+    k0 = max(a, c); const uint32_t t1 = min(a, c);
+    k3 = min(b, d); const uint32_t t2 = max(b, d);
+    k1 = max(t1, t2); k2 = min(t1, t2);
+  }
+  uint32_t top[K + 1];
+  top[0] = wave_max_u32(k0);
+  if (k0 == top[0]) { k0 = k1; k1 = k2; k2 = k3; k3 = 0u; }
+  const float m = bf16_to_f32(bf16_unkey(top[0] >> 8));
+  float sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) { p[q] = expf(bf16_to_f32(lb[q]) - m); sum += p[q]; }
+#pragma unroll
+  for (int r = 1; r <= K; ++r) {
+    top[r] = wave_max_u32(k0);
+    if (k0 == top[r]) { k0 = k1; k1 = k2; k2 = k3; k3 = 0u; }
+  }
+  sum = wave_sum_f32(sum);
+  const float rs = 1.0f / sum;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) p[q] *= rs;
+  uint32_t mine = top[0];
+#pragma unroll
+  for (int r = 1; r <= K; ++r) mine = lane == r ? top[r] : mine;
+  const float ps = expf(bf16_to_f32(bf16_unkey(mine >> 8)) - m) * rs;
+  const float nxt = __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(ps), 0x101, 0xF, 0xF, false));
+  const uint64_t ties = __ballot(lane < K && ps == nxt);       // p_r == p_{r+1}, r < K
+  if (((ties >> (K - 1)) & 1ull) || (ties && exact_order)) return false;
+  float tot = 0.0f;
+#pragma unroll
+  for (int r = 0; r < K; ++r) tot += readlane_f32(ps, r);
+  if (lane < K) {
+    const float wv = ps / tot;
+    ids[lane] = 255 - (int)(mine & 255u);
+    wf[lane] = wv;
+    wb[lane] = (uint16_t)f32_to_bf16(wv);
+  }
+  return true;
 }
 
 template <int XDT>
 __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
-  constexpr int H = 2048, I = 512, E = 256, K = 8, IS = 512;
+  constexpr int H = 2048, I = 512, E = 256, K = 8, IS = 512, ISX = IS / kXcd;
   __shared__ float s_x[H];
   __shared__ TopkLds tk;                 // the exact replay's scratch (ties only)
-  __shared__ float s_k[I];               // this workgroup's slot's routed activations
-  __shared__ float s_sh[IS];             // shared-expert activations (wave 4)
+  __shared__ float s_k[I];               // routed activations of this XCD's slot
+  __shared__ float s_sh[ISX];            // shared activations of this XCD's slice
+  __shared__ float s_y[64];              // this workgroup's 64 down-projection outputs
+  __shared__ float s_shp[64];            // and its 64 shared-down partials
   __shared__ int s_ids[K];
   __shared__ float s_w[K];
   __shared__ float s_wf[K];
   __shared__ uint16_t s_wb[K];
   __shared__ int s_order[K];
-  __shared__ float sh_raw[8];
-  __shared__ float ys[K][8];
+  __shared__ float s_comb[2][K][8];      // [y | shared partial][slot | xcd][row]
   __shared__ float s_gate;
-  __shared__ double s_red[kThreads / 64];
+  __shared__ double s_red[2][kThreads / 64];
+  __shared__ int s_role[4];
+  __shared__ uint4 s_occ[kOccPad];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int l16 = lane & 15;
-  const int g = blockIdx.x;
-  const int slot = g >> 5, blk = g & 31;
-  int* err = a.sync + 3;
-  const uint32_t epoch =
-      (uint32_t)__hip_atomic_load(a.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  int* err = a.sync + kErrWord;
+  // x and the norm weight do not depend on the role: request them first
+  float4 xin;
+  if (XDT == MOE_DT_F32) {
+    xin = reinterpret_cast<const float4*>(a.x)[t];
+  } else {
+    const uint2 u = reinterpret_cast<const uint2*>(a.x)[t];
+    xin = make_float4(bf16_to_f32(u.x & 0xFFFFu), bf16_to_f32(u.x >> 16),
+                      bf16_to_f32(u.y & 0xFFFFu), bf16_to_f32(u.y >> 16));
+  }
+  const float4 nw = a.norm_w ? reinterpret_cast<const float4*>(a.norm_w)[t] : make_float4(1.f, 1.f, 1.f, 1.f);
+  if (t == 0) {
+    // role and launch count: the CU table word (one load), else a ticket and a per-role epoch
+    const int xcd = (int)xcc_id() & (kXcd - 1);
+    const int slot = cu_slot();
+    const int valid = aload(a.sync + kTableValid);
+    const int w = aload(a.sync + kCuTable + 64 * xcd + slot);
+    int rank, ep, mode;
+    if (valid == 1 && (w & 255) != 0) {
+      rank = (w & 255) - 1;
+      ep = (int)((uint32_t)w >> 8);
+      mode = 0;
+    } else {
+      if (valid == 1) atomicOr(err, kErrRole);      // a CU the probe did not see
+      rank = __hip_atomic_fetch_add(a.sync + kTicket + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & (kPer - 1);
+      ep = aload(a.sync + kRoleEpoch + kPer * xcd + rank);
+      mode = 1;
+    }
+    s_role[0] = xcd;
+    s_role[1] = rank;
+    s_role[2] = ep;
+    s_role[3] = mode ? -1 : slot;
+  }
+  // the LDS footprint keeps one workgroup per CU; this never-true branch keeps the array
+  const bool never = a.nx_ssg == reinterpret_cast<const uint16_t*>(a.sync);
+  if (never) s_occ[t] = make_uint4(t, 0, 0, 0);
+  __syncthreads();
+  if (never) atomicOr(err, (int)s_occ[t ^ 1].x);
+  const int x = s_role[0], r = s_role[1];
+  const uint32_t epoch = (uint32_t)s_role[2] + 1u;
   uint32_t* xb = a.xch + (epoch & 1u) * XW_BUF;          // this launch's words
   uint32_t* xn = a.xch + ((epoch & 1u) ^ 1u) * XW_BUF;   // the next launch's, zeroed here
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(xb, 0, XW_BUF * 4, 0x00020000);
+  const int j = kPer * x + r;            // combine rows [8j, 8j+8)
 
-  // x into LDS as f32 (RMS-normalized first when norm_w is given); the residual of this
-  // workgroup's 8 output rows; the next buffer's slice
+  // ------------------------------------------------------------------ start: loads, x, norm --
+  // routing-independent weights: router row 8r + wave; shared gate and up rows i = 64x + 2r + wave
+  // (waves 0-1); the scalar gate row (wave 2); shared-down rows 64r + (lane >> 3) + 8q, cols
+  // 64x + 8 (lane & 7) .. +8 (wave 4, used while wave 0 selects the experts)
+  uint4 wr4[4], sgw[4], suw[4], sdw[8];
+  const float bias_e = a.bias ? a.bias[8 * r + wave] : 0.0f;
   {
-    float4 v;
-    if (XDT == MOE_DT_F32) {
-      v = reinterpret_cast<const float4*>(a.x)[t];
-    } else {
-      const uint2 u = reinterpret_cast<const uint2*>(a.x)[t];
-      v = make_float4(bf16_to_f32(u.x & 0xFFFFu), bf16_to_f32(u.x >> 16),
-                      bf16_to_f32(u.y & 0xFFFFu), bf16_to_f32(u.y >> 16));
-    }
-    if (a.norm_w) {
-      // r = f32(1 / sqrt(mean(x^2) + eps)) in f64: every square is exact, one final rounding
-      const float4 nw = reinterpret_cast<const float4*>(a.norm_w)[t];
-      double ss = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-      ss = wave_sum_f64(ss);
-      if (lane == 0) s_red[wave] = ss;
-      __syncthreads();
-      double tot = 0.0;
+    const uint16_t* wr = a.w_router + (size_t)(8 * r + wave) * H;
 #pragma unroll
-      for (int j = 0; j < kThreads / 64; ++j) tot += s_red[j];
-      const float r = (float)(1.0 / sqrt(tot / (double)H + (double)a.norm_eps));
-      v = make_float4((v.x * r) * nw.x, (v.y * r) * nw.y, (v.z * r) * nw.z, (v.w * r) * nw.w);
+    for (int c = 0; c < 4; ++c) wr4[c] = *reinterpret_cast<const uint4*>(wr + 512 * c + 8 * lane);
+    if (wave < 2) {
+      const int i = ISX * x + 2 * r + wave;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        sgw[c] = *reinterpret_cast<const uint4*>(a.sg + (size_t)i * H + 512 * c + 8 * lane);
+        suw[c] = *reinterpret_cast<const uint4*>(a.su + (size_t)i * H + 512 * c + 8 * lane);
+      }
+    } else if (wave == 2) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sgw[c] = *reinterpret_cast<const uint4*>(a.ssg + 512 * c + 8 * lane);
+    } else if (wave == 4) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        sdw[q] = *reinterpret_cast<const uint4*>(a.sd + (size_t)(64 * r + (lane >> 3) + 8 * q) * IS +
+                                                 ISX * x + 8 * (lane & 7));
+    }
+  }
+  const float resid = (t < 8 && a.residual) ? a.residual[8 * j + t] : 0.0f;
+  {
+    // norm: r = f32(1 / sqrt(mean(x^2) + eps)) in f64 (every square exact, one final rounding);
+    // xl1 >= |input|_1 for the router's error bound, from sum |x_j nw_j| (exact products)
+    double ss = (double)xin.x * xin.x + (double)xin.y * xin.y + (double)xin.z * xin.z + (double)xin.w * xin.w;
+    double sa = fabs((double)xin.x * nw.x) + fabs((double)xin.y * nw.y) + fabs((double)xin.z * nw.z) +
+                fabs((double)xin.w * nw.w);
+    ss = wave_sum_f64(ss);
+    sa = wave_sum_f64(sa);
+    if (lane == 0) { s_red[0][wave] = ss; s_red[1][wave] = sa; }
+    __syncthreads();
+    double tot = 0.0, tabs = 0.0;
+#pragma unroll
+    for (int q = 0; q < kThreads / 64; ++q) { tot += s_red[0][q]; tabs += s_red[1][q]; }
+    float4 v = xin;
+    double xl1 = tabs * (1.0 + 0x1p-20);
+    if (a.norm_w) {
+      const float rs = (float)(1.0 / sqrt(tot / (double)H + (double)a.norm_eps));
+      v = make_float4((v.x * rs) * nw.x, (v.y * rs) * nw.y, (v.z * rs) * nw.z, (v.w * rs) * nw.w);
+      xl1 *= (double)rs;
     }
     reinterpret_cast<float4*>(s_x)[t] = v;
-  }
-  const float resid = (t < 8 && a.residual) ? a.residual[8 * g + t] : 0.0f;
-  if (t < kClearPerWg && kClearPerWg * g + t < XW_BUF) xstore(xn + kClearPerWg * g + t, 0u);
-  // wave 4: shared-down weights, row 8g + (lane >> 3), cols 64 (lane & 7) + 0..63
-  uint4 sdw[8];
-  if (wave == 4) {
-    const uint16_t* dr = a.sd + (size_t)(8 * g + (lane >> 3)) * IS + 64 * (lane & 7);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) sdw[c] = reinterpret_cast<const uint4*>(dr)[c];
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // ------------------------------------------------------------------------------ phase 1 --
-  if (wave < 4) {
+    // ---------------------------------------------------------------------------- phase 1 --
     // x at cols 512c + 8 lane (c = 0..3)
     float xv[4][8];
 #pragma unroll
@@ -209,158 +474,120 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       xv[c][0] = u0.x; xv[c][1] = u0.y; xv[c][2] = u0.z; xv[c][3] = u0.w;
       xv[c][4] = u1.x; xv[c][5] = u1.y; xv[c][6] = u1.z; xv[c][7] = u1.w;
     }
-    if (wave == 0) {
-      const uint16_t* wr = a.w_router + (size_t)g * H;
-      uint4 wv4[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) wv4[c] = *reinterpret_cast<const uint4*>(wr + 512 * c + 8 * lane);
-      double acc = 0.0, xsq = 0.0, wsq = 0.0;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t ww[4] = {wv4[c].x, wv4[c].y, wv4[c].z, wv4[c].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const double w0 = bf16_to_f32(ww[i] & 0xFFFFu), w1 = bf16_to_f32(ww[i] >> 16);
-          const double x0 = xv[c][2 * i], x1 = xv[c][2 * i + 1];
-          acc = fma(x0, w0, acc);
-          acc = fma(x1, w1, acc);
-          xsq = fma(x0, x0, xsq);
-          xsq = fma(x1, x1, xsq);
-          wsq = fma(w0, w0, wsq);
-          wsq = fma(w1, w1, wsq);
-        }
-      }
-      acc = wave_sum_f64(acc);
-      xsq = wave_sum_f64(xsq);
-      wsq = wave_sum_f64(wsq);
-      const double bval = a.bias ? (double)a.bias[g] : 0.0;
-      const double nrm = sqrt(xsq) * sqrt(wsq) + fabs(bval);
-      uint32_t bits;
-      if (!round_bf16_certified(acc + bval, 4.0 * (double)(H + 3) * 0x1p-53 * nrm, &bits)) {
-        DD d = {0.0, 0.0};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t ww[4] = {wv4[c].x, wv4[c].y, wv4[c].z, wv4[c].w};
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const double w_ = bf16_to_f32((i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu));
-            d = dd_add(d, DD{(double)xv[c][i] * w_, 0.0});
-          }
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-          DD other = {__shfl_xor(d.hi, o, 64), __shfl_xor(d.lo, o, 64)};
-          d = dd_add(d, other);
-        }
-        d = dd_add(d, DD{bval, 0.0});
-        bits = round_bf16_dd(d, (double)(H + 64) * 0x1p-104 * 16.0 * nrm);
-      }
-      if (lane == 0) xstore(xb + XW_LOGITS + g, ~bits);
-    } else if (wave <= 2) {
-      const int i = 2 * g + (wave - 1);
-      const uint16_t* gr = a.sg + (size_t)i * H;
-      const uint16_t* ur = a.su + (size_t)i * H;
-      uint4 gw[4], uw[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        gw[c] = *reinterpret_cast<const uint4*>(gr + 512 * c + 8 * lane);
-        uw[c] = *reinterpret_cast<const uint4*>(ur + 512 * c + 8 * lane);
-      }
+    const int e = 8 * r + wave;
+    const uint32_t bits = router_row_bits(wr4, xv, (double)bias_e, xl1);
+    if (lane == 0) lstore(xr, 4 * (XW_LOG + 256 * x + e), ~bits);
+    if (wave < 2) {
       float ag = 0.0f, au = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        ag += dot8_bf16(gw[c], xv[c]);
-        au += dot8_bf16(uw[c], xv[c]);
+        ag += dot8_bf16(sgw[c], xv[c]);
+        au += dot8_bf16(suw[c], xv[c]);
       }
       ag = wave_sum_f32(ag);
       au = wave_sum_f32(au);
-      if (lane == 0) xstore(xb + XW_SSH + i, xenc(silu_f32(ag) * au));
-    } else if (g == 0) {
+      if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + wave), xenc(silu_f32(ag) * au));
+    } else if (wave == 2) {
       float gs = 0.0f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        gs += dot8_bf16(*reinterpret_cast<const uint4*>(a.ssg + 512 * c + 8 * lane), xv[c]);
+      for (int c = 0; c < 4; ++c) gs += dot8_bf16(sgw[c], xv[c]);
       gs = wave_sum_f32(gs);
       const float p = 1.0f / (1.0f + expf(-gs));
-      if (lane < 4) xstore(xb + XW_GATE + lane, xenc(p));   // the whole 16-byte group
-      if (lane == 0 && a.gate_prob_out) a.gate_prob_out[0] = p;
+      if (lane == 0) {
+        s_gate = p;
+        if (j == 0 && a.gate_prob_out) a.gate_prob_out[0] = p;
+      }
     }
   }
 
   // ------------------------------------------------------------------------------ phase 2 --
   if (wave == 0) {
     uint32_t lw[4];
-    xwait<4>(xb + XW_LOGITS + lane, 64, err, lw);
-    float lg[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) lg[j] = bf16_to_f32(~lw[j] & 0xFFFFu);
-    // R2, the same arithmetic as route_softmax, from registers
-    float m = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
-    m = wave_max_f32(m);
-    float p[4], sum = 0.0f;
+    for (int q = 0; q < 4; ++q) lw[q] = lload(xr, 4 * (XW_LOG + 256 * x + lane + 64 * q));
+    for (int spins = 0;; ++spins) {
+      const bool ok = lw[0] && lw[1] && lw[2] && lw[3];
+      if (ok) break;
+      if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); break; }
+      __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { p[j] = expf(lg[j] - m); sum += p[j]; }
-    sum = wave_sum_f32(sum);
-    const float rs = 1.0f / sum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) p[j] *= rs;
-    if (g == 0 && a.logits_out) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a.logits_out[64 * j + lane] = (uint16_t)(~lw[j] & 0xFFFFu);
+      for (int q = 0; q < 4; ++q)
+        if (lw[q] == 0u) lw[q] = lload(xr, 4 * (XW_LOG + 256 * x + lane + 64 * q));
     }
-    int my_id;
-    float my_val, tot;
-    const int code = wave_topk32<K>(p, lane, my_id, my_val, tot);
-    if (code == 0 || (code == 1 && !a.exact_order)) {
-      if (lane < K) {
-        const float wv = my_val / tot;
-        s_ids[lane] = my_id;
-        s_wf[lane] = wv;
-        s_wb[lane] = (uint16_t)f32_to_bf16(wv);
-      }
-    } else {
+    uint32_t lb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lb[q] = ~lw[q] & 0xFFFFu;
+    if (j == 0 && a.logits_out) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a.logits_out[64 * q + lane] = (uint16_t)lb[q];
+    }
+    float p[4];
+    if (!wave_route_keys<K>(lb, lane, a.exact_order != 0, p, s_ids, s_wf, s_wb))
       route_replay_and_write(tk, p, E, K, lane, s_ids, s_wf, s_wb, nullptr);
-    }
     wave_sync();
     if (lane < K) {
       const int id = s_ids[lane];
       int rank = 0;
 #pragma unroll
-      for (int j = 0; j < K; ++j) rank += (s_ids[j] < id) ? 1 : 0;
+      for (int q = 0; q < K; ++q) rank += (s_ids[q] < id) ? 1 : 0;
       s_order[rank] = lane;              // ascending expert id (ids are distinct)
       s_w[lane] = bf16_to_f32(s_wb[lane]);
-      if (g == 0) {
+      if (j == 0) {
         if (a.ids_out) a.ids_out[lane] = id;
         if (a.w_f32_out) a.w_f32_out[lane] = s_wf[lane];
         if (a.w_bf16_out) a.w_bf16_out[lane] = s_wb[lane];
       }
     }
+  } else if (wave == 4) {
+    // meanwhile: the shared-down partial over this XCD's 64 shared activations, rows
+    // h = 64r + (lane >> 3) + 8q (published with the outputs in phase 4)
+    {
+      const uint4 v = lane < ISX / 4 ? lwait4(xr, 4 * (XW_SSH + ISX * x) + 16 * lane, err) : make_uint4(0, 0, 0, 0);
+      if (lane < ISX / 4)
+        reinterpret_cast<float4*>(s_sh)[lane] = make_float4(xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w));
+    }
+    wave_sync();
+    float sv[8];
+    {
+      const float4 u0 = *reinterpret_cast<const float4*>(s_sh + 8 * (lane & 7));
+      const float4 u1 = *reinterpret_cast<const float4*>(s_sh + 8 * (lane & 7) + 4);
+      sv[0] = u0.x; sv[1] = u0.y; sv[2] = u0.z; sv[3] = u0.w;
+      sv[4] = u1.x; sv[5] = u1.y; sv[6] = u1.z; sv[7] = u1.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float acc = dot8_bf16(sdw[q], sv);
+      acc += dpp_f32<0xB1>(acc);
+      acc += dpp_f32<0x4E>(acc);
+      acc += dpp_f32<0x141>(acc);        // sum over the 8 lanes of the row
+      if ((lane & 7) == 0) s_shp[(lane >> 3) + 8 * q] = acc;
+    }
   }
   __syncthreads();
-  const int e = s_ids[slot];
-  // phase-3 weights: down rows h = 64 blk + 2 (t >> 4) + pass of expert e; 16 lanes per row,
+  const int e = s_ids[x];
+  // phase-3 weights: down rows h = 64 r + 2 (t >> 4) + pass of expert e; 16 lanes per row,
   // lane: super-block b = l16 >> 3, 16-byte nibble chunk c = l16 & 7
   constexpr size_t drowb = (I / 256) * 144;
   uint4 dh[2], dq[2];
   {
     // routed gate/up: intermediate rows i0, i0+1 (gate and up) per wave
-    const int i0 = 16 * blk + 2 * wave;
+    const int i0 = 16 * r + 2 * wave;
     const int b = lane >> 3, c = lane & 7, gq = c >> 1, l0 = 16 * (c & 1);
     constexpr size_t rowb = (H / 256) * 144;
     const uint8_t* ebase = a.gu + (size_t)e * 2 * I * rowb;
     uint4 hdr[4], qs[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = (r & 1) ? (I + i0 + (r >> 1)) : (i0 + (r >> 1));
+    for (int q = 0; q < 4; ++q) {
+      const int row = (q & 1) ? (I + i0 + (q >> 1)) : (i0 + (q >> 1));
       const uint8_t* p = ebase + (size_t)row * rowb + (size_t)b * 144;
-      hdr[r] = *reinterpret_cast<const uint4*>(p);
-      qs[r] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
+      hdr[q] = *reinterpret_cast<const uint4*>(p);
+      qs[q] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
     }
     {
       const int db = l16 >> 3, dc = l16 & 7;
 #pragma unroll
       for (int pass = 0; pass < 2; ++pass) {
-        const int h = 64 * blk + 2 * (t >> 4) + pass;
+        const int h = 64 * r + 2 * (t >> 4) + pass;
         const uint8_t* p = a.dn + ((size_t)e * H + h) * drowb + (size_t)db * 144;
         dh[pass] = *reinterpret_cast<const uint4*>(p);
         dq[pass] = *reinterpret_cast<const uint4*>(p + 16 + 16 * dc);
@@ -382,44 +609,16 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     for (int i = 0; i < 16; ++i) { sxl += xl[i]; sxh += xh[i]; }
     float acc[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = wave_sum_f32(q4k_chunk_dot(hdr[r], qs[r], gq, xl, xh, sxl, sxh));
+    for (int q = 0; q < 4; ++q) acc[q] = wave_sum_f32(q4k_chunk_dot(hdr[q], qs[q], gq, xl, xh, sxl, sxh));
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-      if (lane == r) xstore(xb + XW_SR + slot * I + i0 + r, xenc(silu_f32(acc[2 * r]) * acc[2 * r + 1]));
-  }
-  if (wave == 4) {
-    // shared down, rows 8g..8g+7: the 512 shared activations once into LDS, then 8 lanes a row
-    uint4 sb[2];
-    {
-      const int off[2] = {4 * (XW_SSH + 8 * lane), 4 * (XW_SSH + 8 * lane) + 16};
-      xwait4<2>(xr, off, err, sb);
-    }
-    reinterpret_cast<float4*>(s_sh)[2 * lane] = make_float4(xdec(sb[0].x), xdec(sb[0].y), xdec(sb[0].z), xdec(sb[0].w));
-    reinterpret_cast<float4*>(s_sh)[2 * lane + 1] = make_float4(xdec(sb[1].x), xdec(sb[1].y), xdec(sb[1].z), xdec(sb[1].w));
-    wave_sync();
-    float acc = 0.0f;
-    const float* sp = s_sh + 64 * (lane & 7);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float sv[8];
-      const float4 u0 = *reinterpret_cast<const float4*>(sp + 8 * c);
-      const float4 u1 = *reinterpret_cast<const float4*>(sp + 8 * c + 4);
-      sv[0] = u0.x; sv[1] = u0.y; sv[2] = u0.z; sv[3] = u0.w;
-      sv[4] = u1.x; sv[5] = u1.y; sv[6] = u1.z; sv[7] = u1.w;
-      acc += dot8_bf16(sdw[c], sv);
-    }
-    acc += dpp_f32<0xB1>(acc);
-    acc += dpp_f32<0x4E>(acc);
-    acc += dpp_f32<0x141>(acc);          // sum over the 8 lanes of the row
-    if ((lane & 7) == 0) sh_raw[lane >> 3] = acc;
+    for (int q = 0; q < 2; ++q)
+      if (lane == q) lstore(xr, 4 * (XW_SR + I * x + i0 + q), xenc(silu_f32(acc[2 * q]) * acc[2 * q + 1]));
   }
 
   // ------------------------------------------------------------------------------ phase 3 --
   if (t < I / 4) {
-    const int off[1] = {4 * (XW_SR + slot * I) + 16 * t};
-    uint4 sv[1];
-    xwait4<1>(xr, off, err, sv);
-    reinterpret_cast<float4*>(s_k)[t] = make_float4(xdec(sv[0].x), xdec(sv[0].y), xdec(sv[0].z), xdec(sv[0].w));
+    const uint4 v = lwait4(xr, 4 * (XW_SR + I * x) + 16 * t, err);
+    reinterpret_cast<float4*>(s_k)[t] = make_float4(xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w));
   }
   __syncthreads();
   {
@@ -436,48 +635,74 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       const float v = row16_sum_f32(q4k_chunk_dot(dh[pass], dq[pass], gq, xl, xh, sxl, sxh));
-      if (l16 == 0) {
-        const int h = 64 * blk + 2 * (t >> 4) + pass;
-        xstore(xb + XW_Y + slot * H + h, xenc(v));
-        if (a.expert_raw) a.expert_raw[(size_t)slot * H + h] = v;
-      }
+      if (l16 == 0) s_y[2 * (t >> 4) + pass] = v;
     }
   }
+  __syncthreads();
 
   // ------------------------------------------------------------------------------ phase 4 --
-  // y[k][8g..8g+7] for the 8 slots (two 16-byte groups each) and the shared gate, polled together
-  // by lanes 0..16 of wave 0
-  if (t < 17) {
-    const int off[1] = {t < 16 ? 4 * (XW_Y + (t >> 1) * H + 8 * g) + 16 * (t & 1) : 4 * XW_GATE};
-    uint4 yv[1];
-    xwait4<1>(xr, off, err, yv);
-    if (t < 16) {
-      float* yo = &ys[t >> 1][4 * (t & 1)];
-      yo[0] = xdec(yv[0].x); yo[1] = xdec(yv[0].y); yo[2] = xdec(yv[0].z); yo[3] = xdec(yv[0].w);
-    } else {
-      s_gate = xdec(yv[0].x);
-    }
-  }
-  wave_sync();
-  if (t < 8) {
-    const int h = 8 * g + t;
-    float acc = 0.0f;
+  // wave 1 publishes the 64 outputs and shared partials (agent scope), wave 0 collects its
+  // combine rows, waves 4-7 warm the next layer's weights: the wave that polls has no store of
+  // its own in flight (a wait on a load also waits for the older stores' acknowledgements)
+  if (wave == 1) {
+    const float v = s_y[lane];
+    xstore(xb + XW_Y + H * x + 64 * r + lane, xenc(v));
+    xstore(xb + XW_SHP + H * x + 64 * r + lane, xenc(s_shp[lane]));
+    if (a.expert_raw) a.expert_raw[(size_t)x * H + 64 * r + lane] = v;
+  } else if (wave >= 4) {
+    if (a.nx_router) {
+      // warm XCD x's L2 with what role (x, r) reads first in the next layer
+      const int u = t - 256;
+      uint32_t acc = 0;
+      const uint4* nr = reinterpret_cast<const uint4*>(a.nx_router + (size_t)8 * r * H);
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-      const int k = s_order[j];
-      acc += s_w[k] * ys[k][t];
+      for (int q = 0; q < 8; ++q) acc ^= xor4(nr[u + 256 * q]);
+      const int i0 = ISX * x + 2 * r;
+      const uint4* ng = reinterpret_cast<const uint4*>(a.nx_sg + (size_t)i0 * H);
+      const uint4* nu = reinterpret_cast<const uint4*>(a.nx_su + (size_t)i0 * H);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) acc ^= xor4(ng[u + 256 * q]) ^ xor4(nu[u + 256 * q]);
+      acc ^= xor4(reinterpret_cast<const uint4*>(a.nx_ssg)[u]);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int row = 64 * r + ((u + 256 * q) >> 3), cc = (u + 256 * q) & 7;
+        acc ^= xor4(*reinterpret_cast<const uint4*>(a.nx_sd + (size_t)row * IS + ISX * x + 8 * cc));
+      }
+      if (acc == 0x9E3779B9u && a.nx_ssg == reinterpret_cast<const uint16_t*>(a.sync)) atomicOr(err, 0);
     }
-    const float sh = s_gate * sh_raw[t];
-    if (a.routed_sum) a.routed_sum[h] = acc;
-    if (a.shared_out) a.shared_out[h] = sh;
-    a.out[h] = resid + acc + sh;
-  }
-  // the last workgroup out advances the epoch for the next launch
-  if (t == 0) {
-    const int arrived = __hip_atomic_fetch_add(a.sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (arrived == kG - 1) {
-      __hip_atomic_store(a.sync + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(a.sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the next launch's exchange words (its epoch parity), cleared last: nothing here waits on them
+    if (t - 256 < kClearPerWg && kClearPerWg * j + t - 256 < XW_BUF) xstore(xn + kClearPerWg * j + t - 256, 0u);
+  } else if (wave == 0) {
+    // y[k][8j..8j+7] for the 8 slots and the 8 XCDs' shared partials (two 16-byte groups each)
+    if (t < 32) {
+      const int k = t >> 2, kind = (t >> 1) & 1, half = t & 1;
+      const uint4 v = xwait4(xr, 4 * ((kind ? XW_SHP : XW_Y) + H * k + 8 * j) + 16 * half, err);
+      float* o = &s_comb[kind][k][4 * half];
+      o[0] = xdec(v.x); o[1] = xdec(v.y); o[2] = xdec(v.z); o[3] = xdec(v.w);
+    }
+    wave_sync();
+    if (t < 8) {
+      const int h = 8 * j + t;
+      float acc = 0.0f;
+#pragma unroll
+      for (int q = 0; q < K; ++q) {
+        const int k = s_order[q];
+        acc += s_w[k] * s_comb[0][k][t];
+      }
+      float shr = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kXcd; ++q) shr += s_comb[1][q][t];
+      const float sh = s_gate * shr;
+      if (a.routed_sum) a.routed_sum[h] = acc;
+      if (a.shared_out) a.shared_out[h] = sh;
+      a.out[h] = resid + acc + sh;
+    }
+    // this CU's (or, without a table, this role's) launch count for the next launch
+    if (t == 0) {
+      if (s_role[3] >= 0)
+        astore(a.sync + kCuTable + 64 * x + s_role[3], (int)((epoch << 8) | (uint32_t)(r + 1)));
+      else
+        astore(a.sync + kRoleEpoch + kPer * x + r, (int)epoch);
     }
   }
 }
@@ -494,11 +719,22 @@ bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, 
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       ncu = 0;
   }
-  return ncu >= kG && H == 2048 && I == 512 && E == 256 && K == 8 && Is == 512 &&
-         gu_fmt == MOE_FMT_Q4_K && dn_fmt == MOE_FMT_Q4_K;
+  // 8 XCDs with at least 32 CUs each (MI355X: exactly 32)
+  return ncu >= kG && ncu % kXcd == 0 && H == 2048 && I == 512 && E == 256 && K == 8 &&
+         Is == 512 && gu_fmt == MOE_FMT_Q4_K && dn_fmt == MOE_FMT_Q4_K;
 }
 
 size_t moe_layer_exchange_bytes() { return (size_t)2 * XW_BUF * 4; }
+
+int moe_launch_cu_probe(int* sync, hipStream_t st) {
+  int dev = 0, ncu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return moe_set_error(MOE_E_HIP, "cu_probe: device query failed");
+  if (ncu < kG) return MOE_OK;          // the single-launch layer does not run here
+  hipLaunchKernelGGL(k_cu_probe, dim3(kG), dim3(64), 0, st, sync);
+  return moe_check_launch("cu_probe");
+}
 
 int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st) {
   LayerArgs a;
@@ -513,6 +749,12 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   a.exact_order = (L.ids_out_requested || L.expert_raw) ? 1 : 0;
   a.norm_w = L.norm_w;
   a.norm_eps = L.norm_eps;
+  const bool nx = L.nx_router && L.nx_sg && L.nx_su && L.nx_sd && L.nx_ssg;
+  a.nx_router = nx ? (const uint16_t*)L.nx_router : nullptr;
+  a.nx_sg = nx ? (const uint16_t*)L.nx_sg : nullptr;
+  a.nx_su = nx ? (const uint16_t*)L.nx_su : nullptr;
+  a.nx_sd = nx ? (const uint16_t*)L.nx_sd : nullptr;
+  a.nx_ssg = nx ? (const uint16_t*)L.nx_ssg : nullptr;
   if (L.x_dtype == MOE_DT_F32)
     hipLaunchKernelGGL(k_dec_layer<MOE_DT_F32>, dim3(kG), dim3(kThreads), 0, st, a);
   else

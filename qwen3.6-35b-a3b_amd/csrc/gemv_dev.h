@@ -34,20 +34,43 @@ __device__ __forceinline__ void load_x32(const void* x, size_t off, float* xl, f
   }
 }
 
-// partial dot of one lane's 16-byte Q4_K chunk with its 32 activations
+// v & mask, opaque to the optimizer: it would otherwise fold the mask into each later byte
+// extraction (v_bfe_u32 + v_cvt_f32_ubyte0 per value instead of one v_cvt_f32_ubyteN)
+__device__ __forceinline__ uint32_t and_opaque(uint32_t v, uint32_t mask) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "s"(mask));
+  return r;
+}
+
+// partial dot of one lane's 16-byte Q4_K chunk with its 32 activations: chunk g (0..3) of a
+// super-block holds sub-blocks 2g (low nibbles) and 2g+1 (high nibbles). The nibbles are masked
+// four at a time and converted by byte (v_cvt_f32_ubyte0..3: one instruction per value); the
+// 6-bit scales of get_scale_min_k4 (tools/gguf_reader.py:165-175) are extracted without branches.
 __device__ __forceinline__ float q4k_chunk_dot(uint4 hdr, uint4 qs, int g, const float* xl,
                                                const float* xh, float sxl, float sxh) {
   const float d = f16_to_f32(hdr.x & 0xFFFFu), dmin = f16_to_f32(hdr.x >> 16);
-  uint32_t sc0, m0, sc1, m1;
-  q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g, sc0, m0);
-  q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g + 1, sc1, m1);
+  // sub-blocks j = 2g + h, byte b = j & 3 of the 12 scale bytes s0 = hdr.y, s1 = hdr.z, s2 = hdr.w
+  const uint32_t sh0 = 16u * (uint32_t)(g & 1), sh1 = sh0 + 8u;
+  const bool lowj = g < 2;               // sub-blocks 0..3: plain 6-bit fields
+  const uint32_t y0 = hdr.y >> sh0, z0 = hdr.z >> sh0, w0 = hdr.w >> sh0;
+  const uint32_t y1 = hdr.y >> sh1, z1 = hdr.z >> sh1, w1 = hdr.w >> sh1;
+  const uint32_t sc0 = lowj ? (y0 & 63u) : ((w0 & 15u) | ((y0 >> 2) & 48u));
+  const uint32_t m0 = lowj ? (z0 & 63u) : (((w0 >> 4) & 15u) | ((z0 >> 2) & 48u));
+  const uint32_t sc1 = lowj ? (y1 & 63u) : ((w1 & 15u) | ((y1 >> 2) & 48u));
+  const uint32_t m1 = lowj ? (z1 & 63u) : (((w1 >> 4) & 15u) | ((z1 >> 2) & 48u));
   const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
   float dl = 0.0f, dh = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-    dl = fmaf(xl[i], (float)(byte & 15u), dl);
-    dh = fmaf(xh[i], (float)(byte >> 4), dh);
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = and_opaque(w[i], 0x0F0F0F0Fu), hi = and_opaque(w[i] >> 4, 0x0F0F0F0Fu);
+    dl = fmaf(xl[4 * i], (float)(lo & 0xFFu), dl);
+    dh = fmaf(xh[4 * i], (float)(hi & 0xFFu), dh);
+    dl = fmaf(xl[4 * i + 1], (float)((lo >> 8) & 0xFFu), dl);
+    dh = fmaf(xh[4 * i + 1], (float)((hi >> 8) & 0xFFu), dh);
+    dl = fmaf(xl[4 * i + 2], (float)((lo >> 16) & 0xFFu), dl);
+    dh = fmaf(xh[4 * i + 2], (float)((hi >> 16) & 0xFFu), dh);
+    dl = fmaf(xl[4 * i + 3], (float)(lo >> 24), dl);
+    dh = fmaf(xh[4 * i + 3], (float)(hi >> 24), dh);
   }
   return d * ((float)sc0 * dl + (float)sc1 * dh) - dmin * ((float)m0 * sxl + (float)m1 * sxh);
 }

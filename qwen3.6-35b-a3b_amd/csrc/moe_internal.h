@@ -108,6 +108,9 @@ struct MoeDecodeLaunch {
   int ids_out_requested;   // the caller asked for topk_ids / weights: keep torch's slot order
   const float* norm_w;     // post-attention RMSNorm weight [H] f32, or NULL (x is the input)
   float norm_eps;
+  // the next layer's routing-independent weights (single-launch layer's L2 warm-up), or NULL
+  const void *nx_router = nullptr, *nx_sg = nullptr, *nx_su = nullptr, *nx_sd = nullptr,
+             *nx_ssg = nullptr;
 };
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
 // xn[T,H] f32 = (x * f32(1/sqrt(mean_f64(x^2) + eps))) * w   (norm.hip)
@@ -116,13 +119,17 @@ int moe_launch_rmsnorm(const void* x, int x_dtype, int T, int H, const float* w,
 int moe_launch_zero_words(int* p, int n, hipStream_t st);
 
 // The first kSyncBytes of every workspace hold the library's device-side sync words (block
-// tickets, the decode layer's epoch and arrival counter, its two exchange buffers). They
-// must be zero before the first call (moe_workspace_init); calls keep them consistent.
-constexpr size_t kSyncBytes = 262144;
+// tickets, the decode layer's epoch, arrival counter and per-XCD tickets, its two exchange
+// buffers). They must be zero before the first call (moe_workspace_init); calls keep them
+// consistent.
+constexpr size_t kSyncBytes = 524288;
 // single-launch decode layer (decode_layer.hip): 256 co-resident workgroups, model geometry only
 bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, int dn_fmt);
 size_t moe_layer_exchange_bytes();
 int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st);
+// records this device's CU layout (rank of each CU inside its XCD) into the sync words; part of
+// moe_workspace_init (no-op on devices where the single-launch layer does not run)
+int moe_launch_cu_probe(int* sync, hipStream_t st);
 
 // workspace carving
 struct MoeWs {

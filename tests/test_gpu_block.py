@@ -246,3 +246,23 @@ def test_batched_with_post_attention_norm(pkg, layer_zipf, dev, path):
     st = pkg.abi.block_forward(x1, lw, path=path, stages={"topk_ids"}, residual=x1, norm_w=w)
     assert torch.equal(st["topk_ids"].cpu().long(), ref["topk_ids"]), path
     assert_close(st["combined_out"].cpu() - x1.cpu(), ref["combined_out"], f"norm path {path}")
+
+
+def test_decode_next_layer_hint_same_bits(pkg, layer_c0, layer_zipf, dev):
+    """moe_block_forward_prefetch (the next layer's routing-independent weights warmed into the
+    L2 of the XCD that reads them first) gives the same bits as moe_block_forward, through a
+    two-layer chain h <- h + MoE(rmsnorm(h)) run for several tokens."""
+    lw0, _ = layer_c0
+    lw1, _ = layer_zipf
+    layers = [(lw0, _norm_weight(51, 2048, dev)), (lw1, _norm_weight(52, 2048, dev))]
+    x = pkg.synth.make_input(1, seed=51, device=dev)
+    a, b = x.clone(), x.clone()
+    for step in range(6):
+        for l, (lw, w) in enumerate(layers):
+            nxt = layers[(l + 1) % 2][0]
+            pkg.abi.block_forward(a, lw, out=a, residual=a, norm_w=w)
+            pkg.abi.block_forward(b, lw, out=b, residual=b, norm_w=w, next_layer=nxt)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), step
+        assert torch.isfinite(a).all()
+    assert pkg.abi.device_error_bits(dev) == 0
