@@ -218,7 +218,8 @@ def pmc_workload(pkg, torch, dev, L: int) -> None:
     x = synth.make_input(1, seed=0, device=dev)
     for _ in range(4):
         for l, (lw, nw) in enumerate(zip(layers, norms)):
-            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw, next_layer=layers[(l + 1) % L])
+            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw, next_layer=layers[(l + 1) % L],
+                              next_norm_w=norms[(l + 1) % L])
         x.copy_(synth.rms_normalize(x))
     torch.cuda.synchronize()
     del layers
@@ -240,7 +241,8 @@ def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> floa
     def layer_launches():
         for l, lw in enumerate(layers):
             abi.block_forward(xs[l:l + 1], lw, out=ys[l:l + 1], residual=xs[l:l + 1],
-                              norm_w=norms[l], next_layer=layers[(l + 1) % L])
+                              norm_w=norms[l], next_layer=layers[(l + 1) % L],
+                              next_norm_w=norms[(l + 1) % L])
 
     layer_launches()
     torch.cuda.synchronize()
@@ -320,7 +322,7 @@ def main():
         # names the next layer so its routing-independent weights are warmed into L2
         for l, (lw, nw) in enumerate(zip(layers, norms)):
             abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw,
-                              next_layer=layers[(l + 1) % L])
+                              next_layer=layers[(l + 1) % L], next_norm_w=norms[(l + 1) % L])
         xbuf.copy_(synth.rms_normalize(xbuf))
 
     for _ in range(3):

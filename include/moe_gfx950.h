@@ -137,12 +137,14 @@ int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, in
                       void *ws, size_t ws_bytes, void *stream);
 
 /* The routing-independent weights of the layer that the same stream runs next (its router, its
- * shared expert and the shared expert's scalar gate; shapes as in moe_block_forward). */
+ * shared expert and the shared expert's scalar gate, its post-attention norm weight; shapes as in
+ * moe_block_forward). */
 typedef struct moe_next_layer {
   const void *w_router;         /* [E,H] bf16 */
   const void *ws_gate, *ws_up;  /* [I_s,H] bf16 */
   const void *ws_down;          /* [H,I_s] bf16 */
   const void *ws_scalar_gate;   /* [H] bf16 */
+  const float *norm_w;          /* [H] f32, or NULL when the next call passes no norm weight */
 } moe_next_layer;
 
 /* moe_block_forward with a hint: `next` (may be NULL) names the next layer's routing-independent

@@ -194,15 +194,15 @@ def combine(y: torch.Tensor, grouping: dict, ids: torch.Tensor, w_bf16: torch.Te
 def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False,
                   out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
                   norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
-                  next_layer=None) -> dict:
+                  next_layer=None, next_norm_w: torch.Tensor | None = None) -> dict:
     """The whole block in one library call (moe_block_forward). `lw` is a LayerWeights;
     `stages` is False, True (every stage output) or a set of stage names to return;
     out = residual + MoE(input) when `residual` (f32 [T,H], may be `out` or `x` itself) is given.
     input = x, or the post-attention RMSNorm of x when `norm_w` (f32 [H], the artifact's 1+w) is
     given: engine/m3_forward.py:732-737 is then block_forward(x1, lw, norm_w=w, residual=x1).
-    `next_layer` (a LayerWeights, optional) is the layer this stream runs next: its
-    routing-independent weights are warmed into L2 by the single-launch decode layer
-    (moe_block_forward_prefetch); results do not depend on it."""
+    `next_layer` (a LayerWeights, optional) is the layer this stream runs next and `next_norm_w`
+    its norm weight: their routing-independent weights are warmed into L2 by the single-launch
+    decode layer (moe_block_forward_prefetch); results do not depend on them."""
     _need(x, "x")
     T, H = x.shape
     if norm_w is not None:
@@ -239,8 +239,11 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
                         ("next shared_up", nl.shared_up), ("next shared_down", nl.shared_down),
                         ("next shared_scalar_gate", nl.shared_scalar_gate)):
             _need(t, name, device=dev)
+        if next_norm_w is not None:
+            _need(next_norm_w, "next_norm_w", torch.float32, (H,), dev)
         hint = L.NextLayer(nl.router.data_ptr(), nl.shared_gate.data_ptr(), nl.shared_up.data_ptr(),
-                           nl.shared_down.data_ptr(), nl.shared_scalar_gate.data_ptr())
+                           nl.shared_down.data_ptr(), nl.shared_scalar_gate.data_ptr(),
+                           None if next_norm_w is None else next_norm_w.data_ptr())
         _check(L.lib.moe_block_forward_prefetch(*args, ctypes.byref(hint)), "block_forward")
     st["combined_out"] = out
     return st

@@ -320,7 +320,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     L.norm_eps = norm_eps;
     if (next) {
       L.nx_router = next->w_router; L.nx_sg = next->ws_gate; L.nx_su = next->ws_up;
-      L.nx_sd = next->ws_down; L.nx_ssg = next->ws_scalar_gate;
+      L.nx_sd = next->ws_down; L.nx_ssg = next->ws_scalar_gate; L.nx_norm = next->norm_w;
     }
     if (!L.logits || !L.ids || !L.w_f32 || !L.w_bf16 || !L.s_shared || !L.gate_prob || !L.shared_raw || !L.s_routed)
       return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");

@@ -93,6 +93,7 @@ struct LayerArgs {
   const uint16_t* nx_su;
   const uint16_t* nx_sd;
   const uint16_t* nx_ssg;
+  const float* nx_norm;                 // the next layer's norm weight, or NULL
 };
 
 // exchange buffer layout (uint32 words; every region starts 16-byte aligned)
@@ -352,8 +353,6 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ TopkLds tk;                 // the exact replay's scratch (ties only)
   __shared__ float s_k[I];               // routed activations of this XCD's slot
   __shared__ float s_sh[ISX];            // shared activations of this XCD's slice
-  __shared__ float s_y[64];              // this workgroup's 64 down-projection outputs
-  __shared__ float s_shp[64];            // and its 64 shared-down partials
   __shared__ int s_ids[K];
   __shared__ float s_w[K];
   __shared__ float s_wf[K];
@@ -414,23 +413,24 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   const int j = kPer * x + r;            // combine rows [8j, 8j+8)
 
   // ------------------------------------------------------------------ start: loads, x, norm --
-  // routing-independent weights: router row 8r + wave; shared gate and up rows i = 64x + 2r + wave
-  // (waves 0-1); the scalar gate row (wave 2); shared-down rows 64r + (lane >> 3) + 8q, cols
-  // 64x + 8 (lane & 7) .. +8 (wave 4, used while wave 0 selects the experts)
+  // routing-independent weights: router row 8r + wave; shared gate and up rows
+  // i = 64x + 2r + (wave - 5) (waves 5-6); the scalar gate row (wave 7); shared-down rows
+  // 64r + (lane >> 3) + 8q, cols 64x + 8 (lane & 7) .. +8 (wave 4, used while wave 0 selects the
+  // experts). Wave 0, which polls the logits, carries none of the extras.
   uint4 wr4[4], sgw[4], suw[4], sdw[8];
   const float bias_e = a.bias ? a.bias[8 * r + wave] : 0.0f;
   {
     const uint16_t* wr = a.w_router + (size_t)(8 * r + wave) * H;
 #pragma unroll
     for (int c = 0; c < 4; ++c) wr4[c] = *reinterpret_cast<const uint4*>(wr + 512 * c + 8 * lane);
-    if (wave < 2) {
-      const int i = ISX * x + 2 * r + wave;
+    if (wave == 5 || wave == 6) {
+      const int i = ISX * x + 2 * r + (wave - 5);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         sgw[c] = *reinterpret_cast<const uint4*>(a.sg + (size_t)i * H + 512 * c + 8 * lane);
         suw[c] = *reinterpret_cast<const uint4*>(a.su + (size_t)i * H + 512 * c + 8 * lane);
       }
-    } else if (wave == 2) {
+    } else if (wave == 7) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) sgw[c] = *reinterpret_cast<const uint4*>(a.ssg + 512 * c + 8 * lane);
     } else if (wave == 4) {
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     const int e = 8 * r + wave;
     const uint32_t bits = router_row_bits(wr4, xv, (double)bias_e, xl1);
     if (lane == 0) lstore(xr, 4 * (XW_LOG + 256 * x + e), ~bits);
-    if (wave < 2) {
+    if (wave == 5 || wave == 6) {
       float ag = 0.0f, au = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -486,8 +486,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       }
       ag = wave_sum_f32(ag);
       au = wave_sum_f32(au);
-      if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + wave), xenc(silu_f32(ag) * au));
-    } else if (wave == 2) {
+      if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + (wave - 5)), xenc(silu_f32(ag) * au));
+    } else if (wave == 7) {
       float gs = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) gs += dot8_bf16(sgw[c], xv[c]);
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     }
   } else if (wave == 4) {
     // meanwhile: the shared-down partial over this XCD's 64 shared activations, rows
-    // h = 64r + (lane >> 3) + 8q (published with the outputs in phase 4)
+    // h = 64r + (lane >> 3) + 8q, published to the combining workgroups (agent scope)
     {
       const uint4 v = lane < ISX / 4 ? lwait4(xr, 4 * (XW_SSH + ISX * x) + 16 * lane, err) : make_uint4(0, 0, 0, 0);
       if (lane < ISX / 4)
@@ -560,7 +560,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       acc += dpp_f32<0xB1>(acc);
       acc += dpp_f32<0x4E>(acc);
       acc += dpp_f32<0x141>(acc);        // sum over the 8 lanes of the row
-      if ((lane & 7) == 0) s_shp[(lane >> 3) + 8 * q] = acc;
+      if ((lane & 7) == 0) xstore(xb + XW_SHP + H * x + 64 * r + (lane >> 3) + 8 * q, xenc(acc));
     }
   }
   __syncthreads();
@@ -635,21 +635,18 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       const float v = row16_sum_f32(q4k_chunk_dot(dh[pass], dq[pass], gq, xl, xh, sxl, sxh));
-      if (l16 == 0) s_y[2 * (t >> 4) + pass] = v;
+      if (l16 == 0) {
+        const int h = 64 * r + 2 * (t >> 4) + pass;
+        xstore(xb + XW_Y + H * x + h, xenc(v));
+        if (a.expert_raw) a.expert_raw[(size_t)x * H + h] = v;
+      }
     }
   }
-  __syncthreads();
 
   // ------------------------------------------------------------------------------ phase 4 --
-  // wave 1 publishes the 64 outputs and shared partials (agent scope), wave 0 collects its
-  // combine rows, waves 4-7 warm the next layer's weights: the wave that polls has no store of
-  // its own in flight (a wait on a load also waits for the older stores' acknowledgements)
-  if (wave == 1) {
-    const float v = s_y[lane];
-    xstore(xb + XW_Y + H * x + 64 * r + lane, xenc(v));
-    xstore(xb + XW_SHP + H * x + 64 * r + lane, xenc(s_shp[lane]));
-    if (a.expert_raw) a.expert_raw[(size_t)x * H + 64 * r + lane] = v;
-  } else if (wave >= 4) {
+  // wave 0 collects its combine rows, waves 4-7 warm the next layer's weights and clear the next
+  // launch's exchange words
+  if (wave >= 4) {
     if (a.nx_router) {
       // warm XCD x's L2 with what role (x, r) reads first in the next layer
       const int u = t - 256;
@@ -663,6 +660,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) acc ^= xor4(ng[u + 256 * q]) ^ xor4(nu[u + 256 * q]);
       acc ^= xor4(reinterpret_cast<const uint4*>(a.nx_ssg)[u]);
+      if (a.nx_norm) {
+        const uint4* nn = reinterpret_cast<const uint4*>(a.nx_norm);
+        acc ^= xor4(nn[u]) ^ xor4(nn[u + 256]);
+      }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int row = 64 * r + ((u + 256 * q) >> 3), cc = (u + 256 * q) & 7;
@@ -755,6 +756,7 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   a.nx_su = nx ? (const uint16_t*)L.nx_su : nullptr;
   a.nx_sd = nx ? (const uint16_t*)L.nx_sd : nullptr;
   a.nx_ssg = nx ? (const uint16_t*)L.nx_ssg : nullptr;
+  a.nx_norm = nx ? L.nx_norm : nullptr;
   if (L.x_dtype == MOE_DT_F32)
     hipLaunchKernelGGL(k_dec_layer<MOE_DT_F32>, dim3(kG), dim3(kThreads), 0, st, a);
   else

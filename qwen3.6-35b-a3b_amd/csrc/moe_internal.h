@@ -111,6 +111,7 @@ struct MoeDecodeLaunch {
   // the next layer's routing-independent weights (single-launch layer's L2 warm-up), or NULL
   const void *nx_router = nullptr, *nx_sg = nullptr, *nx_su = nullptr, *nx_sd = nullptr,
              *nx_ssg = nullptr;
+  const float* nx_norm = nullptr;
 };
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
 // xn[T,H] f32 = (x * f32(1/sqrt(mean_f64(x^2) + eps))) * w   (norm.hip)

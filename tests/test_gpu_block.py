@@ -259,9 +259,10 @@ def test_decode_next_layer_hint_same_bits(pkg, layer_c0, layer_zipf, dev):
     a, b = x.clone(), x.clone()
     for step in range(6):
         for l, (lw, w) in enumerate(layers):
-            nxt = layers[(l + 1) % 2][0]
+            nxt, nxt_w = layers[(l + 1) % 2]
             pkg.abi.block_forward(a, lw, out=a, residual=a, norm_w=w)
-            pkg.abi.block_forward(b, lw, out=b, residual=b, norm_w=w, next_layer=nxt)
+            pkg.abi.block_forward(b, lw, out=b, residual=b, norm_w=w, next_layer=nxt,
+                                  next_norm_w=nxt_w if step % 2 else None)
         torch.cuda.synchronize()
         assert torch.equal(a, b), step
         assert torch.isfinite(a).all()
