@@ -65,10 +65,14 @@ def parse():
     ap.add_argument("--no-c2", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill timing (what the prefill profile covers)")
+    ap.add_argument("--c2-only", action="store_true",
+                    help="only the config-2 batched-decode timing (what the c2 profile covers)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing (what the kernel-trace profile covers)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--pmc", action="store_true")
+    ap.add_argument("--no-hint", action="store_true",
+                    help="call moe_block_forward (no next-layer L2 warm-up) in the decode runs")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("DIR_FETCH", "DIR_WRITE"))
     ap.add_argument("--stats-summary", nargs="+", metavar="DIR [CMD]")
     return ap.parse_args()
@@ -210,7 +214,7 @@ def committed_traffic():
 
 
 # ------------------------------------------------------------------------------------ workloads --
-def pmc_workload(pkg, torch, dev, L: int) -> None:
+def pmc_workload(pkg, torch, dev, L: int, hint: bool) -> None:
     """What the PMC passes profile: 4 tokens through L decode layers (eager), then the copy."""
     synth, abi = pkg.synth, pkg.abi
     layers = [synth.make_layer(seed=1000 + l, device=dev) for l in range(L)]
@@ -218,8 +222,9 @@ def pmc_workload(pkg, torch, dev, L: int) -> None:
     x = synth.make_input(1, seed=0, device=dev)
     for _ in range(4):
         for l, (lw, nw) in enumerate(zip(layers, norms)):
-            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw, next_layer=layers[(l + 1) % L],
-                              next_norm_w=norms[(l + 1) % L])
+            abi.block_forward(x, lw, out=x, residual=x, norm_w=nw,
+                              next_layer=layers[(l + 1) % L] if hint else None,
+                              next_norm_w=norms[(l + 1) % L] if hint else None)
         x.copy_(synth.rms_normalize(x))
     torch.cuda.synchronize()
     del layers
@@ -230,7 +235,7 @@ def pmc_workload(pkg, torch, dev, L: int) -> None:
     log(f"pmc workload done: {4 * L} decode-layer launches, one {COPY_MIB} MiB elementwise copy")
 
 
-def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> float:
+def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int, hint: bool = True) -> float:
     """Average launch period of the single-launch decode layer (norm fused, as in the decode
     chain): a graph of len(layers) back-to-back launches on independent inputs, replayed `reps`
     times, HIP events on the stream the graph runs on."""
@@ -241,8 +246,8 @@ def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> floa
     def layer_launches():
         for l, lw in enumerate(layers):
             abi.block_forward(xs[l:l + 1], lw, out=ys[l:l + 1], residual=xs[l:l + 1],
-                              norm_w=norms[l], next_layer=layers[(l + 1) % L],
-                              next_norm_w=norms[(l + 1) % L])
+                              norm_w=norms[l], next_layer=layers[(l + 1) % L] if hint else None,
+                              next_norm_w=norms[(l + 1) % L] if hint else None)
 
     layer_launches()
     torch.cuda.synchronize()
@@ -251,6 +256,26 @@ def dominant_kernel_ms(torch, synth, abi, layers, norms, dev, reps: int) -> floa
         gk.replay()
     torch.cuda.synchronize()
     return time_stream(gk.replay, reps, torch) / L
+
+
+def c2_step(torch, synth, abi, dev, reps: int) -> dict:
+    """Config 2: one block over T = 64 tokens with Zipf-skewed routing, captured in a HIP graph;
+    HBM rate over the unique experts the step hits (each read once) plus the shared expert."""
+    lz = synth.make_layer(seed=1, device=dev, zipf=True)
+    xz = synth.make_input(64, seed=1, device=dev)
+    oz = torch.empty_like(xz)
+    r = abi.router_topk(xz, lz.router, lz.top_k, bias=lz.router_bias)
+    uniq = int(torch.unique(r["topk_ids"]).numel())
+    for _ in range(3):
+        abi.block_forward(xz, lz, out=oz)
+    torch.cuda.synchronize()
+    gz = capture(torch, lambda: abi.block_forward(xz, lz, out=oz))
+    ms_z = time_stream(gz.replay, reps, torch)
+    bytes_z = uniq * lz.routed_bytes_per_expert() + lz.shared_bytes()
+    out = {"c2_us_per_step": round(ms_z * 1000, 2), "c2_unique_experts": uniq,
+           "c2_gbps": round(bytes_z / (ms_z * 1e-3) / 1e9, 1)}
+    log(f"c2 T=64 zipf: {ms_z * 1000:.1f} us/step, {uniq} unique experts, {out['c2_gbps']:.0f} GB/s")
+    return out
 
 
 def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
@@ -291,7 +316,11 @@ def main():
     synth, abi = pkg.synth, pkg.abi
     L = args.layers
     if args.pmc:
-        pmc_workload(pkg, torch, dev, L)
+        pmc_workload(pkg, torch, dev, L, not args.no_hint)
+        return
+
+    if args.c2_only:
+        print(json.dumps(c2_step(torch, synth, abi, dev, 50)), flush=True)
         return
 
     if args.prefill_only:
@@ -309,7 +338,8 @@ def main():
     active = synth.decode_active_bytes(layers[0])
     if args.kernel_only:
         norms = [synth.make_norm_weight(seed=5000 + l, device=dev) for l in range(L)]
-        ms_k = dominant_kernel_ms(torch, synth, abi, layers, norms, dev, args.kernel_reps)
+        ms_k = dominant_kernel_ms(torch, synth, abi, layers, norms, dev, args.kernel_reps,
+                                  not args.no_hint)
         log(f"{DECODE_KERNEL}: {ms_k * 1000:.2f} us per launch (graph of {L} launches), "
             f"{active / (ms_k * 1e-3) / 1e9:.0f} GB/s on {active} B")
         return
@@ -322,7 +352,8 @@ def main():
         # names the next layer so its routing-independent weights are warmed into L2
         for l, (lw, nw) in enumerate(zip(layers, norms)):
             abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw,
-                              next_layer=layers[(l + 1) % L], next_norm_w=norms[(l + 1) % L])
+                              next_layer=None if args.no_hint else layers[(l + 1) % L],
+                              next_norm_w=None if args.no_hint else norms[(l + 1) % L])
         xbuf.copy_(synth.rms_normalize(xbuf))
 
     for _ in range(3):
@@ -338,7 +369,8 @@ def main():
     log(f"decode: {ms:.3f} ms/token over {L} layers = {us_tok_layer:.2f} us/token/layer, "
         f"{gbps:.0f} GB/s on {active} active B/token-layer")
 
-    ms_k = dominant_kernel_ms(torch, synth, abi, layers, norms, dev, args.kernel_reps)
+    ms_k = dominant_kernel_ms(torch, synth, abi, layers, norms, dev, args.kernel_reps,
+                              not args.no_hint)
     kern_gbps = active / (ms_k * 1e-3) / 1e9
     traffic = committed_traffic()
     log(f"{DECODE_KERNEL}: {ms_k * 1000:.2f} us per launch (graph of {L} launches), "
@@ -348,24 +380,7 @@ def main():
         log(f"WARNING: device error bits {err_bits:#x} (a bounded spin timed out)")
 
     # ---------------------------------------------------------------- batched decode, config 2
-    c2 = {}
-    if not args.no_c2:
-        lz = synth.make_layer(seed=1, device=dev, zipf=True)
-        xz = synth.make_input(64, seed=1, device=dev)
-        oz = torch.empty_like(xz)
-        r = abi.router_topk(xz, lz.router, lz.top_k, bias=lz.router_bias)
-        uniq = int(torch.unique(r["topk_ids"]).numel())
-        for _ in range(3):
-            abi.block_forward(xz, lz, out=oz)
-        torch.cuda.synchronize()
-        gz = capture(torch, lambda: abi.block_forward(xz, lz, out=oz))
-        ms_z = time_stream(gz.replay, 50, torch)
-        bytes_z = uniq * lz.routed_bytes_per_expert() + lz.shared_bytes()
-        c2 = {"c2_us_per_step": round(ms_z * 1000, 2), "c2_unique_experts": uniq,
-              "c2_gbps": round(bytes_z / (ms_z * 1e-3) / 1e9, 1)}
-        log(f"c2 T=64 zipf: {ms_z * 1000:.1f} us/step, {uniq} unique experts, "
-            f"{c2['c2_gbps']:.0f} GB/s")
-        del lz
+    c2 = c2_step(torch, synth, abi, dev, 50) if not args.no_c2 else {}
 
     # ---------------------------------------------------------------- prefill, config 3
     prefill = {}

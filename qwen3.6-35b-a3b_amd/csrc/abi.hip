@@ -153,9 +153,9 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
   const size_t gu_row = gu_fmt == MOE_FMT_Q4_K ? (size_t)H / 256 * 144 : gu_fmt == MOE_FMT_Q6_K ? (size_t)H / 256 * 210 : (size_t)H * 2;
   const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
   const uint8_t* g = reinterpret_cast<const uint8_t*>(gu);
-  const bool v2 = path == MOE_PATH_MFMA && moe_gemm2_supports(gu_fmt) && moe_gemm2_supports(dn_fmt) &&
+  const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_supports(dn_fmt) &&
                   H % 256 == 0 && I % 256 == 0;
-  const int bm = v2 ? MOE_GEMM2_BM : MOE_GEMM_BM;
+  const int bm = v2 ? MOE_GEMM3_BM : MOE_GEMM_BM;
   const int max_tiles = moe_max_mtiles(P, E, bm);
   int32_t* tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
   uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
@@ -168,8 +168,14 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
       MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
       x16 = c;
     }
-    MOE_TRY(moe_launch_gemm3_gateup(x16, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
-                                    max_tiles, T, offsets, sorted_pairs, K, H, I, S, st));
+    if (gu_fmt == MOE_FMT_Q4_K)
+      MOE_TRY(moe_launch_gemm4_gateup(x16, g, g + (size_t)I * gu_row, 2 * (size_t)I * gu_row, tiles,
+                                      max_tiles, offsets, sorted_pairs, K, H, I, S, st));
+    else
+      MOE_TRY(moe_launch_gemm3_gateup(x16, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
+                                      max_tiles, T, offsets, sorted_pairs, K, H, I, S, st));
+    if (dn_fmt == MOE_FMT_Q4_K)
+      return moe_launch_gemm4_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, st);
     return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, st);
   }
   const int opb = path == MOE_PATH_MFMA_BF16;

@@ -1,17 +1,20 @@
 // Prefill-path grouped GEMM, warp-specialized form (gfx950, v_mfma_f32_32x32x16_f16, f32 acc).
 //
-// Work: one tile of up to 128 sorted (token, slot) rows of one expert (k_build_tiles, 128-row
-// tiles) times one output slab per block, in the XCD-aware order of gemm2.hip. Block = 8 waves,
+// Work: one tile of up to 160 sorted (token, slot) rows of one expert (k_build_tiles, 160-row
+// tiles: at 4096 tokens an expert averages 128 rows, so almost every expert is one tile and its
+// weights are loaded and decoded once) times one output slab per block. Tiles are dealt to XCDs
+// so the slabs of one tile run on one XCD and share its activation rows in L2. Block = 8 waves,
 // one producer and one consumer per SIMD:
-//   producers (waves 4..7): per 64-wide K step, load the activation rows (f16) and the raw Q4_K /
+//   producers (waves 4..7): per 64-wide K step, load the activation rows (f16; eight lanes per
+//     128-byte row segment, so a load instruction touches eight cache lines) and the raw Q4_K /
 //     bf16 bytes of the slab's weight rows, decode the weights to f16 once, and store both tiles
-//     into LDS (double buffered);
-//   consumers (waves 0..3): read A and B fragments from LDS and issue the MFMAs; each owns all 128
+//     into LDS (double buffered), the loads running four steps ahead in registers;
+//   consumers (waves 0..3): read A and B fragments from LDS and issue the MFMAs; each owns all 160
 //     rows x (32 gate + 32 up) columns (gate_up) or 64 down columns (down).
 // A producer's VALU decode and a consumer's MFMAs on the same SIMD run concurrently, and every
 // weight element is decoded exactly once per block. One barrier per step hands the buffers over.
 //
-// Decode arithmetic (mantissa trick, as in gemm2.hip): low nibble q under the f16 0x6400 (1024)
+// Decode arithmetic (mantissa trick): low nibble q under the f16 0x6400 (1024)
 // gives 1024 + q, a high nibble left at bits 4-7 under 0x5400 (64, ulp 1/16) gives 64 + q; one
 // packed subtract leaves q exactly and one packed FMA gives q * f16(d * sc) - f16(dmin * m).
 #include "common.h"
@@ -25,7 +28,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace g3 {
 
-constexpr int kBM = MOE_GEMM2_BM;       // 128 rows per tile
+constexpr int kBM = MOE_GEMM3_BM;       // 160 rows per tile (5 MFMA row groups)
+constexpr int kMG = kBM / 32;
 constexpr int kBK = 64;                 // K per step
 constexpr int kS = 72;                  // LDS row stride in f16 (144 B)
 constexpr int kXcd = 8;
@@ -154,54 +158,57 @@ __device__ __forceinline__ int tile_rows(const int32_t* tiles, const int32_t* of
 }
 
 struct Smem {
-  uint16_t A[2][kBM * kS];              // 2 x 18 KB
+  uint16_t A[2][kBM * kS];              // 2 x 22.5 KB
   uint16_t B[2][kBN * kS];              // 2 x 36 KB
 };
 
-// Producer thread p (0..255): weight row p of the slab (one 64-wide K step = 64 elements) and
-// half an activation row: row p >> 1, elements [32 (p & 1), +32) (4 x 16 B). Two named sets of
-// raw registers alternate by step parity (compile time, so nothing is indexed at run time).
+// Activation rows of one producer thread p (0..255): 16-byte chunk p & 7 of rows (p >> 3) + 32 i,
+// i < kMG (pointers to the row starts; rows past the tile repeat its last row, never stored).
+struct ARows {
+  const uint16_t* r[kMG];
+};
+
+// Producer thread p: weight row p of the slab (one 64-wide K step = 64 elements) and the
+// activation chunks of ARows. kD sets of raw registers form a ring indexed at compile time.
 template <int WFMT>
 struct PSet {
   WRaw<WFMT> w;
-  uint4 a[4];
-  __device__ __forceinline__ void load(const uint8_t* wrow, const uint16_t* asrc, int k0, int p) {
+  uint4 a[kMG];
+  __device__ __forceinline__ void load(const uint8_t* wrow, const ARows& ar, int k0, int p) {
     w.load(wrow, k0);
-    const uint4* s = reinterpret_cast<const uint4*>(asrc + k0 + 32 * (p & 1));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a[j] = s[j];
+    for (int i = 0; i < kMG; ++i) a[i] = *reinterpret_cast<const uint4*>(ar.r[i] + k0 + 8 * (p & 7));
   }
   __device__ __forceinline__ void store(int k0, int p, uint16_t* As, uint16_t* Bs) const {
     w.decode(k0, Bs + p * kS);
-    uint4* d = reinterpret_cast<uint4*>(As + (p >> 1) * kS + 32 * (p & 1));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) d[j] = a[j];
+    for (int i = 0; i < kMG; ++i)
+      *reinterpret_cast<uint4*>(As + ((p >> 3) + 32 * i) * kS + 8 * (p & 7)) = a[i];
   }
 };
 
-// consumers read buffer J for step ks; fill buffer J ^ 1 with step ks + 1 (set `nxt`) and request
-// step ks + 2's bytes into set `cur` (consumed a step ago)
-template <int WFMT, int J>
-__device__ __forceinline__ void pstep(PSet<WFMT>& cur, PSet<WFMT>& nxt, int ks, int nk,
-                                      const uint16_t* asrc, const uint8_t* wrow, int p, Smem& sm) {
-  nxt.store(min(ks + 1, nk - 1) * kBK, p, sm.A[J ^ 1], sm.B[J ^ 1]);
-  cur.load(wrow, asrc, min(ks + 2, nk - 1) * kBK, p);
-  __syncthreads();
-}
-
+// Producer ring of kD register sets: at step ks the consumers read LDS buffer ks & 1, the producer
+// stores step ks + 1 (set (ks + 1) % kD) into the other buffer and requests step ks + kD into the
+// set it just freed, so each request has kD - 1 steps to land. kD is even and divides the step
+// count (H / 64 = 32 for gate_up, I / 64 = 8 for down), so set and buffer indices are compile-time.
+// Q4_K sets are 28 registers (4 deep); bf16 sets 48 (2 deep, within the 256-register budget).
 template <int WFMT>
-__device__ __forceinline__ void produce(int nk, const uint16_t* asrc, const uint8_t* wrow, int p,
+__device__ __forceinline__ void produce(int nk, const ARows& asrc, const uint8_t* wrow, int p,
                                         Smem& sm) {
-  PSet<WFMT> s0, s1;
-  s0.load(wrow, asrc, 0, p);
-  s1.load(wrow, asrc, min(1, nk - 1) * kBK, p);
-  s0.store(0, p, sm.A[0], sm.B[0]);
+  constexpr int kD = WFMT == MOE_FMT_Q4_K ? 4 : 2;
+  PSet<WFMT> s[kD];
+#pragma unroll
+  for (int i = 0; i < kD; ++i) s[i].load(wrow, asrc, min(i, nk - 1) * kBK, p);
+  s[0].store(0, p, sm.A[0], sm.B[0]);
   __syncthreads();
-  for (int k2 = 0; k2 < nk; k2 += 2) {
-    // step k2: buffer 0 is read; s1 (step k2 + 1) is stored, s0 reloads step k2 + 2
-    pstep<WFMT, 0>(s0, s1, k2, nk, asrc, wrow, p, sm);
-    // step k2 + 1: buffer 1 is read; s0 (step k2 + 2) is stored, s1 reloads step k2 + 3
-    pstep<WFMT, 1>(s1, s0, k2 + 1, nk, asrc, wrow, p, sm);
+  for (int k0 = 0; k0 < nk; k0 += kD) {
+#pragma unroll
+    for (int j = 0; j < kD; ++j) {
+      const int ks = k0 + j;
+      s[(j + 1) % kD].store(min(ks + 1, nk - 1) * kBK, p, sm.A[(j + 1) & 1], sm.B[(j + 1) & 1]);
+      s[j].load(wrow, asrc, min(ks + kD, nk - 1) * kBK, p);
+      __syncthreads();
+    }
   }
 }
 
@@ -212,7 +219,7 @@ __device__ __forceinline__ uint4 frag(const uint16_t* S, int row, int s, int lan
 // Consumer wave c (0..3): all 128 rows (NG active 32-row groups) x B rows {b0 + lane%32} and
 // {b1 + lane%32} of the slab.
 template <int NG>
-__device__ __forceinline__ void consume(int nk, int b0, int b1, Smem& sm, f32x16_t (&acc)[4][2]) {
+__device__ __forceinline__ void consume(int nk, int b0, int b1, Smem& sm, f32x16_t (&acc)[kMG][2]) {
   const int lane = threadIdx.x & 63;
   __syncthreads();
   for (int k2 = 0; k2 < nk; k2 += 2) {
@@ -238,9 +245,10 @@ __device__ __forceinline__ void consume(int nk, int b0, int b1, Smem& sm, f32x16
 
 template <int NG>
 __device__ __forceinline__ void consume_n(int ng, int nk, int b0, int b1, Smem& sm,
-                                          f32x16_t (&acc)[4][2]) {
+                                          f32x16_t (&acc)[kMG][2]) {
   (void)NG;
-  if (ng >= 4) consume<4>(nk, b0, b1, sm, acc);
+  if (ng >= 5) consume<5>(nk, b0, b1, sm, acc);
+  else if (ng == 4) consume<4>(nk, b0, b1, sm, acc);
   else if (ng == 3) consume<3>(nk, b0, b1, sm, acc);
   else if (ng == 2) consume<2>(nk, b0, b1, sm, acc);
   else consume<1>(nk, b0, b1, sm, acc);
@@ -264,22 +272,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nk = H / kBK;
   if (wave >= 4) {
     const int p = t - 256;
-    const int m = min(m0 + (p >> 1), mend - 1);
-    const uint16_t* asrc = x16 + (size_t)(tiles ? sorted_pairs[m] / K : m) * H;
+    ARows ar;
+#pragma unroll
+    for (int i = 0; i < kMG; ++i) {
+      const int m = min(m0 + (p >> 3) + 32 * i, mend - 1);
+      ar.r[i] = x16 + (size_t)(tiles ? sorted_pairs[m] / K : m) * H;
+    }
     const int r = p & 127;
     const uint8_t* wrow = (p < 128 ? wg : wu) + (size_t)e * estride +
                           (size_t)(col * 128 + r) * row_bytes(WFMT, H);
-    produce<WFMT>(nk, asrc, wrow, p, sm);
+    produce<WFMT>(nk, ar, wrow, p, sm);
     return;
   }
-  f32x16_t acc[4][2];
+  f32x16_t acc[kMG][2];
 #pragma unroll
-  for (int mg = 0; mg < 4; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
+  for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
   const int ng = __builtin_amdgcn_readfirstlane((mend - m0 + 31) >> 5);
   consume_n<0>(ng, nk, 32 * wave, 128 + 32 * wave, sm, acc);
   const int n = col * 128 + 32 * wave + (lane & 31), h = lane >> 5;
 #pragma unroll
-  for (int mg = 0; mg < 4; ++mg) {
+  for (int mg = 0; mg < kMG; ++mg) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -307,19 +319,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nk = I / kBK;
   if (wave >= 4) {
     const int p = t - 256;
-    const uint16_t* asrc = S + (size_t)min(m0 + (p >> 1), mend - 1) * I;
+    ARows ar;
+#pragma unroll
+    for (int i = 0; i < kMG; ++i) ar.r[i] = S + (size_t)min(m0 + (p >> 3) + 32 * i, mend - 1) * I;
     const uint8_t* wrow = wd + (size_t)e * estride + (size_t)(col * kBN + p) * row_bytes(WFMT, I);
-    produce<WFMT>(nk, asrc, wrow, p, sm);
+    produce<WFMT>(nk, ar, wrow, p, sm);
     return;
   }
-  f32x16_t acc[4][2];
+  f32x16_t acc[kMG][2];
 #pragma unroll
-  for (int mg = 0; mg < 4; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
+  for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
   const int ng = __builtin_amdgcn_readfirstlane((mend - m0 + 31) >> 5);
   consume_n<0>(ng, nk, 64 * wave, 64 * wave + 32, sm, acc);
   const int nb = col * kBN + 64 * wave + (lane & 31), h = lane >> 5;
 #pragma unroll
-  for (int mg = 0; mg < 4; ++mg) {
+  for (int mg = 0; mg < kMG; ++mg) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -331,9 +345,51 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ------------------------------------------------------------------------- f32 / bf16 -> f16 --
+template <int XDT>
+__global__ __launch_bounds__(256) void k_to_f16(const void* __restrict__ x, size_t n8,
+                                                uint16_t* __restrict__ out) {
+  for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+    // f16 RNE, saturated to +-65504 (an activation past f16's range would otherwise become inf)
+    auto pk = [](float u, float v) {
+      u = fminf(fmaxf(u, -65504.0f), 65504.0f);
+      v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+      return __builtin_bit_cast(uint32_t, (f16x2_t){(_Float16)u, (_Float16)v});
+    };
+    uint4 o;
+    if (XDT == MOE_DT_BF16) {
+      const uint4 v = reinterpret_cast<const uint4*>(x)[i];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      uint32_t r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = pk(__uint_as_float(w[j] << 16), __uint_as_float(w[j] & 0xFFFF0000u));
+      o = make_uint4(r[0], r[1], r[2], r[3]);
+    } else {
+      const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
+      const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+      o = make_uint4(pk(a.x, a.y), pk(a.z, a.w), pk(b.x, b.y), pk(b.z, b.w));
+    }
+    reinterpret_cast<uint4*>(out)[i] = o;
+  }
+}
+
 }  // namespace moe
 
 using namespace moe;
+
+bool moe_gemm3_supports(int fmt) { return fmt == MOE_FMT_Q4_K || fmt == MOE_FMT_BF16; }
+
+int moe_launch_to_f16(const void* x, int x_dtype, size_t n, uint16_t* out, hipStream_t st) {
+  if (n % 8) return moe_set_error(MOE_E_UNSUPPORTED, "to_f16: n %% 8 != 0");
+  const size_t n8 = n / 8;
+  const int grid = (int)((n8 + 255) / 256 < 2048 ? (n8 + 255) / 256 : 2048);
+  if (x_dtype == MOE_DT_BF16)
+    hipLaunchKernelGGL(k_to_f16<MOE_DT_BF16>, dim3(grid), dim3(256), 0, st, x, n8, out);
+  else
+    hipLaunchKernelGGL(k_to_f16<MOE_DT_F32>, dim3(grid), dim3(256), 0, st, x, n8, out);
+  return moe_check_launch("to_f16");
+}
+
 
 int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int fmt,
                             size_t expert_stride, const int32_t* tiles, int max_tiles, int T,

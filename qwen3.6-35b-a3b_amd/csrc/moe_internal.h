@@ -26,26 +26,19 @@ int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t*
                     int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st);
 
 // MFMA tile list: [count, (expert, row0) x count], rows per tile = bm (MOE_GEMM_BM for gemm.hip,
-// MOE_GEMM2_BM for gemm2.hip)
+// MOE_GEMM3_BM for gemm3.hip)
 #define MOE_GEMM_BM 64
-#define MOE_GEMM2_BM 128
+#define MOE_GEMM3_BM 160
 int moe_max_mtiles(int P, int E, int bm = MOE_GEMM_BM);
 int moe_launch_build_tiles(const int32_t* offsets, const int32_t* hit_list, int E, int P,
                            int32_t* tiles, hipStream_t st, int bm = MOE_GEMM_BM);
-// gemm2.hip: f16-operand grouped GEMM, weights decoded straight into MFMA registers.
-// x16: activations already in f16 ([T,H]); S: [rows, I] f16; y: [rows, H] f32. tiles == NULL:
-// identity rows 0..T-1 (shared expert). Formats: Q4_K and BF16 (others: gemm.hip).
+// f16 activation operand of the MFMA paths: x [n] f32 / bf16 -> f16 (RNE, saturated)
 int moe_launch_to_f16(const void* x, int x_dtype, size_t n, uint16_t* out, hipStream_t st);
-int moe_launch_gemm2_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int fmt,
-                            size_t expert_stride, const int32_t* tiles, int max_tiles, int T,
-                            const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
-                            int I, uint16_t* S, hipStream_t st);
-int moe_launch_gemm2_down(const uint16_t* S, const void* w_down, int fmt, size_t expert_stride,
-                          const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
-                          int H, int I, float* y, hipStream_t st);
-bool moe_gemm2_supports(int fmt);
-// gemm3.hip: warp-specialized form of the same contraction (producer waves decode into LDS,
-// consumer waves run the MFMAs); same arguments and results as the gemm2 launchers.
+// gemm3.hip: warp-specialized grouped GEMM (producer waves decode Q4_K / bf16 into LDS as f16,
+// consumer waves run the MFMAs). x16: activations in f16 ([T,H]); S: [rows, I] f16; y: [rows, H]
+// f32. tiles == NULL: identity rows 0..T-1 (shared expert). Formats: Q4_K and BF16 (others:
+// gemm.hip).
+bool moe_gemm3_supports(int fmt);
 int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int fmt,
                             size_t expert_stride, const int32_t* tiles, int max_tiles, int T,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
@@ -53,6 +46,17 @@ int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void*
 int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
                           int H, int I, float* y, hipStream_t st);
+
+// gemm4.hip: Q4_K gate_up and down with the weight decode in the MFMA waves (producers move raw
+// super-blocks and f16 activations into LDS); same tiles (MOE_GEMM3_BM rows), arguments and
+// results as the gemm3 launchers for Q4_K.
+int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
+                            size_t expert_stride, const int32_t* tiles, int max_tiles,
+                            const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
+                            int I, uint16_t* S, hipStream_t st);
+int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_stride,
+                          const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
+                          float* y, hipStream_t st);
 
 // decode GEMV path: S [P, I] f32 (sorted order), then y [P, H] f32
 int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gu, int fmt,

@@ -23,9 +23,9 @@
 
 namespace moe {
 
-// ------------------------------------------------------------------ R1, small T (T <= 8) -------
-// One wave per expert row; the row (H bf16) is read once and applied to every token.
-// grid.x = ceil(E/4), block = 256 (4 waves).
+// ----------------------------------------------------------------- R1, small T (T <= 256) -------
+// One wave per (expert row, 8-token slice): the row (H bf16) is read once per slice and applied to
+// each of the slice's tokens. grid = (ceil(E/4), ceil(T/8)), block = 256 (4 waves).
 template <int XDT>
 __global__ __launch_bounds__(256) void k_router_logits_gemv(
     const void* __restrict__ xv, const uint16_t* __restrict__ w, const float* __restrict__ bias,
@@ -47,7 +47,8 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
     }
   }
   wsq = wave_sum_f64(wsq);
-  for (int t = 0; t < T; ++t) {
+  const int t_end = min(T, 8 * (int)blockIdx.y + 8);
+  for (int t = 8 * blockIdx.y; t < t_end; ++t) {
     double acc = 0.0, xsq = 0.0;
     for (int c = 0; c < nchunk; ++c) {
       uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
@@ -354,8 +355,8 @@ using namespace moe;
 int moe_launch_router_logits(const void* x, int x_dtype, const void* w, const float* bias, int T,
                              int H, int E, uint16_t* logits, hipStream_t st) {
   const uint16_t* wr = reinterpret_cast<const uint16_t*>(w);
-  if (T <= 8) {
-    dim3 grid((E + 3) / 4);
+  if (T <= 256) {
+    dim3 grid((E + 3) / 4, (T + 7) / 8);
     if (x_dtype == MOE_DT_F32)
       hipLaunchKernelGGL(k_router_logits_gemv<MOE_DT_F32>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
     else

@@ -102,20 +102,23 @@ __device__ __forceinline__ void qswap(TopkLds& s, int a, int b) {
 // greater-than on queue positions (values only; NaN does not occur on this path)
 __device__ __forceinline__ bool qgt(const TopkLds& s, int a, int b) { return s.v[a] > s.v[b]; }
 
-// stable insertion sort, descending, of positions [lo, hi) — lane 0 only
-__device__ void q_insertion_sort(TopkLds& s, int lo, int hi) {
-  for (int i = lo + 1; i < hi; ++i) {
-    float v = s.v[i];
-    int id = s.i[i];
-    int j = i;
-    while (j > lo && v > s.v[j - 1]) {
-      s.v[j] = s.v[j - 1];
-      s.i[j] = s.i[j - 1];
-      --j;
-    }
-    s.v[j] = v;
-    s.i[j] = id;
+// Stable descending insertion sort (libstdc++ __insertion_sort with greater) of positions
+// [lo, lo + n), n <= 64, done by the wave:
+// an element's final position is its rank, the number of elements greater than it plus the
+// number of equal ones before it (insertion sort moves an element only past strictly smaller
+// ones, so equal values keep their order).
+__device__ void wave_stable_sort_small(TopkLds& s, int lo, int n, int lane) {
+  float v = 0.0f;
+  int id = 0;
+  if (lane < n) { v = s.v[lo + lane]; id = s.i[lo + lane]; }
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const float vj = readlane_f32(v, j);
+    rank += (vj > v || (vj == v && j < lane)) ? 1 : 0;
   }
+  wave_sync();
+  if (lane < n) { s.v[lo + rank] = v; s.i[lo + rank] = id; }
+  wave_sync();
 }
 
 // libstdc++ heap helpers, comparator "greater" — lane 0 only
@@ -254,29 +257,28 @@ __device__ int wave_torch_topk(TopkLds& s, int n, int k, int lane) {
     }
     --depth;
     const int mid = lo + (hi - lo) / 2;
-    if (lane == 0) {
-      // move_median_to_first(lo, lo+1, mid, hi-1)
+    {
+      // move_median_to_first(lo, lo+1, mid, hi-1): the three candidates read in parallel
       const int a = lo + 1, b = mid, c = hi - 1;
+      const float cand = s.v[lane == 0 ? a : (lane == 1 ? b : c)];
+      const float va = readlane_f32(cand, 0), vb = readlane_f32(cand, 1), vc = readlane_f32(cand, 2);
       int pick;
-      if (qgt(s, a, b)) {
-        if (qgt(s, b, c)) pick = b;
-        else if (qgt(s, a, c)) pick = c;
+      if (va > vb) {
+        if (vb > vc) pick = b;
+        else if (va > vc) pick = c;
         else pick = a;
-      } else if (qgt(s, a, c)) pick = a;
-      else if (qgt(s, b, c)) pick = c;
+      } else if (va > vc) pick = a;
+      else if (vb > vc) pick = c;
       else pick = b;
-      qswap(s, lo, pick);
+      if (lane == 0) qswap(s, lo, pick);
     }
     wave_sync();
     const int cut = wave_partition(s, lo + 1, hi, lane);
     if (cut <= nth) lo = cut;
     else hi = cut;
   }
-  if (lane == 0) {
-    if (!heap) q_insertion_sort(s, lo, hi);
-    q_insertion_sort(s, 0, k - 1);
-  }
-  wave_sync();
+  if (!heap) wave_stable_sort_small(s, lo, hi - lo, lane);
+  wave_stable_sort_small(s, 0, k - 1, lane);
   return heap;
 }
 
