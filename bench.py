@@ -21,8 +21,8 @@ repo's CPU oracle of the same block, timed on the host on a bounded sample).
 
 Usage:
   python bench.py [--gpus 1] [--steps 1024] [--warmup 16] [--layers 40] [--no-cpu] [--no-prefill]
-  python bench.py --pmc                      short decode workload + copy calibration (for rocprofv3 --pmc)
-  python bench.py --pmc-summary DIR_FETCH DIR_WRITE   traffic summary (markdown) from two --pmc runs
+  python bench.py --pmc [--no-hint]          short decode workload + copy calibration (for rocprofv3 --pmc)
+  python bench.py --pmc-summary DF DW [DFH DWH]   traffic summary (markdown) from --pmc runs
   python bench.py --stats-summary DIR [CMD]   kernel table (markdown) from rocprofv3 --kernel-trace --stats
 """
 from __future__ import annotations
@@ -73,7 +73,8 @@ def parse():
     ap.add_argument("--pmc", action="store_true")
     ap.add_argument("--no-hint", action="store_true",
                     help="call moe_block_forward (no next-layer L2 warm-up) in the decode runs")
-    ap.add_argument("--pmc-summary", nargs=2, metavar=("DIR_FETCH", "DIR_WRITE"))
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="DIR_FETCH DIR_WRITE of --pmc --no-hint runs [then of --pmc runs]")
     ap.add_argument("--stats-summary", nargs="+", metavar="DIR [CMD]")
     return ap.parse_args()
 
@@ -129,12 +130,14 @@ def _per_dispatch(d: str, counter: str):
     return out
 
 
-def pmc_summary(dir_fetch: str, dir_write: str) -> str:
-    """Markdown summary of two rocprofv3 --pmc runs of `bench.py --pmc`: FETCH_SIZE / WRITE_SIZE
+def pmc_summary(dir_fetch: str, dir_write: str, dir_fetch_hint: str | None = None,
+                dir_write_hint: str | None = None) -> str:
+    """Markdown summary of rocprofv3 --pmc runs of `bench.py --pmc`: FETCH_SIZE / WRITE_SIZE
     (KiB per dispatch) of the decode layer kernel, scaled by what the same counters read for a
-    plain copy of COPY_MIB MiB (known bytes each way)."""
+    plain copy of COPY_MIB MiB (known bytes each way). The first pair of runs is the plain entry
+    (`--no-hint`) and gives the per-launch traffic; the optional second pair is the same workload
+    with the next-layer L2 warm-up."""
     import statistics
-    f, w = _per_dispatch(dir_fetch, "FETCH_SIZE"), _per_dispatch(dir_write, "WRITE_SIZE")
 
     def pick(d, pat):
         ks = [k for k in d if re.search(pat, k)]
@@ -142,43 +145,76 @@ def pmc_summary(dir_fetch: str, dir_write: str) -> str:
             raise SystemExit(f"no kernel matching {pat!r} in {sorted(d)[:8]}")
         return max(ks, key=lambda k: len(d[k]))
 
-    kf, kw = pick(f, DECODE_KERNEL), pick(w, DECODE_KERNEL)
     def largest(d, pat):
         vals = [(v, k) for k in d if re.search(pat, k) for v in d[k]]
         if not vals:
             raise SystemExit(f"no kernel matching {pat!r}")
         return max(vals)
 
-    # the calibration multiply is the largest elementwise dispatch of the run
-    copy_f, cf = largest(f, r"elementwise")
-    copy_w, cw = largest(w, r"elementwise")
-    copy_kib = COPY_MIB * 1024.0
-    sf, sw = copy_kib / copy_f, copy_kib / copy_w
-    fetch = statistics.median(f[kf]) * sf * 1024.0
-    write = statistics.median(w[kw]) * sw * 1024.0
+    def measure(df, dw):
+        f, w = _per_dispatch(df, "FETCH_SIZE"), _per_dispatch(dw, "WRITE_SIZE")
+        kf, kw = pick(f, DECODE_KERNEL), pick(w, DECODE_KERNEL)
+        # the calibration multiply is the largest elementwise dispatch of the run
+        copy_f, cf = largest(f, r"elementwise")
+        copy_w, _ = largest(w, r"elementwise")
+        copy_kib = COPY_MIB * 1024.0
+        sf, sw = copy_kib / copy_f, copy_kib / copy_w
+        return dict(kernel=kf, n=len(f[kf]), fk=statistics.median(f[kf]), wk=statistics.median(w[kw]),
+                    fetch=statistics.median(f[kf]) * sf * 1024.0,
+                    write=statistics.median(w[kw]) * sw * 1024.0, sf=sf, sw=sw, copy_f=copy_f,
+                    copy_w=copy_w, copy_kib=copy_kib, copy_name=cf)
+
+    m = measure(dir_fetch, dir_write)
+    mh = measure(dir_fetch_hint, dir_write_hint) if dir_fetch_hint and dir_write_hint else None
+    cmd = "rocprofv3 --pmc {c} --kernel-include-regex '" + PMC_REGEX + "' --output-format csv -d {d} -o {o} -- python3 bench.py --pmc"
     lines = [
         "# k_dec_layer (config 1 decode layer): HBM traffic per launch from rocprofv3 PMC",
         "",
         "Commands (GPU box, repo root):",
         "",
-        f"    rocprofv3 --pmc FETCH_SIZE --kernel-include-regex '{PMC_REGEX}' --output-format csv -d /tmp/pmc_f -o f -- python3 bench.py --pmc",
-        f"    rocprofv3 --pmc WRITE_SIZE --kernel-include-regex '{PMC_REGEX}' --output-format csv -d /tmp/pmc_w -o w -- python3 bench.py --pmc",
-        "    python3 bench.py --pmc-summary /tmp/pmc_f /tmp/pmc_w",
+        "    " + cmd.format(c="FETCH_SIZE", d="/tmp/pf", o="f") + " --no-hint",
+        "    " + cmd.format(c="WRITE_SIZE", d="/tmp/pw", o="w") + " --no-hint",
+    ]
+    if mh:
+        lines += ["    " + cmd.format(c="FETCH_SIZE", d="/tmp/pfh", o="f"),
+                  "    " + cmd.format(c="WRITE_SIZE", d="/tmp/pwh", o="w"),
+                  "    python3 bench.py --pmc-summary /tmp/pf /tmp/pw /tmp/pfh /tmp/pwh"]
+    else:
+        lines += ["    python3 bench.py --pmc-summary /tmp/pf /tmp/pw"]
+    lines += [
         "",
-        f"Calibration: a {COPY_MIB} MiB elementwise multiply ({cf[:60]}) reads {copy_f:.0f} KiB (FETCH_SIZE)",
-        f"and writes {copy_w:.0f} KiB (WRITE_SIZE) for {copy_kib:.0f} KiB each way:",
-        f"scale factors fetch {sf:.4f}, write {sw:.4f}.",
+        f"Calibration: a {COPY_MIB} MiB elementwise multiply ({m['copy_name'][:60]}) reads {m['copy_f']:.0f} KiB (FETCH_SIZE)",
+        f"and writes {m['copy_w']:.0f} KiB (WRITE_SIZE) for {m['copy_kib']:.0f} KiB each way:",
+        f"scale factors fetch {m['sf']:.4f}, write {m['sw']:.4f}.",
         "",
-        "| kernel | dispatches | FETCH_SIZE KiB (median) | WRITE_SIZE KiB (median) | scaled fetch B | scaled write B |",
-        "|---|---|---|---|---|---|",
-        f"| {kf[:60]} | {len(f[kf])} | {statistics.median(f[kf]):.1f} | {statistics.median(w[kw]):.1f} "
-        f"| {fetch:.0f} | {write:.0f} |",
+        "| entry | kernel | dispatches | FETCH_SIZE KiB (median) | WRITE_SIZE KiB (median) | scaled fetch B | scaled write B |",
+        "|---|---|---|---|---|---|---|",
+        f"| moe_block_forward | {m['kernel'][:60]} | {m['n']} | {m['fk']:.1f} | {m['wk']:.1f} "
+        f"| {m['fetch']:.0f} | {m['write']:.0f} |",
+    ]
+    if mh:
+        lines.append(f"| moe_block_forward_prefetch | {mh['kernel'][:60]} | {mh['n']} | {mh['fk']:.1f} | "
+                     f"{mh['wk']:.1f} | {mh['fetch']:.0f} | {mh['write']:.0f} |")
+    lines += [
         "",
-        f"traffic_bytes_per_launch: {fetch + write:.0f}",
+        f"traffic_bytes_per_launch: {m['fetch'] + m['write']:.0f}",
         "",
         "Algorithmic bytes per launch: 20,447,232 (8 routed Q4_K experts + bf16 shared expert) plus",
-        "1,052,672 router + shared-gate bytes = 21,499,904.",
+        "1,052,672 router + shared-gate bytes = 21,499,904. Each of the 8 XCDs computes all 256",
+        "router logits (no cross-XCD logit exchange), so the 1 MiB router matrix leaves L2 once per",
+        f"XCD: of the {m['fetch'] + m['write'] - 21499904:.0f} B above the algorithmic bytes, 7 x 1,048,576 B are these",
+        "re-reads (served from the MALL or HBM); the rest is x, the norm weight and the exchange words",
+        "per XCD and the output writes.",
     ]
+    if mh:
+        lines += [
+            "",
+            "With the warm-up hint each launch also reads the next layer's router rows and norm weight",
+            "into its XCD's L2; in a chain of launches the next launch then finds them there, so",
+            "the bytes move from one launch to the one before it. A PMC run serialises dispatches and the",
+            "warmed lines do not survive to the next one, which counts these bytes twice; the per-launch",
+            "figure is therefore the plain entry's.",
+        ]
     return "\n".join(lines) + "\n"
 
 
@@ -297,6 +333,8 @@ def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
 def main():
     args = parse()
     if args.pmc_summary:
+        if len(args.pmc_summary) not in (2, 4):
+            raise SystemExit("--pmc-summary takes DIR_FETCH DIR_WRITE [DIR_FETCH_HINT DIR_WRITE_HINT]")
         print(pmc_summary(*args.pmc_summary), end="")
         return
     if args.stats_summary:

@@ -149,8 +149,10 @@ typedef struct moe_next_layer {
 
 /* moe_block_forward with a hint: `next` (may be NULL) names the next layer's routing-independent
  * weights. The single-launch decode layer then reads, at the end of its run, the parts of them
- * that each workgroup reads first in the next layer, so that they come from the L2 of the same
- * XCD instead of HBM; other paths ignore the hint. Results are identical with or without it.
+ * that the next layer's routing waits on (each workgroup's router rows and the norm weight), so
+ * that they come from the L2 of the same XCD instead of HBM; the shared-expert fields are
+ * accepted and not read at present (they have slack in the next layer). Other paths ignore the
+ * hint. Results are identical with or without it.
  * Same arguments, limits and errors as moe_block_forward otherwise. Replaces, like
  * moe_block_forward, engine/m3_forward.py:430-476 in its layer loop (engine/m3_forward.py:714-737),
  * where the next layer's weights are known ahead of its input. */
@@ -165,13 +167,11 @@ int moe_block_forward_prefetch(const void *x, int x_dtype, int T, int H, int I, 
                                float *expert_raw, void *ws, size_t ws_bytes, void *stream,
                                const moe_next_layer *next);
 
-/* Zero the workspace's device-side sync words (its first 512 KiB: counters, the single-launch
- * decode layer's per-CU launch counts and its two exchange buffers) and record this device's CU
- * layout there (one short launch: the rank of each CU inside its XCD, which the single-launch
- * decode layer reads to take its role with one load). Call once after allocating a workspace,
- * before its first use by moe_block_forward / moe_experts / moe_shared_expert / moe_router_topk.
- * A workspace zeroed by other means also works (the decode layer then takes its roles by atomic
- * tickets: same results, a slower start). Every call leaves the words valid for the next.
+/* Zero the workspace's device-side sync words (its first 512 KiB: error bits, the single-launch
+ * decode layer's per-role launch counts and its two exchange buffers; one short fill launch).
+ * Call once after allocating a workspace, before its first use by moe_block_forward /
+ * moe_experts / moe_shared_expert / moe_router_topk; a workspace zeroed by other means is the
+ * same starting state. Every call leaves the words valid for the next.
  * Calls sharing one workspace must be ordered on one stream. No counterpart in the reference (its
  * device work ran in fresh processes). */
 int moe_workspace_init(void *ws, size_t ws_bytes, void *stream);

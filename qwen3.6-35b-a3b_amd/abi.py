@@ -81,8 +81,8 @@ def workspace_bytes(T: int, H: int, I: int, E: int, K: int, I_s: int) -> int:
 
 def device_error_bits(device) -> int:
     """The workspace's device-side error word of the single-launch decode layer: bit 0, a bounded
-    spin timed out (its workgroups were not all co-resident); bit 1, an XCD received more
-    workgroups than it has CUs (no role for some). Zero when every launch ran as designed.
+    spin timed out (its workgroups were not all co-resident, or not placed on the XCDs round
+    robin as the single-launch decode layer assumes). Zero when every launch ran as designed.
     Reading it synchronises."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WS_CACHE.get(key)

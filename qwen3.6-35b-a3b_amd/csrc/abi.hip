@@ -325,8 +325,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     L.norm_w = one_launch ? norm_w : nullptr;
     L.norm_eps = norm_eps;
     if (next) {
-      L.nx_router = next->w_router; L.nx_sg = next->ws_gate; L.nx_su = next->ws_up;
-      L.nx_sd = next->ws_down; L.nx_ssg = next->ws_scalar_gate; L.nx_norm = next->norm_w;
+      L.nx_router = next->w_router;
+      L.nx_norm = next->norm_w;
     }
     if (!L.logits || !L.ids || !L.w_f32 || !L.w_bf16 || !L.s_shared || !L.gate_prob || !L.shared_raw || !L.s_routed)
       return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
@@ -393,8 +393,7 @@ int moe_block_forward_prefetch(const void* x, int x_dtype, int T, int H, int I, 
 
 int moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {
   if (!ws || ws_bytes < kSyncBytes) return moe_set_error(MOE_E_ARG, "moe_workspace_init: workspace smaller than %zu bytes", kSyncBytes);
-  MOE_TRY(moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream));
-  return moe_launch_cu_probe(reinterpret_cast<int*>(ws), (hipStream_t)stream);
+  return moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -2,10 +2,14 @@
 //
 // A persistent grid of 256 workgroups of 8 waves (one per CU; the LDS footprint keeps it at one,
 // so every XCD holds exactly 32) runs the block's dependent phases and hands data between them
-// through self-validating exchange words. A workgroup's role is (x, r): x = the XCD it runs on
-// (hardware register XCC_ID), r = the rank of its CU among that XCD's 32, read from a table that
-// moe_workspace_init's probe launch records (one load; a per-XCD atomic ticket instead, when no
-// table was recorded, costs 1.5-3 us of contention at the start).
+// through self-validating exchange words. A workgroup's role is (x, r) = (blockIdx mod 8,
+// blockIdx / 8): the dispatcher hands a launch's workgroups to the 8 XCDs round robin, workgroup
+// b to XCD (b + c) mod 8 with one offset c per launch (c is 0 or 7 depending on the hardware
+// queue; measured over 4000 launches, eager, graph-replayed and alternating between streams, with
+// other kernels of odd grids in between), so the 32 workgroups of role group x share one XCD and
+// the role costs no memory round trip: the weights it selects are requested at entry. ("XCD x"
+// below is the XCD that role group x runs on.) Were the placement ever different, the XCD-local
+// exchanges below would time out and record the spin error bit rather than hang.
 // XCD x owns routed slot k = x and the 64-wide slice [64x, 64x+64) of the shared expert's
 // intermediate axis, so two of the three exchanges stay among the 32 workgroups of one XCD:
 //
@@ -20,21 +24,24 @@
 //   phase 3  wait for slot x's 512 activations (XCD-local); down rows h in [64r, 64r+64)
 //   phase 4  wg (x, r) combines rows [8j, 8j+8), j = 32x + r: the 8 slots' outputs in ascending
 //            expert id, the 8 shared-down partials in ascending x, gate, residual
-//   (hint)   with the next layer's routing-independent weights given, waves 4-7 read the parts
-//            that role (x, r) will need into XCD x's L2 while phase 4 waits
+//   (hint)   with the next layer's weights named, waves 4-7 read the router rows and the norm
+//            weight that role (x, r) will need first into XCD x's L2 while phase 4 waits
 //
 // Exchange words are 32-bit: a value is stored as the complement of its bit pattern (NaNs made
 // canonical first), so 0 never encodes a value and means "not written yet". Each word is written
-// once per launch by one dword store that bypasses the non-coherent L2 (agent-scope relaxed atomic
-// store, sc1) and read the same way (sc1 loads, 16 bytes at a time); a reader re-polls all of its
-// missing words in parallel until every word it needs is non-zero. Exchange latency grows with the
-// number of workgroups reading the same lines, which is why no region here has more than 32
-// readers. Two buffers alternate by the launch's epoch parity, and each launch zeroes the buffer
+// once per launch by one dword store and polled 16 bytes at a time; a reader re-polls all of its
+// missing words in parallel until every word it needs is non-zero. Words that cross XCDs (expert
+// outputs, shared-down partials) go past the XCDs' non-coherent L2s (agent-scope relaxed atomic
+// stores and loads, sc1); words read only inside one XCD (logits, shared and routed activations)
+// use non-temporal stores and loads, which meet in that XCD's L2 and take half the round trip.
+// Exchange latency grows with the number of workgroups reading the same lines, which is why no
+// region here has more than 32 readers. Two buffers alternate by the launch's epoch parity, and each launch zeroes the buffer
 // the next launch will use, so a zeroed workspace is a valid starting state and graph replays
-// work. The launch count (epoch) is kept per CU, in the CU's table word next to its rank: the one
-// workgroup a launch places on that CU reads it at the start and writes it back incremented at
-// the end, so no launch ends on a contended atomic. Every spin is bounded: on a timeout the
-// workgroup records an error bit and carries on (no hang).
+// work. The launch count (epoch) is kept per role: the one workgroup of role (x, r) reads its word
+// at entry (the read overlaps the x and weight loads; the parity is first used at the logit
+// store) and writes it back incremented at the end, so no launch starts or ends on a contended
+// atomic. Every spin is bounded: on a timeout the workgroup records an error bit and carries on
+// (no hang).
 #include "common.h"
 #include "moe_internal.h"
 #include "router_dev.h"
@@ -50,17 +57,10 @@ constexpr int kSpinLimit = 1 << 20;     // polls (each a memory round trip) befo
 constexpr int kOccPad = 5120;           // uint4s of LDS that keep the grid at one workgroup per CU
 // sync words (int32 index into the workspace's first kSyncBytes)
 constexpr int kErrWord = 3;             // error bits
-constexpr int kTableValid = 4;          // 1: the CU table below is complete; 2: the probe failed
-constexpr int kProbeArrive = 5;         // probe launch: arrival counter
-constexpr int kProbeBad = 6;            // probe launch: nonzero when a CU was seen twice
-constexpr int kTicket = 32;             // fallback per-XCD tickets (32..39), taken modulo kPer
-constexpr int kProbeCount = 40;         // probe launch: workgroups seen per XCD (40..47)
-constexpr int kCuTable = 114688;        // [xcd][64]: (epoch << 8) | (rank + 1), slot = se*16 + cu
-constexpr int kRoleEpoch = kCuTable + kXcd * 64;   // fallback: epoch per role [256]
+constexpr int kRoleEpoch = 114688;      // [xcd][kPer]: launches run by role (x, r), past the exchange
 
 // error bits (sync word 3)
 constexpr int kErrSpin = 1;             // a bounded wait timed out
-constexpr int kErrRole = 2;             // an XCD received more than kPer workgroups
 
 struct LayerArgs {
   const void* x;
@@ -73,7 +73,7 @@ struct LayerArgs {
   const uint16_t* su;
   const uint16_t* sd;
   const uint16_t* ssg;
-  int* sync;                            // sync words (see kErrWord .. kRoleEpoch)
+  int* sync;                            // sync words (kErrWord, kRoleEpoch)
   uint32_t* xch;                        // two exchange buffers of XW_BUF words
   uint16_t* logits_out;
   int32_t* ids_out;
@@ -87,13 +87,9 @@ struct LayerArgs {
   int exact_order;                      // stage outputs requested: keep torch's slot order
   const float* norm_w;                  // post-attention RMSNorm weight [H] f32, or NULL
   float norm_eps;
-  // the next layer's routing-independent weights (L2 warm-up hint), or NULL
+  // the next layer's router weight and norm weight (L2 warm-up hint), or NULL
   const uint16_t* nx_router;
-  const uint16_t* nx_sg;
-  const uint16_t* nx_su;
-  const uint16_t* nx_sd;
-  const uint16_t* nx_ssg;
-  const float* nx_norm;                 // the next layer's norm weight, or NULL
+  const float* nx_norm;
 };
 
 // exchange buffer layout (uint32 words; every region starts 16-byte aligned)
@@ -105,49 +101,13 @@ constexpr int XW_SHP = XW_Y + kXcd * 2048;      // [xcd][2048] shared-down parti
 constexpr int XW_BUF = XW_SHP + kXcd * 2048;    // words per buffer
 constexpr int kClearPerWg = (XW_BUF + kG - 1) / kG;
 
-__device__ __forceinline__ uint32_t xcc_id() {
-  uint32_t v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  return v & 15u;
-}
-// the CU's slot inside its XCD: shader engine (HW_ID bits 13-15) x 16 + CU (bits 8-11)
-__device__ __forceinline__ int cu_slot() {
-  uint32_t v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(v));
-  return (int)(((v >> 13) & 3u) * 16u + ((v >> 8) & 15u));
-}
+__device__ const float kZeroBias = 0.0f;  // the logit bias of a router without one
+
 __device__ __forceinline__ int aload(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void astore(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Probe launch (moe_workspace_init): one workgroup per CU (same LDS footprint as the layer), each
-// records its CU's rank within the XCD; the table is valid when every XCD saw exactly kPer
-// distinct CUs.
-__global__ __launch_bounds__(64) void k_cu_probe(int* sync) {
-  __shared__ uint4 s_occ[kOccPad + 1024];
-  // the LDS footprint is the point (one workgroup per CU); this never-true branch keeps it
-  const bool never = sync[kErrWord] == 0x7FFFFFFF;
-  if (never) s_occ[threadIdx.x] = make_uint4(1, 2, 3, 4);
-  __syncthreads();
-  if (never) sync[kProbeBad] += (int)s_occ[threadIdx.x ^ 1].x;
-  if (threadIdx.x != 0) return;
-  const int xcd = (int)xcc_id() & (kXcd - 1);
-  const int slot = cu_slot();
-  const int rank = __hip_atomic_fetch_add(sync + kProbeCount + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  int expected = 0;
-  const bool fresh = __hip_atomic_compare_exchange_strong(
-      sync + kCuTable + 64 * xcd + slot, &expected, rank + 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-      __HIP_MEMORY_SCOPE_AGENT);
-  if (!fresh || rank >= kPer) __hip_atomic_fetch_add(sync + kProbeBad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int arrived = __hip_atomic_fetch_add(sync + kProbeArrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (arrived == kG - 1) {
-    bool ok = aload(sync + kProbeBad) == 0;
-    for (int q = 0; q < kXcd; ++q) ok = ok && aload(sync + kProbeCount + q) == kPer;
-    astore(sync + kTableValid, ok ? 1 : 2);
-  }
 }
 
 __device__ __forceinline__ uint32_t xenc(float v) {
@@ -361,13 +321,18 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ float s_comb[2][K][8];      // [y | shared partial][slot | xcd][row]
   __shared__ float s_gate;
   __shared__ double s_red[2][kThreads / 64];
-  __shared__ int s_role[4];
+  __shared__ int s_role[1];
   __shared__ uint4 s_occ[kOccPad];
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int l16 = lane & 15;
   int* err = a.sync + kErrWord;
-  // x and the norm weight do not depend on the role: request them first
+  // the role (x, r) from the launch's round-robin placement; the role's launch count is read
+  // first, the input row and every routing-independent weight this role uses right behind it
+  const int x = (int)blockIdx.x & (kXcd - 1), r = (int)blockIdx.x >> 3;
+  const int j = kPer * x + r;            // combine rows [8j, 8j+8)
+  int ep = 0;
+  if (t == 0) ep = aload(a.sync + kRoleEpoch + kPer * x + r);
   float4 xin;
   if (XDT == MOE_DT_F32) {
     xin = reinterpret_cast<const float4*>(a.x)[t];
@@ -377,80 +342,73 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
                       bf16_to_f32(u.y & 0xFFFFu), bf16_to_f32(u.y >> 16));
   }
   const float4 nw = a.norm_w ? reinterpret_cast<const float4*>(a.norm_w)[t] : make_float4(1.f, 1.f, 1.f, 1.f);
-  if (t == 0) {
-    // role and launch count: the CU table word (one load), else a ticket and a per-role epoch
-    const int xcd = (int)xcc_id() & (kXcd - 1);
-    const int slot = cu_slot();
-    const int valid = aload(a.sync + kTableValid);
-    const int w = aload(a.sync + kCuTable + 64 * xcd + slot);
-    int rank, ep, mode;
-    if (valid == 1 && (w & 255) != 0) {
-      rank = (w & 255) - 1;
-      ep = (int)((uint32_t)w >> 8);
-      mode = 0;
-    } else {
-      if (valid == 1) atomicOr(err, kErrRole);      // a CU the probe did not see
-      rank = __hip_atomic_fetch_add(a.sync + kTicket + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & (kPer - 1);
-      ep = aload(a.sync + kRoleEpoch + kPer * xcd + rank);
-      mode = 1;
-    }
-    s_role[0] = xcd;
-    s_role[1] = rank;
-    s_role[2] = ep;
-    s_role[3] = mode ? -1 : slot;
-  }
-  // the LDS footprint keeps one workgroup per CU; this never-true branch keeps the array
-  const bool never = a.nx_ssg == reinterpret_cast<const uint16_t*>(a.sync);
-  if (never) s_occ[t] = make_uint4(t, 0, 0, 0);
-  __syncthreads();
-  if (never) atomicOr(err, (int)s_occ[t ^ 1].x);
-  const int x = s_role[0], r = s_role[1];
-  const uint32_t epoch = (uint32_t)s_role[2] + 1u;
-  uint32_t* xb = a.xch + (epoch & 1u) * XW_BUF;          // this launch's words
-  uint32_t* xn = a.xch + ((epoch & 1u) ^ 1u) * XW_BUF;   // the next launch's, zeroed here
-  const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc(xb, 0, XW_BUF * 4, 0x00020000);
-  const int j = kPer * x + r;            // combine rows [8j, 8j+8)
 
   // ------------------------------------------------------------------ start: loads, x, norm --
   // routing-independent weights: router row 8r + wave; shared gate and up rows
   // i = 64x + 2r + (wave - 5) (waves 5-6); the scalar gate row (wave 7); shared-down rows
   // 64r + (lane >> 3) + 8q, cols 64x + 8 (lane & 7) .. +8 (wave 4, used while wave 0 selects the
   // experts). Wave 0, which polls the logits, carries none of the extras.
-  uint4 wr4[4], sgw[4], suw[4], sdw[8];
-  const float bias_e = a.bias ? a.bias[8 * r + wave] : 0.0f;
+  // the router rows now; the shared expert's rows (waves 4-7, wx) once these and the input row
+  // have landed (below): requested together, they would slow the loads the routing waits on
+  uint4 wr4[4], wx[8];
   {
     const uint16_t* wr = a.w_router + (size_t)(8 * r + wave) * H;
 #pragma unroll
     for (int c = 0; c < 4; ++c) wr4[c] = *reinterpret_cast<const uint4*>(wr + 512 * c + 8 * lane);
-    if (wave == 5 || wave == 6) {
-      const int i = ISX * x + 2 * r + (wave - 5);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        sgw[c] = *reinterpret_cast<const uint4*>(a.sg + (size_t)i * H + 512 * c + 8 * lane);
-        suw[c] = *reinterpret_cast<const uint4*>(a.su + (size_t)i * H + 512 * c + 8 * lane);
-      }
-    } else if (wave == 7) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) sgw[c] = *reinterpret_cast<const uint4*>(a.ssg + 512 * c + 8 * lane);
-    } else if (wave == 4) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        sdw[q] = *reinterpret_cast<const uint4*>(a.sd + (size_t)(64 * r + (lane >> 3) + 8 * q) * IS +
-                                                 ISX * x + 8 * (lane & 7));
-    }
   }
+  // waves 5-6: shared gate row wx[0..3], up row wx[4..7]; wave 7: the scalar gate row wx[0..3];
+  // wave 4: shared-down rows 64r + (lane >> 3) + 8q at cols 64x + 8 (lane & 7), q = 0..7
+  // the logit bias, read unconditionally (a device zero when there is none) after the weights
+  const float bias_e = *(a.bias ? a.bias + 8 * r + wave : &kZeroBias);
   const float resid = (t < 8 && a.residual) ? a.residual[8 * j + t] : 0.0f;
+  // norm: r = f32(1 / sqrt(mean(x^2) + eps)) in f64 (every square exact, one final rounding);
+  // xl1 >= |input|_1 for the router's error bound, from sum |x_j nw_j| (exact products)
   {
-    // norm: r = f32(1 / sqrt(mean(x^2) + eps)) in f64 (every square exact, one final rounding);
-    // xl1 >= |input|_1 for the router's error bound, from sum |x_j nw_j| (exact products)
     double ss = (double)xin.x * xin.x + (double)xin.y * xin.y + (double)xin.z * xin.z + (double)xin.w * xin.w;
     double sa = fabs((double)xin.x * nw.x) + fabs((double)xin.y * nw.y) + fabs((double)xin.z * nw.z) +
                 fabs((double)xin.w * nw.w);
     ss = wave_sum_f64(ss);
     sa = wave_sum_f64(sa);
     if (lane == 0) { s_red[0][wave] = ss; s_red[1][wave] = sa; }
-    __syncthreads();
+  }
+  if (t == 0) s_role[0] = ep;
+  // the LDS footprint keeps one workgroup per CU; this never-true branch keeps the array
+  const bool never = a.out == reinterpret_cast<float*>(a.sync);
+  if (never) s_occ[t] = make_uint4(t, 0, 0, 0);
+  __syncthreads();
+  if (never) atomicOr(err, (int)s_occ[t ^ 1].x);
+  const uint32_t epoch = (uint32_t)s_role[0] + 1u;
+  if (wave >= 4) {
+    // one wave-uniform block with per-wave bases (p_lo: loads 0-3, p_hi: 4-7, stride st) rather
+    // than a branch per wave, whose register reuse makes the compiler wait on loads the wave
+    // never issued
+    const uint16_t *p_lo, *p_hi;
+    size_t st;
+    if (wave == 4) {
+      p_lo = a.sd + (size_t)(64 * r + (lane >> 3)) * IS + ISX * x + 8 * (lane & 7);
+      p_hi = p_lo + (size_t)32 * IS;
+      st = (size_t)8 * IS;
+    } else if (wave == 7) {
+      p_lo = a.ssg + 8 * lane;
+      p_hi = p_lo;
+      st = 512;
+    } else {
+      const int i = ISX * x + 2 * r + (wave - 5);
+      p_lo = a.sg + (size_t)i * H + 8 * lane;
+      p_hi = a.su + (size_t)i * H + 8 * lane;
+      st = 512;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wx[q] = *reinterpret_cast<const uint4*>(p_lo + st * q);
+      wx[4 + q] = *reinterpret_cast<const uint4*>(p_hi + st * q);
+    }
+  }
+  uint32_t* xb = a.xch + (epoch & 1u) * XW_BUF;          // this launch's words
+  uint32_t* xn = a.xch + ((epoch & 1u) ^ 1u) * XW_BUF;   // the next launch's, zeroed here
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(xb, 0, XW_BUF * 4, 0x00020000);
+  {
     double tot = 0.0, tabs = 0.0;
 #pragma unroll
     for (int q = 0; q < kThreads / 64; ++q) { tot += s_red[0][q]; tabs += s_red[1][q]; }
@@ -481,8 +439,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       float ag = 0.0f, au = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        ag += dot8_bf16(sgw[c], xv[c]);
-        au += dot8_bf16(suw[c], xv[c]);
+        ag += dot8_bf16(wx[c], xv[c]);
+        au += dot8_bf16(wx[4 + c], xv[c]);
       }
       ag = wave_sum_f32(ag);
       au = wave_sum_f32(au);
@@ -490,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     } else if (wave == 7) {
       float gs = 0.0f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) gs += dot8_bf16(sgw[c], xv[c]);
+      for (int c = 0; c < 4; ++c) gs += dot8_bf16(wx[c], xv[c]);
       gs = wave_sum_f32(gs);
       const float p = 1.0f / (1.0f + expf(-gs));
       if (lane == 0) {
@@ -556,7 +514,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      float acc = dot8_bf16(sdw[q], sv);
+      float acc = dot8_bf16(wx[q], sv);
       acc += dpp_f32<0xB1>(acc);
       acc += dpp_f32<0x4E>(acc);
       acc += dpp_f32<0x141>(acc);        // sum over the 8 lanes of the row
@@ -566,7 +524,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __syncthreads();
   const int e = s_ids[x];
   // phase-3 weights: down rows h = 64 r + 2 (t >> 4) + pass of expert e; 16 lanes per row,
-  // lane: super-block b = l16 >> 3, 16-byte nibble chunk c = l16 & 7
+  // lane: super-block b = l16 >> 3, 16-byte nibble chunk c = l16 & 7 (requested with phase 2's)
   constexpr size_t drowb = (I / 256) * 144;
   uint4 dh[2], dq[2];
   {
@@ -632,20 +590,26 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       sxl += xl[i];
       sxh += xh[i];
     }
+    // both rows before either store: a load wait placed after an agent-scope store would also
+    // wait for that store's write-through (vmcnt counts both)
+    float v[2];
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) v[pass] = row16_sum_f32(q4k_chunk_dot(dh[pass], dq[pass], gq, xl, xh, sxl, sxh));
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
-      const float v = row16_sum_f32(q4k_chunk_dot(dh[pass], dq[pass], gq, xl, xh, sxl, sxh));
       if (l16 == 0) {
         const int h = 64 * r + 2 * (t >> 4) + pass;
-        xstore(xb + XW_Y + H * x + h, xenc(v));
-        if (a.expert_raw) a.expert_raw[(size_t)x * H + h] = v;
+        xstore(xb + XW_Y + H * x + h, xenc(v[pass]));
+        if (a.expert_raw) a.expert_raw[(size_t)x * H + h] = v[pass];
       }
     }
   }
 
   // ------------------------------------------------------------------------------ phase 4 --
-  // wave 0 collects its combine rows, waves 4-7 warm the next layer's weights and clear the next
-  // launch's exchange words
+  // wave 0 collects its combine rows, waves 4-7 warm the next layer's router rows and norm weight
+  // and clear the next launch's exchange words. Only what the next layer's routing waits on is
+  // warmed: its shared-expert rows have slack there, and reading them here (6.3 MB more) slowed
+  // this layer's combine exchange by more than they saved.
   if (wave >= 4) {
     if (a.nx_router) {
       // warm XCD x's L2 with what role (x, r) reads first in the next layer
@@ -654,22 +618,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       const uint4* nr = reinterpret_cast<const uint4*>(a.nx_router + (size_t)8 * r * H);
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc ^= xor4(nr[u + 256 * q]);
-      const int i0 = ISX * x + 2 * r;
-      const uint4* ng = reinterpret_cast<const uint4*>(a.nx_sg + (size_t)i0 * H);
-      const uint4* nu = reinterpret_cast<const uint4*>(a.nx_su + (size_t)i0 * H);
-#pragma unroll
-      for (int q = 0; q < 2; ++q) acc ^= xor4(ng[u + 256 * q]) ^ xor4(nu[u + 256 * q]);
-      acc ^= xor4(reinterpret_cast<const uint4*>(a.nx_ssg)[u]);
       if (a.nx_norm) {
         const uint4* nn = reinterpret_cast<const uint4*>(a.nx_norm);
         acc ^= xor4(nn[u]) ^ xor4(nn[u + 256]);
       }
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int row = 64 * r + ((u + 256 * q) >> 3), cc = (u + 256 * q) & 7;
-        acc ^= xor4(*reinterpret_cast<const uint4*>(a.nx_sd + (size_t)row * IS + ISX * x + 8 * cc));
-      }
-      if (acc == 0x9E3779B9u && a.nx_ssg == reinterpret_cast<const uint16_t*>(a.sync)) atomicOr(err, 0);
+      if (acc == 0x9E3779B9u && a.out == reinterpret_cast<float*>(a.sync)) atomicOr(err, 0);
     }
     // the next launch's exchange words (its epoch parity), cleared last: nothing here waits on them
     if (t - 256 < kClearPerWg && kClearPerWg * j + t - 256 < XW_BUF) xstore(xn + kClearPerWg * j + t - 256, 0u);
@@ -698,13 +651,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       if (a.shared_out) a.shared_out[h] = sh;
       a.out[h] = resid + acc + sh;
     }
-    // this CU's (or, without a table, this role's) launch count for the next launch
-    if (t == 0) {
-      if (s_role[3] >= 0)
-        astore(a.sync + kCuTable + 64 * x + s_role[3], (int)((epoch << 8) | (uint32_t)(r + 1)));
-      else
-        astore(a.sync + kRoleEpoch + kPer * x + r, (int)epoch);
-    }
+    // this role's launch count, for the next launch
+    if (t == 0) astore(a.sync + kRoleEpoch + kPer * x + r, (int)epoch);
   }
 }
 
@@ -727,16 +675,6 @@ bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, 
 
 size_t moe_layer_exchange_bytes() { return (size_t)2 * XW_BUF * 4; }
 
-int moe_launch_cu_probe(int* sync, hipStream_t st) {
-  int dev = 0, ncu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return moe_set_error(MOE_E_HIP, "cu_probe: device query failed");
-  if (ncu < kG) return MOE_OK;          // the single-launch layer does not run here
-  hipLaunchKernelGGL(k_cu_probe, dim3(kG), dim3(64), 0, st, sync);
-  return moe_check_launch("cu_probe");
-}
-
 int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st) {
   LayerArgs a;
   a.x = L.x; a.residual = L.residual; a.w_router = (const uint16_t*)L.w_router; a.bias = L.bias;
@@ -750,13 +688,8 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   a.exact_order = (L.ids_out_requested || L.expert_raw) ? 1 : 0;
   a.norm_w = L.norm_w;
   a.norm_eps = L.norm_eps;
-  const bool nx = L.nx_router && L.nx_sg && L.nx_su && L.nx_sd && L.nx_ssg;
-  a.nx_router = nx ? (const uint16_t*)L.nx_router : nullptr;
-  a.nx_sg = nx ? (const uint16_t*)L.nx_sg : nullptr;
-  a.nx_su = nx ? (const uint16_t*)L.nx_su : nullptr;
-  a.nx_sd = nx ? (const uint16_t*)L.nx_sd : nullptr;
-  a.nx_ssg = nx ? (const uint16_t*)L.nx_ssg : nullptr;
-  a.nx_norm = nx ? L.nx_norm : nullptr;
+  a.nx_router = (const uint16_t*)L.nx_router;
+  a.nx_norm = L.nx_router ? L.nx_norm : nullptr;
   if (L.x_dtype == MOE_DT_F32)
     hipLaunchKernelGGL(k_dec_layer<MOE_DT_F32>, dim3(kG), dim3(kThreads), 0, st, a);
   else

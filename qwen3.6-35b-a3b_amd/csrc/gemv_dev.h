@@ -51,13 +51,16 @@ __device__ __forceinline__ float q4k_chunk_dot(uint4 hdr, uint4 qs, int g, const
   const float d = f16_to_f32(hdr.x & 0xFFFFu), dmin = f16_to_f32(hdr.x >> 16);
   // sub-blocks j = 2g + h, byte b = j & 3 of the 12 scale bytes s0 = hdr.y, s1 = hdr.z, s2 = hdr.w
   const uint32_t sh0 = 16u * (uint32_t)(g & 1), sh1 = sh0 + 8u;
-  const bool lowj = g < 2;               // sub-blocks 0..3: plain 6-bit fields
+  // sub-blocks 0..3 take plain 6-bit fields, 4..7 the split ones; both forms are computed and one
+  // is picked by a lane mask (a select the compiler keeps as bit operations, not as two
+  // exec-masked paths)
+  const uint32_t low = 0u - (uint32_t)(g < 2);
   const uint32_t y0 = hdr.y >> sh0, z0 = hdr.z >> sh0, w0 = hdr.w >> sh0;
   const uint32_t y1 = hdr.y >> sh1, z1 = hdr.z >> sh1, w1 = hdr.w >> sh1;
-  const uint32_t sc0 = lowj ? (y0 & 63u) : ((w0 & 15u) | ((y0 >> 2) & 48u));
-  const uint32_t m0 = lowj ? (z0 & 63u) : (((w0 >> 4) & 15u) | ((z0 >> 2) & 48u));
-  const uint32_t sc1 = lowj ? (y1 & 63u) : ((w1 & 15u) | ((y1 >> 2) & 48u));
-  const uint32_t m1 = lowj ? (z1 & 63u) : (((w1 >> 4) & 15u) | ((z1 >> 2) & 48u));
+  const uint32_t sc0 = ((y0 & 63u) & low) | (((w0 & 15u) | ((y0 >> 2) & 48u)) & ~low);
+  const uint32_t m0 = ((z0 & 63u) & low) | ((((w0 >> 4) & 15u) | ((z0 >> 2) & 48u)) & ~low);
+  const uint32_t sc1 = ((y1 & 63u) & low) | (((w1 & 15u) | ((y1 >> 2) & 48u)) & ~low);
+  const uint32_t m1 = ((z1 & 63u) & low) | ((((w1 >> 4) & 15u) | ((z1 >> 2) & 48u)) & ~low);
   const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
   float dl = 0.0f, dh = 0.0f;
 #pragma unroll

@@ -113,8 +113,7 @@ struct MoeDecodeLaunch {
   const float* norm_w;     // post-attention RMSNorm weight [H] f32, or NULL (x is the input)
   float norm_eps;
   // the next layer's routing-independent weights (single-launch layer's L2 warm-up), or NULL
-  const void *nx_router = nullptr, *nx_sg = nullptr, *nx_su = nullptr, *nx_sd = nullptr,
-             *nx_ssg = nullptr;
+  const void* nx_router = nullptr;      // the next layer's router and norm weights (warm-up hint)
   const float* nx_norm = nullptr;
 };
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
@@ -132,9 +131,6 @@ constexpr size_t kSyncBytes = 524288;
 bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, int dn_fmt);
 size_t moe_layer_exchange_bytes();
 int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st);
-// records this device's CU layout (rank of each CU inside its XCD) into the sync words; part of
-// moe_workspace_init (no-op on devices where the single-launch layer does not run)
-int moe_launch_cu_probe(int* sync, hipStream_t st);
 
 // workspace carving
 struct MoeWs {
