@@ -41,8 +41,10 @@ enum {
 /* dtypes of activations / outputs */
 enum { MOE_DT_F32 = 0, MOE_DT_BF16 = 1 };
 
-/* weight formats: ggml_type ids (tools/gguf_reader.py:10-51 block table) */
-enum { MOE_FMT_Q4_K = 12, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
+/* weight formats: ggml_type ids (tools/gguf_reader.py:10-51 block table). Routed gate_up: Q4_K,
+ * Q6_K or BF16; routed down: Q4_K, Q5_K (the shipped artifact's down in 37 of its 40 layers,
+ * engine/README.md:33,115), Q6_K or BF16; moe_dequant: Q4_K, Q5_K, Q6_K. */
+enum { MOE_FMT_Q4_K = 12, MOE_FMT_Q5_K = 13, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
 
 /* expert contraction path: GEMV = fused decode + f32 GEMV; MFMA = tiles decoded to f16 in LDS on
  * MFMA (f32 accumulation); MFMA_BF16 = the same with bf16 operands (8 significant bits instead of
@@ -60,8 +62,8 @@ const char *moe_last_error(void);
 size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s);
 
 /* Bit-exact super-block decode: n_elts elements of `fmt` blocks -> f32 or bf16 (RNE of the exact
- * f32 value). Replaces tools/gguf_reader.py:248-268 (_deq_q4_k), :299-322 (_deq_q6_k) and
- * tools/gguf_fast_dequant.py:87-152 (dequant_np). n_elts % 256 == 0. */
+ * f32 value). Replaces tools/gguf_reader.py:248-268 (_deq_q4_k), :271-296 (_deq_q5_k),
+ * :299-322 (_deq_q6_k) and tools/gguf_fast_dequant.py:87-152 (dequant_np). n_elts % 256 == 0. */
 int moe_dequant(const void *blocks, int fmt, int64_t n_elts, void *out, int out_dtype,
                 void *stream);
 

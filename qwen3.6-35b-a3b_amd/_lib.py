@@ -23,6 +23,7 @@ ERROR_NAMES = {MOE_E_ARG: "bad-argument", MOE_E_FORMAT: "unsupported-format",
 MOE_DT_F32 = 0
 MOE_DT_BF16 = 1
 MOE_FMT_Q4_K = 12
+MOE_FMT_Q5_K = 13
 MOE_FMT_Q6_K = 14
 MOE_FMT_BF16 = 30
 MOE_PATH_AUTO = 0

@@ -97,6 +97,7 @@ int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_
   if (out_dtype != MOE_DT_F32 && out_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_dequant: bad out_dtype %d", out_dtype);
   if (fmt == MOE_FMT_Q4_K && !aligned16(blocks)) return moe_set_error(MOE_E_ARG, "moe_dequant: Q4_K blocks must be 16-byte aligned");
   if (fmt == MOE_FMT_Q6_K && (reinterpret_cast<uintptr_t>(blocks) & 1u)) return moe_set_error(MOE_E_ARG, "moe_dequant: Q6_K blocks must be 2-byte aligned");
+  if (fmt == MOE_FMT_Q5_K && !aligned16(blocks)) return moe_set_error(MOE_E_ARG, "moe_dequant: Q5_K blocks must be 16-byte aligned");
   return moe_launch_dequant(blocks, fmt, n_elts, out, out_dtype, (hipStream_t)stream);
 }
 
@@ -151,9 +152,12 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
     return moe_launch_gemv_down(S, dn, dn_fmt, offsets, hit_list, max_hits, H, I, y, st);
   }
   const size_t gu_row = gu_fmt == MOE_FMT_Q4_K ? (size_t)H / 256 * 144 : gu_fmt == MOE_FMT_Q6_K ? (size_t)H / 256 * 210 : (size_t)H * 2;
-  const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
+  const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q5_K ? (size_t)I / 256 * 176
+                      : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
   const uint8_t* g = reinterpret_cast<const uint8_t*>(gu);
-  const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_supports(dn_fmt) &&
+  if (dn_fmt == MOE_FMT_Q5_K && path == MOE_PATH_MFMA_BF16)
+    return moe_set_error(MOE_E_FORMAT, "moe_experts: Q5_K down runs on the GEMV and MFMA (f16) paths");
+  const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_down_supports(dn_fmt) &&
                   H % 256 == 0 && I % 256 == 0;
   const int bm = v2 ? MOE_GEMM3_BM : MOE_GEMM_BM;
   const int max_tiles = moe_max_mtiles(P, E, bm);
@@ -187,7 +191,7 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
 static int check_wfmt(int gu_fmt, int dn_fmt, const void* gu, const void* dn, const char* who) {
   if (gu_fmt != MOE_FMT_Q4_K && gu_fmt != MOE_FMT_Q6_K && gu_fmt != MOE_FMT_BF16)
     return moe_set_error(MOE_E_FORMAT, "%s: unsupported gate_up format %d", who, gu_fmt);
-  if (dn_fmt != MOE_FMT_Q4_K && dn_fmt != MOE_FMT_Q6_K && dn_fmt != MOE_FMT_BF16)
+  if (dn_fmt != MOE_FMT_Q4_K && dn_fmt != MOE_FMT_Q5_K && dn_fmt != MOE_FMT_Q6_K && dn_fmt != MOE_FMT_BF16)
     return moe_set_error(MOE_E_FORMAT, "%s: unsupported down format %d", who, dn_fmt);
   if (!aligned16(gu) || !aligned16(dn)) return moe_set_error(MOE_E_ARG, "%s: expert weights must be 16-byte aligned", who);
   return MOE_OK;
@@ -203,7 +207,7 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, int gate_up_f
   MOE_TRY(check_geom(T, H, I, E, K, "moe_experts"));
   MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, down_q, "moe_experts"));
   if (path == MOE_PATH_GEMV && gate_up_fmt != MOE_FMT_Q4_K) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K gate_up only");
-  if (path == MOE_PATH_GEMV && down_fmt == MOE_FMT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K / Q6_K down only");
+  if (path == MOE_PATH_GEMV && down_fmt == MOE_FMT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K / Q5_K / Q6_K down only");
   if (!aligned16(x)) return moe_set_error(MOE_E_ARG, "moe_experts: x must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
@@ -294,7 +298,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   int* sync = reinterpret_cast<int*>(w.take(kSyncBytes));
   const int rpath = pick_path(path, T, gate_up_fmt);
   const bool decode = T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
-                      (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q6_K) && I_s % 128 == 0 && E % 4 == 0;
+                      (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q5_K || down_fmt == MOE_FMT_Q6_K) &&
+                      I_s % 128 == 0 && E % 4 == 0;
   const bool one_launch = decode && path != MOE_PATH_GEMV_MULTI &&
                           moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt);
   if (norm_w && !one_launch) {

@@ -204,24 +204,29 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecodeArgs a) {
 }
 
 // down-row dot for 16 lanes: (row of I elements of down weights) . s (I floats), lanes l16 of
-// the group; Q4_K: lane = 8*block + chunk over a 512-element window; Q6_K: lane = 8*block + 4g + k
+// the group; Q4_K / Q5_K: lane = 8*block + chunk over a 512-element window; Q6_K: lane =
+// 8*block + 4g + k
 template <int DFMT>
 __device__ __forceinline__ float down_dot16(const uint8_t* rowp, const float* sv, int I, int l16) {
   float acc = 0.0f;
   const int b = l16 >> 3, c = l16 & 7;
-  if (DFMT == MOE_FMT_Q4_K) {
+  if (DFMT == MOE_FMT_Q4_K || DFMT == MOE_FMT_Q5_K) {
+    constexpr int kBB = DFMT == MOE_FMT_Q5_K ? 176 : 144, kQs = DFMT == MOE_FMT_Q5_K ? 48 : 16;
     const int g = c >> 1, l0 = 16 * (c & 1);
     for (int bg = 0; bg < I / 512; ++bg) {
       const int blk = bg * 2 + b;
-      const uint8_t* p = rowp + (size_t)blk * 144;
+      const uint8_t* p = rowp + (size_t)blk * kBB;
       const uint4 hdr = *reinterpret_cast<const uint4*>(p);
-      const uint4 qs = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
+      const uint4 qs = *reinterpret_cast<const uint4*>(p + kQs + 16 * c);
       float xl[16], xh[16];
       load_x32<MOE_DT_F32>(sv, (size_t)256 * blk + 64 * g + l0, xl, xh);
       float sxl = 0.0f, sxh = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) { sxl += xl[i]; sxh += xh[i]; }
-      acc += q4k_chunk_dot(hdr, qs, g, xl, xh, sxl, sxh);
+      if (DFMT == MOE_FMT_Q5_K)
+        acc += q5k_chunk_dot(hdr, qs, *reinterpret_cast<const uint4*>(p + 16 + l0), g, xl, xh, sxl, sxh);
+      else
+        acc += q4k_chunk_dot(hdr, qs, g, xl, xh, sxl, sxh);
     }
   } else {
     const int g = c >> 2, k = c & 3;
@@ -258,7 +263,7 @@ __global__ __launch_bounds__(256) void k_dec_down_combine(DecodeArgs a) {
   __shared__ int order[8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g4 = lane >> 4;
   const int h0 = blockIdx.x * 8;
-  const size_t rowb = (size_t)(a.I / 256) * (DFMT == MOE_FMT_Q4_K ? 144 : 210);
+  const size_t rowb = (size_t)(a.I / 256) * (DFMT == MOE_FMT_Q4_K ? 144 : DFMT == MOE_FMT_Q5_K ? 176 : 210);
   if (threadIdx.x == 0) {
     // slots in ascending expert id (bubble sort on (id, slot) pairs, constant indices only)
     int id[8], sl[8];
@@ -340,6 +345,8 @@ int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st) {
   }
   if (L.dn_fmt == MOE_FMT_Q4_K)
     hipLaunchKernelGGL(k_dec_down_combine<MOE_FMT_Q4_K>, dim3(L.H / 8), dim3(256), 0, st, a);
+  else if (L.dn_fmt == MOE_FMT_Q5_K)
+    hipLaunchKernelGGL(k_dec_down_combine<MOE_FMT_Q5_K>, dim3(L.H / 8), dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL(k_dec_down_combine<MOE_FMT_Q6_K>, dim3(L.H / 8), dim3(256), 0, st, a);
   return moe_check_launch("decode_fused");

@@ -42,6 +42,48 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
   }
 }
 
+// Q5_K: one thread per 16-byte quarter of the nibble array as in Q4_K, plus the 16 qh bytes of its
+// element positions (176-byte blocks are 16-byte aligned); q = nibble | 5th bit << 4 <= 31, so
+// (d*sc)*q is exact in f32 (<= 22 bits) and fma(d*sc, q, -(dmin*m)) again rounds once.
+template <int OUT>
+__global__ __launch_bounds__(256) void k_dequant_q5k(const uint8_t* __restrict__ blk, int64_t nb,
+                                                      void* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t b = gid >> 3;
+  const int c = gid & 7;
+  if (b >= nb) return;
+  const uint8_t* p = blk + b * 176;
+  const uint4 hdr = *reinterpret_cast<const uint4*>(p);
+  const int g = c >> 1, l0 = 16 * (c & 1);
+  const uint4 qh = *reinterpret_cast<const uint4*>(p + 16 + l0);
+  const uint4 qs = *reinterpret_cast<const uint4*>(p + 48 + 16 * c);
+  const float d = f16_to_f32(hdr.x & 0xFFFFu), dmin = f16_to_f32(hdr.x >> 16);
+  uint32_t sc0, m0, sc1, m1;
+  q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g, sc0, m0);
+  q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g + 1, sc1, m1);
+  const float ds0 = d * (float)sc0, dm0 = dmin * (float)m0;
+  const float ds1 = d * (float)sc1, dm1 = dmin * (float)m1;
+  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+  const uint32_t h[4] = {qh.x, qh.y, qh.z, qh.w};
+  const int64_t e0 = b * 256 + 64 * g + l0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    const uint32_t hb = (h[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    const uint32_t q0 = (byte & 15u) | (((hb >> (2 * g)) & 1u) << 4);
+    const uint32_t q1 = (byte >> 4) | (((hb >> (2 * g + 1)) & 1u) << 4);
+    const float v0 = fmaf(ds0, (float)q0, -dm0);
+    const float v1 = fmaf(ds1, (float)q1, -dm1);
+    if (OUT == MOE_DT_F32) {
+      reinterpret_cast<float*>(out)[e0 + i] = v0;
+      reinterpret_cast<float*>(out)[e0 + 32 + i] = v1;
+    } else {
+      reinterpret_cast<uint16_t*>(out)[e0 + i] = (uint16_t)f32_to_bf16(v0);
+      reinterpret_cast<uint16_t*>(out)[e0 + 32 + i] = (uint16_t)f32_to_bf16(v1);
+    }
+  }
+}
+
 // one thread per 32-element chunk (g, k) of a Q6_K block; bytes read one at a time because the
 // 210-byte blocks are only 2-byte aligned.
 template <int OUT>
@@ -81,6 +123,9 @@ int moe_launch_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, i
   if (fmt == MOE_FMT_Q4_K) {
     if (out_dtype == MOE_DT_F32) hipLaunchKernelGGL(k_dequant_q4k<MOE_DT_F32>, grid, dim3(256), 0, st, b, nb, out);
     else hipLaunchKernelGGL(k_dequant_q4k<MOE_DT_BF16>, grid, dim3(256), 0, st, b, nb, out);
+  } else if (fmt == MOE_FMT_Q5_K) {
+    if (out_dtype == MOE_DT_F32) hipLaunchKernelGGL(k_dequant_q5k<MOE_DT_F32>, grid, dim3(256), 0, st, b, nb, out);
+    else hipLaunchKernelGGL(k_dequant_q5k<MOE_DT_BF16>, grid, dim3(256), 0, st, b, nb, out);
   } else if (fmt == MOE_FMT_Q6_K) {
     if (out_dtype == MOE_DT_F32) hipLaunchKernelGGL(k_dequant_q6k<MOE_DT_F32>, grid, dim3(256), 0, st, b, nb, out);
     else hipLaunchKernelGGL(k_dequant_q6k<MOE_DT_BF16>, grid, dim3(256), 0, st, b, nb, out);

@@ -70,6 +70,36 @@ __device__ __forceinline__ void q4_16(uint4 w, f16x2_t ds, f16x2_t ndm, uint4& o
   o1.w = q4_pair<HIGH>(w.w, 0x0C030C02u, ds, ndm);
 }
 
+// Q5_K: the same with the 5th bits (bytes of qh at the same positions; hs = the bit of each byte:
+// 2g for the low nibbles, 2g + 1 for the high): under 0x6400 the bit goes to mantissa bit 4
+// (1024 + q, q <= 31), under 0x5400 to mantissa bit 8 (64 + q). Shifting the permuted qh pair
+// right by hs <= 7 puts each lane's bit at the lane's bit 0 and moves the upper byte's other
+// bits to lane bit 9 or above, so the 1-bit masks read each lane's own byte.
+template <bool HIGH>
+__device__ __forceinline__ uint32_t q5_pair(uint32_t w, uint32_t h, uint32_t sel, uint32_t hs,
+                                            f16x2_t ds, f16x2_t ndm) {
+  const uint32_t p = __builtin_amdgcn_perm(0u, w, sel);
+  const uint32_t hp = __builtin_amdgcn_perm(0u, h, sel) >> hs;
+  const uint32_t magic = HIGH ? and_or_s(p, 0x00F000F0u, 0x54005400u) | ((hp << 8) & 0x01000100u)
+                              : and_or_s(p, 0x000F000Fu, 0x64006400u) | ((hp << 4) & 0x00100010u);
+  const _Float16 off = HIGH ? (_Float16)64.0f : (_Float16)1024.0f;
+  const f16x2_t q = __builtin_bit_cast(f16x2_t, magic) - (f16x2_t){off, off};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, ds, ndm));
+}
+
+template <bool HIGH>
+__device__ __forceinline__ void q5_16(uint4 w, uint4 h, uint32_t hs, f16x2_t ds, f16x2_t ndm,
+                                      uint4& o0, uint4& o1) {
+  o0.x = q5_pair<HIGH>(w.x, h.x, 0x0C010C00u, hs, ds, ndm);
+  o0.y = q5_pair<HIGH>(w.x, h.x, 0x0C030C02u, hs, ds, ndm);
+  o0.z = q5_pair<HIGH>(w.y, h.y, 0x0C010C00u, hs, ds, ndm);
+  o0.w = q5_pair<HIGH>(w.y, h.y, 0x0C030C02u, hs, ds, ndm);
+  o1.x = q5_pair<HIGH>(w.z, h.z, 0x0C010C00u, hs, ds, ndm);
+  o1.y = q5_pair<HIGH>(w.z, h.z, 0x0C030C02u, hs, ds, ndm);
+  o1.z = q5_pair<HIGH>(w.w, h.w, 0x0C010C00u, hs, ds, ndm);
+  o1.w = q5_pair<HIGH>(w.w, h.w, 0x0C030C02u, hs, ds, ndm);
+}
+
 __device__ __forceinline__ void q4_scales(uint4 hdr, int j, f16x2_t& ds, f16x2_t& ndm) {
   uint32_t sc, m;
   q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
@@ -117,6 +147,37 @@ struct WRaw<MOE_FMT_Q4_K> {
   }
 };
 template <>
+struct WRaw<MOE_FMT_Q5_K> {
+  uint4 hdr, lo, hi, h0, h1;            // header, the step group's 32 nibble bytes, qh[0..31]
+  __device__ __forceinline__ void load(const uint8_t* row, int k0) {
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 176;
+    const int g = (k0 >> 6) & 3;
+    hdr = *reinterpret_cast<const uint4*>(b);
+    h0 = *reinterpret_cast<const uint4*>(b + 16);
+    h1 = *reinterpret_cast<const uint4*>(b + 32);
+    lo = *reinterpret_cast<const uint4*>(b + 48 + 32 * g);
+    hi = *reinterpret_cast<const uint4*>(b + 48 + 32 * g + 16);
+  }
+  // 64 f16 in k order: sub-block 2g (low nibbles, qh bit 2g) then 2g + 1 (high, bit 2g + 1)
+  __device__ __forceinline__ void decode(int k0, uint16_t* dst) const {
+    const int g = (k0 >> 6) & 3;
+    const uint32_t hs = 2u * (uint32_t)g;
+    f16x2_t ds0, nd0, ds1, nd1;
+    q4_scales(hdr, 2 * g, ds0, nd0);
+    q4_scales(hdr, 2 * g + 1, ds1, nd1);
+    uint4 a, b;
+    uint4* d = reinterpret_cast<uint4*>(dst);
+    q5_16<false>(lo, h0, hs, ds0, nd0, a, b);     // elements 0..15
+    d[0] = a; d[1] = b;
+    q5_16<false>(hi, h1, hs, ds0, nd0, a, b);     // 16..31
+    d[2] = a; d[3] = b;
+    q5_16<true>(lo, h0, hs + 1, ds1, nd1, a, b);  // 32..47
+    d[4] = a; d[5] = b;
+    q5_16<true>(hi, h1, hs + 1, ds1, nd1, a, b);  // 48..63
+    d[6] = a; d[7] = b;
+  }
+};
+template <>
 struct WRaw<MOE_FMT_BF16> {
   uint4 q[8];
   __device__ __forceinline__ void load(const uint8_t* row, int k0) {
@@ -133,7 +194,8 @@ struct WRaw<MOE_FMT_BF16> {
 };
 
 __device__ __forceinline__ size_t row_bytes(int fmt, int cols) {
-  return fmt == MOE_FMT_Q4_K ? (size_t)(cols / 256) * 144 : (size_t)cols * 2;
+  return fmt == MOE_FMT_Q4_K ? (size_t)(cols / 256) * 144
+       : fmt == MOE_FMT_Q5_K ? (size_t)(cols / 256) * 176 : (size_t)cols * 2;
 }
 
 __device__ __forceinline__ int tile_rows(const int32_t* tiles, const int32_t* offsets, int T,
@@ -191,11 +253,12 @@ struct PSet {
 // stores step ks + 1 (set (ks + 1) % kD) into the other buffer and requests step ks + kD into the
 // set it just freed, so each request has kD - 1 steps to land. kD is even and divides the step
 // count (H / 64 = 32 for gate_up, I / 64 = 8 for down), so set and buffer indices are compile-time.
-// Q4_K sets are 28 registers (4 deep); bf16 sets 48 (2 deep, within the 256-register budget).
+// Q4_K sets are 28 registers and Q5_K 40 (4 deep); bf16 sets 48 (2 deep, within the
+// 256-register budget).
 template <int WFMT>
 __device__ __forceinline__ void produce(int nk, const ARows& asrc, const uint8_t* wrow, int p,
                                         Smem& sm) {
-  constexpr int kD = WFMT == MOE_FMT_Q4_K ? 4 : 2;
+  constexpr int kD = WFMT == MOE_FMT_BF16 ? 2 : 4;
   PSet<WFMT> s[kD];
 #pragma unroll
   for (int i = 0; i < kD; ++i) s[i].load(wrow, asrc, min(i, nk - 1) * kBK, p);
@@ -378,6 +441,9 @@ __global__ __launch_bounds__(256) void k_to_f16(const void* __restrict__ x, size
 using namespace moe;
 
 bool moe_gemm3_supports(int fmt) { return fmt == MOE_FMT_Q4_K || fmt == MOE_FMT_BF16; }
+bool moe_gemm3_down_supports(int fmt) {
+  return fmt == MOE_FMT_Q4_K || fmt == MOE_FMT_Q5_K || fmt == MOE_FMT_BF16;
+}
 
 int moe_launch_to_f16(const void* x, int x_dtype, size_t n, uint16_t* out, hipStream_t st) {
   if (n % 8) return moe_set_error(MOE_E_UNSUPPORTED, "to_f16: n %% 8 != 0");
@@ -420,6 +486,8 @@ int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t
   const dim3 grid(g3::kXcd * ((ntile + g3::kXcd - 1) / g3::kXcd) * (H / g3::kBN));
   if (fmt == MOE_FMT_Q4_K)
     hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q4_K>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
+  else if (fmt == MOE_FMT_Q5_K)
+    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q5_K>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
   else if (fmt == MOE_FMT_BF16)
     hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_BF16>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
   else

@@ -1,4 +1,4 @@
-// Decode-path expert contraction: fused Q4_K / Q6_K super-block decode + f32 GEMV, one pass over
+// Decode-path expert contraction: fused Q4_K / Q5_K / Q6_K super-block decode + f32 GEMV, one pass over
 // each hit expert's bytes (engine/m3_forward.py:452-463; speccheck/moe_ref.py:367-392).
 //
 // Q4_K gate_up (rows of H = 8 blocks x 144 B): a wave covers one full 2048-wide row per step,
@@ -61,9 +61,11 @@ __global__ __launch_bounds__(256) void k_gemv_gateup_q4k(
   }
 }
 
-// ------------------------------------------------------------------------------ down, Q4_K --
-// grid (H/64, max_hits); wave w: rows 64*bx + 16w + 4*step + (lane>>4), step 0..3
-__global__ __launch_bounds__(256) void k_gemv_down_q4k(const float* __restrict__ S,
+// ----------------------------------------------------------------------- down, Q4_K / Q5_K --
+// grid (H/64, max_hits); wave w: rows 64*bx + 16w + 4*step + (lane>>4), step 0..3. Q5_K rows
+// (176-byte blocks) add the lane's 16 qh bytes to the Q4_K chunk.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gemv_down_k(const float* __restrict__ S,
                                                         const uint8_t* __restrict__ dn,
                                                         const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ hit_list,
@@ -75,7 +77,9 @@ __global__ __launch_bounds__(256) void k_gemv_down_q4k(const float* __restrict__
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, rsub = lane >> 4;
   const int b = l16 >> 3, c = l16 & 7, g = c >> 1, l0 = 16 * (c & 1);
-  const size_t rowb = (size_t)(I / 256) * 144;
+  constexpr int kBB = FMT == MOE_FMT_Q5_K ? 176 : 144;     // block bytes
+  constexpr int kQs = FMT == MOE_FMT_Q5_K ? 48 : 16;       // nibble array offset
+  const size_t rowb = (size_t)(I / 256) * kBB;
   const uint8_t* ebase = dn + (size_t)e * H * rowb;
   const int rbase = blockIdx.x * 64 + wave * 16;
   const int nbg = I / 512;
@@ -88,16 +92,19 @@ __global__ __launch_bounds__(256) void k_gemv_down_q4k(const float* __restrict__
       float sxl = 0.0f, sxh = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) { sxl += xl[i]; sxh += xh[i]; }
-      uint4 hdr[4], qs[4];
+      uint4 hdr[4], qs[4], qh[4];
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int row = rbase + 4 * st + rsub;
-        const uint8_t* p = ebase + (size_t)row * rowb + (size_t)blk * 144;
+        const uint8_t* p = ebase + (size_t)row * rowb + (size_t)blk * kBB;
         hdr[st] = *reinterpret_cast<const uint4*>(p);
-        qs[st] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
+        qs[st] = *reinterpret_cast<const uint4*>(p + kQs + 16 * c);
+        if (FMT == MOE_FMT_Q5_K) qh[st] = *reinterpret_cast<const uint4*>(p + 16 + l0);
       }
 #pragma unroll
-      for (int st = 0; st < 4; ++st) acc[st] += q4k_chunk_dot(hdr[st], qs[st], g, xl, xh, sxl, sxh);
+      for (int st = 0; st < 4; ++st)
+        acc[st] += FMT == MOE_FMT_Q5_K ? q5k_chunk_dot(hdr[st], qs[st], qh[st], g, xl, xh, sxl, sxh)
+                                       : q4k_chunk_dot(hdr[st], qs[st], g, xl, xh, sxl, sxh);
     }
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -207,10 +214,12 @@ int moe_launch_gemv_down(const float* S, const void* dn, int fmt, const int32_t*
   dim3 grid(H / 64, max_hits);
   const uint8_t* w = reinterpret_cast<const uint8_t*>(dn);
   if (fmt == MOE_FMT_Q4_K)
-    hipLaunchKernelGGL(k_gemv_down_q4k, grid, dim3(256), 0, st, S, w, offsets, hit_list, H, I, y);
+    hipLaunchKernelGGL(k_gemv_down_k<MOE_FMT_Q4_K>, grid, dim3(256), 0, st, S, w, offsets, hit_list, H, I, y);
+  else if (fmt == MOE_FMT_Q5_K)
+    hipLaunchKernelGGL(k_gemv_down_k<MOE_FMT_Q5_K>, grid, dim3(256), 0, st, S, w, offsets, hit_list, H, I, y);
   else if (fmt == MOE_FMT_Q6_K)
     hipLaunchKernelGGL(k_gemv_down_q6k, grid, dim3(256), 0, st, S, w, offsets, hit_list, H, I, y);
   else
-    return moe_set_error(MOE_E_FORMAT, "GEMV down supports Q4_K / Q6_K (got %d)", fmt);
+    return moe_set_error(MOE_E_FORMAT, "GEMV down supports Q4_K / Q5_K / Q6_K (got %d)", fmt);
   return moe_check_launch("gemv_down");
 }

@@ -1,4 +1,5 @@
-// Device helpers of the fused-decode GEMV kernels (shared by gemv.hip, shared.hip, decode.hip).
+// Device helpers of the fused-decode GEMV kernels (shared by gemv.hip, shared.hip, decode.hip,
+// decode_layer.hip).
 #pragma once
 #include "common.h"
 
@@ -66,6 +67,43 @@ __device__ __forceinline__ float q4k_chunk_dot(uint4 hdr, uint4 qs, int g, const
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t lo = and_opaque(w[i], 0x0F0F0F0Fu), hi = and_opaque(w[i] >> 4, 0x0F0F0F0Fu);
+    dl = fmaf(xl[4 * i], (float)(lo & 0xFFu), dl);
+    dh = fmaf(xh[4 * i], (float)(hi & 0xFFu), dh);
+    dl = fmaf(xl[4 * i + 1], (float)((lo >> 8) & 0xFFu), dl);
+    dh = fmaf(xh[4 * i + 1], (float)((hi >> 8) & 0xFFu), dh);
+    dl = fmaf(xl[4 * i + 2], (float)((lo >> 16) & 0xFFu), dl);
+    dh = fmaf(xh[4 * i + 2], (float)((hi >> 16) & 0xFFu), dh);
+    dl = fmaf(xl[4 * i + 3], (float)(lo >> 24), dl);
+    dh = fmaf(xh[4 * i + 3], (float)(hi >> 24), dh);
+  }
+  return d * ((float)sc0 * dl + (float)sc1 * dh) - dmin * ((float)m0 * sxl + (float)m1 * sxh);
+}
+
+// The same for a Q5_K chunk: qs holds the low 4 bits as in Q4_K and qh the 16 bytes qh[l0..l0+15]
+// of its element positions; the 5th bit of element 64g + l is bit 2g of qh[l], that of element
+// 64g + 32 + l bit 2g + 1 (tools/gguf_reader.py:271-296). Shifting a qh word right by 2g puts
+// each byte's bit 2g at that byte's bit 0 (bits leaving the next byte land at bit 2 or above), so
+// one shift and one mask per word place the 5th bits at bit 4 of each byte, next to the nibble.
+__device__ __forceinline__ float q5k_chunk_dot(uint4 hdr, uint4 qs, uint4 qh, int g, const float* xl,
+                                               const float* xh, float sxl, float sxh) {
+  const float d = f16_to_f32(hdr.x & 0xFFFFu), dmin = f16_to_f32(hdr.x >> 16);
+  const uint32_t sh0 = 16u * (uint32_t)(g & 1), sh1 = sh0 + 8u;
+  const uint32_t low = 0u - (uint32_t)(g < 2);
+  const uint32_t y0 = hdr.y >> sh0, z0 = hdr.z >> sh0, w0 = hdr.w >> sh0;
+  const uint32_t y1 = hdr.y >> sh1, z1 = hdr.z >> sh1, w1 = hdr.w >> sh1;
+  const uint32_t sc0 = ((y0 & 63u) & low) | (((w0 & 15u) | ((y0 >> 2) & 48u)) & ~low);
+  const uint32_t m0 = ((z0 & 63u) & low) | ((((w0 >> 4) & 15u) | ((z0 >> 2) & 48u)) & ~low);
+  const uint32_t sc1 = ((y1 & 63u) & low) | (((w1 & 15u) | ((y1 >> 2) & 48u)) & ~low);
+  const uint32_t m1 = ((z1 & 63u) & low) | ((((w1 >> 4) & 15u) | ((z1 >> 2) & 48u)) & ~low);
+  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+  const uint32_t h[4] = {qh.x, qh.y, qh.z, qh.w};
+  const uint32_t hs = 2u * (uint32_t)g;
+  float dl = 0.0f, dh = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t hb = h[i] >> hs;
+    const uint32_t lo = and_opaque(w[i], 0x0F0F0F0Fu) | ((hb << 4) & 0x10101010u);
+    const uint32_t hi = and_opaque(w[i] >> 4, 0x0F0F0F0Fu) | ((hb << 3) & 0x10101010u);
     dl = fmaf(xl[4 * i], (float)(lo & 0xFFu), dl);
     dh = fmaf(xh[4 * i], (float)(hi & 0xFFu), dh);
     dl = fmaf(xl[4 * i + 1], (float)((lo >> 8) & 0xFFu), dl);

@@ -38,7 +38,8 @@ int moe_launch_to_f16(const void* x, int x_dtype, size_t n, uint16_t* out, hipSt
 // consumer waves run the MFMAs). x16: activations in f16 ([T,H]); S: [rows, I] f16; y: [rows, H]
 // f32. tiles == NULL: identity rows 0..T-1 (shared expert). Formats: Q4_K and BF16 (others:
 // gemm.hip).
-bool moe_gemm3_supports(int fmt);
+bool moe_gemm3_supports(int fmt);          // gate_up formats of the 160-row kernels
+bool moe_gemm3_down_supports(int fmt);     // down formats
 int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int fmt,
                             size_t expert_stride, const int32_t* tiles, int max_tiles, int T,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,

@@ -1,4 +1,4 @@
-"""GGUF K-quant packers: float weights -> Q4_K / Q6_K super-block bytes (torch, CPU or GPU).
+"""GGUF K-quant packers: float weights -> Q4_K / Q5_K / Q6_K super-block bytes (torch, CPU or GPU).
 
 These produce weight bytes in the exact GGUF layout the device kernels consume (the same bytes the
 reference reads, tools/gguf_reader.py:17-51). The fit is a plain min/max fit of this package's own
@@ -10,6 +10,9 @@ the device (the benchmark's 40 x 256 synthetic experts), chunked to bound tempor
 Layouts written here:
   Q4_K (144 B / 256 elements): f16 d | f16 dmin | 12 B packed 6-bit (sc, m) x 8 | 128 B nibbles,
        element 64g + l (l < 32) in the low nibble of qs[32g + l], 64g + 32 + l in its high nibble.
+  Q5_K (176 B / 256 elements): f16 d | f16 dmin | 12 B scales (as Q4_K) | qh[32] | 128 B nibbles;
+       the Q4_K nibble layout for the low 4 bits of q in [0, 31], and the 5th bit of element e
+       at bit e >> 5 of qh[e & 31] (tools/gguf_reader.py:271-296).
   Q6_K (210 B / 256 elements): ql[128] | qh[64] | int8 sc[16] | f16 d; element 128g + 32k + l has
        its low 4 bits in nibble (k >> 1) of ql[64g + 32(k & 1) + l] and its high 2 bits at bit 2k
        of qh[32g + l]; the stored value is q + 32 for q in [-32, 31].
@@ -21,11 +24,13 @@ import torch
 
 QK_K = 256
 Q4K_BYTES = 144
+Q5K_BYTES = 176
 Q6K_BYTES = 210
 FMT_Q4_K = 12
+FMT_Q5_K = 13
 FMT_Q6_K = 14
 FMT_BF16 = 30
-BLOCK_BYTES = {FMT_Q4_K: Q4K_BYTES, FMT_Q6_K: Q6K_BYTES}
+BLOCK_BYTES = {FMT_Q4_K: Q4K_BYTES, FMT_Q5_K: Q5K_BYTES, FMT_Q6_K: Q6K_BYTES}
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
@@ -48,13 +53,15 @@ def pack_q4k_scales(sc: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
     return _u8(torch.cat([s0, s1, s2], dim=-1))
 
 
-def _q4k_rows(w: torch.Tensor) -> torch.Tensor:
+def _kquant_fit(w: torch.Tensor, qmax: int):
+    """The min/max fit shared by Q4_K (qmax 15) and Q5_K (qmax 31): per super-block f16 d, dmin;
+    per 32-element sub-block 6-bit sc, m; per element q in [0, qmax] with v ~ d*sc*q - dmin*m."""
     rows, cols = w.shape
     nb = cols // QK_K
     x = w.reshape(rows, nb, 8, 32).float()
     mn = torch.clamp(x.amin(dim=-1), max=0.0)                  # (rows, nb, 8)
     mx = x.amax(dim=-1)
-    scale = (mx - mn) / 15.0
+    scale = (mx - mn) / float(qmax)
     minv = -mn
     d = (scale.amax(dim=-1) / 63.0).to(torch.float16).float()  # (rows, nb)
     dmin = (minv.amax(dim=-1) / 63.0).to(torch.float16).float()
@@ -66,11 +73,34 @@ def _q4k_rows(w: torch.Tensor) -> torch.Tensor:
     off = dmin[..., None] * mm
     q = torch.where(step[..., None] > 0,
                     torch.round((x + off[..., None]) / step[..., None].clamp_min(1e-30)),
-                    torch.zeros_like(x)).clamp(0, 15).to(torch.int32)    # (rows, nb, 8, 32)
+                    torch.zeros_like(x)).clamp(0, qmax).to(torch.int32)  # (rows, nb, 8, 32)
+    return d, dmin, sc, mm, q
+
+
+def _q4k_rows(w: torch.Tensor) -> torch.Tensor:
+    rows, cols = w.shape
+    nb = cols // QK_K
+    d, dmin, sc, mm, q = _kquant_fit(w, 15)
     qg = q.reshape(rows, nb, 4, 2, 32)
     qs = _u8(qg[..., 0, :] | (qg[..., 1, :] << 4)).reshape(rows, nb, 128)
     out = torch.cat([_f16_bytes(d), _f16_bytes(dmin), pack_q4k_scales(sc, mm), qs], dim=-1)
     return out.reshape(rows, nb * Q4K_BYTES)
+
+
+def _q5k_rows(w: torch.Tensor) -> torch.Tensor:
+    rows, cols = w.shape
+    nb = cols // QK_K
+    d, dmin, sc, mm, q = _kquant_fit(w, 31)
+    lo = q & 15
+    qg = lo.reshape(rows, nb, 4, 2, 32)
+    qs = _u8(qg[..., 0, :] | (qg[..., 1, :] << 4)).reshape(rows, nb, 128)
+    # bit j of qh[l] is the 5th bit of element 32 j + l (sub-block j)
+    hi = (q >> 4).reshape(rows, nb, 8, 32)
+    qh = torch.zeros(rows, nb, 32, dtype=torch.int32, device=w.device)
+    for j in range(8):
+        qh |= hi[:, :, j, :] << j
+    out = torch.cat([_f16_bytes(d), _f16_bytes(dmin), pack_q4k_scales(sc, mm), _u8(qh), qs], dim=-1)
+    return out.reshape(rows, nb * Q5K_BYTES)
 
 
 def _q6k_rows(w: torch.Tensor) -> torch.Tensor:
@@ -103,7 +133,7 @@ def quantize(w, fmt: int, chunk_rows: int = 16384) -> torch.Tensor:
         w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float32))
     if w.dim() != 2 or w.shape[1] % QK_K:
         raise ValueError(f"expected [rows, cols] with cols % 256 == 0, got {tuple(w.shape)}")
-    fn = {FMT_Q4_K: _q4k_rows, FMT_Q6_K: _q6k_rows}.get(fmt)
+    fn = {FMT_Q4_K: _q4k_rows, FMT_Q5_K: _q5k_rows, FMT_Q6_K: _q6k_rows}.get(fmt)
     if fn is None:
         raise ValueError(f"unsupported format {fmt}")
     rows = w.shape[0]
@@ -115,6 +145,10 @@ def quantize(w, fmt: int, chunk_rows: int = 16384) -> torch.Tensor:
 
 def quantize_q4k(w) -> torch.Tensor:
     return quantize(w, FMT_Q4_K)
+
+
+def quantize_q5k(w) -> torch.Tensor:
+    return quantize(w, FMT_Q5_K)
 
 
 def quantize_q6k(w) -> torch.Tensor:

@@ -52,3 +52,12 @@ def layer_q6k(pkg, dev):
     lw = pkg.synth.make_layer(seed=3, device=dev, down_fmt=pkg.quant.FMT_Q6_K, zipf=True)
     torch.cuda.synchronize()
     return lw, O.from_device(lw)
+
+
+@pytest.fixture(scope="session")
+def layer_q5k(pkg, dev):
+    """The shipped artifact's expert widths: Q4_K gate_up + Q5_K down (seed 5, uniform routing)."""
+    from oracle import moe_oracle as O
+    lw = pkg.synth.make_layer(seed=5, device=dev, down_fmt=pkg.quant.FMT_Q5_K)
+    torch.cuda.synchronize()
+    return lw, O.from_device(lw)

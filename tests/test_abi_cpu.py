@@ -28,7 +28,7 @@ def test_abi_version_and_enums_match_header(pkg):
     text = HEADER.read_text()
     assert pkg._lib.lib.moe_abi_version() == int(re.search(r"MOE_ABI_VERSION (\d+)", text).group(1))
     for name in ("MOE_OK", "MOE_E_ARG", "MOE_E_FORMAT", "MOE_E_HIP", "MOE_E_WORKSPACE",
-                 "MOE_E_UNSUPPORTED", "MOE_DT_F32", "MOE_DT_BF16", "MOE_FMT_Q4_K", "MOE_FMT_Q6_K",
+                 "MOE_E_UNSUPPORTED", "MOE_DT_F32", "MOE_DT_BF16", "MOE_FMT_Q4_K", "MOE_FMT_Q5_K", "MOE_FMT_Q6_K",
                  "MOE_FMT_BF16", "MOE_PATH_AUTO", "MOE_PATH_GEMV", "MOE_PATH_MFMA",
                  "MOE_PATH_MFMA_BF16", "MOE_PATH_GEMV_MULTI"):
         m = re.search(name + r"\s*=\s*(-?\d+)", text)

@@ -267,3 +267,22 @@ def test_decode_next_layer_hint_same_bits(pkg, layer_c0, layer_zipf, dev):
         assert torch.equal(a, b), step
         assert torch.isfinite(a).all()
     assert pkg.abi.device_error_bits(dev) == 0
+
+
+def test_decode_q5k_down(pkg, layer_q5k, dev):
+    """Single tokens with Q5_K down (the three-launch decode path) match the oracle."""
+    lw, ow = layer_q5k
+    for seed in (1, 2, 3):
+        x = pkg.synth.make_input(1, seed=60 + seed, device=dev)
+        st = pkg.block.moe_block(x, lw, pkg.load_geometry())
+        _compare(st, O.moe_block(x.cpu(), ow), tag=f"q5k decode seed={seed}")
+
+
+def test_prefill_q5k_down_sampled_rows(pkg, layer_q5k, dev):
+    """T = 2048 bf16 activations with Q5_K down on the MFMA path (160-row kernels)."""
+    lw, ow = layer_q5k
+    x = pkg.synth.make_input(2048, seed=5, device=dev, dtype=torch.bfloat16)
+    st = pkg.block.moe_block(x, lw, pkg.load_geometry())
+    rows = torch.randperm(2048, generator=torch.Generator().manual_seed(5))[:96]
+    ref = O.moe_block(x.cpu()[rows], ow)
+    _compare(st, ref, rows=rows, tag="q5k prefill")

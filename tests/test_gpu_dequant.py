@@ -27,7 +27,8 @@ def _random_blocks(nb, nbytes, seed, sane_scale_at=None):
     return raw
 
 
-@pytest.mark.parametrize("fmt,nbytes,scales", [(GQ.GGML_Q4_K, 144, (0, 2)), (GQ.GGML_Q6_K, 210, (208,))])
+@pytest.mark.parametrize("fmt,nbytes,scales", [(GQ.GGML_Q4_K, 144, (0, 2)), (GQ.GGML_Q5_K, 176, (0, 2)),
+                                                (GQ.GGML_Q6_K, 210, (208,))])
 def test_dequant_random_bytes_bitexact(pkg, dev, fmt, nbytes, scales):
     nb = 4096
     raw = _random_blocks(nb, nbytes, seed=fmt, sane_scale_at=scales)
@@ -36,7 +37,7 @@ def test_dequant_random_bytes_bitexact(pkg, dev, fmt, nbytes, scales):
     assert _bits_equal(got, want)
 
 
-@pytest.mark.parametrize("fmt", [GQ.GGML_Q4_K, GQ.GGML_Q6_K])
+@pytest.mark.parametrize("fmt", [GQ.GGML_Q4_K, GQ.GGML_Q5_K, GQ.GGML_Q6_K])
 def test_dequant_quantized_weights_bitexact_f32_and_bf16(pkg, dev, fmt):
     g = torch.Generator().manual_seed(5)
     w = torch.randn(512, 2048, generator=g) * 0.02
@@ -68,3 +69,26 @@ def test_dequant_refuses_bad_args(pkg, dev):
     with pytest.raises(pkg.Refused) as ei:
         pkg.abi.dequant(blk, 99, 256)
     assert ei.value.tag == "unsupported-format"
+
+
+def test_dequant_q5k_hand_block(pkg, dev):
+    """d = dmin = 1, every 6-bit field 63: all q = 0 -> -63, all q = 31 -> 1890; one qh bit
+    (bit 3 of qh[5], element 101's 5th bit) with zero nibbles and mins -> only element 101 = 1008."""
+    blk = np.zeros(176, dtype=np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:4] = [0x00, 0x3C]
+    blk[4:16] = 0xFF
+    got = pkg.abi.dequant(torch.from_numpy(blk.copy()).to(dev), GQ.GGML_Q5_K, 256).cpu().numpy()
+    assert np.all(got == -63.0)
+    blk[16:] = 0xFF
+    got = pkg.abi.dequant(torch.from_numpy(blk.copy()).to(dev), GQ.GGML_Q5_K, 256).cpu().numpy()
+    assert np.all(got == 1890.0)
+    one = np.zeros(176, dtype=np.uint8)
+    one[0:2] = [0x00, 0x3C]
+    one[4:8] = 63                                     # sc[0..3] = 63, all mins 0
+    one[12:16] = 0x0F                                 # sc[4..7] low bits 15 ...
+    one[0 + 4:4 + 4] |= 0xC0                          # ... high bits 3 -> 63
+    one[16 + 5] = 1 << 3
+    got = pkg.abi.dequant(torch.from_numpy(one).to(dev), GQ.GGML_Q5_K, 256).cpu().numpy()
+    assert np.nonzero(got)[0].tolist() == [101] and got[101] == 1008.0
+    assert np.array_equal(got, GQ.dequant_q5k(one, 256))

@@ -48,6 +48,18 @@ def test_routed_experts_q6k_down(pkg, layer_q6k, dev):
         assert_close(raw, want, f"expert_raw q6k T={T} path={path}", max_abs=BOUND[path])
 
 
+def test_routed_experts_q5k_down(pkg, layer_q5k, dev):
+    lw, ow = layer_q5k
+    for T, path in ((1, 1), (9, 1), (160, 2)):
+        x = pkg.synth.make_input(T, seed=30 + T, device=dev)
+        r, gr = _route_and_group(pkg, lw, x)
+        y = pkg.abi.experts(x, lw.gate_up_q, lw.gate_up_fmt, lw.down_q, lw.down_fmt, gr, 8, path)
+        torch.cuda.synchronize()
+        raw = y.cpu()[gr["pair_pos"].cpu().long()].view(T, 8, -1)
+        want = _oracle_raw(ow, x.cpu(), r["topk_ids"].cpu())
+        assert_close(raw, want, f"expert_raw q5k T={T} path={path}", max_abs=BOUND[path])
+
+
 @pytest.mark.parametrize("T,path,dtype", [(1, 1, torch.float32), (16, 1, torch.float32),
                                           (64, 2, torch.float32), (257, 2, torch.bfloat16),
                                           (64, 3, torch.bfloat16)])

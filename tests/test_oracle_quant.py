@@ -1,4 +1,4 @@
-"""Pins of the oracle's Q4_K / Q6_K decoders (CPU only). Each check is chosen so a plausible
+"""Pins of the oracle's Q4_K / Q5_K / Q6_K decoders (CPU only). Each check is chosen so a plausible
 mistake fails it: a swapped scale/min field, a wrong nibble or sub-block index, a dropped min
 term, a wrong Q6_K bit shift, a double rounding."""
 import numpy as np
@@ -216,3 +216,102 @@ def test_q6k_negative_control_wrong_shift_is_caught():
     bad = blk.copy()
     bad[128:192] = np.roll(bad[128:192], 1)
     assert not np.array_equal(GQ.dequant_q6k(bad, 256), good)
+
+
+def _pack_q5k_fields(d, dmin, sc, m, q):
+    """Encoder route for Q5_K from the fields (the packing order of tools/audit_published_quant.py
+    :1047-1072): the Q4_K scale bytes, the low 4 bits of q as Q4_K nibbles, and the 5th bit of
+    element 64n + j at bit 2n of qh[j], of element 64n + 32 + j at bit 2n + 1."""
+    blk = np.zeros(176, dtype=np.uint8)
+    head = _pack_q4k_fields(d, dmin, sc, m, np.asarray(q) & 15)
+    blk[0:16] = head[0:16]
+    blk[48:176] = head[16:144]
+    for n in range(4):
+        for j in range(32):
+            if q[64 * n + j] > 15:
+                blk[16 + j] |= 1 << (2 * n)
+            if q[64 * n + 32 + j] > 15:
+                blk[16 + j] |= 2 << (2 * n)
+    return blk
+
+
+def test_q5k_fields_roundtrip_vs_affine_definition():
+    """value(e) = d*sc[e//32]*q[e] - dmin*m[e//32], q in [0, 31], rounded once to f32
+    (tools/audit_published_quant.py:1036-1044 `expect_k`), 200 random blocks."""
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        d = float(np.float16(rng.uniform(1e-4, 0.1)))
+        dmin = float(np.float16(rng.uniform(1e-4, 0.1)))
+        sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        q = rng.integers(0, 32, 256)
+        got = GQ.dequant_q5k(_pack_q5k_fields(d, dmin, sc, m, q), 256)
+        want = np.array([np.float32(d * sc[e // 32] * q[e] - dmin * m[e // 32]) for e in range(256)],
+                        dtype=np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q5k_hand_blocks():
+    """Closed forms with d = dmin = 1 and every 6-bit field 63: q = 0 -> -63, q = 31 -> 1890
+    (63 * 31 - 63), and a single qh bit: bit 3 of qh[5] is element 32*3 + 5 = 101's 5th bit, so
+    with all nibbles 0 and all mins 0 exactly that element reads 63 * 16 = 1008."""
+    blk = np.zeros(176, dtype=np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:4] = [0x00, 0x3C]
+    blk[4:16] = 0xFF
+    assert np.all(GQ.dequant_q5k(blk, 256) == -63.0)
+    blk[16:] = 0xFF
+    assert np.all(GQ.dequant_q5k(blk, 256) == 1890.0)
+    one = np.zeros(176, dtype=np.uint8)
+    one[0:2] = [0x00, 0x3C]
+    one[4:16] = _pack_q4k_fields(1.0, 0.0, [63] * 8, [0] * 8, [0] * 256)[4:16]
+    one[16 + 5] = 1 << 3
+    v = GQ.dequant_q5k(one, 256)
+    assert np.nonzero(v)[0].tolist() == [101] and v[101] == 1008.0
+
+
+def test_q5k_negative_control_wrong_high_bit_is_caught():
+    """A decoder that took the 5th bit from the wrong qh byte (or bit) would differ: the round
+    trip above must be able to fail."""
+    rng = np.random.default_rng(6)
+    q = rng.integers(0, 32, 256)
+    blk = _pack_q5k_fields(0.5, 0.25, rng.integers(1, 64, 8), rng.integers(0, 64, 8), q)
+    good = GQ.dequant_q5k(blk, 256)
+    bad = blk.copy()
+    bad[16:48] = np.roll(bad[16:48], 1)
+    assert not np.array_equal(GQ.dequant_q5k(bad, 256), good)
+    bad2 = blk.copy()
+    bad2[16:48] = (bad2[16:48].astype(np.int64) << 1 & 0xFF).astype(np.uint8)
+    assert not np.array_equal(GQ.dequant_q5k(bad2, 256), good)
+
+
+def test_q5k_packer_roundtrip_and_f64_route():
+    """The package's Q5_K packer: its bytes decode (oracle) to the f64 route's values rounded once,
+    and the fit is the finer one a 5-bit code gives."""
+    import torch
+    import importlib.util
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("q_", root / "qwen3.6-35b-a3b_amd" / "quant.py")
+    Q = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(Q)
+    w = torch.randn(64, 2048, generator=torch.Generator().manual_seed(7)) * 0.02
+    raw = Q.quantize(w, Q.FMT_Q5_K).numpy().reshape(-1, 176)
+    got = GQ.dequant_q5k(raw, raw.shape[0] * 256)
+    d = GQ.f16_to_f64(raw[:, 0:2].copy().view(np.uint16).reshape(-1))
+    dmin = GQ.f16_to_f64(raw[:, 2:4].copy().view(np.uint16).reshape(-1))
+    sc, m = GQ.q4k_scale_min(raw[:, 4:16])
+    qh = raw[:, 16:48].astype(np.int64)
+    qs = raw[:, 48:].reshape(-1, 4, 32).astype(np.int64)
+    q = np.stack([qs & 15, qs >> 4], axis=2)
+    for j in range(8):
+        q[:, j // 2, j % 2, :] += 16 * ((qh >> j) & 1)
+    assert q.max() > 15                               # the 5th bit is in use
+    f64 = (d.reshape(-1, 1, 1, 1) * sc.reshape(-1, 4, 2, 1)) * q - dmin.reshape(-1, 1, 1, 1) * m.reshape(-1, 4, 2, 1)
+    assert np.array_equal(got, f64.reshape(-1).astype(np.float32))
+    # the 5th bit halves the quantisation step: the Q5_K fit's RMS error must be well under the
+    # Q4_K fit's on the same weights (a misplaced 5th bit would not be)
+    wv = w.numpy().reshape(-1).astype(np.float64)
+    e5 = np.sqrt(np.mean((got.astype(np.float64) - wv) ** 2))
+    r4 = Q.quantize(w, Q.FMT_Q4_K).numpy().reshape(-1, 144)
+    e4 = np.sqrt(np.mean((GQ.dequant_q4k(r4, r4.shape[0] * 256).astype(np.float64) - wv) ** 2))
+    assert e5 < 0.6 * e4 and e5 < 0.08 * np.sqrt(np.mean(wv ** 2)), (e5, e4)
