@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 1
+#define MOE_ABI_VERSION 2
 
 enum {
   MOE_OK = 0,
@@ -72,11 +72,13 @@ int moe_dequant(const void *blocks, int fmt, int64_t n_elts, void *out, int out_
  *   R1 logits[t,e] = bf16 of the correctly rounded sum_j x[t,j]*W[e,j] (+ logit_bias[e])
  *   R2 probs = softmax over E in f32; R3 top-K with torch CPU's tie order;
  *   R4 w_f32 = renormalised top-K probs; R5 w_bf16 = bf16(w_f32).
- * x: [T,H] f32 or bf16; w_router: [E,H] bf16; logit_bias: [E] f32 or NULL.
+ * x: [T,H] f32 or bf16; w_router: [E,H] in w_dtype: MOE_DT_BF16, or MOE_DT_F32 (the shipped
+ * artifact's F32 ffn_gate_inp, engine/block_forward.py:221-231; x*W products stay exact in f64,
+ * so R1 is correctly rounded either way); logit_bias: [E] f32 or NULL.
  * logits_bf16 [T,E], probs [T,E] may be NULL; topk_ids [T,K] int32; w_f32, w_bf16 [T,K].
  * Limits: H % 512 == 0, E <= 256, K <= 16, K * 64 > E (torch's nth_element branch). */
-int moe_router_topk(const void *x, int x_dtype, const void *w_router, const float *logit_bias,
-                    int T, int H, int E, int K, void *logits_bf16, float *probs,
+int moe_router_topk(const void *x, int x_dtype, const void *w_router, int w_dtype,
+                    const float *logit_bias, int T, int H, int E, int K, void *logits_bf16, float *probs,
                     int32_t *topk_ids, float *w_f32, void *w_bf16, void *ws, size_t ws_bytes,
                     void *stream);
 
@@ -84,7 +86,8 @@ int moe_router_topk(const void *x, int x_dtype, const void *w_router, const floa
  * bit-exact vs torch.argsort(ids.flatten(), stable=True). Replaces the grouping in
  * speccheck/moe_ref.py:433-439 and engine/m3_forward.py:448-452.
  * expert_offsets [E+1]; sorted_pairs [T*K] (value p); pair_pos [T*K] (inverse permutation);
- * hit_list [E+1] = n_hit, then the hit expert ids ascending. */
+ * hit_list [E+1] = n_hit, then the hit expert ids ascending. ws: as every entry point's, its
+ * first 512 KiB are the sync words (left untouched); T*K > 64 needs scratch after them. */
 int moe_sort_permute(const int32_t *topk_ids, int T, int K, int E, int32_t *expert_offsets,
                      int32_t *sorted_pairs, int32_t *pair_pos, int32_t *hit_list, void *ws,
                      size_t ws_bytes, void *stream);
@@ -92,23 +95,26 @@ int moe_sort_permute(const int32_t *topk_ids, int T, int K, int E, int32_t *expe
 /* The K routed SwiGLU experts of every token, grouped so each hit expert's weights are read once
  * per step. Replaces speccheck/moe_ref.py:367-451 (_expert_apply, expert_gather) and
  * engine/m3_forward.py:452-463. gate_up_q: [E][2I rows][H/256 blocks], gate rows first
- * (spec §11.4); down_q: [E][H rows][I/256 blocks]. y [T*K, H] f32 in sorted-pair order
+ * (spec §11.4), when up_q is NULL; else gate_up_q holds the gate rows [E][I rows][H/256 blocks]
+ * and up_q the up rows in the same layout (the artifact's separate ffn_gate_exps and
+ * ffn_up_exps). down_q: [E][H rows][I/256 blocks]. y [T*K, H] f32 in sorted-pair order
  * (expert_raw before the routing weight). path: GEMV = fused dequant + f32 GEMV (decode),
  * MFMA / MFMA_BF16 = tiles dequantised to f16 / bf16 in LDS, contracted on MFMA (prefill);
  * AUTO picks GEMV for T <= 16 with Q4_K gate_up, MFMA otherwise. */
-int moe_experts(const void *x, int x_dtype, const void *gate_up_q, int gate_up_fmt,
+int moe_experts(const void *x, int x_dtype, const void *gate_up_q, const void *up_q, int gate_up_fmt,
                 const void *down_q, int down_fmt, const int32_t *expert_offsets,
                 const int32_t *sorted_pairs, const int32_t *hit_list, int T, int H, int I, int E,
                 int K, int path, float *y, void *ws, size_t ws_bytes, void *stream);
 
 /* Shared expert and its scalar sigmoid gate. Replaces speccheck/moe_ref.py:480-495,
  * engine/block_forward.py:639-649 and engine/m3_forward.py:436-442.
- * w_gate, w_up: [I_s,H] bf16; w_down: [H,I_s] bf16; w_scalar_gate: [H] bf16.
+ * w_gate, w_up: [I_s,H]; w_down: [H,I_s], in shared_fmt (MOE_FMT_BF16); w_scalar_gate: [H] in
+ * gate_dtype (MOE_DT_BF16, or MOE_DT_F32 as the artifact's ffn_gate_inp_shexp).
  * shared_raw [T,H] = down(silu(gate x) * up x); gate_prob [T] = sigmoid(w_scalar_gate . x). */
 int moe_shared_expert(const void *x, int x_dtype, const void *w_gate, const void *w_up,
-                      const void *w_down, const void *w_scalar_gate, int T, int H, int I_s,
-                      int path, float *shared_raw, float *gate_prob, void *ws, size_t ws_bytes,
-                      void *stream);
+                      const void *w_down, int shared_fmt, const void *w_scalar_gate, int gate_dtype,
+                      int T, int H, int I_s, int path, float *shared_raw, float *gate_prob, void *ws,
+                      size_t ws_bytes, void *stream);
 
 /* Top-K weighted combine, ascending expert id, weight reached by rank, plus the gated shared
  * expert. Replaces speccheck/moe_ref.py:452-476, :516-518 and engine/block_forward.py:664-667,
@@ -137,6 +143,43 @@ int moe_block_forward(const void *x, int x_dtype, int T, int H, int I, int E, in
                       int32_t *topk_ids, void *topk_w_bf16, float *topk_w_f32,
                       float *routed_sum, float *shared_out, float *gate_prob, float *expert_raw,
                       void *ws, size_t ws_bytes, void *stream);
+
+/* One layer's MoE weights with their formats: what the layer loop of engine/m3_forward.py:714-737
+ * reads per layer (E.read roles, engine/m3_forward.py:235-283), in the widths a caller holds them:
+ * the synthetic configs' bf16 router / fused gate_up / bf16 shared expert, or the shipped
+ * artifact's F32 router and scalar gate, separate gate and up tensors and Q5_K / Q6_K down
+ * (engine/README.md:33, engine/block_forward.py:221-231). */
+typedef struct moe_layer_weights {
+  const void *w_router;          /* [E,H] */
+  int router_dtype;              /* MOE_DT_BF16 or MOE_DT_F32 */
+  const float *logit_bias;       /* [E] f32 or NULL */
+  const void *gate_q;            /* fused gate_up [E][2I rows] (up_q NULL) or gate [E][I rows] */
+  const void *up_q;              /* up [E][I rows], or NULL */
+  int gate_up_fmt;               /* MOE_FMT_Q4_K (also Q6_K / BF16 off the decode paths) */
+  const void *down_q;            /* [E][H rows] */
+  int down_fmt;                  /* MOE_FMT_Q4_K, Q5_K, Q6_K (BF16 off the decode paths) */
+  const void *ws_gate, *ws_up;   /* [I_s,H] */
+  const void *ws_down;           /* [H,I_s] */
+  int shared_fmt;                /* MOE_FMT_BF16 */
+  const void *ws_scalar_gate;    /* [H] */
+  int scalar_gate_dtype;         /* MOE_DT_BF16 or MOE_DT_F32 */
+  const float *norm_w;           /* [H] f32 post-attention norm weight, or NULL */
+} moe_layer_weights;
+
+/* moe_block_forward over a moe_layer_weights (w; norm_w and every weight pointer from there) and an
+ * optional next-layer hint (next: as moe_block_forward_prefetch, the router rows and norm weight of
+ * a bf16-router next layer). Same outputs, limits and errors as moe_block_forward. The
+ * single-launch decode layer takes a bf16 router and scalar gate with Q4_K gate/up (fused or
+ * split) and Q4_K, Q5_K or Q6_K down; an f32 router or scalar gate runs the three-launch decode
+ * path at T = 1, and the grouped paths above it.
+ * Replaces engine/m3_forward.py:430-476 and engine/block_forward.py:670-681 on the policy-A
+ * weights (engine/block_forward.py:211-231). */
+int moe_block_forward_w(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                        const moe_layer_weights *w, float norm_eps, int path, const float *residual,
+                        float *out, void *logits_bf16, int32_t *topk_ids, void *topk_w_bf16,
+                        float *topk_w_f32, float *routed_sum, float *shared_out, float *gate_prob,
+                        float *expert_raw, void *ws, size_t ws_bytes, void *stream,
+                        const moe_layer_weights *next);
 
 /* The routing-independent weights of the layer that the same stream runs next (its router, its
  * shared expert and the shared expert's scalar gate, its post-attention norm weight; shapes as in

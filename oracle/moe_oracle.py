@@ -268,11 +268,16 @@ def metrics(a: torch.Tensor, b: torch.Tensor, name: str = "") -> dict:
 
 def from_device(lw) -> LayerWeights:
     """Copy a device-side weight set (any object with the LayerWeights field names) to the host
-    form this oracle reads; the bytes are the same bytes the kernels read."""
+    form this oracle reads; the bytes are the same bytes the kernels read. Separate gate and up
+    records (an `up_q` field) are stacked gate first, the fused record's row order."""
     def host(t):
         return None if t is None else t.detach().cpu()
+    gu = host(lw.gate_up_q).numpy()
+    up = getattr(lw, "up_q", None)
+    if up is not None:
+        gu = np.concatenate([gu, host(up).numpy()], axis=1)
     return LayerWeights(
-        router=host(lw.router), gate_up_q=host(lw.gate_up_q).numpy(), gate_up_fmt=lw.gate_up_fmt,
+        router=host(lw.router), gate_up_q=gu, gate_up_fmt=lw.gate_up_fmt,
         down_q=host(lw.down_q).numpy(), down_fmt=lw.down_fmt, shared_gate=host(lw.shared_gate),
         shared_up=host(lw.shared_up), shared_down=host(lw.shared_down),
         shared_scalar_gate=host(lw.shared_scalar_gate), router_bias=host(lw.router_bias))

@@ -31,7 +31,21 @@ MOE_PATH_GEMV = 1
 MOE_PATH_MFMA = 2
 MOE_PATH_MFMA_BF16 = 3
 MOE_PATH_GEMV_MULTI = 4
+# every workspace starts with this many bytes of device-side sync words
+SYNC_BYTES = 512 * 1024
 
+
+
+class LayerWeightsC(ctypes.Structure):
+    """moe_layer_weights: one layer's MoE weights with their formats (include/moe_gfx950.h)."""
+    _fields_ = [("w_router", ctypes.c_void_p), ("router_dtype", ctypes.c_int),
+                ("logit_bias", ctypes.c_void_p), ("gate_q", ctypes.c_void_p),
+                ("up_q", ctypes.c_void_p), ("gate_up_fmt", ctypes.c_int),
+                ("down_q", ctypes.c_void_p), ("down_fmt", ctypes.c_int),
+                ("ws_gate", ctypes.c_void_p), ("ws_up", ctypes.c_void_p),
+                ("ws_down", ctypes.c_void_p), ("shared_fmt", ctypes.c_int),
+                ("ws_scalar_gate", ctypes.c_void_p), ("scalar_gate_dtype", ctypes.c_int),
+                ("norm_w", ctypes.c_void_p)]
 
 
 class NextLayer(ctypes.Structure):
@@ -48,13 +62,13 @@ SIGNATURES = {
     "moe_last_error": (_CP, []),
     "moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "moe_dequant": (_I, [_VP, _I, _I64, _VP, _I, _VP]),
-    "moe_router_topk": (_I, [_VP, _I, _VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP,
+    "moe_router_topk": (_I, [_VP, _I, _VP, _I, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP,
                              _SZ, _VP]),
     "moe_sort_permute": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
-    "moe_experts": (_I, [_VP, _I, _VP, _I, _VP, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP,
-                         _VP, _SZ, _VP]),
-    "moe_shared_expert": (_I, [_VP, _I, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _SZ,
-                               _VP]),
+    "moe_experts": (_I, [_VP, _I, _VP, _VP, _I, _VP, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
+                         _VP, _VP, _SZ, _VP]),
+    "moe_shared_expert": (_I, [_VP, _I, _VP, _VP, _VP, _I, _VP, _I, _I, _I, _I, _I, _VP, _VP, _VP,
+                               _SZ, _VP]),
     "moe_combine": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
     "moe_block_forward": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, _VP, ctypes.c_float,
                                _VP, _VP, _VP, _I, _VP, _I, _VP,
@@ -65,6 +79,9 @@ SIGNATURES = {
                                         _VP, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                         _VP, _VP, _VP, _VP, _SZ, _VP,
                                         ctypes.POINTER(NextLayer)]),
+    "moe_block_forward_w": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(LayerWeightsC),
+                                 ctypes.c_float, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                                 _VP, _VP, _SZ, _VP, ctypes.POINTER(LayerWeightsC)]),
     "moe_workspace_init": (_I, [_VP, _SZ, _VP]),
 }
 

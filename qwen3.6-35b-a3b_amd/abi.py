@@ -51,6 +51,15 @@ def _need(t: torch.Tensor, name: str, dtype=None, shape=None, device=None):
     return t
 
 
+def _wdt(t: torch.Tensor, name: str) -> int:
+    """bf16 or f32 weight vectors / matrices (router, scalar shared gate)."""
+    if t.dtype == torch.float32:
+        return L.MOE_DT_F32
+    if t.dtype == torch.bfloat16:
+        return L.MOE_DT_BF16
+    raise Refused("bad-argument", f"{name} must be bfloat16 or float32, got {t.dtype}")
+
+
 def _xdt(x: torch.Tensor) -> int:
     if x.dtype == torch.float32:
         return L.MOE_DT_F32
@@ -103,11 +112,13 @@ def dequant(blocks: torch.Tensor, fmt: int, n_elts: int, out_dtype=torch.float32
 
 def router_topk(x: torch.Tensor, w_router: torch.Tensor, top_k: int,
                 bias: torch.Tensor | None = None, want_probs: bool = False) -> dict:
-    """R1-R5 (speccheck/moe_ref.py:318-363). Returns logits (bf16), ids (int32), w_f32, w_bf16."""
+    """R1-R5 (speccheck/moe_ref.py:318-363). Returns logits (bf16), ids (int32), w_f32, w_bf16.
+    w_router is bf16 or f32 (the artifact's F32 ffn_gate_inp)."""
     _need(x, "x")
     T, H = x.shape
     E = w_router.shape[0]
-    _need(w_router, "w_router", torch.bfloat16, (E, H), x.device)
+    wdt = _wdt(w_router, "w_router")
+    _need(w_router, "w_router", None, (E, H), x.device)
     if bias is not None:
         _need(bias, "logit_bias", torch.float32, (E,), x.device)
     dev = x.device
@@ -116,7 +127,7 @@ def router_topk(x: torch.Tensor, w_router: torch.Tensor, top_k: int,
     ids = torch.empty(T, top_k, dtype=torch.int32, device=dev)
     wf = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     wb = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
-    _check(L.lib.moe_router_topk(_p(x), _xdt(x), _p(w_router), _p(bias), T, H, E, top_k,
+    _check(L.lib.moe_router_topk(_p(x), _xdt(x), _p(w_router), wdt, _p(bias), T, H, E, top_k,
                                  _p(logits), _p(probs), _p(ids), _p(wf), _p(wb), None, 0,
                                  _stream(x)), "router_topk")
     return {"router_logits": logits, "router_probs": probs, "topk_ids": ids,
@@ -133,24 +144,29 @@ def sort_permute(ids: torch.Tensor, n_experts: int) -> dict:
     srt = torch.empty(P, dtype=torch.int32, device=dev)
     pos = torch.empty(P, dtype=torch.int32, device=dev)
     hits = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
-    ws = workspace(dev, ((P + 1023) // 1024) * n_experts * 4 + 256)
+    # the sync words, then one int32 histogram row per 1024-pair chunk
+    ws = workspace(dev, L.SYNC_BYTES + ((P + 1023) // 1024 * n_experts * 4 + 255) // 256 * 256)
     _check(L.lib.moe_sort_permute(_p(ids), T, K, n_experts, _p(off), _p(srt), _p(pos), _p(hits),
                                   _p(ws), ws.numel(), _stream(ids)), "sort_permute")
     return {"expert_offsets": off, "sorted_pairs": srt, "pair_pos": pos, "hit_list": hits}
 
 
 def experts(x: torch.Tensor, gate_up_q: torch.Tensor, gate_up_fmt: int, down_q: torch.Tensor,
-            down_fmt: int, grouping: dict, top_k: int, path: int = L.MOE_PATH_AUTO) -> torch.Tensor:
-    """y [T*K, H] f32 in sorted-pair order (expert_raw before the routing weight)."""
+            down_fmt: int, grouping: dict, top_k: int, path: int = L.MOE_PATH_AUTO,
+            up_q: torch.Tensor | None = None) -> torch.Tensor:
+    """y [T*K, H] f32 in sorted-pair order (expert_raw before the routing weight). gate_up_q is the
+    fused [E, 2I, ...] record, or the gate rows [E, I, ...] when up_q (the up rows) is given."""
     _need(x, "x")
     T, H = x.shape
     _need(gate_up_q, "gate_up_q", torch.uint8, device=x.device)
     _need(down_q, "down_q", torch.uint8, device=x.device)
-    E, two_i = gate_up_q.shape[0], gate_up_q.shape[1]
-    I = two_i // 2
+    if up_q is not None:
+        _need(up_q, "up_q", torch.uint8, tuple(gate_up_q.shape), x.device)
+    E = gate_up_q.shape[0]
+    I = gate_up_q.shape[1] if up_q is not None else gate_up_q.shape[1] // 2
     y = torch.empty(T * top_k, H, dtype=torch.float32, device=x.device)
     ws = workspace(x.device, workspace_bytes(T, H, I, E, top_k, I))
-    _check(L.lib.moe_experts(_p(x), _xdt(x), _p(gate_up_q), gate_up_fmt, _p(down_q), down_fmt,
+    _check(L.lib.moe_experts(_p(x), _xdt(x), _p(gate_up_q), _p(up_q), gate_up_fmt, _p(down_q), down_fmt,
                              _p(grouping["expert_offsets"]), _p(grouping["sorted_pairs"]),
                              _p(grouping["hit_list"]), T, H, I, E, top_k, path, _p(y), _p(ws),
                              ws.numel(), _stream(x)), "experts")
@@ -159,19 +175,22 @@ def experts(x: torch.Tensor, gate_up_q: torch.Tensor, gate_up_fmt: int, down_q: 
 
 def shared_expert(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
                   w_scalar_gate: torch.Tensor, path: int = L.MOE_PATH_AUTO):
-    """(shared_raw [T,H] f32, gate_prob [T] f32)."""
+    """(shared_raw [T,H] f32, gate_prob [T] f32). w_scalar_gate is bf16 or f32 (the artifact's
+    F32 ffn_gate_inp_shexp)."""
     _need(x, "x")
     T, H = x.shape
     Is = w_gate.shape[0]
     for n, t, shp in (("w_gate", w_gate, (Is, H)), ("w_up", w_up, (Is, H)),
-                      ("w_down", w_down, (H, Is)), ("w_scalar_gate", w_scalar_gate, (1, H))):
+                      ("w_down", w_down, (H, Is))):
         _need(t, n, torch.bfloat16, shp, x.device)
+    gdt = _wdt(w_scalar_gate, "w_scalar_gate")
+    _need(w_scalar_gate, "w_scalar_gate", None, (1, H), x.device)
     raw = torch.empty(T, H, dtype=torch.float32, device=x.device)
     prob = torch.empty(T, dtype=torch.float32, device=x.device)
     ws = workspace(x.device, workspace_bytes(T, H, Is, 256, 8, Is))
     _check(L.lib.moe_shared_expert(_p(x), _xdt(x), _p(w_gate), _p(w_up), _p(w_down),
-                                   _p(w_scalar_gate), T, H, Is, path, _p(raw), _p(prob), _p(ws),
-                                   ws.numel(), _stream(x)), "shared_expert")
+                                   L.MOE_FMT_BF16, _p(w_scalar_gate), gdt, T, H, Is, path, _p(raw),
+                                   _p(prob), _p(ws), ws.numel(), _stream(x)), "shared_expert")
     return raw, prob
 
 
@@ -191,6 +210,23 @@ def combine(y: torch.Tensor, grouping: dict, ids: torch.Tensor, w_bf16: torch.Te
     return {"combined_out": out, "routed_sum": routed, "shared_out": shared_out, "expert_raw": raw}
 
 
+def _need_layer(lw, H: int, dev, tag: str) -> None:
+    """Device, dtype and leading-shape checks of a LayerWeights passed by descriptor."""
+    E = lw.router.shape[0]
+    _wdt(lw.router, tag + "router")
+    _need(lw.router, tag + "router", None, (E, H), dev)
+    _wdt(lw.shared_scalar_gate, tag + "shared_scalar_gate")
+    _need(lw.shared_scalar_gate, tag + "shared_scalar_gate", None, (1, H), dev)
+    for n in ("shared_gate", "shared_up", "shared_down"):
+        _need(getattr(lw, n), tag + n, torch.bfloat16, device=dev)
+    for n in ("gate_up_q", "down_q"):
+        _need(getattr(lw, n), tag + n, torch.uint8, device=dev)
+    if lw.up_q is not None:
+        _need(lw.up_q, tag + "up_q", torch.uint8, tuple(lw.gate_up_q.shape), dev)
+    if lw.router_bias is not None:
+        _need(lw.router_bias, tag + "router_bias", torch.float32, (E,), dev)
+
+
 def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False,
                   out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
                   norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
@@ -202,7 +238,9 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
     given: engine/m3_forward.py:732-737 is then block_forward(x1, lw, norm_w=w, residual=x1).
     `next_layer` (a LayerWeights, optional) is the layer this stream runs next and `next_norm_w`
     its norm weight: their routing-independent weights are warmed into L2 by the single-launch
-    decode layer (moe_block_forward_prefetch); results do not depend on them."""
+    decode layer (moe_block_forward_prefetch); results do not depend on them. Weights in other
+    widths than the bf16 router / fused gate_up / bf16 scalar gate (the artifact's F32 router and
+    scalar gate, separate gate and up tensors) go through moe_block_forward_w."""
     _need(x, "x")
     T, H = x.shape
     if norm_w is not None:
@@ -223,6 +261,22 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
     st = {n: torch.empty(*shapes[n][0], dtype=shapes[n][1], device=dev) for n in want}
     ws = workspace(dev, workspace_bytes(T, H, I, E, K, Is))
     g = st.get
+    if not lw.default_widths or (next_layer is not None and not next_layer.default_widths):
+        _need_layer(lw, H, dev, "")
+        if next_layer is not None:
+            _need_layer(next_layer, H, dev, "next ")
+            if next_norm_w is not None:
+                _need(next_norm_w, "next_norm_w", torch.float32, (H,), dev)
+        W = lw.c_struct(norm_w)
+        N = next_layer.c_struct(next_norm_w) if next_layer is not None else None
+        _check(L.lib.moe_block_forward_w(
+            _p(x), _xdt(x), T, H, I, E, K, Is, ctypes.byref(W), float(norm_eps), path, _p(residual),
+            _p(out), _p(g("router_logits")), _p(g("topk_ids")), _p(g("topk_weights")),
+            _p(g("topk_weights_f32")), _p(g("routed_sum")), _p(g("shared_out")),
+            _p(g("shared_gate_prob")), _p(g("expert_raw")), _p(ws), ws.numel(), _stream(x),
+            None if N is None else ctypes.byref(N)), "block_forward")
+        st["combined_out"] = out
+        return st
     args = (
         _p(x), _xdt(x), T, H, I, E, K, Is, _p(norm_w), float(norm_eps), _p(lw.router), _p(lw.router_bias), _p(lw.gate_up_q),
         lw.gate_up_fmt, _p(lw.down_q), lw.down_fmt, _p(lw.shared_gate), _p(lw.shared_up),

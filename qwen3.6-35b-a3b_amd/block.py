@@ -46,7 +46,7 @@ def moe_routed(g_row, W, cfg, route, path: int = L.MOE_PATH_AUTO):
     ids = route["topk_ids"].to(torch.int32).contiguous()
     grouping = abi.sort_permute(ids, W.n_experts)
     y = abi.experts(x, W.gate_up_q, W.gate_up_fmt, W.down_q, W.down_fmt, grouping, ids.shape[1],
-                    path)
+                    path, up_q=W.up_q)
     T, H = x.shape
     zeros = torch.zeros(T, H, dtype=torch.float32, device=x.device)
     gp = torch.zeros(T, dtype=torch.float32, device=x.device)

@@ -101,12 +101,13 @@ int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_
   return moe_launch_dequant(blocks, fmt, n_elts, out, out_dtype, (hipStream_t)stream);
 }
 
-int moe_router_topk(const void* x, int x_dtype, const void* w_router, const float* logit_bias,
-                    int T, int H, int E, int K, void* logits_bf16, float* probs,
+int moe_router_topk(const void* x, int x_dtype, const void* w_router, int w_dtype,
+                    const float* logit_bias, int T, int H, int E, int K, void* logits_bf16, float* probs,
                     int32_t* topk_ids, float* w_f32, void* w_bf16, void* ws, size_t ws_bytes,
                     void* stream) {
   if (!x || !w_router || !topk_ids || !w_f32 || !w_bf16) return moe_set_error(MOE_E_ARG, "moe_router_topk: NULL pointer");
   if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_router_topk: bad x_dtype %d", x_dtype);
+  if (w_dtype != MOE_DT_F32 && w_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_router_topk: router weights must be bf16 or f32 (got %d)", w_dtype);
   if (T < 1 || H < 1 || H % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_router_topk: need T >= 1 and H %% 512 == 0");
   if (E < 1 || E > 256 || K < 1 || K > 16 || K > E || K * 64 <= E)
     return moe_set_error(MOE_E_UNSUPPORTED, "moe_router_topk: need E <= 256, K <= 16, K*64 > E (E=%d K=%d)", E, K);
@@ -119,7 +120,7 @@ int moe_router_topk(const void* x, int x_dtype, const void* w_router, const floa
     logits = reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
     if (!logits) return moe_set_error(MOE_E_WORKSPACE, "moe_router_topk: workspace too small for the logits");
   }
-  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, logit_bias, T, H, E, logits, st));
+  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, w_dtype, logit_bias, T, H, E, logits, st));
   return moe_launch_route_topk(logits, T, E, K, probs, topk_ids, w_f32,
                                reinterpret_cast<uint16_t*>(w_bf16), nullptr, st);
 }
@@ -131,14 +132,24 @@ int moe_sort_permute(const int32_t* topk_ids, int T, int K, int E, int32_t* expe
     return moe_set_error(MOE_E_ARG, "moe_sort_permute: NULL pointer");
   if (T < 1 || K < 1 || E < 1 || E > 256) return moe_set_error(MOE_E_UNSUPPORTED, "moe_sort_permute: need T, K >= 1 and 1 <= E <= 256");
   const int P = T * K;
-  if (P > 64 && (!ws || ws_bytes < moe_sort_ws_bytes(P, E)))
-    return moe_set_error(MOE_E_WORKSPACE, "moe_sort_permute: workspace needs %zu bytes", moe_sort_ws_bytes(P, E));
-  return moe_launch_sort(topk_ids, P, E, expert_offsets, sorted_pairs, pair_pos, hit_list, ws,
+  // the workspace's first kSyncBytes are the sync words every entry point leaves in place
+  MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+  void* sort_ws = nullptr;
+  if (P > 64) {
+    w.take(kSyncBytes);
+    sort_ws = w.take(moe_sort_ws_bytes(P, E));
+    if (!sort_ws)
+      return moe_set_error(MOE_E_WORKSPACE, "moe_sort_permute: workspace needs %zu bytes",
+                           kSyncBytes + moe_sort_ws_bytes(P, E));
+  }
+  return moe_launch_sort(topk_ids, P, E, expert_offsets, sorted_pairs, pair_pos, hit_list, sort_ws,
                          (hipStream_t)stream);
 }
 
 // x16: the rows already in f16 (the MFMA paths' activation operand), or NULL to convert here
-static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const void* gu, int gu_fmt,
+// gate / up: the routed gate and up rows of expert e at gate + e * estride and up + e * estride
+static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const void* gate,
+                        const void* up, size_t estride, int gu_fmt,
                         const void* dn, int dn_fmt, const int32_t* offsets,
                         const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
                         int E, int K, int path, float* y, MoeWs& w, hipStream_t st) {
@@ -148,13 +159,11 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
   if (path == MOE_PATH_GEMV) {
     float* S = reinterpret_cast<float*>(w.take((size_t)P * I * 4));
     if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
-    MOE_TRY(moe_launch_gemv_gateup(x, x_dtype, gu, gu_fmt, offsets, sorted_pairs, hit_list, max_hits, H, I, K, S, st));
+    MOE_TRY(moe_launch_gemv_gateup(x, x_dtype, gate, up, estride, gu_fmt, offsets, sorted_pairs, hit_list, max_hits, H, I, K, S, st));
     return moe_launch_gemv_down(S, dn, dn_fmt, offsets, hit_list, max_hits, H, I, y, st);
   }
-  const size_t gu_row = gu_fmt == MOE_FMT_Q4_K ? (size_t)H / 256 * 144 : gu_fmt == MOE_FMT_Q6_K ? (size_t)H / 256 * 210 : (size_t)H * 2;
   const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q5_K ? (size_t)I / 256 * 176
                       : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
-  const uint8_t* g = reinterpret_cast<const uint8_t*>(gu);
   if (dn_fmt == MOE_FMT_Q5_K && path == MOE_PATH_MFMA_BF16)
     return moe_set_error(MOE_E_FORMAT, "moe_experts: Q5_K down runs on the GEMV and MFMA (f16) paths");
   const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_down_supports(dn_fmt) &&
@@ -173,31 +182,52 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
       x16 = c;
     }
     if (gu_fmt == MOE_FMT_Q4_K)
-      MOE_TRY(moe_launch_gemm4_gateup(x16, g, g + (size_t)I * gu_row, 2 * (size_t)I * gu_row, tiles,
-                                      max_tiles, offsets, sorted_pairs, K, H, I, S, st));
+      MOE_TRY(moe_launch_gemm4_gateup(x16, gate, up, estride, tiles, max_tiles, offsets, sorted_pairs,
+                                      K, H, I, S, st));
     else
-      MOE_TRY(moe_launch_gemm3_gateup(x16, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
-                                      max_tiles, T, offsets, sorted_pairs, K, H, I, S, st));
+      MOE_TRY(moe_launch_gemm3_gateup(x16, gate, up, gu_fmt, estride, tiles, max_tiles, T, offsets,
+                                      sorted_pairs, K, H, I, S, st));
     if (dn_fmt == MOE_FMT_Q4_K)
       return moe_launch_gemm4_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, st);
     return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, st);
   }
   const int opb = path == MOE_PATH_MFMA_BF16;
-  MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, g, g + (size_t)I * gu_row, gu_fmt, 2 * (size_t)I * gu_row, tiles,
-                                 max_tiles, T, offsets, sorted_pairs, K, H, I, opb, S, st));
+  MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, gate, up, gu_fmt, estride, tiles, max_tiles, T, offsets,
+                                 sorted_pairs, K, H, I, opb, S, st));
   return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, opb, y, st);
 }
 
-static int check_wfmt(int gu_fmt, int dn_fmt, const void* gu, const void* dn, const char* who) {
+static int check_wfmt(int gu_fmt, int dn_fmt, const void* gu, const void* up, const void* dn, const char* who) {
   if (gu_fmt != MOE_FMT_Q4_K && gu_fmt != MOE_FMT_Q6_K && gu_fmt != MOE_FMT_BF16)
     return moe_set_error(MOE_E_FORMAT, "%s: unsupported gate_up format %d", who, gu_fmt);
   if (dn_fmt != MOE_FMT_Q4_K && dn_fmt != MOE_FMT_Q5_K && dn_fmt != MOE_FMT_Q6_K && dn_fmt != MOE_FMT_BF16)
     return moe_set_error(MOE_E_FORMAT, "%s: unsupported down format %d", who, dn_fmt);
-  if (!aligned16(gu) || !aligned16(dn)) return moe_set_error(MOE_E_ARG, "%s: expert weights must be 16-byte aligned", who);
+  if (!aligned16(gu) || !aligned16(dn) || (up && !aligned16(up)))
+    return moe_set_error(MOE_E_ARG, "%s: expert weights must be 16-byte aligned", who);
   return MOE_OK;
 }
 
-int moe_experts(const void* x, int x_dtype, const void* gate_up_q, int gate_up_fmt,
+static size_t gate_up_row_bytes(int fmt, int H) {
+  return fmt == MOE_FMT_Q4_K ? (size_t)H / 256 * 144 : fmt == MOE_FMT_Q6_K ? (size_t)H / 256 * 210 : (size_t)H * 2;
+}
+
+// (gate, up, estride) of the routed gate/up rows: a fused record [E][2I rows] (up_q NULL, gate
+// rows first) or the separate gate and up tensors [E][I rows] (engine/README.md: the artifact
+// stores ffn_gate_exps and ffn_up_exps apart)
+static void gate_up_bases(const void* gate_q, const void* up_q, int fmt, int H, int I,
+                          const void*& gate, const void*& up, size_t& estride) {
+  const size_t row = gate_up_row_bytes(fmt, H);
+  gate = gate_q;
+  if (up_q) {
+    up = up_q;
+    estride = (size_t)I * row;
+  } else {
+    up = reinterpret_cast<const uint8_t*>(gate_q) + (size_t)I * row;
+    estride = (size_t)2 * I * row;
+  }
+}
+
+int moe_experts(const void* x, int x_dtype, const void* gate_up_q, const void* up_q, int gate_up_fmt,
                 const void* down_q, int down_fmt, const int32_t* expert_offsets,
                 const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I, int E,
                 int K, int path, float* y, void* ws, size_t ws_bytes, void* stream) {
@@ -205,28 +235,31 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, int gate_up_f
     return moe_set_error(MOE_E_ARG, "moe_experts: NULL pointer");
   if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_experts: bad x_dtype %d", x_dtype);
   MOE_TRY(check_geom(T, H, I, E, K, "moe_experts"));
-  MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, down_q, "moe_experts"));
+  MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, up_q, down_q, "moe_experts"));
   if (path == MOE_PATH_GEMV && gate_up_fmt != MOE_FMT_Q4_K) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K gate_up only");
   if (path == MOE_PATH_GEMV && down_fmt == MOE_FMT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K / Q5_K / Q6_K down only");
   if (!aligned16(x)) return moe_set_error(MOE_E_ARG, "moe_experts: x must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
-  return experts_impl(x, x_dtype, nullptr, gate_up_q, gate_up_fmt, down_q, down_fmt, expert_offsets,
+  const void *gate, *up;
+  size_t estride;
+  gate_up_bases(gate_up_q, up_q, gate_up_fmt, H, I, gate, up, estride);
+  return experts_impl(x, x_dtype, nullptr, gate, up, estride, gate_up_fmt, down_q, down_fmt, expert_offsets,
                       sorted_pairs, hit_list, T, H, I, E, K, path, y, w, (hipStream_t)stream);
 }
 
 static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const void* wg,
-                       const void* wu, const void* wd, const void* wsg, int T, int H, int Is,
-                       int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st) {
+                       const void* wu, const void* wd, const void* wsg, int gate_dtype, int T, int H,
+                       int Is, int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st) {
   if (path == MOE_PATH_AUTO) path = T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
   if (path == MOE_PATH_GEMV || path == MOE_PATH_GEMV_MULTI) {
     float* s = reinterpret_cast<float*>(w.take((size_t)T * Is * 4));
     if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
-    return moe_launch_shared_gemv(x, x_dtype, wg, wu, wd, wsg, T, H, Is, s, shared_raw, gate_prob, st);
+    return moe_launch_shared_gemv(x, x_dtype, wg, wu, wd, wsg, gate_dtype, T, H, Is, s, shared_raw, gate_prob, st);
   }
   uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
   if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
-  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, T, H, gate_prob, st));
+  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
   if (path == MOE_PATH_MFMA && H % 256 == 0 && Is % 256 == 0) {
     if (!x16) {
       uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
@@ -242,20 +275,29 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
   return moe_launch_gemm_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, opb, shared_raw, st);
 }
 
+static int check_shared_fmt(int shared_fmt, int gate_dtype, const char* who) {
+  if (shared_fmt != MOE_FMT_BF16)
+    return moe_set_error(MOE_E_FORMAT, "%s: shared-expert weights must be bf16 (got %d)", who, shared_fmt);
+  if (gate_dtype != MOE_DT_BF16 && gate_dtype != MOE_DT_F32)
+    return moe_set_error(MOE_E_FORMAT, "%s: the scalar shared gate must be bf16 or f32 (got %d)", who, gate_dtype);
+  return MOE_OK;
+}
+
 int moe_shared_expert(const void* x, int x_dtype, const void* w_gate, const void* w_up,
-                      const void* w_down, const void* w_scalar_gate, int T, int H, int I_s,
-                      int path, float* shared_raw, float* gate_prob, void* ws, size_t ws_bytes,
-                      void* stream) {
+                      const void* w_down, int shared_fmt, const void* w_scalar_gate, int gate_dtype,
+                      int T, int H, int I_s, int path, float* shared_raw, float* gate_prob, void* ws,
+                      size_t ws_bytes, void* stream) {
   if (!x || !w_gate || !w_up || !w_down || !w_scalar_gate || !shared_raw || !gate_prob)
     return moe_set_error(MOE_E_ARG, "moe_shared_expert: NULL pointer");
   if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_shared_expert: bad x_dtype %d", x_dtype);
+  MOE_TRY(check_shared_fmt(shared_fmt, gate_dtype, "moe_shared_expert"));
   if (T < 1 || H % 2048 || I_s % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_shared_expert: need T >= 1, H %% 2048 == 0, I_s %% 512 == 0");
   if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) || !aligned16(w_scalar_gate))
     return moe_set_error(MOE_E_ARG, "moe_shared_expert: pointers must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
-  return shared_impl(x, x_dtype, nullptr, w_gate, w_up, w_down, w_scalar_gate, T, H, I_s, path,
-                     shared_raw, gate_prob, w, (hipStream_t)stream);
+  return shared_impl(x, x_dtype, nullptr, w_gate, w_up, w_down, w_scalar_gate, gate_dtype, T, H, I_s,
+                     path, shared_raw, gate_prob, w, (hipStream_t)stream);
 }
 
 int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids,
@@ -271,20 +313,32 @@ int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids
 }
 
 static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
-                      const float* norm_w, float norm_eps,
-                      const void* w_router, const float* logit_bias, const void* gate_up_q,
-                      int gate_up_fmt, const void* down_q, int down_fmt, const void* ws_gate,
-                      const void* ws_up, const void* ws_down, const void* ws_scalar_gate,
-                      int path, const float* residual, float* out, void* logits_bf16,
-                      int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
-                      float* shared_out, float* gate_prob, float* expert_raw, void* ws,
-                      size_t ws_bytes, void* stream,
-                              const moe_next_layer* next) {
+                              const moe_layer_weights& Wt, float norm_eps, int path,
+                              const float* residual, float* out, void* logits_bf16,
+                              int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32,
+                              float* routed_sum, float* shared_out, float* gate_prob,
+                              float* expert_raw, void* ws, size_t ws_bytes, void* stream,
+                              const moe_layer_weights* next) {
+  const void* w_router = Wt.w_router;
+  const float* logit_bias = Wt.logit_bias;
+  const void* gate_up_q = Wt.gate_q;
+  const int gate_up_fmt = Wt.gate_up_fmt;
+  const void* down_q = Wt.down_q;
+  const int down_fmt = Wt.down_fmt;
+  const void *ws_gate = Wt.ws_gate, *ws_up = Wt.ws_up, *ws_down = Wt.ws_down;
+  const void* ws_scalar_gate = Wt.ws_scalar_gate;
+  const float* norm_w = Wt.norm_w;
   if (!x || !w_router || !gate_up_q || !down_q || !ws_gate || !ws_up || !ws_down || !ws_scalar_gate || !out)
     return moe_set_error(MOE_E_ARG, "moe_block_forward: NULL pointer");
   if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_block_forward: bad x_dtype %d", x_dtype);
+  if (Wt.router_dtype != MOE_DT_F32 && Wt.router_dtype != MOE_DT_BF16)
+    return moe_set_error(MOE_E_FORMAT, "moe_block_forward: router weights must be bf16 or f32 (got %d)", Wt.router_dtype);
+  MOE_TRY(check_shared_fmt(Wt.shared_fmt, Wt.scalar_gate_dtype, "moe_block_forward"));
   MOE_TRY(check_geom(T, H, I, E, K, "moe_block_forward"));
-  MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, down_q, "moe_block_forward"));
+  MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, Wt.up_q, down_q, "moe_block_forward"));
+  const void *gate, *up;
+  size_t gu_estride;
+  gate_up_bases(gate_up_q, Wt.up_q, gate_up_fmt, H, I, gate, up, gu_estride);
   if (I_s % 512) return moe_set_error(MOE_E_UNSUPPORTED, "moe_block_forward: need I_s %% 512 == 0");
   if (!aligned16(x) || !aligned16(w_router) || !aligned16(ws_gate) || !aligned16(ws_up) || !aligned16(ws_down) || !aligned16(ws_scalar_gate))
     return moe_set_error(MOE_E_ARG, "moe_block_forward: pointers must be 16-byte aligned");
@@ -300,7 +354,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   const bool decode = T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
                       (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q5_K || down_fmt == MOE_FMT_Q6_K) &&
                       I_s % 128 == 0 && E % 4 == 0;
-  const bool one_launch = decode && path != MOE_PATH_GEMV_MULTI &&
+  const bool one_launch = decode && path != MOE_PATH_GEMV_MULTI && Wt.router_dtype == MOE_DT_BF16 &&
+                          Wt.scalar_gate_dtype == MOE_DT_BF16 &&
                           moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt);
   if (norm_w && !one_launch) {
     // every other path reads the normalized rows from the workspace (f32)
@@ -313,8 +368,10 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   if (decode) {
     MoeDecodeLaunch L;
     L.x = x; L.x_dtype = x_dtype; L.residual = residual; L.w_router = w_router; L.bias = logit_bias;
-    L.gu = gate_up_q; L.dn = down_q; L.dn_fmt = down_fmt;
-    L.sg = ws_gate; L.su = ws_up; L.sd = ws_down; L.ssg = ws_scalar_gate;
+    L.router_dt = Wt.router_dtype;
+    L.gu = gate; L.gu_up = up; L.gu_estride = gu_estride;
+    L.dn = down_q; L.dn_fmt = down_fmt;
+    L.sg = ws_gate; L.su = ws_up; L.sd = ws_down; L.ssg = ws_scalar_gate; L.ssg_dt = Wt.scalar_gate_dtype;
     L.logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)E * 2));
     L.ids = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w.take(K * 4));
     L.w_f32 = topk_w_f32 ? topk_w_f32 : reinterpret_cast<float*>(w.take(K * 4));
@@ -329,7 +386,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     L.ids_out_requested = (topk_ids || topk_w_bf16 || topk_w_f32) ? 1 : 0;
     L.norm_w = one_launch ? norm_w : nullptr;
     L.norm_eps = norm_eps;
-    if (next) {
+    if (next && next->router_dtype == MOE_DT_BF16) {
       L.nx_router = next->w_router;
       L.nx_norm = next->norm_w;
     }
@@ -360,15 +417,30 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
     MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
   }
-  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, logit_bias, T, H, E, logits, st));
+  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st));
   MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
   MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
   MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
-  MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate, T, H, I_s, path, sraw, gp, w2, st));
-  MOE_TRY(experts_impl(x, x_dtype, x16, gate_up_q, gate_up_fmt, down_q, down_fmt, offsets, sorted, hits,
-                       T, H, I, E, K, path, y, w, st));
+  MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate, Wt.scalar_gate_dtype, T, H,
+                      I_s, path, sraw, gp, w2, st));
+  MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets, sorted,
+                       hits, T, H, I, E, K, path, y, w, st));
   return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                             shared_out, expert_raw, st);
+}
+
+static moe_layer_weights bf16_layer(const float* norm_w, const void* w_router, const float* logit_bias,
+                                    const void* gate_up_q, int gate_up_fmt, const void* down_q,
+                                    int down_fmt, const void* ws_gate, const void* ws_up,
+                                    const void* ws_down, const void* ws_scalar_gate) {
+  moe_layer_weights W;
+  W.w_router = w_router; W.router_dtype = MOE_DT_BF16; W.logit_bias = logit_bias;
+  W.gate_q = gate_up_q; W.up_q = nullptr; W.gate_up_fmt = gate_up_fmt;
+  W.down_q = down_q; W.down_fmt = down_fmt;
+  W.ws_gate = ws_gate; W.ws_up = ws_up; W.ws_down = ws_down; W.shared_fmt = MOE_FMT_BF16;
+  W.ws_scalar_gate = ws_scalar_gate; W.scalar_gate_dtype = MOE_DT_BF16;
+  W.norm_w = norm_w;
+  return W;
 }
 
 int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
@@ -380,7 +452,11 @@ int moe_block_forward(const void* x, int x_dtype, int T, int H, int I, int E, in
                       int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32, float* routed_sum,
                       float* shared_out, float* gate_prob, float* expert_raw, void* ws,
                       size_t ws_bytes, void* stream) {
-  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, norm_w, norm_eps, w_router, logit_bias, gate_up_q, gate_up_fmt, down_q, down_fmt, ws_gate, ws_up, ws_down, ws_scalar_gate, path, residual, out, logits_bf16, topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob, expert_raw, ws, ws_bytes, stream, nullptr);
+  const moe_layer_weights W = bf16_layer(norm_w, w_router, logit_bias, gate_up_q, gate_up_fmt, down_q,
+                                         down_fmt, ws_gate, ws_up, ws_down, ws_scalar_gate);
+  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, W, norm_eps, path, residual, out, logits_bf16,
+                            topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob,
+                            expert_raw, ws, ws_bytes, stream, nullptr);
 }
 
 int moe_block_forward_prefetch(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
@@ -393,7 +469,27 @@ int moe_block_forward_prefetch(const void* x, int x_dtype, int T, int H, int I, 
                       float* shared_out, float* gate_prob, float* expert_raw, void* ws,
                       size_t ws_bytes, void* stream,
                                const moe_next_layer* next) {
-  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, norm_w, norm_eps, w_router, logit_bias, gate_up_q, gate_up_fmt, down_q, down_fmt, ws_gate, ws_up, ws_down, ws_scalar_gate, path, residual, out, logits_bf16, topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob, expert_raw, ws, ws_bytes, stream, next);
+  const moe_layer_weights W = bf16_layer(norm_w, w_router, logit_bias, gate_up_q, gate_up_fmt, down_q,
+                                         down_fmt, ws_gate, ws_up, ws_down, ws_scalar_gate);
+  moe_layer_weights N{};
+  if (next)
+    N = bf16_layer(next->norm_w, next->w_router, nullptr, nullptr, MOE_FMT_Q4_K, nullptr, MOE_FMT_Q4_K,
+                   next->ws_gate, next->ws_up, next->ws_down, next->ws_scalar_gate);
+  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, W, norm_eps, path, residual, out, logits_bf16,
+                            topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob,
+                            expert_raw, ws, ws_bytes, stream, next ? &N : nullptr);
+}
+
+int moe_block_forward_w(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                        const moe_layer_weights* w, float norm_eps, int path, const float* residual,
+                        float* out, void* logits_bf16, int32_t* topk_ids, void* topk_w_bf16,
+                        float* topk_w_f32, float* routed_sum, float* shared_out, float* gate_prob,
+                        float* expert_raw, void* ws, size_t ws_bytes, void* stream,
+                        const moe_layer_weights* next) {
+  if (!w) return moe_set_error(MOE_E_ARG, "moe_block_forward_w: NULL weights");
+  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, *w, norm_eps, path, residual, out, logits_bf16,
+                            topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob,
+                            expert_raw, ws, ws_bytes, stream, next);
 }
 
 int moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {

@@ -19,14 +19,18 @@ namespace moe {
 struct DecodeArgs {
   const void* x;
   const float* residual;
-  const uint16_t* w_router;
+  const void* w_router;
+  int router_dt;                // router weights: bf16 or f32
   const float* bias;
-  const uint8_t* gu;
+  const uint8_t* gu;            // gate rows of expert e at gu + e * gu_estride
+  const uint8_t* gu_up;         // up rows likewise
+  size_t gu_estride;
   const uint8_t* dn;
   const uint16_t* sg;
   const uint16_t* su;
   const uint16_t* sd;
-  const uint16_t* ssg;
+  const void* ssg;
+  int ssg_dt;                   // scalar shared gate: bf16 or f32
   uint16_t* logits;
   int32_t* ids;
   float* w_f32;
@@ -43,27 +47,38 @@ struct DecodeArgs {
   int H, I, E, K, Is;
 };
 
+// 8 router weights of row wr (bf16 or f32; f32 x f32 products are still exact in f64)
+template <int WDT>
+__device__ __forceinline__ void router_w8(const void* wr, int i, double* o) {
+  if (WDT == MOE_DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(wr) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(wr) + i + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(wr) + i);
+    const uint32_t ww[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { o[2 * k] = bf16_to_f32(ww[k] & 0xFFFFu); o[2 * k + 1] = bf16_to_f32(ww[k] >> 16); }
+  }
+}
+
 // One router logit (R1) for a single token, computed by one wave; returns the bf16 bits.
-template <int XDT>
-__device__ __forceinline__ uint32_t router_logit_wave(const void* xv, const uint16_t* wr,
+template <int XDT, int WDT>
+__device__ __forceinline__ uint32_t router_logit_wave(const void* xv, const void* wr,
                                                       float bias, int H, int lane) {
   const int nchunk = H / 512;
   double acc = 0.0, xsq = 0.0, wsq = 0.0;
   for (int c = 0; c < nchunk; ++c) {
-    const uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
+    double wd[8];
+    router_w8<WDT>(wr, c * 512 + lane * 8, wd);
     float xf[8];
     load_x8<XDT>(xv, (size_t)c * 512 + lane * 8, xf);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const double w0 = bf16_to_f32(ww[i] & 0xFFFFu), w1 = bf16_to_f32(ww[i] >> 16);
-      const double x0 = xf[2 * i], x1 = xf[2 * i + 1];
-      acc = fma(x0, w0, acc);
-      acc = fma(x1, w1, acc);
+    for (int i = 0; i < 8; ++i) {
+      const double x0 = xf[i];
+      acc = fma(x0, wd[i], acc);
       xsq = fma(x0, x0, xsq);
-      xsq = fma(x1, x1, xsq);
-      wsq = fma(w0, w0, wsq);
-      wsq = fma(w1, w1, wsq);
+      wsq = fma(wd[i], wd[i], wsq);
     }
   }
   acc = wave_sum_f64(acc);
@@ -76,15 +91,12 @@ __device__ __forceinline__ uint32_t router_logit_wave(const void* xv, const uint
   if (round_bf16_certified(s, 4.0 * (double)(H + 3) * 0x1p-53 * nrm, &bits)) return bits;
   DD d = {0.0, 0.0};
   for (int c = 0; c < nchunk; ++c) {
-    const uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
+    double wd[8];
+    router_w8<WDT>(wr, c * 512 + lane * 8, wd);
     float xf[8];
     load_x8<XDT>(xv, (size_t)c * 512 + lane * 8, xf);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const double wv_ = bf16_to_f32((i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu));
-      d = dd_add(d, DD{(double)xf[i] * wv_, 0.0});
-    }
+    for (int i = 0; i < 8; ++i) d = dd_add(d, DD{(double)xf[i] * wd[i], 0.0});
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -105,8 +117,11 @@ __global__ __launch_bounds__(256) void k_dec_route_shared(DecodeArgs a) {
   if (bid < NR) {
     const int e = bid * 4 + wave;
     if (e < a.E) {
-      const uint32_t bits = router_logit_wave<XDT>(a.x, a.w_router + (size_t)e * a.H,
-                                                   a.bias ? a.bias[e] : 0.0f, a.H, lane);
+      const float bv = a.bias ? a.bias[e] : 0.0f;
+      const uint32_t bits =
+          a.router_dt == MOE_DT_F32
+              ? router_logit_wave<XDT, MOE_DT_F32>(a.x, reinterpret_cast<const float*>(a.w_router) + (size_t)e * a.H, bv, a.H, lane)
+              : router_logit_wave<XDT, MOE_DT_BF16>(a.x, reinterpret_cast<const uint16_t*>(a.w_router) + (size_t)e * a.H, bv, a.H, lane);
       if (lane == 0) a.logits[e] = (uint16_t)bits;
     }
     __threadfence();                       // publish this wave's logit device-wide
@@ -144,7 +159,7 @@ __global__ __launch_bounds__(256) void k_dec_route_shared(DecodeArgs a) {
     for (int c = 0; c < a.H / 512; ++c) {
       float xv[8];
       load_x8<XDT>(a.x, (size_t)512 * c + 8 * lane, xv);
-      g += dot8_bf16(*reinterpret_cast<const uint4*>(a.ssg + 512 * c + 8 * lane), xv);
+      g += dot8_w(a.ssg, (size_t)512 * c + 8 * lane, a.ssg_dt, xv);
     }
     g = wave_sum_f32(g);
     if (lane == 0) a.gate_prob[0] = 1.0f / (1.0f + expf(-g));
@@ -163,15 +178,15 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecodeArgs a) {
     const int e = a.ids[k];
     const int b = lane >> 3, c = lane & 7, g = c >> 1, l0 = 16 * (c & 1);
     const size_t rowb = (size_t)(a.H / 256) * 144;
-    const uint8_t* ebase = a.gu + (size_t)e * 2 * a.I * rowb;
+    const uint8_t* gbase = a.gu + (size_t)e * a.gu_estride;
+    const uint8_t* ubase = a.gu_up + (size_t)e * a.gu_estride;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int bg = 0; bg < a.H / 2048; ++bg) {
       const int blk = bg * 8 + b;
       uint4 hdr[8], qs[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const int row = (r & 1) ? (a.I + i0 + (r >> 1)) : (i0 + (r >> 1));
-        const uint8_t* p = ebase + (size_t)row * rowb + (size_t)blk * 144;
+        const uint8_t* p = ((r & 1) ? ubase : gbase) + (size_t)(i0 + (r >> 1)) * rowb + (size_t)blk * 144;
         hdr[r] = *reinterpret_cast<const uint4*>(p);
         qs[r] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
       }
@@ -326,10 +341,15 @@ int moe_launch_zero_words(int* p, int n, hipStream_t st) {
 
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st) {
   DecodeArgs a;
-  a.x = L.x; a.residual = L.residual; a.w_router = (const uint16_t*)L.w_router; a.bias = L.bias;
+  a.x = L.x; a.residual = L.residual; a.w_router = L.w_router; a.router_dt = L.router_dt; a.bias = L.bias;
   a.gu = (const uint8_t*)L.gu; a.dn = (const uint8_t*)L.dn;
+  {
+    const size_t rowb = (size_t)(L.H / 256) * 144;
+    a.gu_estride = L.gu_estride ? L.gu_estride : (size_t)2 * L.I * rowb;
+    a.gu_up = L.gu_up ? (const uint8_t*)L.gu_up : a.gu + (size_t)L.I * rowb;
+  }
   a.sg = (const uint16_t*)L.sg; a.su = (const uint16_t*)L.su; a.sd = (const uint16_t*)L.sd;
-  a.ssg = (const uint16_t*)L.ssg;
+  a.ssg = L.ssg; a.ssg_dt = L.ssg_dt;
   a.logits = L.logits; a.ids = L.ids; a.w_f32 = L.w_f32; a.w_bf16 = L.w_bf16;
   a.s_shared = L.s_shared; a.gate_prob = L.gate_prob; a.shared_raw = L.shared_raw;
   a.s_routed = L.s_routed; a.out = L.out; a.routed_sum = L.routed_sum; a.shared_out = L.shared_out;

@@ -67,7 +67,9 @@ struct LayerArgs {
   const float* residual;
   const uint16_t* w_router;
   const float* bias;
-  const uint8_t* gu;
+  const uint8_t* gu;                    // gate rows of expert e at gu + e * gu_estride
+  const uint8_t* gu_up;                 // up rows likewise (a fused record: gu + I rows)
+  size_t gu_estride;
   const uint8_t* dn;
   const uint16_t* sg;
   const uint16_t* su;
@@ -532,12 +534,12 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     const int i0 = 16 * r + 2 * wave;
     const int b = lane >> 3, c = lane & 7, gq = c >> 1, l0 = 16 * (c & 1);
     constexpr size_t rowb = (H / 256) * 144;
-    const uint8_t* ebase = a.gu + (size_t)e * 2 * I * rowb;
+    const uint8_t* gbase = a.gu + (size_t)e * a.gu_estride;
+    const uint8_t* ubase = a.gu_up + (size_t)e * a.gu_estride;
     uint4 hdr[4], qs[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int row = (q & 1) ? (I + i0 + (q >> 1)) : (i0 + (q >> 1));
-      const uint8_t* p = ebase + (size_t)row * rowb + (size_t)b * 144;
+      const uint8_t* p = ((q & 1) ? ubase : gbase) + (size_t)(i0 + (q >> 1)) * rowb + (size_t)b * 144;
       hdr[q] = *reinterpret_cast<const uint4*>(p);
       qs[q] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
     }
@@ -679,6 +681,11 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   LayerArgs a;
   a.x = L.x; a.residual = L.residual; a.w_router = (const uint16_t*)L.w_router; a.bias = L.bias;
   a.gu = (const uint8_t*)L.gu; a.dn = (const uint8_t*)L.dn;
+  {
+    const size_t rowb = (size_t)(L.H / 256) * 144;
+    a.gu_estride = L.gu_estride ? L.gu_estride : (size_t)2 * L.I * rowb;
+    a.gu_up = L.gu_up ? (const uint8_t*)L.gu_up : a.gu + (size_t)L.I * rowb;
+  }
   a.sg = (const uint16_t*)L.sg; a.su = (const uint16_t*)L.su; a.sd = (const uint16_t*)L.sd;
   a.ssg = (const uint16_t*)L.ssg;
   a.sync = sync; a.xch = xch;

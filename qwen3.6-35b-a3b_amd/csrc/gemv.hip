@@ -6,8 +6,9 @@
 // chunk c of a block is qs bytes [16c, 16c+16), i.e. elements 64(c>>1) + 16(c&1) + i (low
 // nibbles, sub-block 2(c>>1)) and the same +32 (high nibbles, sub-block 2(c>>1)+1). The row dot is
 //   sum_sub d*sc_j * sum(q x) - dmin*m_j * sum(x)
-// so the min term costs one multiply per 16 elements. gate row i and up row I+i (gate first,
-// spec §11.4) are contracted together and s = silu(gate)*up is written in f32.
+// so the min term costs one multiply per 16 elements. gate row i and up row i (gate first,
+// spec §11.4: rows i and I + i of a fused record, or row i of the separate gate and up tensors)
+// are contracted together and s = silu(gate)*up is written in f32.
 //
 // down (rows of I = 512 = 2 blocks): 16 lanes per row, 4 rows per wave step.
 #include "common.h"
@@ -19,9 +20,9 @@ namespace moe {
 // grid (I/16, max_hits), block 256; wave w handles intermediate rows i0 = 16*bx + 4w .. +4
 template <int XDT>
 __global__ __launch_bounds__(256) void k_gemv_gateup_q4k(
-    const void* __restrict__ x, const uint8_t* __restrict__ gu, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ hit_list, int H, int I,
-    int K, float* __restrict__ S) {
+    const void* __restrict__ x, const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+    size_t estride, const int32_t* __restrict__ offsets, const int32_t* __restrict__ sorted_pairs,
+    const int32_t* __restrict__ hit_list, int H, int I, int K, float* __restrict__ S) {
   const int hidx = blockIdx.y;
   if (hidx >= hit_list[0]) return;
   const int e = hit_list[1 + hidx];
@@ -29,7 +30,8 @@ __global__ __launch_bounds__(256) void k_gemv_gateup_q4k(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = lane >> 3, c = lane & 7, g = c >> 1, l0 = 16 * (c & 1);
   const size_t rowb = (size_t)(H / 256) * 144;
-  const uint8_t* ebase = gu + (size_t)e * 2 * I * rowb;
+  const uint8_t* gbase = gate + (size_t)e * estride;
+  const uint8_t* ubase = up + (size_t)e * estride;
   const int i0 = blockIdx.x * 16 + wave * 4;
   const int nbg = H / 2048;
   for (int q = p0; q < p1; ++q) {
@@ -45,8 +47,7 @@ __global__ __launch_bounds__(256) void k_gemv_gateup_q4k(
       uint4 hdr[8], qs[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const int row = (r & 1) ? (I + i0 + (r >> 1)) : (i0 + (r >> 1));
-        const uint8_t* p = ebase + (size_t)row * rowb + (size_t)blk * 144;
+        const uint8_t* p = ((r & 1) ? ubase : gbase) + (size_t)(i0 + (r >> 1)) * rowb + (size_t)blk * 144;
         hdr[r] = *reinterpret_cast<const uint4*>(p);
         qs[r] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
       }
@@ -189,8 +190,8 @@ __global__ __launch_bounds__(256) void k_gemv_down_q6k(const float* __restrict__
 
 using namespace moe;
 
-int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gu, int fmt,
-                           const int32_t* offsets, const int32_t* sorted_pairs,
+int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gate, const void* up, size_t estride,
+                           int fmt, const int32_t* offsets, const int32_t* sorted_pairs,
                            const int32_t* hit_list, int max_hits, int H, int I, int K, float* S,
                            hipStream_t st) {
   if (fmt != MOE_FMT_Q4_K)
@@ -198,11 +199,12 @@ int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gu, int fmt,
   if (H % 2048 || I % 16)
     return moe_set_error(MOE_E_UNSUPPORTED, "GEMV gate_up needs H %% 2048 == 0, I %% 16 == 0");
   dim3 grid(I / 16, max_hits);
-  const uint8_t* w = reinterpret_cast<const uint8_t*>(gu);
+  const uint8_t* g = reinterpret_cast<const uint8_t*>(gate);
+  const uint8_t* u = reinterpret_cast<const uint8_t*>(up);
   if (x_dtype == MOE_DT_F32)
-    hipLaunchKernelGGL(k_gemv_gateup_q4k<MOE_DT_F32>, grid, dim3(256), 0, st, x, w, offsets, sorted_pairs, hit_list, H, I, K, S);
+    hipLaunchKernelGGL(k_gemv_gateup_q4k<MOE_DT_F32>, grid, dim3(256), 0, st, x, g, u, estride, offsets, sorted_pairs, hit_list, H, I, K, S);
   else
-    hipLaunchKernelGGL(k_gemv_gateup_q4k<MOE_DT_BF16>, grid, dim3(256), 0, st, x, w, offsets, sorted_pairs, hit_list, H, I, K, S);
+    hipLaunchKernelGGL(k_gemv_gateup_q4k<MOE_DT_BF16>, grid, dim3(256), 0, st, x, g, u, estride, offsets, sorted_pairs, hit_list, H, I, K, S);
   return moe_check_launch("gemv_gateup");
 }
 

@@ -146,4 +146,19 @@ __device__ __forceinline__ float dot8_bf16(uint4 w, const float* x) {
   return a;
 }
 
+// 8 weights from element i of a bf16 or f32 vector (dt = MOE_DT_BF16 / MOE_DT_F32, uniform across
+// the wave) dotted with 8 activations: the scalar shared gate is bf16 in the synthetic configs and
+// f32 in the shipped artifact (ffn_gate_inp_shexp, engine/block_forward.py:221-231).
+__device__ __forceinline__ float dot8_w(const void* w, size_t i, int dt, const float* x) {
+  if (dt == MOE_DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + i + 4);
+    float s = fmaf(a.x, x[0], 0.0f);
+    s = fmaf(a.y, x[1], s); s = fmaf(a.z, x[2], s); s = fmaf(a.w, x[3], s);
+    s = fmaf(b.x, x[4], s); s = fmaf(b.y, x[5], s); s = fmaf(b.z, x[6], s); s = fmaf(b.w, x[7], s);
+    return s;
+  }
+  return dot8_bf16(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + i), x);
+}
+
 }  // namespace moe

@@ -15,8 +15,8 @@ int moe_check_launch(const char* what);
 int moe_launch_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
                        hipStream_t st);
 
-int moe_launch_router_logits(const void* x, int x_dtype, const void* w, const float* bias, int T,
-                             int H, int E, uint16_t* logits, hipStream_t st);
+int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
+                             int T, int H, int E, uint16_t* logits, hipStream_t st);
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
                           float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st);
 
@@ -60,10 +60,10 @@ int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_s
                           float* y, hipStream_t st);
 
 // decode GEMV path: S [P, I] f32 (sorted order), then y [P, H] f32
-int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gu, int fmt,
-                           const int32_t* offsets, const int32_t* sorted_pairs,
-                           const int32_t* hit_list, int max_hits, int H, int I, int K,
-                           float* S, hipStream_t st);
+int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gate, const void* up, size_t estride,
+                           int fmt, const int32_t* offsets, const int32_t* sorted_pairs,
+                           const int32_t* hit_list, int max_hits, int H, int I, int K, float* S,
+                           hipStream_t st);
 int moe_launch_gemv_down(const float* S, const void* dn, int fmt, const int32_t* offsets,
                          const int32_t* hit_list, int max_hits, int H, int I, float* y,
                          hipStream_t st);
@@ -81,9 +81,9 @@ int moe_launch_gemm_down(const uint16_t* S, const void* w_down, int fmt, size_t 
 
 // shared expert
 int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const void* wu,
-                           const void* wd, const void* wsg, int T, int H, int Is, float* s_tmp,
-                           float* shared_raw, float* gate_prob, hipStream_t st);
-int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int T, int H,
+                           const void* wd, const void* wsg, int gate_dtype, int T, int H, int Is,
+                           float* s_tmp, float* shared_raw, float* gate_prob, hipStream_t st);
+int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int gate_dtype, int T, int H,
                            float* gate_prob, hipStream_t st);
 
 // combine
@@ -98,11 +98,15 @@ struct MoeDecodeLaunch {
   int x_dtype;
   const float* residual;
   const void* w_router;
+  int router_dt = MOE_DT_BF16;             // router weight dtype (bf16 or f32)
   const float* bias;
-  const void* gu;
+  const void* gu;                          // gate rows of expert e at gu + e * gu_estride
+  const void* gu_up = nullptr;             // up rows likewise (NULL: fused, up = gate + I rows)
+  size_t gu_estride = 0;                   // bytes per expert (0: fused, 2 I rows)
   const void* dn;
   int dn_fmt;
   const void *sg, *su, *sd, *ssg;
+  int ssg_dt = MOE_DT_BF16;                // scalar shared gate dtype (bf16 or f32)
   uint16_t* logits;
   int32_t* ids;
   float* w_f32;
@@ -139,7 +143,10 @@ struct MoeWs {
   size_t left;
   void* take(size_t bytes) {
     bytes = (bytes + 255) & ~size_t(255);
-    if (bytes > left) return nullptr;
+    if (bytes > left) {
+      left = 0;   // sticky: nothing after a failed take (the sync words first of all) is handed out
+      return nullptr;
+    }
     void* r = p;
     p += bytes;
     left -= bytes;

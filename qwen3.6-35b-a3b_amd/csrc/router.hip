@@ -23,36 +23,70 @@
 
 namespace moe {
 
+// Router weights are bf16 (the synthetic configs, HF checkpoints) or f32 (the shipped artifact's
+// ffn_gate_inp, engine/block_forward.py:221-231). Either way every x * W product is exact in f64
+// (at most 24 + 24 significant bits), so the certificate below holds unchanged.
+template <int WDT>
+__device__ __forceinline__ double w_at(const void* w, size_t i) {
+  if constexpr (WDT == MOE_DT_F32) return (double)reinterpret_cast<const float*>(w)[i];
+  else return (double)bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[i]);
+}
+// 8 consecutive weights from element i (i % 8 == 0)
+template <int WDT>
+__device__ __forceinline__ void w_load8(const void* w, size_t i, double* o) {
+  if constexpr (WDT == MOE_DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + i + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + i);
+    const uint32_t ww[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = bf16_to_f32(ww[k] & 0xFFFFu);
+      o[2 * k + 1] = bf16_to_f32(ww[k] >> 16);
+    }
+  }
+}
+// 4 consecutive weights from element i (i % 4 == 0)
+template <int WDT>
+__device__ __forceinline__ void w_load4(const void* w, size_t i, double* o) {
+  if constexpr (WDT == MOE_DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + i);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  } else {
+    const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(w) + i);
+    o[0] = bf16_to_f32(a.x & 0xFFFFu); o[1] = bf16_to_f32(a.x >> 16);
+    o[2] = bf16_to_f32(a.y & 0xFFFFu); o[3] = bf16_to_f32(a.y >> 16);
+  }
+}
+
 // ----------------------------------------------------------------- R1, small T (T <= 256) -------
 // One wave per (expert row, 8-token slice): the row (H bf16) is read once per slice and applied to
 // each of the slice's tokens. grid = (ceil(E/4), ceil(T/8)), block = 256 (4 waves).
-template <int XDT>
+template <int XDT, int WDT>
 __global__ __launch_bounds__(256) void k_router_logits_gemv(
-    const void* __restrict__ xv, const uint16_t* __restrict__ w, const float* __restrict__ bias,
+    const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias,
     int T, int H, int E, uint16_t* __restrict__ logits) {
   const int lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (e >= E) return;
-  const uint16_t* wr = w + (size_t)e * H;
-  const int nchunk = H / 512;                         // 8 bf16 per lane per chunk
+  const size_t wr = (size_t)e * H;                    // the row's first element
+  const int nchunk = H / 512;                         // 8 weights per lane per chunk
   double wsq = 0.0;
   for (int c = 0; c < nchunk; ++c) {
-    uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    double wd[8];
+    w_load8<WDT>(w, wr + c * 512 + lane * 8, wd);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      double a = bf16_to_f32(ww[i] & 0xFFFFu), b = bf16_to_f32(ww[i] >> 16);
-      wsq = fma(a, a, wsq);
-      wsq = fma(b, b, wsq);
-    }
+    for (int i = 0; i < 8; ++i) wsq = fma(wd[i], wd[i], wsq);
   }
   wsq = wave_sum_f64(wsq);
   const int t_end = min(T, 8 * (int)blockIdx.y + 8);
   for (int t = 8 * blockIdx.y; t < t_end; ++t) {
     double acc = 0.0, xsq = 0.0;
     for (int c = 0; c < nchunk; ++c) {
-      uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      double wd[8];
+      w_load8<WDT>(w, wr + c * 512 + lane * 8, wd);
       float xf[8];
       if (XDT == MOE_DT_F32) {
         const float* xp = reinterpret_cast<const float*>(xv) + (size_t)t * H + c * 512 + lane * 8;
@@ -71,12 +105,9 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const double w0 = bf16_to_f32(ww[i] & 0xFFFFu), w1 = bf16_to_f32(ww[i] >> 16);
-        acc = fma((double)xf[2 * i], w0, acc);
-        acc = fma((double)xf[2 * i + 1], w1, acc);
-        xsq = fma((double)xf[2 * i], (double)xf[2 * i], xsq);
-        xsq = fma((double)xf[2 * i + 1], (double)xf[2 * i + 1], xsq);
+      for (int i = 0; i < 8; ++i) {
+        acc = fma((double)xf[i], wd[i], acc);
+        xsq = fma((double)xf[i], (double)xf[i], xsq);
       }
     }
     acc = wave_sum_f64(acc);
@@ -90,8 +121,8 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
       // double-double recompute, error-free per lane, then across the wave
       DD d = {0.0, 0.0};
       for (int c = 0; c < nchunk; ++c) {
-        uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
-        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+        double wd[8];
+        w_load8<WDT>(w, wr + c * 512 + lane * 8, wd);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           double xv_;
@@ -99,8 +130,7 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
             xv_ = reinterpret_cast<const float*>(xv)[(size_t)t * H + c * 512 + lane * 8 + i];
           else
             xv_ = bf16_to_f32(reinterpret_cast<const uint16_t*>(xv)[(size_t)t * H + c * 512 + lane * 8 + i]);
-          const double wv_ = bf16_to_f32((i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu));
-          d = dd_add(d, DD{xv_ * wv_, 0.0});          // product exact in f64
+          d = dd_add(d, DD{xv_ * wd[i], 0.0});         // product exact in f64
         }
       }
 #pragma unroll
@@ -118,16 +148,16 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
 
 // Rare path of the certificate: one logit recomputed sequentially in double-double (each
 // product is exact in f64, TwoSum accumulation), then rounded to bf16.
-template <int XDT>
+template <int XDT, int WDT>
 __device__ __noinline__ uint32_t logit_dd_recompute(const void* __restrict__ xv,
-                                                    const uint16_t* __restrict__ w, int t, int e,
+                                                    const void* __restrict__ w, int t, int e,
                                                     int H, double bval, double xsq, double wsq) {
   DD d = {0.0, 0.0};
   for (int k = 0; k < H; ++k) {
     const double xk = (XDT == MOE_DT_F32)
                           ? (double)reinterpret_cast<const float*>(xv)[(size_t)t * H + k]
                           : (double)bf16_to_f32(reinterpret_cast<const uint16_t*>(xv)[(size_t)t * H + k]);
-    d = dd_add(d, DD{xk * (double)bf16_to_f32(w[(size_t)e * H + k]), 0.0});
+    d = dd_add(d, DD{xk * w_at<WDT>(w, (size_t)e * H + k), 0.0});
   }
   d = dd_add(d, DD{bval, 0.0});
   const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
@@ -145,15 +175,16 @@ __device__ __noinline__ uint32_t logit_dd_recompute(const void* __restrict__ xv,
 // the block's waves in L1; W, 1 MB at E=256, stays in L2). Each logit gets the same certificate
 // as every R1 kernel here: f64 summation in any order stays within 4 (H+3) 2^-53 ||x|| ||W_e||
 // of the exact sum.
-template <int XDT>
+template <int XDT, int WDT>
 struct RouterRaw {
   using XT = typename std::conditional<XDT == MOE_DT_F32, float4, uint2>::type;
+  using WT = typename std::conditional<WDT == MOE_DT_F32, float4, uint2>::type;
   XT a0, a1;
-  uint2 b0, b1;
+  WT b0, b1;
 };
 
 template <int XDT>
-__device__ __forceinline__ void router_cvt_x(const typename RouterRaw<XDT>::XT& v, double* o) {
+__device__ __forceinline__ void router_cvt_x(const typename RouterRaw<XDT, MOE_DT_BF16>::XT& v, double* o) {
   if constexpr (XDT == MOE_DT_F32) {
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
   } else {
@@ -165,13 +196,17 @@ __device__ __forceinline__ void router_cvt_w(uint2 v, double* o) {
   o[0] = bf16_to_f32(v.x & 0xFFFFu); o[1] = bf16_to_f32(v.x >> 16);
   o[2] = bf16_to_f32(v.y & 0xFFFFu); o[3] = bf16_to_f32(v.y >> 16);
 }
+__device__ __forceinline__ void router_cvt_w(float4 v, double* o) {
+  o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
 
-template <int XDT>
+template <int XDT, int WDT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
-k_router_logits_mfma(const void* __restrict__ xv, const uint16_t* __restrict__ w,
+k_router_logits_mfma(const void* __restrict__ xv, const void* __restrict__ w,
                      const float* __restrict__ bias, int T, int H, int E,
                      uint16_t* __restrict__ logits) {
-  using XT = typename RouterRaw<XDT>::XT;
+  using XT = typename RouterRaw<XDT, WDT>::XT;
+  using WT = typename RouterRaw<XDT, WDT>::WT;
   using d4 = double __attribute__((ext_vector_type(4)));
   constexpr int D = 4;                                  // ring depth in 16-wide k steps
   const int lane = threadIdx.x & 63;
@@ -184,17 +219,19 @@ k_router_logits_mfma(const void* __restrict__ xv, const uint16_t* __restrict__ w
       reinterpret_cast<const char*>(xv) + ((size_t)min(t0 + r, T - 1) * H + 4 * g) * sizeof(XT) / 4);
   const XT* xb = reinterpret_cast<const XT*>(
       reinterpret_cast<const char*>(xv) + ((size_t)min(t0 + 16 + r, T - 1) * H + 4 * g) * sizeof(XT) / 4);
-  const uint2* wa = reinterpret_cast<const uint2*>(w + (size_t)min(e0 + r, E - 1) * H + 4 * g);
-  const uint2* wb = reinterpret_cast<const uint2*>(w + (size_t)min(e0 + 16 + r, E - 1) * H + 4 * g);
-  // one 16-wide k step is 4 XT / 4 uint2 further along each row
-  auto load = [&](RouterRaw<XDT>& q, int step) {
+  const WT* wa = reinterpret_cast<const WT*>(
+      reinterpret_cast<const char*>(w) + ((size_t)min(e0 + r, E - 1) * H + 4 * g) * sizeof(WT) / 4);
+  const WT* wb = reinterpret_cast<const WT*>(
+      reinterpret_cast<const char*>(w) + ((size_t)min(e0 + 16 + r, E - 1) * H + 4 * g) * sizeof(WT) / 4);
+  // one 16-wide k step is 4 XT / 4 WT further along each row
+  auto load = [&](RouterRaw<XDT, WDT>& q, int step) {
     q.a0 = xa[4 * step]; q.a1 = xb[4 * step];
     q.b0 = wa[4 * step]; q.b1 = wb[4 * step];
   };
   d4 c00 = {0, 0, 0, 0}, c01 = c00, c10 = c00, c11 = c00;  // [token half][expert half]
   double xsa = 0, xsb = 0, wsa = 0, wsb = 0;
   const int nst = H / 16;
-  RouterRaw<XDT> q[D];
+  RouterRaw<XDT, WDT> q[D];
 #pragma unroll
   for (int s = 0; s < D; ++s) load(q[s], s);
   for (int it = 0; it < nst; it += D) {
@@ -244,7 +281,7 @@ k_router_logits_mfma(const void* __restrict__ xv, const uint16_t* __restrict__ w
       const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
       uint32_t bits;
       if (!round_bf16_certified(s, bound, &bits))
-        bits = logit_dd_recompute<XDT>(xv, w, t, e, H, bval, xsq, wsq);
+        bits = logit_dd_recompute<XDT, WDT>(xv, w, t, e, H, bval, xsq, wsq);
       logits[(size_t)t * E + e] = (uint16_t)bits;
     }
   }
@@ -253,9 +290,9 @@ k_router_logits_mfma(const void* __restrict__ xv, const uint16_t* __restrict__ w
 // ---------------------------------------------------------------- R1, large T: f64 tile GEMM --
 // Shapes the MFMA kernel does not take (H % 64 != 0): 64 tokens x 64 experts per block of 256
 // threads; each thread owns a 4x4 patch.
-template <int XDT>
+template <int XDT, int WDT>
 __global__ __launch_bounds__(256) void k_router_logits_gemm(
-    const void* __restrict__ xv, const uint16_t* __restrict__ w, const float* __restrict__ bias,
+    const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias,
     int T, int H, int E, uint16_t* __restrict__ logits) {
 
   __shared__ double xs[16][64 + 2];
@@ -284,11 +321,7 @@ __global__ __launch_bounds__(256) void k_router_logits_gemm(
       for (int i = 0; i < 4; ++i) xs[lk + i][lrow] = v[i];
       const int e = e0 + lrow;
       double u[4] = {0, 0, 0, 0};
-      if (e < E) {
-        uint2 a = *reinterpret_cast<const uint2*>(w + (size_t)e * H + k0 + lk);
-        u[0] = bf16_to_f32(a.x & 0xFFFFu); u[1] = bf16_to_f32(a.x >> 16);
-        u[2] = bf16_to_f32(a.y & 0xFFFFu); u[3] = bf16_to_f32(a.y >> 16);
-      }
+      if (e < E) w_load4<WDT>(w, (size_t)e * H + k0 + lk, u);
 #pragma unroll
       for (int i = 0; i < 4; ++i) wsm[lk + i][lrow] = u[i];
     }
@@ -321,7 +354,7 @@ __global__ __launch_bounds__(256) void k_router_logits_gemm(
       const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xsq[i]) * sqrt(wsq[j]) + fabs(bval));
       uint32_t bits;
       if (!round_bf16_certified(s, bound, &bits))
-        bits = logit_dd_recompute<XDT>(xv, w, t, e, H, bval, xsq[i], wsq[j]);
+        bits = logit_dd_recompute<XDT, WDT>(xv, w, t, e, H, bval, xsq[i], wsq[j]);
       logits[(size_t)t * E + e] = (uint16_t)bits;
     }
   }
@@ -352,28 +385,31 @@ __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ 
 
 using namespace moe;
 
-int moe_launch_router_logits(const void* x, int x_dtype, const void* w, const float* bias, int T,
-                             int H, int E, uint16_t* logits, hipStream_t st) {
-  const uint16_t* wr = reinterpret_cast<const uint16_t*>(w);
+template <int XDT, int WDT>
+static void launch_router_logits(const void* x, const void* w, const float* bias, int T, int H,
+                                 int E, uint16_t* logits, hipStream_t st) {
   if (T <= 256) {
-    dim3 grid((E + 3) / 4, (T + 7) / 8);
-    if (x_dtype == MOE_DT_F32)
-      hipLaunchKernelGGL(k_router_logits_gemv<MOE_DT_F32>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
-    else
-      hipLaunchKernelGGL(k_router_logits_gemv<MOE_DT_BF16>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
+    hipLaunchKernelGGL((k_router_logits_gemv<XDT, WDT>), dim3((E + 3) / 4, (T + 7) / 8), dim3(256), 0, st,
+                       x, w, bias, T, H, E, logits);
   } else if (H % 64 == 0) {
-    dim3 grid((T + 31) / 32, (E + 127) / 128);
-    if (x_dtype == MOE_DT_F32)
-      hipLaunchKernelGGL(k_router_logits_mfma<MOE_DT_F32>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
-    else
-      hipLaunchKernelGGL(k_router_logits_mfma<MOE_DT_BF16>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
+    hipLaunchKernelGGL((k_router_logits_mfma<XDT, WDT>), dim3((T + 31) / 32, (E + 127) / 128), dim3(256), 0, st,
+                       x, w, bias, T, H, E, logits);
   } else {
-    dim3 grid((E + 63) / 64, (T + 63) / 64);
-    if (x_dtype == MOE_DT_F32)
-      hipLaunchKernelGGL(k_router_logits_gemm<MOE_DT_F32>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
-    else
-      hipLaunchKernelGGL(k_router_logits_gemm<MOE_DT_BF16>, grid, dim3(256), 0, st, x, wr, bias, T, H, E, logits);
+    hipLaunchKernelGGL((k_router_logits_gemm<XDT, WDT>), dim3((E + 63) / 64, (T + 63) / 64), dim3(256), 0, st,
+                       x, w, bias, T, H, E, logits);
   }
+}
+
+int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
+                             int T, int H, int E, uint16_t* logits, hipStream_t st) {
+  if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32)
+    launch_router_logits<MOE_DT_F32, MOE_DT_F32>(x, w, bias, T, H, E, logits, st);
+  else if (x_dtype == MOE_DT_F32)
+    launch_router_logits<MOE_DT_F32, MOE_DT_BF16>(x, w, bias, T, H, E, logits, st);
+  else if (w_dtype == MOE_DT_F32)
+    launch_router_logits<MOE_DT_BF16, MOE_DT_F32>(x, w, bias, T, H, E, logits, st);
+  else
+    launch_router_logits<MOE_DT_BF16, MOE_DT_BF16>(x, w, bias, T, H, E, logits, st);
   return moe_check_launch("router_logits");
 }
 

@@ -1,4 +1,4 @@
-// Shared expert (bf16 weights) and its scalar sigmoid gate, decode path
+// Shared expert (bf16 weights) and its scalar sigmoid gate (bf16 or f32 weights), decode path
 // (specification/11-moe-block.md §11.6; speccheck/moe_ref.py:480-495; engine/m3_forward.py:436-442).
 //   s[t,i] = silu(gate_i . x_t) * (up_i . x_t)        (f32)
 //   shared_raw[t,h] = down_h . s[t]                   (f32)
@@ -15,7 +15,7 @@ template <int XDT>
 __global__ __launch_bounds__(256) void k_shared_gateup(const void* __restrict__ x,
                                                         const uint16_t* __restrict__ wg,
                                                         const uint16_t* __restrict__ wu,
-                                                        const uint16_t* __restrict__ wsg, int T,
+                                                        const void* __restrict__ wsg, int gdt, int T,
                                                         int H, int Is, float* __restrict__ s,
                                                         float* __restrict__ gate_prob) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -27,7 +27,7 @@ __global__ __launch_bounds__(256) void k_shared_gateup(const void* __restrict__ 
       for (int c = 0; c < nc; ++c) {
         float xv[8];
         load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
-        a += dot8_bf16(*reinterpret_cast<const uint4*>(wsg + 512 * c + 8 * lane), xv);
+        a += dot8_w(wsg, (size_t)512 * c + 8 * lane, gdt, xv);
       }
       a = wave_sum_f32(a);
       if (lane == 0) gate_prob[t] = 1.0f / (1.0f + expf(-a));
@@ -76,14 +76,14 @@ __global__ __launch_bounds__(256) void k_shared_down(const float* __restrict__ s
 // scalar gate only (used beside the MFMA path): one wave per token
 template <int XDT>
 __global__ __launch_bounds__(64) void k_shared_gate(const void* __restrict__ x,
-                                                     const uint16_t* __restrict__ wsg, int T, int H,
-                                                     float* __restrict__ gate_prob) {
+                                                     const void* __restrict__ wsg, int gdt, int T,
+                                                     int H, float* __restrict__ gate_prob) {
   const int t = blockIdx.x, lane = threadIdx.x;
   float a = 0.0f;
   for (int c = 0; c < H / 512; ++c) {
     float xv[8];
     load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
-    a += dot8_bf16(*reinterpret_cast<const uint4*>(wsg + 512 * c + 8 * lane), xv);
+    a += dot8_w(wsg, (size_t)512 * c + 8 * lane, gdt, xv);
   }
   a = wave_sum_f32(a);
   if (lane == 0) gate_prob[t] = 1.0f / (1.0f + expf(-a));
@@ -94,28 +94,26 @@ __global__ __launch_bounds__(64) void k_shared_gate(const void* __restrict__ x,
 using namespace moe;
 
 int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const void* wu,
-                           const void* wd, const void* wsg, int T, int H, int Is, float* s_tmp,
-                           float* shared_raw, float* gate_prob, hipStream_t st) {
+                           const void* wd, const void* wsg, int gate_dtype, int T, int H, int Is,
+                           float* s_tmp, float* shared_raw, float* gate_prob, hipStream_t st) {
   if (H % 512 || Is % 128 || H % 16 || Is % 4)
     return moe_set_error(MOE_E_UNSUPPORTED, "shared GEMV needs H %% 512 == 0, Is %% 128 == 0");
   const uint16_t* g = reinterpret_cast<const uint16_t*>(wg);
   const uint16_t* u = reinterpret_cast<const uint16_t*>(wu);
   const uint16_t* d = reinterpret_cast<const uint16_t*>(wd);
-  const uint16_t* sg = reinterpret_cast<const uint16_t*>(wsg);
   if (x_dtype == MOE_DT_F32)
-    hipLaunchKernelGGL(k_shared_gateup<MOE_DT_F32>, dim3(Is / 4 + 1), dim3(256), 0, st, x, g, u, sg, T, H, Is, s_tmp, gate_prob);
+    hipLaunchKernelGGL(k_shared_gateup<MOE_DT_F32>, dim3(Is / 4 + 1), dim3(256), 0, st, x, g, u, wsg, gate_dtype, T, H, Is, s_tmp, gate_prob);
   else
-    hipLaunchKernelGGL(k_shared_gateup<MOE_DT_BF16>, dim3(Is / 4 + 1), dim3(256), 0, st, x, g, u, sg, T, H, Is, s_tmp, gate_prob);
+    hipLaunchKernelGGL(k_shared_gateup<MOE_DT_BF16>, dim3(Is / 4 + 1), dim3(256), 0, st, x, g, u, wsg, gate_dtype, T, H, Is, s_tmp, gate_prob);
   hipLaunchKernelGGL(k_shared_down, dim3(H / 16), dim3(256), 0, st, s_tmp, d, T, H, Is, shared_raw);
   return moe_check_launch("shared_gemv");
 }
 
-int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int T, int H,
+int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int gate_dtype, int T, int H,
                            float* gate_prob, hipStream_t st) {
-  const uint16_t* sg = reinterpret_cast<const uint16_t*>(wsg);
   if (x_dtype == MOE_DT_F32)
-    hipLaunchKernelGGL(k_shared_gate<MOE_DT_F32>, dim3(T), dim3(64), 0, st, x, sg, T, H, gate_prob);
+    hipLaunchKernelGGL(k_shared_gate<MOE_DT_F32>, dim3(T), dim3(64), 0, st, x, wsg, gate_dtype, T, H, gate_prob);
   else
-    hipLaunchKernelGGL(k_shared_gate<MOE_DT_BF16>, dim3(T), dim3(64), 0, st, x, sg, T, H, gate_prob);
+    hipLaunchKernelGGL(k_shared_gate<MOE_DT_BF16>, dim3(T), dim3(64), 0, st, x, wsg, gate_dtype, T, H, gate_prob);
   return moe_check_launch("shared_gate");
 }

@@ -27,14 +27,18 @@ def zipf_bias(n_experts: int, seed: int, s: float = 1.1, device="cpu") -> torch.
 def make_layer(seed: int, device="cuda", gate_up_fmt: int = Q.FMT_Q4_K,
                down_fmt: int = Q.FMT_Q4_K, zipf: bool = False, n_experts: int = 256,
                hidden: int = 2048, i_e: int = 512, i_s: int = 512, top_k: int = 8,
-               std: float = 0.02, chunk: int = 16) -> LayerWeights:
+               std: float = 0.02, chunk: int = 16, router_dtype=torch.bfloat16,
+               scalar_gate_dtype=torch.bfloat16, split_gate_up: bool = False) -> LayerWeights:
+    """Random-init weights of the block's architecture. router_dtype / scalar_gate_dtype f32 and
+    split_gate_up give the shipped artifact's widths (F32 ffn_gate_inp and ffn_gate_inp_shexp,
+    separate ffn_gate_exps / ffn_up_exps records; engine/block_forward.py:221-231)."""
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(seed)
 
     def randn(*shape):
         return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std
 
-    router = randn(n_experts, hidden).to(torch.bfloat16)
+    router = randn(n_experts, hidden).to(router_dtype)
     gu_row = Q.row_bytes(gate_up_fmt, hidden)
     dn_row = Q.row_bytes(down_fmt, i_e)
     gate_up = torch.empty(n_experts, 2 * i_e, gu_row, dtype=torch.uint8, device=dev)
@@ -52,9 +56,11 @@ def make_layer(seed: int, device="cuda", gate_up_fmt: int = Q.FMT_Q4_K,
         shared_gate=randn(i_s, hidden).to(torch.bfloat16),
         shared_up=randn(i_s, hidden).to(torch.bfloat16),
         shared_down=randn(hidden, i_s).to(torch.bfloat16),
-        shared_scalar_gate=randn(1, hidden).to(torch.bfloat16),
+        shared_scalar_gate=randn(1, hidden).to(scalar_gate_dtype),
         router_bias=zipf_bias(n_experts, seed, device=dev) if zipf else None,
         top_k=top_k)
+    if split_gate_up:
+        lw = lw.split_gate_up()
     lw.validate()
     return lw
 

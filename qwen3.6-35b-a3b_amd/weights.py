@@ -4,11 +4,15 @@ Mirrors the reference's weight handle (engine/block_forward.py:347-483, `W.get(n
 `W.expert_slice('gate'|'up'|'down', e)`) and its geometry dict (engine/block_forward.py:504-531).
 
 HBM layout (all 16-byte aligned, expert axis slowest, as GGUF stores it — engine/loader.py:338-390):
-  router           bf16 [E, H]                      read whole every token
+  router           bf16 or f32 [E, H]               read whole every token (the artifact: f32)
   router_bias      f32  [E] or None                 added inside R1 (synthetic skew only)
-  gate_up_q        u8   [E, 2I, H/256 * blk]        gate rows 0..I-1 then up rows (spec §11.4)
-  down_q           u8   [E, H, I/256 * blk]
-  shared_gate/up   bf16 [I_s, H];  shared_down bf16 [H, I_s];  shared_scalar_gate bf16 [1, H]
+  gate_up_q        u8   [E, 2I, H/256 * blk]        gate rows 0..I-1 then up rows (spec §11.4), or
+                   u8   [E, I, H/256 * blk]         the gate rows alone when up_q is given
+  up_q             u8   [E, I, H/256 * blk] or None the separate up tensor (the artifact's
+                                                    ffn_up_exps beside ffn_gate_exps)
+  down_q           u8   [E, H, I/256 * blk]         Q4_K, Q5_K (the artifact) or Q6_K
+  shared_gate/up   bf16 [I_s, H];  shared_down bf16 [H, I_s]
+  shared_scalar_gate bf16 or f32 [1, H]             (the artifact: f32)
 """
 from __future__ import annotations
 
@@ -41,6 +45,7 @@ class LayerWeights:
     shared_scalar_gate: torch.Tensor
     router_bias: torch.Tensor | None = None
     top_k: int = 8
+    up_q: torch.Tensor | None = None
 
     @property
     def n_experts(self) -> int:
@@ -52,7 +57,13 @@ class LayerWeights:
 
     @property
     def i_e(self) -> int:
-        return self.gate_up_q.shape[1] // 2
+        return self.gate_up_q.shape[1] if self.up_q is not None else self.gate_up_q.shape[1] // 2
+
+    @property
+    def default_widths(self) -> bool:
+        """bf16 router and scalar gate with a fused gate_up record: moe_block_forward's form."""
+        return (self.up_q is None and self.router.dtype == torch.bfloat16
+                and self.shared_scalar_gate.dtype == torch.bfloat16)
 
     @property
     def i_s(self) -> int:
@@ -63,7 +74,8 @@ class LayerWeights:
         return self.router.device
 
     def routed_bytes_per_expert(self) -> int:
-        return self.gate_up_q[0].numel() + self.down_q[0].numel()
+        up = 0 if self.up_q is None else self.up_q[0].numel()
+        return self.gate_up_q[0].numel() + up + self.down_q[0].numel()
 
     def shared_bytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in
@@ -72,19 +84,23 @@ class LayerWeights:
     def validate(self) -> None:
         E, H = self.router.shape
         I = self.i_e
+        rows = I if self.up_q is not None else 2 * I
         want = {
-            "gate_up_q": (self.gate_up_q, torch.uint8, (E, 2 * I, Q.row_bytes(self.gate_up_fmt, H))),
+            "gate_up_q": (self.gate_up_q, torch.uint8, (E, rows, Q.row_bytes(self.gate_up_fmt, H))),
             "down_q": (self.down_q, torch.uint8, (E, H, Q.row_bytes(self.down_fmt, I))),
             "shared_gate": (self.shared_gate, torch.bfloat16, (self.i_s, H)),
             "shared_up": (self.shared_up, torch.bfloat16, (self.i_s, H)),
             "shared_down": (self.shared_down, torch.bfloat16, (H, self.i_s)),
-            "shared_scalar_gate": (self.shared_scalar_gate, torch.bfloat16, (1, H)),
+            "shared_scalar_gate": (self.shared_scalar_gate, self.shared_scalar_gate.dtype, (1, H)),
         }
+        if self.up_q is not None:
+            want["up_q"] = (self.up_q, torch.uint8, (E, I, Q.row_bytes(self.gate_up_fmt, H)))
         for name, (t, dt, shp) in want.items():
             if t.dtype != dt or tuple(t.shape) != tuple(shp) or not t.is_contiguous():
                 raise ValueError(f"{name}: got {t.dtype} {tuple(t.shape)}, want {dt} {shp}")
-        if self.router.dtype != torch.bfloat16:
-            raise ValueError("router must be bf16")
+        for name, t in (("router", self.router), ("shared_scalar_gate", self.shared_scalar_gate)):
+            if t.dtype not in (torch.bfloat16, torch.float32):
+                raise ValueError(f"{name} must be bf16 or f32, got {t.dtype}")
 
     # ----------------------------------------------------- the reference's weight-handle surface
     def get(self, name: str) -> torch.Tensor:
@@ -103,8 +119,32 @@ class LayerWeights:
         from . import abi
         H, I = self.hidden, self.i_e
         if role in ("gate", "up"):
-            rows = self.gate_up_q[e, :I] if role == "gate" else self.gate_up_q[e, I:]
+            if self.up_q is not None:
+                rows = self.gate_up_q[e] if role == "gate" else self.up_q[e]
+            else:
+                rows = self.gate_up_q[e, :I] if role == "gate" else self.gate_up_q[e, I:]
             return abi.dequant(rows.contiguous(), self.gate_up_fmt, I * H).view(I, H)
         if role == "down":
             return abi.dequant(self.down_q[e].contiguous(), self.down_fmt, H * I).view(H, I)
         raise KeyError(role)
+
+    def split_gate_up(self) -> "LayerWeights":
+        """The same weights with gate and up as separate tensors (the artifact's ffn_gate_exps and
+        ffn_up_exps records); the bytes are the same bytes."""
+        import dataclasses
+        I = self.i_e
+        if self.up_q is not None:
+            return self
+        return dataclasses.replace(self, gate_up_q=self.gate_up_q[:, :I].contiguous(),
+                                   up_q=self.gate_up_q[:, I:].contiguous())
+
+    def c_struct(self, norm_w: torch.Tensor | None = None):
+        """moe_layer_weights for moe_block_forward_w (pointers into these tensors)."""
+        from . import _lib as L
+        dt = lambda t: L.MOE_DT_F32 if t.dtype == torch.float32 else L.MOE_DT_BF16
+        p = lambda t: None if t is None else t.data_ptr()
+        return L.LayerWeightsC(
+            p(self.router), dt(self.router), p(self.router_bias), p(self.gate_up_q), p(self.up_q),
+            self.gate_up_fmt, p(self.down_q), self.down_fmt, p(self.shared_gate), p(self.shared_up),
+            p(self.shared_down), L.MOE_FMT_BF16, p(self.shared_scalar_gate),
+            dt(self.shared_scalar_gate), p(norm_w))

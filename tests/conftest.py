@@ -61,3 +61,15 @@ def layer_q5k(pkg, dev):
     lw = pkg.synth.make_layer(seed=5, device=dev, down_fmt=pkg.quant.FMT_Q5_K)
     torch.cuda.synchronize()
     return lw, O.from_device(lw)
+
+
+@pytest.fixture(scope="session")
+def layer_artifact(pkg, dev):
+    """The shipped artifact's widths all at once: F32 router and scalar shared gate, separate
+    Q4_K gate and up records, Q5_K down (seed 7, Zipf routing)."""
+    from oracle import moe_oracle as O
+    lw = pkg.synth.make_layer(seed=7, device=dev, down_fmt=pkg.quant.FMT_Q5_K, zipf=True,
+                              router_dtype=torch.float32, scalar_gate_dtype=torch.float32,
+                              split_gate_up=True)
+    torch.cuda.synchronize()
+    return lw, O.from_device(lw)

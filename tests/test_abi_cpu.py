@@ -24,6 +24,32 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
     assert set(names) == set(pkg._lib.SIGNATURES), set(names) ^ set(pkg._lib.SIGNATURES)
 
 
+def test_binding_arity_matches_header(pkg):
+    """Each ctypes signature has as many parameters as the header's prototype."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, (_, args) in pkg._lib.SIGNATURES.items():
+        m = re.search(r"\b" + name + r"\s*\(([^)]*)\)", text)
+        assert m, name
+        params = [q for q in m.group(1).split(",") if q.strip() and q.strip() != "void"]
+        assert len(params) == len(args), (name, len(params), len(args))
+
+
+def test_layer_struct_matches_header(pkg):
+    """moe_layer_weights field order and kinds match the ctypes Structure."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct moe_layer_weights\s*\{(.*?)\}", text, re.S).group(1)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        kind = "int" if re.match(r"int\b", decl) else "ptr"
+        for nm in decl.split(","):
+            fields.append((re.sub(r"[^A-Za-z0-9_]", " ", nm).split()[-1], kind))
+    got = [(n, "int" if t is ctypes.c_int else "ptr") for n, t in pkg._lib.LayerWeightsC._fields_]
+    assert fields == got
+
+
 def test_abi_version_and_enums_match_header(pkg):
     text = HEADER.read_text()
     assert pkg._lib.lib.moe_abi_version() == int(re.search(r"MOE_ABI_VERSION (\d+)", text).group(1))
@@ -56,7 +82,7 @@ def test_refusals_happen_on_the_host(pkg):
     assert lib.moe_dequant(p, 12, 100, p, 0, None) == pkg._lib.MOE_E_ARG       # not a multiple of 256
     assert lib.moe_dequant(p, 12, 256, p, 5, None) == pkg._lib.MOE_E_ARG       # bad out dtype
     # geometry refusals
-    rc = lib.moe_router_topk(p, 0, p, None, 1, 2048, 256, 2, p, None, p, p, p, None, 0, None)
+    rc = lib.moe_router_topk(p, 0, p, 1, None, 1, 2048, 256, 2, p, None, p, p, p, None, 0, None)
     assert rc == pkg._lib.MOE_E_UNSUPPORTED                                  # K*64 <= E
     assert b"K*64 > E" in lib.moe_last_error()
     rc = lib.moe_block_forward(p, 0, 1, 2048, 512, 256, 8, 512, None, 1e-6, p, None, p, 12, p, 12,
@@ -68,9 +94,39 @@ def test_refusals_happen_on_the_host(pkg):
                                p, p, p, p, 0, None, p, None, None, None, None, None, None, None,
                                None, p, 1 << 30, None)
     assert rc == pkg._lib.MOE_E_ARG
-    rc = lib.moe_experts(p, 0, p, 99, p, 12, p, p, p, 1, 2048, 512, 256, 8, 0, p, p, 1 << 20, None)
+    rc = lib.moe_experts(p, 0, p, None, 99, p, 12, p, p, p, 1, 2048, 512, 256, 8, 0, p, p, 1 << 20,
+                         None)
     assert rc == pkg._lib.MOE_E_FORMAT
+    # the router and the scalar shared gate are bf16 or f32; the shared expert bf16
+    rc = lib.moe_router_topk(p, 0, p, 7, None, 1, 2048, 256, 8, p, None, p, p, p, p, 1 << 20, None)
+    assert rc == pkg._lib.MOE_E_FORMAT
+    rc = lib.moe_shared_expert(p, 0, p, p, p, 12, p, 1, 1, 2048, 512, 0, p, p, p, 1 << 20, None)
+    assert rc == pkg._lib.MOE_E_FORMAT
+    rc = lib.moe_shared_expert(p, 0, p, p, p, 30, p, 7, 1, 2048, 512, 0, p, p, p, 1 << 20, None)
+    assert rc == pkg._lib.MOE_E_FORMAT
+    # the descriptor entry checks the descriptor's formats the same way
+    L = pkg._lib
+    W = L.LayerWeightsC(p.value, 7, None, p.value, None, 12, p.value, 13, p.value, p.value,
+                        p.value, 30, p.value, 0, p.value)
+    rc = lib.moe_block_forward_w(p, 0, 1, 2048, 512, 256, 8, 512, ctypes.byref(W), 1e-6, 0, None,
+                                 p, None, None, None, None, None, None, None, None, p, 1 << 30,
+                                 None, None)
+    assert rc == pkg._lib.MOE_E_FORMAT
+    W.router_dtype = 0
+    W.down_fmt = 99
+    rc = lib.moe_block_forward_w(p, 0, 1, 2048, 512, 256, 8, 512, ctypes.byref(W), 1e-6, 0, None,
+                                 p, None, None, None, None, None, None, None, None, p, 1 << 30,
+                                 None, None)
+    assert rc == pkg._lib.MOE_E_FORMAT
+    rc = lib.moe_block_forward_w(p, 0, 1, 2048, 512, 256, 8, 512, None, 1e-6, 0, None,
+                                 p, None, None, None, None, None, None, None, None, p, 1 << 30,
+                                 None, None)
+    assert rc == pkg._lib.MOE_E_ARG
     assert lib.moe_workspace_init(p, 16, None) == pkg._lib.MOE_E_ARG
+    # the sort's scratch starts after the sync words: a workspace that only holds the scratch
+    # itself is too small
+    rc = lib.moe_sort_permute(p, 16, 8, 256, p, p, p, p, p, 4096, None)
+    assert rc == pkg._lib.MOE_E_WORKSPACE and b"525312" in lib.moe_last_error()   # 512 KiB + 256 x 4 B
 
 
 def test_product_path_never_imports_the_oracle():
