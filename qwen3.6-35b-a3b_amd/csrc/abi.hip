@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "moe_internal.h"
 
 static thread_local char g_err[512] = "";
@@ -46,6 +48,37 @@ static int pick_path(int path, int T, int gate_up_fmt) {
   if (path == MOE_PATH_GEMV || path == MOE_PATH_MFMA || path == MOE_PATH_MFMA_BF16) return path;
   if (gate_up_fmt != MOE_FMT_Q4_K) return MOE_PATH_MFMA;
   return T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
+}
+
+// The grouped paths' shared expert depends on x alone, so from kForkMinT tokens on it runs on a
+// library-owned second stream of the device (default priority, non-blocking) beside the router,
+// sort and routed GEMMs, and the caller's stream waits for it before the combine: its kernels
+// (few workgroups) then fill CUs the routed GEMMs leave idle. The fork and join are events, so
+// the pattern is legal under graph capture. One mutex serialises the enqueue sequence, because
+// the stream and its two events are shared by every call on the device.
+constexpr int kForkMinT = 256;
+constexpr int kMaxDevices = 64;
+struct ForkRes {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static ForkRes g_fork[kMaxDevices];
+static std::mutex g_fork_mu;
+
+// called with g_fork_mu held
+static int fork_res(ForkRes*& r) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return moe_set_error(MOE_E_HIP, "moe_block_forward: no current device for the shared-expert stream");
+  ForkRes& f = g_fork[dev];
+  if (!f.s) {
+    if (hipStreamCreateWithFlags(&f.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess)
+      return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot create the shared-expert stream");
+  }
+  r = &f;
+  return MOE_OK;
 }
 
 struct Carve {
@@ -417,14 +450,38 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
     MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
   }
-  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st));
-  MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
-  MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
-  MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
-  MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate, Wt.scalar_gate_dtype, T, H,
-                      I_s, path, sraw, gp, w2, st));
-  MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets, sorted,
-                       hits, T, H, I, E, K, path, y, w, st));
+  if (T < kForkMinT) {
+    MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st));
+    MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
+    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
+    MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
+    MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate, Wt.scalar_gate_dtype, T, H,
+                        I_s, path, sraw, gp, w2, st));
+    MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets, sorted,
+                         hits, T, H, I, E, K, path, y, w, st));
+    return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
+                              shared_out, expert_raw, st);
+  }
+  // the shared expert on the second stream, its scratch taken before (and disjoint from) the
+  // routed experts'; the join is enqueued on every path out, so the caller's stream never runs
+  // ahead of work still reading this call's workspace
+  std::lock_guard<std::mutex> lock(g_fork_mu);
+  ForkRes* f = nullptr;
+  MOE_TRY(fork_res(f));
+  if (hipEventRecord(f->fork, st) != hipSuccess || hipStreamWaitEvent(f->s, f->fork, 0) != hipSuccess)
+    return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot fork the shared-expert stream");
+  const int rc_sh = shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate,
+                                Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s);
+  int rc = rc_sh;
+  if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st);
+  if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st);
+  if (rc == MOE_OK) rc = moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st);
+  if (rc == MOE_OK)
+    rc = experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
+                      sorted, hits, T, H, I, E, K, path, y, w, st);
+  if (hipEventRecord(f->join, f->s) != hipSuccess || hipStreamWaitEvent(st, f->join, 0) != hipSuccess)
+    return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot join the shared-expert stream");
+  if (rc != MOE_OK) return rc;
   return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                             shared_out, expert_raw, st);
 }

@@ -286,3 +286,34 @@ def test_prefill_q5k_down_sampled_rows(pkg, layer_q5k, dev):
     rows = torch.randperm(2048, generator=torch.Generator().manual_seed(5))[:96]
     ref = O.moe_block(x.cpu()[rows], ow)
     _compare(st, ref, rows=rows, tag="q5k prefill")
+
+
+def test_prefill_shared_stream_fork_same_bits_and_graph(pkg, layer_c0, dev):
+    """From 256 tokens the shared expert runs on the library's second stream (forked from and
+    joined back into the caller's stream by events). The rows equal those of a 255-token call,
+    which runs every kernel on one stream, bit for bit; and the fork/join captured in a graph
+    replays to the eager bits, with eager calls between the replays."""
+    lw, _ = layer_c0
+    x = pkg.synth.make_input(256, seed=71, device=dev, dtype=torch.bfloat16)
+    a = pkg.abi.block_forward(x, lw, stages={"topk_ids"})
+    b = pkg.abi.block_forward(x[:255].contiguous(), lw, stages={"topk_ids"})
+    torch.cuda.synchronize()
+    assert torch.equal(a["topk_ids"][:255], b["topk_ids"])
+    assert torch.equal(a["combined_out"][:255], b["combined_out"])
+    want = a["combined_out"].clone()
+    out = torch.empty_like(want)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            pkg.abi.block_forward(x, lw, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+        other = pkg.abi.block_forward(x, lw)["combined_out"]
+        torch.cuda.synchronize()
+        assert torch.equal(other, want), rep
