@@ -69,6 +69,9 @@ def parse():
                     help="only the config-2 batched-decode timing (what the c2 profile covers)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing (what the kernel-trace profile covers)")
+    ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="only the untied lm_head GEMV timing (what the lm_head profile covers)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--pmc", action="store_true")
     ap.add_argument("--no-hint", action="store_true",
@@ -330,6 +333,34 @@ def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
             "prefill_tflops": tflops, "prefill_mfma_util": tflops / BF16_PEAK_TFLOPS}
 
 
+def lm_head_bench(torch, pkg, dev, reps: int = 20) -> dict:
+    """The untied lm_head GEMV at the artifact's shape (248320 x 2048), one token, for each table
+    width: kernel time from HIP events on the launching stream and table GB/s (each byte read
+    once per call)."""
+    L_, abi, Q = pkg._lib, pkg.abi, pkg.quant
+    V, H = 248320, 2048
+    g = torch.Generator(device=dev).manual_seed(3)
+    h = torch.randn(1, H, generator=g, device=dev)
+    res = {}
+    for name, fmt in (("q6k", L_.MOE_FMT_Q6_K), ("q8_0", L_.MOE_FMT_Q8_0), ("bf16", L_.MOE_FMT_BF16)):
+        w = torch.randn(V, H, generator=g, device=dev) * 0.02
+        t = w.to(torch.bfloat16) if fmt == L_.MOE_FMT_BF16 else Q.quantize(w, fmt)
+        del w
+        nbytes = t.numel() * t.element_size()
+        for _ in range(3):
+            abi.lm_head(h, t, fmt)
+        torch.cuda.synchronize()
+        ms = time_stream(lambda: abi.lm_head(h, t, fmt), reps, torch)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"lm_head {name}: {ms * 1000:.1f} us per token, {nbytes / 1e6:.0f} MB table, "
+            f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBPS:.1f}% of HBM peak)")
+        res[f"lm_head_{name}_us"] = ms * 1000
+        res[f"lm_head_{name}_gbps"] = gbs
+        del t
+        torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.pmc_summary:
@@ -359,6 +390,11 @@ def main():
 
     if args.c2_only:
         print(json.dumps(c2_step(torch, synth, abi, dev, 50)), flush=True)
+        return
+
+    if args.lm_head_only:
+        r = lm_head_bench(torch, pkg, dev)
+        print(json.dumps({k: round(v, 3) for k, v in r.items()}), flush=True)
         return
 
     if args.prefill_only:
@@ -425,6 +461,9 @@ def main():
     if not args.no_prefill:
         prefill = prefill_c3(torch, synth, abi, layers[0], dev, args.prefill_steps)
 
+    # ---------------------------------------------------------------- untied lm_head GEMV
+    lmh = lm_head_bench(torch, pkg, dev) if not args.no_lm_head else {}
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -468,6 +507,7 @@ def main():
         "cpu_baseline": cpu,
     }
     result.update(c2)
+    result.update({k: round(v, 3) for k, v in lmh.items()})
     result.update({k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()})
     print(json.dumps(result), flush=True)
 

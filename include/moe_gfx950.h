@@ -44,7 +44,7 @@ enum { MOE_DT_F32 = 0, MOE_DT_BF16 = 1 };
 /* weight formats: ggml_type ids (tools/gguf_reader.py:10-51 block table). Routed gate_up: Q4_K,
  * Q6_K or BF16; routed down: Q4_K, Q5_K (the shipped artifact's down in 37 of its 40 layers,
  * engine/README.md:33,115), Q6_K or BF16; moe_dequant: Q4_K, Q5_K, Q6_K. */
-enum { MOE_FMT_Q4_K = 12, MOE_FMT_Q5_K = 13, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
+enum { MOE_FMT_Q8_0 = 8, MOE_FMT_Q4_K = 12, MOE_FMT_Q5_K = 13, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
 
 /* expert contraction path: GEMV = fused decode + f32 GEMV; MFMA = tiles decoded to f16 in LDS on
  * MFMA (f32 accumulation); MFMA_BF16 = the same with bf16 operands (8 significant bits instead of
@@ -211,6 +211,19 @@ int moe_block_forward_prefetch(const void *x, int x_dtype, int T, int H, int I, 
                                float *routed_sum, float *shared_out, float *gate_prob,
                                float *expert_raw, void *ws, size_t ws_bytes, void *stream,
                                const moe_next_layer *next);
+
+/* Untied lm_head GEMV: logits[b, j] = sum_k h[b, k] * W[row_j, k] in f32 for b < B (1..8) and
+ * j < n_rows, with row_j = j (dense: row_ids NULL, n_rows <= V) or row_j = row_ids[j] (gather; an
+ * id outside [0, V) gives NaN for that output). h: [B, H] f32 or bf16 (h_dtype); W: V rows of H
+ * in w_fmt: MOE_FMT_Q6_K (H/256 x 210 B per row: the shipped artifact's output.weight,
+ * engine/README.md:33), MOE_FMT_Q8_0 (H/32 x 34 B) or MOE_FMT_BF16 (H x 2 B); W 16-byte aligned.
+ * logits: [B, n_rows] f32. Limits: H == 2048. Tokens go in passes of up to 4, each reading the
+ * table once. Results are f32 dots in this kernel's association order: they lie within the
+ * reference's band gamma_n * sum_k |h_k w_k| (n = K-1 for exact products, 2K-1 otherwise;
+ * prototype/lm_head/gate.py:214-240) of the exact dot. Replaces prototype/lm_head/
+ * lm_head_kernels.h:474-512 (lmh_dot_batch) as launched by prototype/lm_head/lm_head.hip:51. */
+int moe_lm_head(const void *h, int h_dtype, int B, int H, const void *w, int w_fmt, int64_t V,
+                const int32_t *row_ids, int64_t n_rows, float *logits, void *stream);
 
 /* Zero the workspace's device-side sync words (its first 512 KiB: error bits, the single-launch
  * decode layer's per-role launch counts and its two exchange buffers; one short fill launch).

@@ -22,6 +22,7 @@ ERROR_NAMES = {MOE_E_ARG: "bad-argument", MOE_E_FORMAT: "unsupported-format",
 
 MOE_DT_F32 = 0
 MOE_DT_BF16 = 1
+MOE_FMT_Q8_0 = 8
 MOE_FMT_Q4_K = 12
 MOE_FMT_Q5_K = 13
 MOE_FMT_Q6_K = 14
@@ -83,6 +84,7 @@ SIGNATURES = {
                                  ctypes.c_float, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                  _VP, _VP, _SZ, _VP, ctypes.POINTER(LayerWeightsC)]),
     "moe_workspace_init": (_I, [_VP, _SZ, _VP]),
+    "moe_lm_head": (_I, [_VP, _I, _I, _I, _VP, _I, _I64, _VP, _I64, _VP, _VP]),
 }
 
 

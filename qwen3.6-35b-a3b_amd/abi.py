@@ -301,3 +301,28 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
         _check(L.lib.moe_block_forward_prefetch(*args, ctypes.byref(hint)), "block_forward")
     st["combined_out"] = out
     return st
+
+
+def lm_head(h: torch.Tensor, table: torch.Tensor, fmt: int,
+            row_ids: torch.Tensor | None = None) -> torch.Tensor:
+    """Untied lm_head GEMV (moe_lm_head): logits f32 [B, n] = h [B, 2048] (f32 or bf16, B <= 8)
+    against the table rows (all V rows, or row_ids int32 [n] for the gather form).
+    table: uint8 [V, row_bytes] for MOE_FMT_Q6_K / MOE_FMT_Q8_0, bfloat16 [V, 2048] for
+    MOE_FMT_BF16. Replaces prototype/lm_head/lm_head_kernels.h:474-512 (lmh_dot_batch)."""
+    _need(h, "h")
+    B, H = h.shape
+    dev = h.device
+    if fmt == L.MOE_FMT_BF16:
+        _need(table, "table", torch.bfloat16, device=dev)
+    else:
+        _need(table, "table", torch.uint8, device=dev)
+    V = table.shape[0]
+    if row_ids is not None:
+        _need(row_ids, "row_ids", torch.int32, device=dev)
+        n = row_ids.numel()
+    else:
+        n = V
+    out = torch.empty(B, n, dtype=torch.float32, device=dev)
+    _check(L.lib.moe_lm_head(_p(h), _xdt(h), B, H, _p(table), fmt, V, _p(row_ids), n, _p(out),
+                             _stream(h)), "lm_head")
+    return out

@@ -549,6 +549,22 @@ int moe_block_forward_w(const void* x, int x_dtype, int T, int H, int I, int E, 
                             expert_raw, ws, ws_bytes, stream, next);
 }
 
+int moe_lm_head(const void* h, int h_dtype, int B, int H, const void* w, int w_fmt, int64_t V,
+                const int32_t* row_ids, int64_t n_rows, float* logits, void* stream) {
+  if (!h || !w || !logits) return moe_set_error(MOE_E_ARG, "moe_lm_head: NULL pointer");
+  if (h_dtype != MOE_DT_F32 && h_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_lm_head: bad h_dtype %d", h_dtype);
+  if (w_fmt != MOE_FMT_Q6_K && w_fmt != MOE_FMT_Q8_0 && w_fmt != MOE_FMT_BF16)
+    return moe_set_error(MOE_E_FORMAT, "moe_lm_head: table format %d (want Q6_K, Q8_0 or BF16)", w_fmt);
+  if (B < 1 || B > 8 || V < 1 || n_rows < 1 || (!row_ids && n_rows > V))
+    return moe_set_error(MOE_E_ARG, "moe_lm_head: need 1 <= B <= 8, V >= 1, 1 <= n_rows (<= V when dense)");
+  if (!moe_lm_head_supported(H, w_fmt)) return moe_set_error(MOE_E_UNSUPPORTED, "moe_lm_head: need H == 2048 (got %d)", H);
+  if (!aligned16(w) || (reinterpret_cast<uintptr_t>(h) & (h_dtype == MOE_DT_F32 ? 3u : 1u)) ||
+      (reinterpret_cast<uintptr_t>(logits) & 3u) || (row_ids && (reinterpret_cast<uintptr_t>(row_ids) & 3u)))
+    return moe_set_error(MOE_E_ARG, "moe_lm_head: W must be 16-byte aligned, h / logits / row_ids element aligned");
+  return moe_launch_lm_head(h, h_dtype, B, w, w_fmt, (long long)V, row_ids, (long long)n_rows, logits,
+                            (hipStream_t)stream);
+}
+
 int moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {
   if (!ws || ws_bytes < kSyncBytes) return moe_set_error(MOE_E_ARG, "moe_workspace_init: workspace smaller than %zu bytes", kSyncBytes);
   return moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream);

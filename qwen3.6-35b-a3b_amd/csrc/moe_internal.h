@@ -137,6 +137,11 @@ bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, 
 size_t moe_layer_exchange_bytes();
 int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st);
 
+// untied lm_head GEMV (lm_head.hip): H = 2048; Q6_K, Q8_0 or BF16 rows; B tokens in passes of 4
+bool moe_lm_head_supported(int H, int fmt);
+int moe_launch_lm_head(const void* h, int h_dtype, int B, const void* w, int fmt, long long V,
+                       const int32_t* row_ids, long long n_rows, float* logits, hipStream_t st);
+
 // workspace carving
 struct MoeWs {
   char* p;

@@ -30,7 +30,10 @@ FMT_Q4_K = 12
 FMT_Q5_K = 13
 FMT_Q6_K = 14
 FMT_BF16 = 30
-BLOCK_BYTES = {FMT_Q4_K: Q4K_BYTES, FMT_Q5_K: Q5K_BYTES, FMT_Q6_K: Q6K_BYTES}
+FMT_Q8_0 = 8
+Q8_0_BYTES = 34                      # f16 d + 32 x int8, per 32 elements
+# bytes per 256 elements
+BLOCK_BYTES = {FMT_Q4_K: Q4K_BYTES, FMT_Q5_K: Q5K_BYTES, FMT_Q6_K: Q6K_BYTES, FMT_Q8_0: 8 * Q8_0_BYTES}
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
@@ -126,6 +129,19 @@ def _q6k_rows(w: torch.Tensor) -> torch.Tensor:
     return out.reshape(rows, nb * Q6K_BYTES)
 
 
+def _q8_0_rows(w: torch.Tensor) -> torch.Tensor:
+    """Q8_0: per 32 elements d = f16(max|x| / 127), q = round(x / d) as int8 (the GGUF block
+    tools/gguf_reader.py:238-245 decodes)."""
+    rows, cols = w.shape
+    nb = cols // 32
+    x = w.reshape(rows, nb, 32).float()
+    d = (x.abs().amax(dim=-1) / 127.0).to(torch.float16).float()
+    q = torch.where(d[..., None] > 0, torch.round(x / d[..., None].clamp_min(1e-30)),
+                    torch.zeros_like(x)).clamp(-127, 127).to(torch.int8).view(torch.uint8)
+    out = torch.cat([_f16_bytes(d), q], dim=-1)
+    return out.reshape(rows, nb * Q8_0_BYTES)
+
+
 def quantize(w, fmt: int, chunk_rows: int = 16384) -> torch.Tensor:
     """float[rows, cols] (torch or numpy; cols % 256 == 0) -> uint8[rows, row_bytes(fmt, cols)]
     on the same device as `w`."""
@@ -133,7 +149,7 @@ def quantize(w, fmt: int, chunk_rows: int = 16384) -> torch.Tensor:
         w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float32))
     if w.dim() != 2 or w.shape[1] % QK_K:
         raise ValueError(f"expected [rows, cols] with cols % 256 == 0, got {tuple(w.shape)}")
-    fn = {FMT_Q4_K: _q4k_rows, FMT_Q5_K: _q5k_rows, FMT_Q6_K: _q6k_rows}.get(fmt)
+    fn = {FMT_Q4_K: _q4k_rows, FMT_Q5_K: _q5k_rows, FMT_Q6_K: _q6k_rows, FMT_Q8_0: _q8_0_rows}.get(fmt)
     if fn is None:
         raise ValueError(f"unsupported format {fmt}")
     rows = w.shape[0]
