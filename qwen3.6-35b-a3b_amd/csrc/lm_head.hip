@@ -2,14 +2,14 @@
 // V rows of H = 2048 in Q6_K (the shipped artifact's output.weight), Q8_0 or bf16, over all rows
 // (dense) or a list of row ids (gather). This is prototype/lm_head/lm_head_kernels.h:474-512
 // (lmh_dot_batch: one row's dot for up to LMH_MAX_BATCH = 8 hidden vectors) on the path
-// lm_head.hip:51 launches, with the Q6_K width the prototype defers (results.md:341-343).
+// lm_head.hip:51 launches, with the Q6_K width the prototype defers (prototype/lm_head/results.md:341-343).
 //
 // HBM-bound: every table byte is read once per pass (one pass per 4 tokens), 1680 B per row in
 // Q6_K (417 MB at V = 248320), 2176 B in Q8_0, 4096 B in bf16. Layout of the work:
 //   * one row per wave; each lane owns a fixed set of 32 element positions of every row, so its
 //     slice of the hidden vectors (32 floats per token) stays in registers for the whole sweep;
 //   * Q6_K / Q8_0 rows (2-byte-aligned blocks of 210 / 34 B) are staged into LDS by the block with
-//     coalesced 16-byte loads, 16 rows per iteration, double buffered (the next iteration's loads
+//     coalesced 16-byte loads, 8 or 16 rows per iteration, double buffered (the next iteration's loads
 //     are in flight while the current rows are decoded); lanes then read their bytes from LDS as
 //     aligned dwords and realign them with v_alignbyte;
 //   * bf16 rows are read straight from HBM, 64 lanes x 16 B contiguous per load, two rows in
@@ -26,9 +26,15 @@ namespace lmh {
 
 constexpr int kH = 2048;                 // the lane mapping covers 64 lanes x 32 positions
 constexpr int kThreads = 256;            // 4 waves
-constexpr int kRowsPerWave = 4;
-constexpr int kRows = 4 * kRowsPerWave;  // rows per block iteration (staged formats)
 constexpr int kPad = 16;                 // LDS slack after the last row (the Q8_0 window overreads 6 B)
+// Rows per wave per block iteration of the staged formats: with one token the decode is light
+// and registers are few, so smaller iterations (less LDS) let four blocks share a CU; with more
+// tokens the FMAs dominate, registers allow two blocks, and longer iterations amortise the sync.
+template <int NB> struct Iter {
+  static constexpr int kRowsPerWave = NB == 1 ? 2 : 4;
+  static constexpr int kRows = 4 * kRowsPerWave;
+  static constexpr int kBlocksPerCu = NB == 1 ? 4 : 2;
+};
 
 template <int FMT> struct Staged;
 template <> struct Staged<MOE_FMT_Q6_K> {
@@ -76,9 +82,10 @@ __global__ __launch_bounds__(kThreads) void k_lm_head_staged(const void* __restr
                                                              long long n_rows,
                                                              float* __restrict__ out) {
   constexpr int kRowB = Staged<FMT>::kRowB;
+  constexpr int kRowsPerWave = Iter<NB>::kRowsPerWave, kRows = Iter<NB>::kRows;
   constexpr int kChunks = kRowB / 16;                               // 105 / 136 per row
   constexpr int kBuf = kRows * kRowB + kPad;
-  constexpr int kLoads = (kRows * kChunks + kThreads - 1) / kThreads;   // 7 / 9 per thread
+  constexpr int kLoads = (kRows * kChunks + kThreads - 1) / kThreads;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][kBuf];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
 
@@ -283,8 +290,10 @@ int cu_count() {
 template <int FMT, int NB, int XDT, int GATHER>
 void launch_staged(const void* h, const uint8_t* w, long long V, const int32_t* ids, long long n,
                    float* out, hipStream_t st) {
-  const long long n_it = (n + lmh::kRows - 1) / lmh::kRows;
-  const long long grid = n_it < 2LL * cu_count() ? n_it : 2LL * cu_count();   // two blocks per CU
+  constexpr int kRows = lmh::Iter<NB>::kRows;
+  const long long n_it = (n + kRows - 1) / kRows;
+  const long long cap = (long long)lmh::Iter<NB>::kBlocksPerCu * cu_count();
+  const long long grid = n_it < cap ? n_it : cap;
   hipLaunchKernelGGL((lmh::k_lm_head_staged<FMT, NB, XDT, GATHER>), dim3((unsigned)grid),
                      dim3(lmh::kThreads), 0, st, h, w, V, ids, n, out);
 }
