@@ -70,6 +70,8 @@ def parse():
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing (what the kernel-trace profile covers)")
     ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--no-artifact", action="store_true",
+                    help="skip the decode chain over the shipped artifact's weight widths")
     ap.add_argument("--lm-head-only", action="store_true",
                     help="only the untied lm_head GEMV timing (what the lm_head profile covers)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -374,7 +376,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU "
-                          "sharding is design-only, described in DESIGN.md)"}))
+                          "sharding is design-only)"}))
         sys.exit(2)
     import torch
     import __graft_entry__ as ge
@@ -453,6 +455,37 @@ def main():
     if err_bits:
         log(f"WARNING: device error bits {err_bits:#x} (a bounded spin timed out)")
 
+    # ------------------------------------------------ decode over the artifact's weight widths
+    art = {}
+    if not args.no_artifact:
+        del layers
+        torch.cuda.empty_cache()
+        alayers = [synth.make_layer(seed=2000 + l, device=dev, down_fmt=pkg.quant.FMT_Q5_K,
+                                    router_dtype=torch.float32, scalar_gate_dtype=torch.float32,
+                                    split_gate_up=True) for l in range(L)]
+        xbuf.copy_(x0)
+
+        def art_token():
+            for l, (lw, nw) in enumerate(zip(alayers, norms)):
+                abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw,
+                                  next_layer=alayers[(l + 1) % L], next_norm_w=norms[(l + 1) % L])
+            xbuf.copy_(synth.rms_normalize(xbuf))
+
+        for _ in range(3):
+            art_token()
+        torch.cuda.synchronize()
+        ga = capture(torch, art_token)
+        for _ in range(args.warmup):
+            ga.replay()
+        torch.cuda.synchronize()
+        ms_a = time_stream(ga.replay, min(args.steps, 256), torch)
+        art = {"decode_artifact_us_per_token_layer": ms_a * 1000.0 / L}
+        log(f"decode, artifact widths (f32 router and scalar gate, split gate/up, Q5_K down): "
+            f"{ms_a * 1000.0 / L:.2f} us/token/layer")
+        del alayers, ga
+        torch.cuda.empty_cache()
+        layers = [synth.make_layer(seed=1000, device=dev)]
+
     # ---------------------------------------------------------------- batched decode, config 2
     c2 = c2_step(torch, synth, abi, dev, 50) if not args.no_c2 else {}
 
@@ -507,6 +540,7 @@ def main():
         "cpu_baseline": cpu,
     }
     result.update(c2)
+    result.update({k: round(v, 3) for k, v in art.items()})
     result.update({k: round(v, 3) for k, v in lmh.items()})
     result.update({k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()})
     print(json.dumps(result), flush=True)

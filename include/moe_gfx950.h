@@ -169,9 +169,9 @@ typedef struct moe_layer_weights {
 /* moe_block_forward over a moe_layer_weights (w; norm_w and every weight pointer from there) and an
  * optional next-layer hint (next: as moe_block_forward_prefetch, the router rows and norm weight of
  * a bf16-router next layer). Same outputs, limits and errors as moe_block_forward. The
- * single-launch decode layer takes a bf16 router and scalar gate with Q4_K gate/up (fused or
- * split) and Q4_K, Q5_K or Q6_K down; an f32 router or scalar gate runs the three-launch decode
- * path at T = 1, and the grouped paths above it.
+ * single-launch decode layer takes a bf16 or f32 router and scalar gate, Q4_K gate/up (fused or
+ * split) and Q4_K or Q5_K down; Q6_K down runs the three-launch decode path at T = 1. The next
+ * layer's router rows (bf16 or f32) and norm weight are the L2 warm-up hint.
  * Replaces engine/m3_forward.py:430-476 and engine/block_forward.py:670-681 on the policy-A
  * weights (engine/block_forward.py:211-231). */
 int moe_block_forward_w(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,

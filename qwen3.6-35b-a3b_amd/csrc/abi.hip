@@ -387,8 +387,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   const bool decode = T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
                       (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q5_K || down_fmt == MOE_FMT_Q6_K) &&
                       I_s % 128 == 0 && E % 4 == 0;
-  const bool one_launch = decode && path != MOE_PATH_GEMV_MULTI && Wt.router_dtype == MOE_DT_BF16 &&
-                          Wt.scalar_gate_dtype == MOE_DT_BF16 &&
+  const bool one_launch = decode && path != MOE_PATH_GEMV_MULTI &&
                           moe_layer_kernel_supported(H, I, E, K, I_s, gate_up_fmt, down_fmt);
   if (norm_w && !one_launch) {
     // every other path reads the normalized rows from the workspace (f32)
@@ -419,8 +418,9 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     L.ids_out_requested = (topk_ids || topk_w_bf16 || topk_w_f32) ? 1 : 0;
     L.norm_w = one_launch ? norm_w : nullptr;
     L.norm_eps = norm_eps;
-    if (next && next->router_dtype == MOE_DT_BF16) {
+    if (next && next->w_router && (next->router_dtype == MOE_DT_BF16 || next->router_dtype == MOE_DT_F32)) {
       L.nx_router = next->w_router;
+      L.nx_router_dt = next->router_dtype;
       L.nx_norm = next->norm_w;
     }
     if (!L.logits || !L.ids || !L.w_f32 || !L.w_bf16 || !L.s_shared || !L.gate_prob || !L.shared_raw || !L.s_routed)

@@ -65,7 +65,7 @@ constexpr int kErrSpin = 1;             // a bounded wait timed out
 struct LayerArgs {
   const void* x;
   const float* residual;
-  const uint16_t* w_router;
+  const void* w_router;                 // bf16 or f32 rows (the kernel's RDT)
   const float* bias;
   const uint8_t* gu;                    // gate rows of expert e at gu + e * gu_estride
   const uint8_t* gu_up;                 // up rows likewise (a fused record: gu + I rows)
@@ -74,7 +74,8 @@ struct LayerArgs {
   const uint16_t* sg;
   const uint16_t* su;
   const uint16_t* sd;
-  const uint16_t* ssg;
+  const uint16_t* ssg;                  // the scalar gate row: bf16, or f32 when ssg_f32
+  int ssg_f32;
   int* sync;                            // sync words (kErrWord, kRoleEpoch)
   uint32_t* xch;                        // two exchange buffers of XW_BUF words
   uint16_t* logits_out;
@@ -91,6 +92,7 @@ struct LayerArgs {
   float norm_eps;
   // the next layer's router weight and norm weight (L2 warm-up hint), or NULL
   const uint16_t* nx_router;
+  int nx_router_f32;                    // the next layer's router rows are f32 (twice the bytes)
   const float* nx_norm;
 };
 
@@ -164,19 +166,32 @@ __device__ __forceinline__ uint4 xwait4(__amdgpu_buffer_rsrc_t r, int off, int* 
 // the certified error bound 4(H+3) 2^-53 (|x|_1 max|w| + |b|), which bounds sum |x_j w_j| + |b|
 // times the summation's error factor; a double-double recompute settles what that does not.
 // xl1 >= |x|_1 is the workgroup's bound on the input's 1-norm.
+// Weight i (0..7) of chunk c of the row a lane holds: bf16 rows take one uint4 per chunk, f32
+// rows two (w[2c], w[2c + 1]); either way x_j w_j is exact in f64.
+template <int RDT>
+__device__ __forceinline__ float router_w(const uint4* w, int c, int i) {
+  if (RDT == MOE_DT_F32) {
+    const uint4 v = w[2 * c + (i >> 2)];
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+    return __uint_as_float(u[i & 3]);
+  }
+  const uint32_t u[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+  return bf16_to_f32((i & 1) ? (u[i >> 1] >> 16) : (u[i >> 1] & 0xFFFFu));
+}
+
+template <int RDT>
 __device__ __forceinline__ uint32_t router_row_bits(const uint4* w, const float (*xv)[8],
                                                    double bval, double xl1) {
   constexpr int H = 2048;
   double acc = 0.0;
-  uint32_t wm = 0;
+  uint32_t wm = 0;                       // max |w| as f32 bits (ordered like the magnitudes)
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc = fma((double)xv[c][2 * i], (double)bf16_to_f32(ww[i] & 0xFFFFu), acc);
-      acc = fma((double)xv[c][2 * i + 1], (double)bf16_to_f32(ww[i] >> 16), acc);
-      wm = max(wm, max(ww[i] & 0x7FFFu, (ww[i] >> 16) & 0x7FFFu));
+    for (int i = 0; i < 8; ++i) {
+      const float wv = router_w<RDT>(w, c, i);
+      acc = fma((double)xv[c][i], (double)wv, acc);
+      wm = max(wm, __float_as_uint(wv) & 0x7FFFFFFFu);
     }
   }
   acc = wave_sum_f64(acc);
@@ -186,18 +201,14 @@ __device__ __forceinline__ uint32_t router_row_bits(const uint4* w, const float 
   wm = max(wm, dpp_u32<0x140>(wm));
   wm = max(max((uint32_t)__builtin_amdgcn_readlane((int)wm, 15), (uint32_t)__builtin_amdgcn_readlane((int)wm, 31)),
            max((uint32_t)__builtin_amdgcn_readlane((int)wm, 47), (uint32_t)__builtin_amdgcn_readlane((int)wm, 63)));
-  const double nrm = xl1 * (double)bf16_to_f32(wm) + fabs(bval);
+  const double nrm = xl1 * (double)__uint_as_float(wm) + fabs(bval);
   uint32_t bits;
   if (!round_bf16_certified(acc + bval, 4.0 * (double)(H + 3) * 0x1p-53 * nrm, &bits)) {
     DD d = {0.0, 0.0};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const double w_ = bf16_to_f32((i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu));
-        d = dd_add(d, DD{(double)xv[c][i] * w_, 0.0});
-      }
+      for (int i = 0; i < 8; ++i) d = dd_add(d, DD{(double)xv[c][i] * (double)router_w<RDT>(w, c, i), 0.0});
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -308,7 +319,9 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
   return true;
 }
 
-template <int XDT>
+// XDT: input x width; RDT: router row width (bf16, or f32 as the shipped artifact's ffn_gate_inp);
+// DFMT: routed down format (Q4_K, or Q5_K as the artifact's ffn_down_exps in 37 of 40 layers)
+template <int XDT, int RDT, int DFMT>
 __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   constexpr int H = 2048, I = 512, E = 256, K = 8, IS = 512, ISX = IS / kXcd;
   __shared__ float s_x[H];
@@ -352,9 +365,14 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   // experts). Wave 0, which polls the logits, carries none of the extras.
   // the router rows now; the shared expert's rows (waves 4-7, wx) once these and the input row
   // have landed (below): requested together, they would slow the loads the routing waits on
-  uint4 wr4[4], wx[8];
-  {
-    const uint16_t* wr = a.w_router + (size_t)(8 * r + wave) * H;
+  uint4 wr4[RDT == MOE_DT_F32 ? 8 : 4], wx[8];
+  if (RDT == MOE_DT_F32) {
+    const float* wr = reinterpret_cast<const float*>(a.w_router) + (size_t)(8 * r + wave) * H;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      wr4[c] = *reinterpret_cast<const uint4*>(wr + 512 * (c >> 1) + 8 * lane + 4 * (c & 1));
+  } else {
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.w_router) + (size_t)(8 * r + wave) * H;
 #pragma unroll
     for (int c = 0; c < 4; ++c) wr4[c] = *reinterpret_cast<const uint4*>(wr + 512 * c + 8 * lane);
   }
@@ -391,9 +409,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       p_hi = p_lo + (size_t)32 * IS;
       st = (size_t)8 * IS;
     } else if (wave == 7) {
-      p_lo = a.ssg + 8 * lane;
-      p_hi = p_lo;
-      st = 512;
+      // bf16 row: 8 elements per load; f32 row: the first and second 4 of those 8 (p_hi)
+      p_lo = a.ssg + (a.ssg_f32 ? 16 : 8) * lane;
+      p_hi = p_lo + (a.ssg_f32 ? 8 : 0);
+      st = a.ssg_f32 ? 1024 : 512;
     } else {
       const int i = ISX * x + 2 * r + (wave - 5);
       p_lo = a.sg + (size_t)i * H + 8 * lane;
@@ -435,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       xv[c][4] = u1.x; xv[c][5] = u1.y; xv[c][6] = u1.z; xv[c][7] = u1.w;
     }
     const int e = 8 * r + wave;
-    const uint32_t bits = router_row_bits(wr4, xv, (double)bias_e, xl1);
+    const uint32_t bits = router_row_bits<RDT>(wr4, xv, (double)bias_e, xl1);
     if (lane == 0) lstore(xr, 4 * (XW_LOG + 256 * x + e), ~bits);
     if (wave == 5 || wave == 6) {
       float ag = 0.0f, au = 0.0f;
@@ -449,8 +468,21 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + (wave - 5)), xenc(silu_f32(ag) * au));
     } else if (wave == 7) {
       float gs = 0.0f;
+      if (a.ssg_f32) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) gs += dot8_bf16(wx[c], xv[c]);
+        for (int c = 0; c < 4; ++c) {
+          const float w8[8] = {__uint_as_float(wx[c].x), __uint_as_float(wx[c].y), __uint_as_float(wx[c].z),
+                               __uint_as_float(wx[c].w), __uint_as_float(wx[4 + c].x), __uint_as_float(wx[4 + c].y),
+                               __uint_as_float(wx[4 + c].z), __uint_as_float(wx[4 + c].w)};
+          float s8 = fmaf(w8[0], xv[c][0], 0.0f);
+#pragma unroll
+          for (int i = 1; i < 8; ++i) s8 = fmaf(w8[i], xv[c][i], s8);
+          gs += s8;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) gs += dot8_bf16(wx[c], xv[c]);
+      }
       gs = wave_sum_f32(gs);
       const float p = 1.0f / (1.0f + expf(-gs));
       if (lane == 0) {
@@ -527,8 +559,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   const int e = s_ids[x];
   // phase-3 weights: down rows h = 64 r + 2 (t >> 4) + pass of expert e; 16 lanes per row,
   // lane: super-block b = l16 >> 3, 16-byte nibble chunk c = l16 & 7 (requested with phase 2's)
-  constexpr size_t drowb = (I / 256) * 144;
-  uint4 dh[2], dq[2];
+  // Q4_K: header + nibble chunk (two loads); Q5_K: also the chunk's 16 qh bytes (tools/gguf_reader.py:271-296)
+  constexpr int kDB = DFMT == MOE_FMT_Q5_K ? 176 : 144, kDQs = DFMT == MOE_FMT_Q5_K ? 48 : 16;
+  constexpr size_t drowb = (I / 256) * kDB;
+  uint4 dh[2], dq[2], dqh[2];
   {
     // routed gate/up: intermediate rows i0, i0+1 (gate and up) per wave
     const int i0 = 16 * r + 2 * wave;
@@ -548,9 +582,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
       for (int pass = 0; pass < 2; ++pass) {
         const int h = 64 * r + 2 * (t >> 4) + pass;
-        const uint8_t* p = a.dn + ((size_t)e * H + h) * drowb + (size_t)db * 144;
+        const uint8_t* p = a.dn + ((size_t)e * H + h) * drowb + (size_t)db * kDB;
         dh[pass] = *reinterpret_cast<const uint4*>(p);
-        dq[pass] = *reinterpret_cast<const uint4*>(p + 16 + 16 * dc);
+        dq[pass] = *reinterpret_cast<const uint4*>(p + kDQs + 16 * dc);
+        if (DFMT == MOE_FMT_Q5_K) dqh[pass] = *reinterpret_cast<const uint4*>(p + 16 + 16 * (dc & 1));
       }
     }
     float xl[16], xh[16];
@@ -596,7 +631,9 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     // wait for that store's write-through (vmcnt counts both)
     float v[2];
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) v[pass] = row16_sum_f32(q4k_chunk_dot(dh[pass], dq[pass], gq, xl, xh, sxl, sxh));
+    for (int pass = 0; pass < 2; ++pass)
+      v[pass] = row16_sum_f32(DFMT == MOE_FMT_Q5_K ? q5k_chunk_dot(dh[pass], dq[pass], dqh[pass], gq, xl, xh, sxl, sxh)
+                                                   : q4k_chunk_dot(dh[pass], dq[pass], gq, xl, xh, sxl, sxh));
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       if (l16 == 0) {
@@ -617,9 +654,14 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       // warm XCD x's L2 with what role (x, r) reads first in the next layer
       const int u = t - 256;
       uint32_t acc = 0;
-      const uint4* nr = reinterpret_cast<const uint4*>(a.nx_router + (size_t)8 * r * H);
+      // rows 8r .. 8r + 7: 2048 uint4 of bf16, 4096 of f32
+      const uint4* nr = reinterpret_cast<const uint4*>(a.nx_router) + (size_t)r * H * (a.nx_router_f32 ? 2 : 1);
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc ^= xor4(nr[u + 256 * q]);
+      if (a.nx_router_f32) {
+#pragma unroll
+        for (int q = 8; q < 16; ++q) acc ^= xor4(nr[u + 256 * q]);
+      }
       if (a.nx_norm) {
         const uint4* nn = reinterpret_cast<const uint4*>(a.nx_norm);
         acc ^= xor4(nn[u]) ^ xor4(nn[u + 256]);
@@ -672,14 +714,26 @@ bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, 
   }
   // 8 XCDs with at least 32 CUs each (MI355X: exactly 32)
   return ncu >= kG && ncu % kXcd == 0 && H == 2048 && I == 512 && E == 256 && K == 8 &&
-         Is == 512 && gu_fmt == MOE_FMT_Q4_K && dn_fmt == MOE_FMT_Q4_K;
+         Is == 512 && gu_fmt == MOE_FMT_Q4_K && (dn_fmt == MOE_FMT_Q4_K || dn_fmt == MOE_FMT_Q5_K);
 }
+
+namespace {
+
+template <int XDT, int RDT>
+void launch_layer_fmt(int dn_fmt, const LayerArgs& a, hipStream_t st) {
+  if (dn_fmt == MOE_FMT_Q5_K)
+    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q5_K>), dim3(kG), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q4_K>), dim3(kG), dim3(kThreads), 0, st, a);
+}
+
+}  // namespace
 
 size_t moe_layer_exchange_bytes() { return (size_t)2 * XW_BUF * 4; }
 
 int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, hipStream_t st) {
   LayerArgs a;
-  a.x = L.x; a.residual = L.residual; a.w_router = (const uint16_t*)L.w_router; a.bias = L.bias;
+  a.x = L.x; a.residual = L.residual; a.w_router = L.w_router; a.bias = L.bias;
   a.gu = (const uint8_t*)L.gu; a.dn = (const uint8_t*)L.dn;
   {
     const size_t rowb = (size_t)(L.H / 256) * 144;
@@ -688,6 +742,7 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   }
   a.sg = (const uint16_t*)L.sg; a.su = (const uint16_t*)L.su; a.sd = (const uint16_t*)L.sd;
   a.ssg = (const uint16_t*)L.ssg;
+  a.ssg_f32 = L.ssg_dt == MOE_DT_F32 ? 1 : 0;
   a.sync = sync; a.xch = xch;
   a.logits_out = L.logits; a.ids_out = L.ids; a.w_f32_out = L.w_f32; a.w_bf16_out = L.w_bf16;
   a.gate_prob_out = L.gate_prob; a.out = L.out; a.routed_sum = L.routed_sum;
@@ -696,10 +751,15 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   a.norm_w = L.norm_w;
   a.norm_eps = L.norm_eps;
   a.nx_router = (const uint16_t*)L.nx_router;
+  a.nx_router_f32 = L.nx_router_dt == MOE_DT_F32 ? 1 : 0;
   a.nx_norm = L.nx_router ? L.nx_norm : nullptr;
-  if (L.x_dtype == MOE_DT_F32)
-    hipLaunchKernelGGL(k_dec_layer<MOE_DT_F32>, dim3(kG), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(k_dec_layer<MOE_DT_BF16>, dim3(kG), dim3(kThreads), 0, st, a);
+  const bool r32 = L.router_dt == MOE_DT_F32;
+  if (L.x_dtype == MOE_DT_F32) {
+    if (r32) launch_layer_fmt<MOE_DT_F32, MOE_DT_F32>(L.dn_fmt, a, st);
+    else launch_layer_fmt<MOE_DT_F32, MOE_DT_BF16>(L.dn_fmt, a, st);
+  } else {
+    if (r32) launch_layer_fmt<MOE_DT_BF16, MOE_DT_F32>(L.dn_fmt, a, st);
+    else launch_layer_fmt<MOE_DT_BF16, MOE_DT_BF16>(L.dn_fmt, a, st);
+  }
   return moe_check_launch("decode_layer");
 }

@@ -119,6 +119,7 @@ struct MoeDecodeLaunch {
   float norm_eps;
   // the next layer's routing-independent weights (single-launch layer's L2 warm-up), or NULL
   const void* nx_router = nullptr;      // the next layer's router and norm weights (warm-up hint)
+  int nx_router_dt = MOE_DT_BF16;
   const float* nx_norm = nullptr;
 };
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);

@@ -164,3 +164,23 @@ def test_next_hint_over_artifact_layers_same_bits(pkg, layer_c0, layer_artifact,
         assert torch.equal(a, b), step
         assert torch.isfinite(a).all()
     assert pkg.abi.device_error_bits(dev) == 0
+
+
+@pytest.mark.parametrize("fixture", ["layer_artifact", "layer_q5k"])
+def test_artifact_decode_single_and_three_launch_agree(pkg, dev, request, fixture):
+    """The single-launch layer with f32 router rows, an f32 scalar gate, split gate/up and Q5_K
+    down, and the three-launch form of the same arithmetic: both match the oracle's routing bit for
+    bit and its outputs within the block tolerance, token by token, and no bounded spin timed out."""
+    lw, ow = request.getfixturevalue(fixture)
+    xs = pkg.synth.make_input(6, seed=810, device=dev)
+    ref = O.moe_block(xs.cpu(), ow)
+    for path in (pkg._lib.MOE_PATH_GEMV, pkg._lib.MOE_PATH_GEMV_MULTI):
+        outs, ids = [], []
+        for i in range(6):
+            st = pkg.abi.block_forward(xs[i:i + 1].contiguous(), lw, path=path, stages={"topk_ids"})
+            outs.append(st["combined_out"])
+            ids.append(st["topk_ids"])
+        torch.cuda.synchronize()
+        assert torch.equal(torch.cat(ids).cpu().long(), ref["topk_ids"]), (fixture, path)
+        assert_close(torch.cat(outs), ref["combined_out"], f"{fixture} decode path {path}")
+    assert pkg.abi.device_error_bits(dev) == 0
