@@ -47,7 +47,9 @@ static int pick_path(int path, int T, int gate_up_fmt) {
   if (path == MOE_PATH_GEMV_MULTI) return MOE_PATH_GEMV;
   if (path == MOE_PATH_GEMV || path == MOE_PATH_MFMA || path == MOE_PATH_MFMA_BF16) return path;
   if (gate_up_fmt != MOE_FMT_Q4_K) return MOE_PATH_MFMA;
-  return T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
+  // measured crossover (block at 2..24 tokens, the shared expert on the second stream from 7):
+  // the GEMV path reads every hit expert once per token group, the MFMA path once per tile
+  return T <= 6 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
 }
 
 // The grouped paths' shared expert depends on x alone, so from kForkMinT tokens on it runs on a
@@ -56,7 +58,9 @@ static int pick_path(int path, int T, int gate_up_fmt) {
 // (few workgroups) then fill CUs the routed GEMMs leave idle. The fork and join are events, so
 // the pattern is legal under graph capture. One mutex serialises the enqueue sequence, because
 // the stream and its two events are shared by every call on the device.
-constexpr int kForkMinT = 256;
+// below kForkMinT the event round trip costs more than the overlap returns (measured: 2 tokens
+// 53 -> 90 us with the fork, 8 tokens 124 -> 116, 64 tokens 184 -> 126)
+constexpr int kForkMinT = 7;
 constexpr int kMaxDevices = 64;
 struct ForkRes {
   hipStream_t s = nullptr;

@@ -289,18 +289,26 @@ def test_prefill_q5k_down_sampled_rows(pkg, layer_q5k, dev):
 
 
 def test_prefill_shared_stream_fork_same_bits_and_graph(pkg, layer_c0, dev):
-    """From 256 tokens the shared expert runs on the library's second stream (forked from and
-    joined back into the caller's stream by events). The rows equal those of a 255-token call,
-    which runs every kernel on one stream, bit for bit; and the fork/join captured in a graph
-    replays to the eager bits, with eager calls between the replays."""
+    """From 7 tokens the shared expert runs on the library's second stream (forked from and joined
+    back into the caller's stream by events). On the same (MFMA) kernels, the rows of a 7-token
+    call equal those of a 6-token call, which runs every kernel on one stream, bit for bit; and the
+    fork/join captured in a graph replays to the eager bits (7 and 256 tokens), with eager calls
+    between the replays."""
     lw, _ = layer_c0
-    x = pkg.synth.make_input(256, seed=71, device=dev, dtype=torch.bfloat16)
-    a = pkg.abi.block_forward(x, lw, stages={"topk_ids"})
-    b = pkg.abi.block_forward(x[:255].contiguous(), lw, stages={"topk_ids"})
+    mfma = pkg._lib.MOE_PATH_MFMA
+    x7 = pkg.synth.make_input(7, seed=70, device=dev)
+    a = pkg.abi.block_forward(x7, lw, path=mfma, stages={"topk_ids"})
+    b = pkg.abi.block_forward(x7[:6].contiguous(), lw, path=mfma, stages={"topk_ids"})
     torch.cuda.synchronize()
-    assert torch.equal(a["topk_ids"][:255], b["topk_ids"])
-    assert torch.equal(a["combined_out"][:255], b["combined_out"])
-    want = a["combined_out"].clone()
+    assert torch.equal(a["topk_ids"][:6], b["topk_ids"])
+    assert torch.equal(a["combined_out"][:6], b["combined_out"])
+    for T in (7, 256):
+        _graph_replays_match(pkg, lw, pkg.synth.make_input(T, seed=71, device=dev, dtype=torch.bfloat16))
+
+
+def _graph_replays_match(pkg, lw, x):
+    want = pkg.abi.block_forward(x, lw)["combined_out"].clone()
+    torch.cuda.synchronize()
     out = torch.empty_like(want)
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
