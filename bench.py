@@ -462,7 +462,8 @@ def main():
         torch.cuda.empty_cache()
         alayers = [synth.make_layer(seed=2000 + l, device=dev, down_fmt=pkg.quant.FMT_Q5_K,
                                     router_dtype=torch.float32, scalar_gate_dtype=torch.float32,
-                                    split_gate_up=True) for l in range(L)]
+                                    split_gate_up=True, shared_fmt=pkg.quant.FMT_Q8_0)
+                   for l in range(L)]
         xbuf.copy_(x0)
 
         def art_token():
@@ -480,7 +481,8 @@ def main():
         torch.cuda.synchronize()
         ms_a = time_stream(ga.replay, min(args.steps, 256), torch)
         art = {"decode_artifact_us_per_token_layer": ms_a * 1000.0 / L}
-        log(f"decode, artifact widths (f32 router and scalar gate, split gate/up, Q5_K down): "
+        log(f"decode, artifact widths (f32 router and scalar gate, split gate/up, Q5_K down, "
+            f"Q8_0 shared expert): "
             f"{ms_a * 1000.0 / L:.2f} us/token/layer")
         del alayers, ga
         torch.cuda.empty_cache()

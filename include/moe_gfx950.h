@@ -43,7 +43,8 @@ enum { MOE_DT_F32 = 0, MOE_DT_BF16 = 1 };
 
 /* weight formats: ggml_type ids (tools/gguf_reader.py:10-51 block table). Routed gate_up: Q4_K,
  * Q6_K or BF16; routed down: Q4_K, Q5_K (the shipped artifact's down in 37 of its 40 layers,
- * engine/README.md:33,115), Q6_K or BF16; moe_dequant: Q4_K, Q5_K, Q6_K. */
+ * engine/README.md:33,115), Q6_K or BF16; shared expert: BF16 or Q8_0 (the artifact's
+ * ffn_*_shexp); lm_head table: Q6_K, Q8_0 or BF16; moe_dequant: Q4_K, Q5_K, Q6_K. */
 enum { MOE_FMT_Q8_0 = 8, MOE_FMT_Q4_K = 12, MOE_FMT_Q5_K = 13, MOE_FMT_Q6_K = 14, MOE_FMT_BF16 = 30 };
 
 /* expert contraction path: GEMV = fused decode + f32 GEMV; MFMA = tiles decoded to f16 in LDS on
@@ -108,7 +109,9 @@ int moe_experts(const void *x, int x_dtype, const void *gate_up_q, const void *u
 
 /* Shared expert and its scalar sigmoid gate. Replaces speccheck/moe_ref.py:480-495,
  * engine/block_forward.py:639-649 and engine/m3_forward.py:436-442.
- * w_gate, w_up: [I_s,H]; w_down: [H,I_s], in shared_fmt (MOE_FMT_BF16); w_scalar_gate: [H] in
+ * w_gate, w_up: [I_s,H]; w_down: [H,I_s], in shared_fmt: MOE_FMT_BF16, or MOE_FMT_Q8_0 (GGUF
+ * rows of 34-byte blocks, the artifact's ffn_*_shexp; H and I_s multiples of 256, 16-byte
+ * aligned tensors); w_scalar_gate: [H] in
  * gate_dtype (MOE_DT_BF16, or MOE_DT_F32 as the artifact's ffn_gate_inp_shexp).
  * shared_raw [T,H] = down(silu(gate x) * up x); gate_prob [T] = sigmoid(w_scalar_gate . x). */
 int moe_shared_expert(const void *x, int x_dtype, const void *w_gate, const void *w_up,
@@ -160,7 +163,7 @@ typedef struct moe_layer_weights {
   int down_fmt;                  /* MOE_FMT_Q4_K, Q5_K, Q6_K (BF16 off the decode paths) */
   const void *ws_gate, *ws_up;   /* [I_s,H] */
   const void *ws_down;           /* [H,I_s] */
-  int shared_fmt;                /* MOE_FMT_BF16 */
+  int shared_fmt;                /* MOE_FMT_BF16 or MOE_FMT_Q8_0 */
   const void *ws_scalar_gate;    /* [H] */
   int scalar_gate_dtype;         /* MOE_DT_BF16 or MOE_DT_F32 */
   const float *norm_w;           /* [H] f32 post-attention norm weight, or NULL */

@@ -276,8 +276,17 @@ def from_device(lw) -> LayerWeights:
     up = getattr(lw, "up_q", None)
     if up is not None:
         gu = np.concatenate([gu, host(up).numpy()], axis=1)
+
+    def shared(t):
+        # Q8_0 rows (uint8) decode to the exact f32 values d * q (tools/gguf_reader.py:238-245)
+        if t.dtype != torch.uint8:
+            return host(t)
+        from .lm_head_oracle import dequant_q8_0
+        b = host(t).numpy()
+        n = b.shape[1] // 34 * 32
+        return torch.from_numpy(dequant_q8_0(b.reshape(-1), b.shape[0] * n).reshape(b.shape[0], n))
     return LayerWeights(
         router=host(lw.router), gate_up_q=gu, gate_up_fmt=lw.gate_up_fmt,
-        down_q=host(lw.down_q).numpy(), down_fmt=lw.down_fmt, shared_gate=host(lw.shared_gate),
-        shared_up=host(lw.shared_up), shared_down=host(lw.shared_down),
+        down_q=host(lw.down_q).numpy(), down_fmt=lw.down_fmt, shared_gate=shared(lw.shared_gate),
+        shared_up=shared(lw.shared_up), shared_down=shared(lw.shared_down),
         shared_scalar_gate=host(lw.shared_scalar_gate), router_bias=host(lw.router_bias))

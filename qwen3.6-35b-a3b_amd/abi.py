@@ -175,21 +175,25 @@ def experts(x: torch.Tensor, gate_up_q: torch.Tensor, gate_up_fmt: int, down_q: 
 
 def shared_expert(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
                   w_scalar_gate: torch.Tensor, path: int = L.MOE_PATH_AUTO):
-    """(shared_raw [T,H] f32, gate_prob [T] f32). w_scalar_gate is bf16 or f32 (the artifact's
-    F32 ffn_gate_inp_shexp)."""
+    """(shared_raw [T,H] f32, gate_prob [T] f32). The expert's rows are bf16 ([I_s,H], [I_s,H],
+    [H,I_s]) or Q8_0 bytes (uint8 [I_s,H/32*34], [I_s,H/32*34], [H,I_s/32*34]: the artifact's
+    ffn_*_shexp); w_scalar_gate is bf16 or f32 (the artifact's F32 ffn_gate_inp_shexp)."""
     _need(x, "x")
     T, H = x.shape
     Is = w_gate.shape[0]
-    for n, t, shp in (("w_gate", w_gate, (Is, H)), ("w_up", w_up, (Is, H)),
-                      ("w_down", w_down, (H, Is))):
-        _need(t, n, torch.bfloat16, shp, x.device)
+    q8 = w_gate.dtype == torch.uint8
+    sfmt = L.MOE_FMT_Q8_0 if q8 else L.MOE_FMT_BF16
+    cols = (lambda c: c // 32 * 34) if q8 else (lambda c: c)
+    for n, t, shp in (("w_gate", w_gate, (Is, cols(H))), ("w_up", w_up, (Is, cols(H))),
+                      ("w_down", w_down, (H, cols(Is)))):
+        _need(t, n, torch.uint8 if q8 else torch.bfloat16, shp, x.device)
     gdt = _wdt(w_scalar_gate, "w_scalar_gate")
     _need(w_scalar_gate, "w_scalar_gate", None, (1, H), x.device)
     raw = torch.empty(T, H, dtype=torch.float32, device=x.device)
     prob = torch.empty(T, dtype=torch.float32, device=x.device)
     ws = workspace(x.device, workspace_bytes(T, H, Is, 256, 8, Is))
     _check(L.lib.moe_shared_expert(_p(x), _xdt(x), _p(w_gate), _p(w_up), _p(w_down),
-                                   L.MOE_FMT_BF16, _p(w_scalar_gate), gdt, T, H, Is, path, _p(raw),
+                                   sfmt, _p(w_scalar_gate), gdt, T, H, Is, path, _p(raw),
                                    _p(prob), _p(ws), ws.numel(), _stream(x)), "shared_expert")
     return raw, prob
 
@@ -217,8 +221,9 @@ def _need_layer(lw, H: int, dev, tag: str) -> None:
     _need(lw.router, tag + "router", None, (E, H), dev)
     _wdt(lw.shared_scalar_gate, tag + "shared_scalar_gate")
     _need(lw.shared_scalar_gate, tag + "shared_scalar_gate", None, (1, H), dev)
+    sdt = torch.uint8 if lw.shared_fmt == L.MOE_FMT_Q8_0 else torch.bfloat16
     for n in ("shared_gate", "shared_up", "shared_down"):
-        _need(getattr(lw, n), tag + n, torch.bfloat16, device=dev)
+        _need(getattr(lw, n), tag + n, sdt, device=dev)
     for n in ("gate_up_q", "down_q"):
         _need(getattr(lw, n), tag + n, torch.uint8, device=dev)
     if lw.up_q is not None:

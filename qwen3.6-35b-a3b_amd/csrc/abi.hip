@@ -286,35 +286,38 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, const void* u
 }
 
 static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const void* wg,
-                       const void* wu, const void* wd, const void* wsg, int gate_dtype, int T, int H,
+                       const void* wu, const void* wd, int sfmt, const void* wsg, int gate_dtype, int T, int H,
                        int Is, int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st) {
   if (path == MOE_PATH_AUTO) path = T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
   if (path == MOE_PATH_GEMV || path == MOE_PATH_GEMV_MULTI) {
     float* s = reinterpret_cast<float*>(w.take((size_t)T * Is * 4));
     if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
-    return moe_launch_shared_gemv(x, x_dtype, wg, wu, wd, wsg, gate_dtype, T, H, Is, s, shared_raw, gate_prob, st);
+    return moe_launch_shared_gemv(x, x_dtype, wg, wu, wd, sfmt, wsg, gate_dtype, T, H, Is, s, shared_raw, gate_prob, st);
   }
   uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
   if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
   MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
-  if (path == MOE_PATH_MFMA && H % 256 == 0 && Is % 256 == 0) {
+  // Q8_0 shared weights take the 160-row f16 kernels on either MFMA path
+  if ((path == MOE_PATH_MFMA || sfmt == MOE_FMT_Q8_0) && H % 256 == 0 && Is % 256 == 0) {
     if (!x16) {
       uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
       if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
       MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
       x16 = c;
     }
-    MOE_TRY(moe_launch_gemm3_gateup(x16, wg, wu, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, s, st));
-    return moe_launch_gemm3_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, shared_raw, st);
+    MOE_TRY(moe_launch_gemm3_gateup(x16, wg, wu, sfmt, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, s, st));
+    return moe_launch_gemm3_down(s, wd, sfmt, 0, nullptr, 0, T, nullptr, H, Is, shared_raw, st);
   }
+  if (sfmt != MOE_FMT_BF16)
+    return moe_set_error(MOE_E_UNSUPPORTED, "moe_shared_expert: Q8_0 shared weights need H and I_s multiples of 256 on the MFMA paths");
   const int opb = path == MOE_PATH_MFMA_BF16;
   MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, wg, wu, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, opb, s, st));
   return moe_launch_gemm_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, opb, shared_raw, st);
 }
 
 static int check_shared_fmt(int shared_fmt, int gate_dtype, const char* who) {
-  if (shared_fmt != MOE_FMT_BF16)
-    return moe_set_error(MOE_E_FORMAT, "%s: shared-expert weights must be bf16 (got %d)", who, shared_fmt);
+  if (shared_fmt != MOE_FMT_BF16 && shared_fmt != MOE_FMT_Q8_0)
+    return moe_set_error(MOE_E_FORMAT, "%s: shared-expert weights must be bf16 or Q8_0 (got %d)", who, shared_fmt);
   if (gate_dtype != MOE_DT_BF16 && gate_dtype != MOE_DT_F32)
     return moe_set_error(MOE_E_FORMAT, "%s: the scalar shared gate must be bf16 or f32 (got %d)", who, gate_dtype);
   return MOE_OK;
@@ -333,8 +336,8 @@ int moe_shared_expert(const void* x, int x_dtype, const void* w_gate, const void
     return moe_set_error(MOE_E_ARG, "moe_shared_expert: pointers must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
-  return shared_impl(x, x_dtype, nullptr, w_gate, w_up, w_down, w_scalar_gate, gate_dtype, T, H, I_s,
-                     path, shared_raw, gate_prob, w, (hipStream_t)stream);
+  return shared_impl(x, x_dtype, nullptr, w_gate, w_up, w_down, shared_fmt, w_scalar_gate, gate_dtype, T,
+                     H, I_s, path, shared_raw, gate_prob, w, (hipStream_t)stream);
 }
 
 int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids,
@@ -407,7 +410,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     L.router_dt = Wt.router_dtype;
     L.gu = gate; L.gu_up = up; L.gu_estride = gu_estride;
     L.dn = down_q; L.dn_fmt = down_fmt;
-    L.sg = ws_gate; L.su = ws_up; L.sd = ws_down; L.ssg = ws_scalar_gate; L.ssg_dt = Wt.scalar_gate_dtype;
+    L.sg = ws_gate; L.su = ws_up; L.sd = ws_down; L.sfmt = Wt.shared_fmt;
+    L.ssg = ws_scalar_gate; L.ssg_dt = Wt.scalar_gate_dtype;
     L.logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)E * 2));
     L.ids = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w.take(K * 4));
     L.w_f32 = topk_w_f32 ? topk_w_f32 : reinterpret_cast<float*>(w.take(K * 4));
@@ -459,8 +463,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
     MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
     MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
-    MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate, Wt.scalar_gate_dtype, T, H,
-                        I_s, path, sraw, gp, w2, st));
+    MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
+                        Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w2, st));
     MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets, sorted,
                          hits, T, H, I, E, K, path, y, w, st));
     return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
@@ -474,7 +478,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   MOE_TRY(fork_res(f));
   if (hipEventRecord(f->fork, st) != hipSuccess || hipStreamWaitEvent(f->s, f->fork, 0) != hipSuccess)
     return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot fork the shared-expert stream");
-  const int rc_sh = shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, ws_scalar_gate,
+  const int rc_sh = shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
                                 Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s);
   int rc = rc_sh;
   if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st);

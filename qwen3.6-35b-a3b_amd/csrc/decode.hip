@@ -26,9 +26,10 @@ struct DecodeArgs {
   const uint8_t* gu_up;         // up rows likewise
   size_t gu_estride;
   const uint8_t* dn;
-  const uint16_t* sg;
-  const uint16_t* su;
-  const uint16_t* sd;
+  const void* sg;               // shared expert rows: bf16, or Q8_0 when sfmt says so
+  const void* su;
+  const void* sd;
+  int sfmt;
   const void* ssg;
   int ssg_dt;                   // scalar shared gate: bf16 or f32
   uint16_t* logits;
@@ -140,14 +141,17 @@ __global__ __launch_bounds__(256) void k_dec_route_shared(DecodeArgs a) {
   }
   if (bid < NR + NS) {
     const int i = (bid - NR) * 4 + wave;
-    const uint16_t* gr = a.sg + (size_t)i * a.H;
-    const uint16_t* ur = a.su + (size_t)i * a.H;
     float ag = 0.0f, au = 0.0f;
     for (int c = 0; c < a.H / 512; ++c) {
       float xv[8];
       load_x8<XDT>(a.x, (size_t)512 * c + 8 * lane, xv);
-      ag += dot8_bf16(*reinterpret_cast<const uint4*>(gr + 512 * c + 8 * lane), xv);
-      au += dot8_bf16(*reinterpret_cast<const uint4*>(ur + 512 * c + 8 * lane), xv);
+      if (a.sfmt == MOE_FMT_Q8_0) {
+        ag += dot8_shared<MOE_FMT_Q8_0>(a.sg, i, a.H, 512 * c + 8 * lane, xv);
+        au += dot8_shared<MOE_FMT_Q8_0>(a.su, i, a.H, 512 * c + 8 * lane, xv);
+      } else {
+        ag += dot8_shared<MOE_FMT_BF16>(a.sg, i, a.H, 512 * c + 8 * lane, xv);
+        au += dot8_shared<MOE_FMT_BF16>(a.su, i, a.H, 512 * c + 8 * lane, xv);
+      }
     }
     ag = wave_sum_f32(ag);
     au = wave_sum_f32(au);
@@ -207,12 +211,12 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecodeArgs a) {
   }
   const int l16 = lane & 15;
   const int row = (bid - a.K * nchunk) * 16 + wave * 4 + (lane >> 4);
-  const uint16_t* dr = a.sd + (size_t)row * a.Is;
   float acc = 0.0f;
   for (int c = 0; c < a.Is / 128; ++c) {
     float sv[8];
     load_x8<MOE_DT_F32>(a.s_shared, (size_t)128 * c + 8 * l16, sv);
-    acc += dot8_bf16(*reinterpret_cast<const uint4*>(dr + 128 * c + 8 * l16), sv);
+    acc += a.sfmt == MOE_FMT_Q8_0 ? dot8_shared<MOE_FMT_Q8_0>(a.sd, row, a.Is, 128 * c + 8 * l16, sv)
+                                  : dot8_shared<MOE_FMT_BF16>(a.sd, row, a.Is, 128 * c + 8 * l16, sv);
   }
   acc = row16_sum_f32(acc);
   if (l16 == 0) a.shared_raw[row] = acc;
@@ -348,7 +352,7 @@ int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st) {
     a.gu_estride = L.gu_estride ? L.gu_estride : (size_t)2 * L.I * rowb;
     a.gu_up = L.gu_up ? (const uint8_t*)L.gu_up : a.gu + (size_t)L.I * rowb;
   }
-  a.sg = (const uint16_t*)L.sg; a.su = (const uint16_t*)L.su; a.sd = (const uint16_t*)L.sd;
+  a.sg = L.sg; a.su = L.su; a.sd = L.sd; a.sfmt = L.sfmt;
   a.ssg = L.ssg; a.ssg_dt = L.ssg_dt;
   a.logits = L.logits; a.ids = L.ids; a.w_f32 = L.w_f32; a.w_bf16 = L.w_bf16;
   a.s_shared = L.s_shared; a.gate_prob = L.gate_prob; a.shared_raw = L.shared_raw;

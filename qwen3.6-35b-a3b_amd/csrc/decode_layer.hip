@@ -320,8 +320,9 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
 }
 
 // XDT: input x width; RDT: router row width (bf16, or f32 as the shipped artifact's ffn_gate_inp);
-// DFMT: routed down format (Q4_K, or Q5_K as the artifact's ffn_down_exps in 37 of 40 layers)
-template <int XDT, int RDT, int DFMT>
+// DFMT: routed down format (Q4_K, or Q5_K as the artifact's ffn_down_exps in 37 of 40 layers);
+// SFMT: shared-expert rows (bf16, or Q8_0 as the artifact's ffn_*_shexp)
+template <int XDT, int RDT, int DFMT, int SFMT>
 __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   constexpr int H = 2048, I = 512, E = 256, K = 8, IS = 512, ISX = IS / kXcd;
   __shared__ float s_x[H];
@@ -340,6 +341,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ uint4 s_occ[kOccPad];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  // 8 shared-expert weights held in a uint4 (bf16 x 8, or Q8_0 d / quants) dotted with x8
+  auto shared_dot = [](uint4 w, const float* x8) -> float {
+    if (SFMT == MOE_FMT_Q8_0) return q8_0_dot8(__uint_as_float(w.x), w.y, w.z, x8);
+    return dot8_bf16(w, x8);
+  };
   const int l16 = lane & 15;
   int* err = a.sync + kErrWord;
   // the role (x, r) from the launch's round-robin placement; the role's launch count is read
@@ -398,7 +404,27 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __syncthreads();
   if (never) atomicOr(err, (int)s_occ[t ^ 1].x);
   const uint32_t epoch = (uint32_t)s_role[0] + 1u;
-  if (wave >= 4) {
+  if (SFMT == MOE_FMT_Q8_0 && wave >= 4 && wave <= 6) {
+    // Q8_0 rows: each 8-element piece as (d, quants 0-3, quants 4-7) in one uint4; wave 4 the 8
+    // shared-down rows' piece, waves 5-6 the gate (wx[0..3]) and up (wx[4..7]) rows' pieces
+    const int i = ISX * x + 2 * r + (wave - 5);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint8_t* row;
+      int e0;
+      if (wave == 4) {
+        row = reinterpret_cast<const uint8_t*>(a.sd) + (size_t)(64 * r + (lane >> 3) + 8 * q) * (IS / 32 * 34);
+        e0 = ISX * x + 8 * (lane & 7);
+      } else {
+        row = reinterpret_cast<const uint8_t*>(q < 4 ? a.sg : a.su) + (size_t)i * (H / 32 * 34);
+        e0 = 512 * (q & 3) + 8 * lane;
+      }
+      float d;
+      uint32_t lo, hi;
+      q8_0_load8(row, e0, d, lo, hi);
+      wx[q] = make_uint4(__float_as_uint(d), lo, hi, 0u);
+    }
+  } else if (wave >= 4) {
     // one wave-uniform block with per-wave bases (p_lo: loads 0-3, p_hi: 4-7, stride st) rather
     // than a branch per wave, whose register reuse makes the compiler wait on loads the wave
     // never issued
@@ -460,8 +486,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       float ag = 0.0f, au = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        ag += dot8_bf16(wx[c], xv[c]);
-        au += dot8_bf16(wx[4 + c], xv[c]);
+        ag += shared_dot(wx[c], xv[c]);
+        au += shared_dot(wx[4 + c], xv[c]);
       }
       ag = wave_sum_f32(ag);
       au = wave_sum_f32(au);
@@ -548,7 +574,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      float acc = dot8_bf16(wx[q], sv);
+      float acc = shared_dot(wx[q], sv);
       acc += dpp_f32<0xB1>(acc);
       acc += dpp_f32<0x4E>(acc);
       acc += dpp_f32<0x141>(acc);        // sum over the 8 lanes of the row
@@ -719,12 +745,18 @@ bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, 
 
 namespace {
 
-template <int XDT, int RDT>
-void launch_layer_fmt(int dn_fmt, const LayerArgs& a, hipStream_t st) {
+template <int XDT, int RDT, int SFMT>
+void launch_layer_sfmt(int dn_fmt, const LayerArgs& a, hipStream_t st) {
   if (dn_fmt == MOE_FMT_Q5_K)
-    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q5_K>), dim3(kG), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q5_K, SFMT>), dim3(kG), dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q4_K>), dim3(kG), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q4_K, SFMT>), dim3(kG), dim3(kThreads), 0, st, a);
+}
+
+template <int XDT, int RDT>
+void launch_layer_fmt(int dn_fmt, int sfmt, const LayerArgs& a, hipStream_t st) {
+  if (sfmt == MOE_FMT_Q8_0) launch_layer_sfmt<XDT, RDT, MOE_FMT_Q8_0>(dn_fmt, a, st);
+  else launch_layer_sfmt<XDT, RDT, MOE_FMT_BF16>(dn_fmt, a, st);
 }
 
 }  // namespace
@@ -755,11 +787,11 @@ int moe_launch_decode_layer(const MoeDecodeLaunch& L, int* sync, uint32_t* xch, 
   a.nx_norm = L.nx_router ? L.nx_norm : nullptr;
   const bool r32 = L.router_dt == MOE_DT_F32;
   if (L.x_dtype == MOE_DT_F32) {
-    if (r32) launch_layer_fmt<MOE_DT_F32, MOE_DT_F32>(L.dn_fmt, a, st);
-    else launch_layer_fmt<MOE_DT_F32, MOE_DT_BF16>(L.dn_fmt, a, st);
+    if (r32) launch_layer_fmt<MOE_DT_F32, MOE_DT_F32>(L.dn_fmt, L.sfmt, a, st);
+    else launch_layer_fmt<MOE_DT_F32, MOE_DT_BF16>(L.dn_fmt, L.sfmt, a, st);
   } else {
-    if (r32) launch_layer_fmt<MOE_DT_BF16, MOE_DT_F32>(L.dn_fmt, a, st);
-    else launch_layer_fmt<MOE_DT_BF16, MOE_DT_BF16>(L.dn_fmt, a, st);
+    if (r32) launch_layer_fmt<MOE_DT_BF16, MOE_DT_F32>(L.dn_fmt, L.sfmt, a, st);
+    else launch_layer_fmt<MOE_DT_BF16, MOE_DT_BF16>(L.dn_fmt, L.sfmt, a, st);
   }
   return moe_check_launch("decode_layer");
 }

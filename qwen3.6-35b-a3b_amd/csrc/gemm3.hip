@@ -193,9 +193,44 @@ struct WRaw<MOE_FMT_BF16> {
   }
 };
 
+// Q8_0 (the shipped artifact's shared expert, ffn_*_shexp): a 64-wide K step is one pair of
+// blocks (f16 d + 32 x int8 each, 68 B, 4-byte aligned in a row of an even block count). Each
+// quant becomes an exact f16 through the mantissa trick on its sign-flipped byte (1024 + q + 128
+// under 0x6400, minus 1152), and one packed multiply rounds d * q to f16 once.
+template <>
+struct WRaw<MOE_FMT_Q8_0> {
+  uint32_t w[17];
+  __device__ __forceinline__ void load(const uint8_t* row, int k0) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)(k0 >> 6) * 68);
+#pragma unroll
+    for (int i = 0; i < 17; ++i) w[i] = p[i];
+  }
+  __device__ __forceinline__ static void q4(uint32_t q, f16x2_t d, uint32_t& o0, uint32_t& o1) {
+    const uint32_t x = q ^ 0x80808080u;
+    const f16x2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - off;
+    const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - off;
+    o0 = __builtin_bit_cast(uint32_t, a * d);
+    o1 = __builtin_bit_cast(uint32_t, b * d);
+  }
+  __device__ __forceinline__ void decode(int, uint16_t* dst) const {
+    const _Float16 d0 = __builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xFFFFu));
+    const _Float16 d1 = __builtin_bit_cast(_Float16, (uint16_t)(w[8] >> 16));
+    uint32_t o[32];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) q4(__builtin_amdgcn_alignbyte(w[m + 1], w[m], 2), (f16x2_t){d0, d0}, o[2 * m], o[2 * m + 1]);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) q4(w[9 + m], (f16x2_t){d1, d1}, o[16 + 2 * m], o[17 + 2 * m]);
+    uint4* d = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+  }
+};
+
 __device__ __forceinline__ size_t row_bytes(int fmt, int cols) {
   return fmt == MOE_FMT_Q4_K ? (size_t)(cols / 256) * 144
-       : fmt == MOE_FMT_Q5_K ? (size_t)(cols / 256) * 176 : (size_t)cols * 2;
+       : fmt == MOE_FMT_Q5_K ? (size_t)(cols / 256) * 176
+       : fmt == MOE_FMT_Q8_0 ? (size_t)(cols / 32) * 34 : (size_t)cols * 2;
 }
 
 __device__ __forceinline__ int tile_rows(const int32_t* tiles, const int32_t* offsets, int T,
@@ -258,7 +293,7 @@ struct PSet {
 template <int WFMT>
 __device__ __forceinline__ void produce(int nk, const ARows& asrc, const uint8_t* wrow, int p,
                                         Smem& sm) {
-  constexpr int kD = WFMT == MOE_FMT_BF16 ? 2 : 4;
+  constexpr int kD = (WFMT == MOE_FMT_BF16 || WFMT == MOE_FMT_Q8_0) ? 2 : 4;
   PSet<WFMT> s[kD];
 #pragma unroll
   for (int i = 0; i < kD; ++i) s[i].load(wrow, asrc, min(i, nk - 1) * kBK, p);
@@ -471,6 +506,8 @@ int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void*
     hipLaunchKernelGGL(k_gemm3_gateup<MOE_FMT_Q4_K>, grid, dim3(512), 0, st, x16, g, u, expert_stride, tiles, offsets, sorted_pairs, K, H, I, T, S);
   else if (fmt == MOE_FMT_BF16)
     hipLaunchKernelGGL(k_gemm3_gateup<MOE_FMT_BF16>, grid, dim3(512), 0, st, x16, g, u, expert_stride, tiles, offsets, sorted_pairs, K, H, I, T, S);
+  else if (fmt == MOE_FMT_Q8_0)
+    hipLaunchKernelGGL(k_gemm3_gateup<MOE_FMT_Q8_0>, grid, dim3(512), 0, st, x16, g, u, expert_stride, tiles, offsets, sorted_pairs, K, H, I, T, S);
   else
     return moe_set_error(MOE_E_FORMAT, "gemm3 gate_up: unsupported format %d", fmt);
   return moe_check_launch("gemm3_gateup");
@@ -490,6 +527,8 @@ int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t
     hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q5_K>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
   else if (fmt == MOE_FMT_BF16)
     hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_BF16>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
+  else if (fmt == MOE_FMT_Q8_0)
+    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q8_0>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
   else
     return moe_set_error(MOE_E_FORMAT, "gemm3 down: unsupported format %d", fmt);
   return moe_check_launch("gemm3_down");

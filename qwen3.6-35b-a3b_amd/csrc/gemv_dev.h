@@ -161,4 +161,42 @@ __device__ __forceinline__ float dot8_w(const void* w, size_t i, int dt, const f
   return dot8_bf16(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + i), x);
 }
 
+// 8 consecutive weights of a Q8_0 row (blocks of f16 d + 32 x int8, 34 B, value d * q:
+// tools/gguf_reader.py:238-245) from element e0 (e0 % 8 == 0), as the block's d and two words of
+// quants. Blocks are 2-byte aligned; a pair of blocks (68 B) is 4-byte aligned when the row is and
+// has an even block count, so the reads are aligned dwords of the pair, realigned with
+// v_alignbyte, and never leave it.
+__device__ __forceinline__ void q8_0_load8(const uint8_t* row, int e0, float& d, uint32_t& qlo,
+                                           uint32_t& qhi) {
+  const int b = e0 >> 5, qq = (e0 >> 3) & 3;
+  const uint32_t* pair = reinterpret_cast<const uint32_t*>(row + 68 * (b >> 1));
+  const int s = (b & 1) * 34;                                  // the block's byte in the pair
+  d = f16_to_f32((pair[s >> 2] >> ((s & 3) * 8)) & 0xFFFFu);
+  const int o = s + 2 + 8 * qq, i0 = o >> 2, sh = o & 3;      // sh: 2 (even block) or 0 (odd)
+  const uint32_t w0 = pair[i0], w1 = pair[i0 + 1];
+  const uint32_t w2 = sh ? pair[i0 + 2] : 0u;
+  qlo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+  qhi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+}
+__device__ __forceinline__ float q8_0_dot8(float d, uint32_t qlo, uint32_t qhi, const float* x) {
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = fmaf(x[i], (float)(int8_t)(qlo >> (8 * i)), a);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = fmaf(x[4 + i], (float)(int8_t)(qhi >> (8 * i)), a);
+  return d * a;
+}
+// the shared expert's weight rows: bf16 (SFMT = MOE_FMT_BF16) or Q8_0 (the shipped artifact's
+// ffn_*_shexp); element e0 of row `row` (cols elements), 8 weights dotted with x
+template <int SFMT>
+__device__ __forceinline__ float dot8_shared(const void* w, size_t row, int cols, int e0, const float* x) {
+  if (SFMT == MOE_FMT_Q8_0) {
+    float d;
+    uint32_t lo, hi;
+    q8_0_load8(reinterpret_cast<const uint8_t*>(w) + row * (size_t)(cols / 32 * 34), e0, d, lo, hi);
+    return q8_0_dot8(d, lo, hi, x);
+  }
+  return dot8_bf16(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + row * cols + e0), x);
+}
+
 }  // namespace moe

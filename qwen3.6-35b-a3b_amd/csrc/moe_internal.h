@@ -81,8 +81,9 @@ int moe_launch_gemm_down(const uint16_t* S, const void* w_down, int fmt, size_t 
 
 // shared expert
 int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const void* wu,
-                           const void* wd, const void* wsg, int gate_dtype, int T, int H, int Is,
-                           float* s_tmp, float* shared_raw, float* gate_prob, hipStream_t st);
+                           const void* wd, int shared_fmt, const void* wsg, int gate_dtype, int T,
+                           int H, int Is, float* s_tmp, float* shared_raw, float* gate_prob,
+                           hipStream_t st);
 int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int gate_dtype, int T, int H,
                            float* gate_prob, hipStream_t st);
 
@@ -106,6 +107,7 @@ struct MoeDecodeLaunch {
   const void* dn;
   int dn_fmt;
   const void *sg, *su, *sd, *ssg;
+  int sfmt = MOE_FMT_BF16;                 // shared-expert rows: bf16 or Q8_0
   int ssg_dt = MOE_DT_BF16;                // scalar shared gate dtype (bf16 or f32)
   uint16_t* logits;
   int32_t* ids;

@@ -28,10 +28,12 @@ def make_layer(seed: int, device="cuda", gate_up_fmt: int = Q.FMT_Q4_K,
                down_fmt: int = Q.FMT_Q4_K, zipf: bool = False, n_experts: int = 256,
                hidden: int = 2048, i_e: int = 512, i_s: int = 512, top_k: int = 8,
                std: float = 0.02, chunk: int = 16, router_dtype=torch.bfloat16,
-               scalar_gate_dtype=torch.bfloat16, split_gate_up: bool = False) -> LayerWeights:
+               scalar_gate_dtype=torch.bfloat16, split_gate_up: bool = False,
+               shared_fmt: int = Q.FMT_BF16) -> LayerWeights:
     """Random-init weights of the block's architecture. router_dtype / scalar_gate_dtype f32 and
     split_gate_up give the shipped artifact's widths (F32 ffn_gate_inp and ffn_gate_inp_shexp,
-    separate ffn_gate_exps / ffn_up_exps records; engine/block_forward.py:221-231)."""
+    separate ffn_gate_exps / ffn_up_exps records; engine/block_forward.py:221-231); shared_fmt
+    Q8_0 stores the shared expert as the artifact's Q8_0 ffn_*_shexp rows."""
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(seed)
 
@@ -51,14 +53,17 @@ def make_layer(seed: int, device="cuda", gate_up_fmt: int = Q.FMT_Q4_K,
         w = randn(n, hidden, i_e)
         down[e0:e0 + n] = Q.quantize(w.reshape(-1, i_e), down_fmt).view(n, hidden, dn_row)
         del w
+    def shared(*shape):
+        w = randn(*shape)
+        return Q.quantize(w, Q.FMT_Q8_0) if shared_fmt == Q.FMT_Q8_0 else w.to(torch.bfloat16)
+
     lw = LayerWeights(
         router=router, gate_up_q=gate_up, gate_up_fmt=gate_up_fmt, down_q=down, down_fmt=down_fmt,
-        shared_gate=randn(i_s, hidden).to(torch.bfloat16),
-        shared_up=randn(i_s, hidden).to(torch.bfloat16),
-        shared_down=randn(hidden, i_s).to(torch.bfloat16),
+        shared_gate=shared(i_s, hidden), shared_up=shared(i_s, hidden),
+        shared_down=shared(hidden, i_s),
         shared_scalar_gate=randn(1, hidden).to(scalar_gate_dtype),
         router_bias=zipf_bias(n_experts, seed, device=dev) if zipf else None,
-        top_k=top_k)
+        top_k=top_k, shared_fmt=shared_fmt)
     if split_gate_up:
         lw = lw.split_gate_up()
     lw.validate()

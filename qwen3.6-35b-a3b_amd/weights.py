@@ -11,7 +11,8 @@ HBM layout (all 16-byte aligned, expert axis slowest, as GGUF stores it — engi
   up_q             u8   [E, I, H/256 * blk] or None the separate up tensor (the artifact's
                                                     ffn_up_exps beside ffn_gate_exps)
   down_q           u8   [E, H, I/256 * blk]         Q4_K, Q5_K (the artifact) or Q6_K
-  shared_gate/up   bf16 [I_s, H];  shared_down bf16 [H, I_s]
+  shared_gate/up   bf16 [I_s, H];  shared_down bf16 [H, I_s]; or Q8_0 rows (uint8 [I_s, H/32*34],
+                   [H, I_s/32*34]: the artifact's ffn_*_shexp) when shared_fmt is Q8_0
   shared_scalar_gate bf16 or f32 [1, H]             (the artifact: f32)
 """
 from __future__ import annotations
@@ -46,6 +47,7 @@ class LayerWeights:
     router_bias: torch.Tensor | None = None
     top_k: int = 8
     up_q: torch.Tensor | None = None
+    shared_fmt: int = Q.FMT_BF16
 
     @property
     def n_experts(self) -> int:
@@ -63,7 +65,7 @@ class LayerWeights:
     def default_widths(self) -> bool:
         """bf16 router and scalar gate with a fused gate_up record: moe_block_forward's form."""
         return (self.up_q is None and self.router.dtype == torch.bfloat16
-                and self.shared_scalar_gate.dtype == torch.bfloat16)
+                and self.shared_scalar_gate.dtype == torch.bfloat16 and self.shared_fmt == Q.FMT_BF16)
 
     @property
     def i_s(self) -> int:
@@ -85,12 +87,17 @@ class LayerWeights:
         E, H = self.router.shape
         I = self.i_e
         rows = I if self.up_q is not None else 2 * I
+        q8 = self.shared_fmt == Q.FMT_Q8_0
+        if self.shared_fmt not in (Q.FMT_BF16, Q.FMT_Q8_0):
+            raise ValueError(f"shared_fmt must be BF16 or Q8_0, got {self.shared_fmt}")
+        sdt = torch.uint8 if q8 else torch.bfloat16
+        scols = (lambda c: c // 32 * Q.Q8_0_BYTES) if q8 else (lambda c: c)
         want = {
             "gate_up_q": (self.gate_up_q, torch.uint8, (E, rows, Q.row_bytes(self.gate_up_fmt, H))),
             "down_q": (self.down_q, torch.uint8, (E, H, Q.row_bytes(self.down_fmt, I))),
-            "shared_gate": (self.shared_gate, torch.bfloat16, (self.i_s, H)),
-            "shared_up": (self.shared_up, torch.bfloat16, (self.i_s, H)),
-            "shared_down": (self.shared_down, torch.bfloat16, (H, self.i_s)),
+            "shared_gate": (self.shared_gate, sdt, (self.i_s, scols(H))),
+            "shared_up": (self.shared_up, sdt, (self.i_s, scols(H))),
+            "shared_down": (self.shared_down, sdt, (H, scols(self.i_s))),
             "shared_scalar_gate": (self.shared_scalar_gate, self.shared_scalar_gate.dtype, (1, H)),
         }
         if self.up_q is not None:
@@ -146,5 +153,5 @@ class LayerWeights:
         return L.LayerWeightsC(
             p(self.router), dt(self.router), p(self.router_bias), p(self.gate_up_q), p(self.up_q),
             self.gate_up_fmt, p(self.down_q), self.down_fmt, p(self.shared_gate), p(self.shared_up),
-            p(self.shared_down), L.MOE_FMT_BF16, p(self.shared_scalar_gate),
+            p(self.shared_down), self.shared_fmt, p(self.shared_scalar_gate),
             dt(self.shared_scalar_gate), p(norm_w))

@@ -66,10 +66,10 @@ def layer_q5k(pkg, dev):
 @pytest.fixture(scope="session")
 def layer_artifact(pkg, dev):
     """The shipped artifact's widths all at once: F32 router and scalar shared gate, separate
-    Q4_K gate and up records, Q5_K down (seed 7, Zipf routing)."""
+    Q4_K gate and up records, Q5_K down, Q8_0 shared expert (seed 7, Zipf routing)."""
     from oracle import moe_oracle as O
     lw = pkg.synth.make_layer(seed=7, device=dev, down_fmt=pkg.quant.FMT_Q5_K, zipf=True,
                               router_dtype=torch.float32, scalar_gate_dtype=torch.float32,
-                              split_gate_up=True)
+                              split_gate_up=True, shared_fmt=pkg.quant.FMT_Q8_0)
     torch.cuda.synchronize()
     return lw, O.from_device(lw)

@@ -47,10 +47,13 @@ def test_f32_router_differs_from_its_bf16_rounding(pkg, layer_artifact, dev):
 
 
 @pytest.mark.parametrize("T,path,dtype", [(1, 1, torch.float32), (16, 1, torch.float32),
-                                          (64, 2, torch.float32), (257, 2, torch.bfloat16)])
-def test_f32_scalar_gate(pkg, layer_artifact, dev, T, path, dtype):
+                                          (64, 2, torch.float32), (257, 2, torch.bfloat16),
+                                          (64, 3, torch.float32)])
+def test_q8_0_shared_expert_and_f32_scalar_gate(pkg, layer_artifact, dev, T, path, dtype):
+    """The shared expert on Q8_0 rows (GEMV at small T; the 160-row f16 MFMA kernels otherwise,
+    also under MOE_PATH_MFMA_BF16) and the f32 scalar gate, against the oracle's exact d * q."""
     lw, ow = layer_artifact
-    assert lw.shared_scalar_gate.dtype == torch.float32
+    assert lw.shared_scalar_gate.dtype == torch.float32 and lw.shared_gate.dtype == torch.uint8
     x = pkg.synth.make_input(T, seed=720 + T, device=dev, dtype=dtype)
     raw, prob = pkg.abi.shared_expert(x, lw.shared_gate, lw.shared_up, lw.shared_down,
                                       lw.shared_scalar_gate, path)

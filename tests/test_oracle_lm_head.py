@@ -85,3 +85,15 @@ def test_table_rows_formats(pkg):
     bf = w.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     got = LO.table_rows(bf, LO.FMT_BF16, rows, 2048)
     assert np.array_equal(got, w.to(torch.bfloat16).float().numpy()[rows])
+
+
+def test_q8_0_oracle_shared_conversion(pkg):
+    """from_device turns Q8_0 shared rows into the exact f32 values d * q the block oracle reads."""
+    from oracle import moe_oracle as O
+    lw = pkg.synth.make_layer(seed=3, device="cpu", n_experts=64, top_k=2, i_s=512,
+                              shared_fmt=pkg.quant.FMT_Q8_0)
+    ow = O.from_device(lw)
+    assert ow.shared_gate.dtype == torch.float32 and tuple(ow.shared_gate.shape) == (512, 2048)
+    assert tuple(ow.shared_down.shape) == (2048, 512)
+    row = lw.shared_down[5].numpy()
+    assert np.array_equal(ow.shared_down[5].numpy(), LO.dequant_q8_0(row, 512))
