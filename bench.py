@@ -70,6 +70,7 @@ def parse():
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing (what the kernel-trace profile covers)")
     ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--no-c4", action="store_true", help="skip the config-4 prefill timing")
     ap.add_argument("--no-artifact", action="store_true",
                     help="skip the decode chain over the shipped artifact's weight widths")
     ap.add_argument("--lm-head-only", action="store_true",
@@ -335,6 +336,28 @@ def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
             "prefill_tflops": tflops, "prefill_mfma_util": tflops / BF16_PEAK_TFLOPS}
 
 
+def prefill_c4(torch, pkg, dev, steps: int, n_layers: int = 40) -> dict:
+    """Config 4: T = 16384 bf16 tokens, Q4_K gate_up + Q6_K down, Zipf(1.1) routing, the step
+    rotating over 40 resident layer instances (each step one block on the next instance)."""
+    synth, abi = pkg.synth, pkg.abi
+    layers = [synth.make_layer(seed=3000 + l, device=dev, down_fmt=pkg.quant.FMT_Q6_K, zipf=True)
+              for l in range(n_layers)]
+    x = synth.make_input(16384, seed=3, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(16384, 2048, dtype=torch.float32, device=dev)
+    for l in range(2):
+        abi.block_forward(x, layers[l], out=out)
+    torch.cuda.synchronize()
+    it = iter(range(10 ** 9))
+    ms = time_stream(lambda: abi.block_forward(x, layers[next(it) % n_layers], out=out), steps, torch)
+    flops = synth.prefill_flops(16384, layers[0])
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"prefill config 4 (T=16384, Q6_K down, Zipf, {n_layers} layers): {ms:.3f} ms, "
+        f"{16384 / (ms * 1e-3):.0f} tok/s, {tflops:.1f} TFLOP/s ({100 * tflops / BF16_PEAK_TFLOPS:.1f}%)")
+    del layers
+    torch.cuda.empty_cache()
+    return {"c4_prefill_ms": ms, "c4_tok_s": 16384 / (ms * 1e-3), "c4_mfma_util": tflops / BF16_PEAK_TFLOPS}
+
+
 def lm_head_bench(torch, pkg, dev, reps: int = 20) -> dict:
     """The untied lm_head GEMV at the artifact's shape (248320 x 2048), one token, for each table
     width: kernel time from HIP events on the launching stream and table GB/s (each byte read
@@ -496,6 +519,9 @@ def main():
     if not args.no_prefill:
         prefill = prefill_c3(torch, synth, abi, layers[0], dev, args.prefill_steps)
 
+    # ---------------------------------------------------------------- prefill, config 4
+    c4 = {} if args.no_c4 else prefill_c4(torch, pkg, dev, args.prefill_steps)
+
     # ---------------------------------------------------------------- untied lm_head GEMV
     lmh = lm_head_bench(torch, pkg, dev) if not args.no_lm_head else {}
 
@@ -544,6 +570,7 @@ def main():
     result.update(c2)
     result.update({k: round(v, 3) for k, v in art.items()})
     result.update({k: round(v, 3) for k, v in lmh.items()})
+    result.update({k: round(v, 4) for k, v in c4.items()})
     result.update({k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()})
     print(json.dumps(result), flush=True)
 

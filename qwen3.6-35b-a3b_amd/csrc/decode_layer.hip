@@ -339,6 +339,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ double s_red[2][kThreads / 64];
   __shared__ int s_role[1];
   __shared__ uint4 s_occ[kOccPad];
+  // Q8_0 shared rows staged for the lanes' block reads: waves 5-6 their gate and up rows (2176 B
+  // each, dwords [1088 (wave - 5), +1088)), wave 4 the 64 rows' 68-byte slices of this XCD
+  // (dwords [2176, 3264))
+  __shared__ uint32_t s_q8[SFMT == MOE_FMT_Q8_0 ? 4 * 544 + 64 * 17 : 1];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   // 8 shared-expert weights held in a uint4 (bf16 x 8, or Q8_0 d / quants) dotted with x8
@@ -404,25 +408,30 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __syncthreads();
   if (never) atomicOr(err, (int)s_occ[t ^ 1].x);
   const uint32_t epoch = (uint32_t)s_role[0] + 1u;
+  // Q8_0 shared rows (34-byte blocks, 2-byte aligned; a row's block pairs are 4-byte aligned),
+  // requested as contiguous bytes and staged through LDS (s_q8) just before use: waves 5-6 the gate
+  // and up rows of their intermediate row (16-byte loads), wave 4 the 64 shared-down rows'
+  // 68-byte slices of this XCD (consecutive dwords). Each lane then reads its own blocks from LDS.
+  uint32_t wq[SFMT == MOE_FMT_Q8_0 ? 20 : 1];
   if (SFMT == MOE_FMT_Q8_0 && wave >= 4 && wave <= 6) {
-    // Q8_0 rows: each 8-element piece as (d, quants 0-3, quants 4-7) in one uint4; wave 4 the 8
-    // shared-down rows' piece, waves 5-6 the gate (wx[0..3]) and up (wx[4..7]) rows' pieces
-    const int i = ISX * x + 2 * r + (wave - 5);
+    if (wave == 4) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint8_t* row;
-      int e0;
-      if (wave == 4) {
-        row = reinterpret_cast<const uint8_t*>(a.sd) + (size_t)(64 * r + (lane >> 3) + 8 * q) * (IS / 32 * 34);
-        e0 = ISX * x + 8 * (lane & 7);
-      } else {
-        row = reinterpret_cast<const uint8_t*>(q < 4 ? a.sg : a.su) + (size_t)i * (H / 32 * 34);
-        e0 = 512 * (q & 3) + 8 * lane;
+      for (int k = 0; k < 17; ++k) {
+        const int g = lane + 64 * k, row = g / 17;
+        wq[k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(a.sd) +
+                                                   (size_t)(64 * r + row) * (IS / 32 * 34) + 68 * x + 4 * (g - 17 * row));
       }
-      float d;
-      uint32_t lo, hi;
-      q8_0_load8(row, e0, d, lo, hi);
-      wx[q] = make_uint4(__float_as_uint(d), lo, hi, 0u);
+    } else {
+      const size_t roff = (size_t)(ISX * x + 2 * r + (wave - 5)) * (H / 32 * 34);
+      const uint4* g = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.sg) + roff);
+      const uint4* u = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.su) + roff);
+      // 136 uint4 per row, gate then up: chunk c = lane + 64 k, k < 4 for every lane, k = 4 for 16
+#pragma unroll
+      for (int k = 0; k < 5; ++k) {
+        const int c = lane + 64 * k;
+        const uint4 v = c < 136 ? g[c] : (c < 272 ? u[c - 136] : make_uint4(0u, 0u, 0u, 0u));
+        wq[4 * k] = v.x; wq[4 * k + 1] = v.y; wq[4 * k + 2] = v.z; wq[4 * k + 3] = v.w;
+      }
     }
   } else if (wave >= 4) {
     // one wave-uniform block with per-wave bases (p_lo: loads 0-3, p_hi: 4-7, stride st) rather
@@ -482,7 +491,32 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     const int e = 8 * r + wave;
     const uint32_t bits = router_row_bits<RDT>(wr4, xv, (double)bias_e, xl1);
     if (lane == 0) lstore(xr, 4 * (XW_LOG + 256 * x + e), ~bits);
-    if (wave == 5 || wave == 6) {
+    if ((wave == 5 || wave == 6) && SFMT == MOE_FMT_Q8_0) {
+      uint32_t* st = s_q8 + 1088 * (wave - 5);
+#pragma unroll
+      for (int k = 0; k < 5; ++k) {
+        const int c = lane + 64 * k;
+        if (c < 272) *reinterpret_cast<uint4*>(st + 4 * c) = make_uint4(wq[4 * k], wq[4 * k + 1], wq[4 * k + 2], wq[4 * k + 3]);
+      }
+      wave_sync();
+      // block `lane` of both rows: the 9 dwords of its pair half, then elements 32 lane .. +31
+      uint32_t bg[9], bu[9];
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        bg[k] = st[17 * (lane >> 1) + 8 * (lane & 1) + k];
+        bu[k] = st[544 + 17 * (lane >> 1) + 8 * (lane & 1) + k];
+      }
+      float xq[32];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float4 u = reinterpret_cast<const float4*>(s_x + 32 * lane)[k];
+        xq[4 * k] = u.x; xq[4 * k + 1] = u.y; xq[4 * k + 2] = u.z; xq[4 * k + 3] = u.w;
+      }
+      float ag = q8_0_block_dot(bg, lane & 1, xq), au = q8_0_block_dot(bu, lane & 1, xq);
+      ag = wave_sum_f32(ag);
+      au = wave_sum_f32(au);
+      if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + (wave - 5)), xenc(silu_f32(ag) * au));
+    } else if (wave == 5 || wave == 6) {
       float ag = 0.0f, au = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -565,6 +599,24 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
         reinterpret_cast<float4*>(s_sh)[lane] = make_float4(xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w));
     }
     wave_sync();
+    if (SFMT == MOE_FMT_Q8_0) {
+      uint32_t* st = s_q8 + 2176;
+#pragma unroll
+      for (int k = 0; k < 17; ++k) st[lane + 64 * k] = wq[k];
+      wave_sync();
+      // row 64 r + lane: its two blocks (this XCD's 64 shared activations) in one lane
+      uint32_t bd[17];
+#pragma unroll
+      for (int k = 0; k < 17; ++k) bd[k] = st[17 * lane + k];
+      float sq[64];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float4 u = reinterpret_cast<const float4*>(s_sh)[k];
+        sq[4 * k] = u.x; sq[4 * k + 1] = u.y; sq[4 * k + 2] = u.z; sq[4 * k + 3] = u.w;
+      }
+      const float acc = q8_0_block_dot(bd, 0, sq) + q8_0_block_dot(bd + 8, 1, sq + 32);
+      xstore(xb + XW_SHP + H * x + 64 * r + lane, xenc(acc));
+    }
     float sv[8];
     {
       const float4 u0 = *reinterpret_cast<const float4*>(s_sh + 8 * (lane & 7));
@@ -573,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       sv[4] = u1.x; sv[5] = u1.y; sv[6] = u1.z; sv[7] = u1.w;
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < (SFMT == MOE_FMT_Q8_0 ? 0 : 8); ++q) {
       float acc = shared_dot(wx[q], sv);
       acc += dpp_f32<0xB1>(acc);
       acc += dpp_f32<0x4E>(acc);

@@ -186,6 +186,22 @@ __device__ __forceinline__ float q8_0_dot8(float d, uint32_t qlo, uint32_t qhi, 
   for (int i = 0; i < 4; ++i) a = fmaf(x[4 + i], (float)(int8_t)(qhi >> (8 * i)), a);
   return d * a;
 }
+// One Q8_0 block held as the 9 aligned dwords of its half of a 4-byte-aligned block pair (odd =
+// the pair's second block: dwords 8..16 of the pair) dotted with its 32 activations x:
+// d * sum_i x_i q_i, the quants as exact floats.
+__device__ __forceinline__ float q8_0_block_dot(const uint32_t* w, int odd, const float* x) {
+  const float d = f16_to_f32(odd ? (w[0] >> 16) : (w[0] & 0xFFFFu));
+  float a = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    // quants start at byte 2 of the window (even block) or byte 4 (odd block)
+    const uint32_t q = odd ? w[m + 1] : __builtin_amdgcn_alignbyte(w[m + 1], w[m], 2);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) a = fmaf(x[4 * m + b], (float)(int8_t)(q >> (8 * b)), a);
+  }
+  return d * a;
+}
+
 // the shared expert's weight rows: bf16 (SFMT = MOE_FMT_BF16) or Q8_0 (the shipped artifact's
 // ffn_*_shexp); element e0 of row `row` (cols elements), 8 weights dotted with x
 template <int SFMT>
