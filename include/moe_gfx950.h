@@ -62,6 +62,13 @@ const char *moe_last_error(void);
  * T-token step of this geometry (an upper bound for every path). */
 size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s);
 
+/* Scratch bytes moe_router_topk can use for T tokens (the sync words, the logits when
+ * logits_bf16 is NULL, and the int8 matrix-core R1's row metadata and router digit planes).
+ * No reference counterpart: a workspace of this size (or of moe_workspace_bytes) lets R1 at
+ * T > 256 run on the int8 matrix cores; a smaller one, or none, keeps it on the f64 matrix cores.
+ * The logits are the same bits either way. */
+size_t moe_router_workspace_bytes(int T, int H, int E);
+
 /* Bit-exact super-block decode: n_elts elements of `fmt` blocks -> f32 or bf16 (RNE of the exact
  * f32 value). Replaces tools/gguf_reader.py:248-268 (_deq_q4_k), :271-296 (_deq_q5_k),
  * :299-322 (_deq_q6_k) and tools/gguf_fast_dequant.py:87-152 (dequant_np). n_elts % 256 == 0. */
@@ -77,7 +84,9 @@ int moe_dequant(const void *blocks, int fmt, int64_t n_elts, void *out, int out_
  * artifact's F32 ffn_gate_inp, engine/block_forward.py:221-231; x*W products stay exact in f64,
  * so R1 is correctly rounded either way); logit_bias: [E] f32 or NULL.
  * logits_bf16 [T,E], probs [T,E] may be NULL; topk_ids [T,K] int32; w_f32, w_bf16 [T,K].
- * Limits: H % 512 == 0, E <= 256, K <= 16, K * 64 > E (torch's nth_element branch). */
+ * Limits: H % 512 == 0, E <= 256, K <= 16, K * 64 > E (torch's nth_element branch).
+ * ws: NULL when logits_bf16 is given, else at least the sync words and the logits; with
+ * moe_router_workspace_bytes(T, H, E) bytes, R1 at T > 256 runs on the int8 matrix cores. */
 int moe_router_topk(const void *x, int x_dtype, const void *w_router, int w_dtype,
                     const float *logit_bias, int T, int H, int E, int K, void *logits_bf16, float *probs,
                     int32_t *topk_ids, float *w_f32, void *w_bf16, void *ws, size_t ws_bytes,

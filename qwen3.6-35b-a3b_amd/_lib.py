@@ -62,6 +62,7 @@ SIGNATURES = {
     "moe_abi_version": (_I, []),
     "moe_last_error": (_CP, []),
     "moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "moe_router_workspace_bytes": (_SZ, [_I, _I, _I]),
     "moe_dequant": (_I, [_VP, _I, _I64, _VP, _I, _VP]),
     "moe_router_topk": (_I, [_VP, _I, _VP, _I, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP,
                              _SZ, _VP]),

@@ -127,9 +127,10 @@ def router_topk(x: torch.Tensor, w_router: torch.Tensor, top_k: int,
     ids = torch.empty(T, top_k, dtype=torch.int32, device=dev)
     wf = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     wb = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
+    ws = workspace(dev, int(L.lib.moe_router_workspace_bytes(T, H, E)))
     _check(L.lib.moe_router_topk(_p(x), _xdt(x), _p(w_router), wdt, _p(bias), T, H, E, top_k,
-                                 _p(logits), _p(probs), _p(ids), _p(wf), _p(wb), None, 0,
-                                 _stream(x)), "router_topk")
+                                 _p(logits), _p(probs), _p(ids), _p(wf), _p(wb), _p(ws),
+                                 ws.numel(), _stream(x)), "router_topk")
     return {"router_logits": logits, "router_probs": probs, "topk_ids": ids,
             "topk_weights": wb, "topk_weights_f32": wf}
 

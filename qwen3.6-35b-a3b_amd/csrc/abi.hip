@@ -87,7 +87,7 @@ static int fork_res(ForkRes*& r) {
 
 struct Carve {
   // every piece a T-token forward can need; sizes are upper bounds over both paths
-  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, xn, x16, flag;
+  size_t logits, ids, wf, wb, offsets, sorted, pos, hits, sort_ws, tiles, S, y, sS, sraw, gprob, xn, x16, flag, rscr;
 };
 
 static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
@@ -111,6 +111,7 @@ static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
   c.xn = r256((size_t)T * H * 4);
   c.x16 = r256((size_t)T * H * 2);
   c.flag = 256;
+  c.rscr = moe_router_i8_scratch_bytes(T, H, E);
   return c;
 }
 
@@ -124,7 +125,12 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s) {
   if (T < 1 || E < 1 || K < 1) return 0;
   const Carve c = carve_sizes(T, H, I, E, K, I_s);
   return kSyncBytes + c.logits + c.ids + c.wf + c.wb + c.offsets + c.sorted + c.pos + c.hits +
-         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.xn + c.x16 + c.flag;
+         c.sort_ws + c.tiles + c.S + c.y + c.sS + c.sraw + c.gprob + c.xn + c.x16 + c.flag + c.rscr;
+}
+
+size_t moe_router_workspace_bytes(int T, int H, int E) {
+  if (T < 1 || H < 1 || E < 1) return 0;
+  return kSyncBytes + r256((size_t)T * E * 2) + moe_router_i8_scratch_bytes(T, H, E);
 }
 
 int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
@@ -151,13 +157,16 @@ int moe_router_topk(const void* x, int x_dtype, const void* w_router, int w_dtyp
   if (!aligned16(x) || !aligned16(w_router)) return moe_set_error(MOE_E_ARG, "moe_router_topk: x and w_router must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   uint16_t* logits = reinterpret_cast<uint16_t*>(logits_bf16);
+  MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
+  w.take(kSyncBytes);
   if (!logits) {
-    MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
-    w.take(kSyncBytes);
     logits = reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
     if (!logits) return moe_set_error(MOE_E_WORKSPACE, "moe_router_topk: workspace too small for the logits");
   }
-  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, w_dtype, logit_bias, T, H, E, logits, st));
+  // room for the int8 matrix-core R1 (large T), else the f64 one; the bits are the same
+  const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);
+  void* rscr = w.take(rsb);
+  MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, w_dtype, logit_bias, T, H, E, logits, rscr, rsb, st));
   return moe_launch_route_topk(logits, T, E, K, probs, topk_ids, w_f32,
                                reinterpret_cast<uint16_t*>(w_bf16), nullptr, st);
 }
@@ -459,7 +468,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
   }
   if (T < kForkMinT) {
-    MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st));
+    MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, nullptr, 0, st));
     MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
     MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
     MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
@@ -481,7 +490,11 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   const int rc_sh = shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
                                 Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s);
   int rc = rc_sh;
-  if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, st);
+  // the router's scratch is dead before the experts take theirs (same stream)
+  MoeWs wr = w;
+  const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);
+  void* rscr = wr.take(rsb);
+  if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, rscr, rsb, st);
   if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st);
   if (rc == MOE_OK) rc = moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st);
   if (rc == MOE_OK)

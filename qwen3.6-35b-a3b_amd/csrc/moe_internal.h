@@ -15,8 +15,16 @@ int moe_check_launch(const char* what);
 int moe_launch_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
                        hipStream_t st);
 
+// scratch (may be NULL) of moe_router_i8_scratch_bytes(T, H, E) bytes lets T > 256 run on the
+// int8 matrix cores; without it R1 runs on the f64 ones. The bits are the same either way.
 int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
-                             int T, int H, int E, uint16_t* logits, hipStream_t st);
+                             int T, int H, int E, uint16_t* logits, void* scratch,
+                             size_t scratch_bytes, hipStream_t st);
+size_t moe_router_i8_scratch_bytes(int T, int H, int E);
+bool moe_router_i8_supported(int T, int H, int E);
+int moe_launch_router_logits_i8(const void* x, int x_dtype, const void* w, int w_dtype,
+                                const float* bias, int T, int H, int E, uint16_t* logits,
+                                void* scratch, hipStream_t st);
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
                           float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st);
 

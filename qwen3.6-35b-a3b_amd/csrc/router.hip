@@ -401,7 +401,10 @@ static void launch_router_logits(const void* x, const void* w, const float* bias
 }
 
 int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
-                             int T, int H, int E, uint16_t* logits, hipStream_t st) {
+                             int T, int H, int E, uint16_t* logits, void* scratch,
+                             size_t scratch_bytes, hipStream_t st) {
+  if (scratch && moe_router_i8_supported(T, H, E) && scratch_bytes >= moe_router_i8_scratch_bytes(T, H, E))
+    return moe_launch_router_logits_i8(x, x_dtype, w, w_dtype, bias, T, H, E, logits, scratch, st);
   if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32)
     launch_router_logits<MOE_DT_F32, MOE_DT_F32>(x, w, bias, T, H, E, logits, st);
   else if (x_dtype == MOE_DT_F32)

@@ -1,0 +1,406 @@
+// R1 for large T on the int8 matrix cores (gfx950 v_mfma_i32_32x32x32_i8), correctly rounded to
+// bf16 like every other R1 kernel here (speccheck/moe_ref.py:318-326: logits = bf16 of the exact
+// sum x . W_e + b_e).
+//
+// Method: error-free splitting into integer digits (Ozaki, Ogita, Oishi, "Error-free
+// transformations of matrix multiplication by using fast routines of matrix multiplication",
+// Numer. Algorithms 59, 2012; integer form as in Ootomo, Ozaki, Yokota, "DGEMM on integer matrix
+// multiplication unit", IJHPCA 2024).
+//   * Every row v (an x row or a router row) gets its exponent E = floor(log2 max|v|) and the
+//     integers N_k = rint(v_k 2^(S-E)), S = 8D - 3, so |N_k| < 2^(8D-2); v^_k = N_k 2^(E-S).
+//   * N = sum_a d_a 256^(D-1-a) with balanced digits d_a in [-128, 127] (the bytes of
+//     (N + 0x80..80) ^ 0x80..80); the top digit lies in [-64, 64].
+//   * x^ . w^ = sum over digit pairs (a, b) of 2^(Ex+Ew-10-8(a+b)) * sum_k dx_a,k dw_b,k. Each
+//     pair sum is an exact int32 (|d d'| <= 2^14, H <= 4096, at most 4 pairs share a level's
+//     accumulator), so level l = a + b holds an exact integer.
+//   * The levels are combined in f64 (Horner from the least significant level), scaled by
+//     2^(Ex+Ew-10) (exact) and the bias is added. The distance to the exact sum x . w + b is at most
+//       sum|x^-x| max|w^| + max|x| sum|w^-w|        (the rows' rounding to the digit grid)
+//     + 2^-52 (sum of the Horner partials' magnitudes) 2^(Ex+Ew-10) + 2^-52 |s|  (f64 roundings),
+//     and that bound certifies the bf16 rounding exactly as the f64 kernels' bound does. x uses
+//     D = 4 digits (exact for elements within 2^21 of the row maximum), bf16 router rows D = 4,
+//     f32 router rows D = 5 (exact within 2^13); what is left over is rare and bounded.
+//   * A logit the bound does not certify is recomputed by its wave in double-double (the whole
+//     wave sums the row in parallel) and rounded from that, ties to even on the midpoint itself.
+//
+// Kernels: k_router_prep (one wave per row: the row metadata for x rows and router rows, and the
+// router rows' digit planes), then k_router_i8 (64 tokens x 64 experts per block; x rows are cut
+// into digits on the fly while staged into LDS, the router digits come from the prep).
+#include <type_traits>
+
+#include "common.h"
+#include "moe_internal.h"
+#include "router_dev.h"
+
+namespace moe {
+namespace ri8 {
+
+constexpr int kXD = 4;                 // digits per x element
+constexpr int kXS = 8 * kXD - 3;       // x scale exponent S
+constexpr int kKC = 64;                // k per LDS stage
+constexpr int kRS = 80;                // LDS row stride (bytes): 16-byte slots of 8 rows distinct
+constexpr int kMaxCh = 8;              // prep: 8-element chunks per lane, so H <= 4096
+
+template <int WDT> struct WDig { static constexpr int D = (WDT == MOE_DT_F32) ? 5 : 4; };
+
+struct alignas(32) RowMeta {
+  int e;          // row exponent E (0 for an all-zero row)
+  int pad;
+  double dsum;    // sum_k |v^_k - v_k|
+  double vmax;    // max_k |v_k|
+  double qmax;    // max_k |v^_k|
+};
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+// staging registers: vector types, so SROA keeps arrays of them in VGPRs (arrays of the struct
+// type uint4 are left as allocas, which the backend then places in LDS)
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+template <int DT>
+__device__ __forceinline__ float elt(const void* p, size_t i) {
+  if constexpr (DT == MOE_DT_F32) return reinterpret_cast<const float*>(p)[i];
+  else return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+// 8 consecutive elements from element i (i % 8 == 0)
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, size_t i, float* o) {
+  if constexpr (DT == MOE_DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = bf16_to_f32(w[k] & 0xFFFFu);
+      o[2 * k + 1] = bf16_to_f32(w[k] >> 16);
+    }
+  }
+}
+
+__device__ __forceinline__ double wave_max_f64(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ------------------------------------------------------------------------------ row metadata --
+// Digits of 8 consecutive elements (n8: the integers N, |N| < 2^(8D-2)) into D planes, 8 bytes
+// each: byte j of plane a = digit a of element j (plane 0 the most significant).
+template <int D>
+__device__ __forceinline__ void store_digits8(const double* n8, int8_t* dst, size_t plane) {
+  if constexpr (D == 4) {
+    // u = (N + 0x80808080) ^ 0x80808080 holds digit a in byte 3 - a; a 4 x 4 byte transpose per
+    // group of four elements
+    uint32_t u[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u[j] = ((uint32_t)(int)n8[j] + 0x80808080u) ^ 0x80808080u;
+    uint32_t p[4][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t* w = u + 4 * q;
+      // t = [w0.b3 w1.b3 w0.b2 w1.b2], t2 = [w0.b1 w1.b1 w0.b0 w1.b0]; s, s2 likewise for w2, w3
+      const uint32_t t = __builtin_amdgcn_perm(w[1], w[0], 0x06020703u);
+      const uint32_t t2 = __builtin_amdgcn_perm(w[1], w[0], 0x04000501u);
+      const uint32_t s = __builtin_amdgcn_perm(w[3], w[2], 0x06020703u);
+      const uint32_t s2 = __builtin_amdgcn_perm(w[3], w[2], 0x04000501u);
+      p[0][q] = __builtin_amdgcn_perm(s, t, 0x05040100u);
+      p[1][q] = __builtin_amdgcn_perm(s, t, 0x07060302u);
+      p[2][q] = __builtin_amdgcn_perm(s2, t2, 0x05040100u);
+      p[3][q] = __builtin_amdgcn_perm(s2, t2, 0x07060302u);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) *reinterpret_cast<uint2*>(dst + a * plane) = make_uint2(p[a][0], p[a][1]);
+  } else {
+    uint64_t u[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      u[j] = ((uint64_t)(int64_t)n8[j] + 0x8080808080ull) ^ 0x8080808080ull;
+#pragma unroll
+    for (int a = 0; a < D; ++a) {
+      const int b = 8 * (D - 1 - a);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lo |= (uint32_t)((u[j] >> b) & 0xFF) << (8 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hi |= (uint32_t)((u[4 + j] >> b) & 0xFF) << (8 * j);
+      *reinterpret_cast<uint2*>(dst + a * plane) = make_uint2(lo, hi);
+    }
+  }
+}
+
+// One wave per row: rows 0..E-1 are the router rows (D = WD; planes [WD][E][H] in wdig), rows
+// E..E+T-1 the x rows (D = kXD; planes [kXD][T][H] in xdig); the metadata goes to meta[t] for
+// x rows and meta[T + e] for router rows. The router rows come first so that their longer
+// digit work starts with the launch. grid = ceil((T+E)/4), block = 256.
+template <int RD, int DT>
+__device__ __forceinline__ void prep_row(const void* __restrict__ base, int r, int nrows, int H,
+                                         int lane, RowMeta* __restrict__ m_out,
+                                         int8_t* __restrict__ dig) {
+  const size_t off = (size_t)r * H;
+  const int nch = H / 512;                          // 8-element chunks per lane (<= kMaxCh)
+  float v[kMaxCh][8];                               // the whole row stays in registers
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    if (c >= nch) break;
+    load8<DT>(base, off + (size_t)(c * 64 + lane) * 8, v[c]);
+  }
+  double vmax = 0.0;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    if (c >= nch) break;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) vmax = fmax(vmax, (double)fabsf(v[c][j]));
+  }
+  vmax = wave_max_f64(vmax);
+  const int e = vmax > 0.0 ? ilogb(vmax) : 0;
+  const int sh = 8 * RD - 3 - e;
+  double dsum = 0.0, qmax = 0.0;
+  const size_t plane = (size_t)nrows * H;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    if (c >= nch) break;
+    double n8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const double y = ldexp((double)v[c][j], sh);  // exact
+      const double n = rint(y);                     // ties to even
+      dsum += fabs(y - n);
+      qmax = fmax(qmax, fabs(n));
+      n8[j] = n;
+    }
+    store_digits8<RD>(n8, dig + off + (size_t)(c * 64 + lane) * 8, plane);
+  }
+  dsum = wave_sum_f64(dsum);
+  qmax = wave_max_f64(qmax);
+  if (lane == 0) {
+    RowMeta m;
+    m.e = e;
+    m.pad = 0;
+    m.dsum = ldexp(dsum, -sh);
+    m.vmax = vmax;
+    m.qmax = ldexp(qmax, -sh);
+    *m_out = m;
+  }
+}
+
+template <int XDT, int WDT>
+__global__ __launch_bounds__(256) void k_router_prep(const void* __restrict__ xv,
+                                                     const void* __restrict__ w, int T, int H,
+                                                     int E, RowMeta* __restrict__ meta,
+                                                     int8_t* __restrict__ xdig,
+                                                     int8_t* __restrict__ wdig) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T + E) return;
+  if (row < E) prep_row<WDig<WDT>::D, WDT>(w, row, E, H, lane, meta + T + row, wdig);
+  else prep_row<kXD, XDT>(xv, row - E, T, H, lane, meta + (row - E), xdig);
+}
+
+// ------------------------------------------------------------------------------ digit GEMM --
+// Nothing moves across this: no memory access (a compiler memory barrier) and no instruction
+// (a scheduling barrier).
+__device__ __forceinline__ void fence_sched() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One wave recomputes logit (t, e) in double-double: lane l sums k = l, l+64, ... (every x*W
+// product is exact in f64), the partial sums meet in a butterfly; bound as logit_dd_recompute's.
+template <int XDT, int WDT>
+__device__ uint32_t wave_dd_logit(const void* __restrict__ xv, const void* __restrict__ w, int t,
+                                  int e, int H, double bval, int lane) {
+  DD d = {0.0, 0.0};
+  double xsq = 0.0, wsq = 0.0;
+  for (int k = lane; k < H; k += 64) {
+    const double xk = elt<XDT>(xv, (size_t)t * H + k);
+    const double wk = elt<WDT>(w, (size_t)e * H + k);
+    d = dd_add(d, DD{xk * wk, 0.0});
+    xsq = fma(xk, xk, xsq);
+    wsq = fma(wk, wk, wsq);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const DD p = {__shfl_xor(d.hi, o, 64), __shfl_xor(d.lo, o, 64)};
+    d = dd_add(d, p);
+    xsq += __shfl_xor(xsq, o, 64);
+    wsq += __shfl_xor(wsq, o, 64);
+  }
+  d = dd_add(d, DD{bval, 0.0});
+  const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
+  return round_bf16_dd(d, ddb);
+}
+
+// grid = 8 * nE * ceil(nT / 8) blocks (nT = ceil(T/64) token tiles, nE = ceil(E/64) expert
+// tiles), block = 256 (4 waves, 2 x 2 of 32 x 32). Blocks are dealt to the 8 XCDs round-robin;
+// the nE blocks of one token tile share an XCD, so its x rows are fetched into one L2.
+template <int XDT, int WDT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
+            const int8_t* __restrict__ xdig, const int8_t* __restrict__ wdig,
+            const RowMeta* __restrict__ meta, const float* __restrict__ bias, int T, int H, int E,
+            uint16_t* __restrict__ logits) {
+  constexpr int WD = WDig<WDT>::D;
+  constexpr int NL = kXD + WD - 1;                  // accumulator levels
+  __shared__ __attribute__((aligned(16))) int8_t sx[2][kXD][64 * kRS];
+  __shared__ __attribute__((aligned(16))) int8_t sw[2][WD][64 * kRS];
+  const int nT = (T + 63) / 64, nE = (E + 63) / 64;
+  const int b = blockIdx.x, xcd = b & 7, jb = b >> 3;
+  const int tt = xcd + 8 * (jb / nE), et = jb % nE;
+  if (tt >= nT) return;
+  const int t0 = tt * 64, e0 = et * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const RowMeta* wmeta = meta + T;
+
+  // staging role: row tid/4 of the tile, 16 bytes at 16 * (tid % 4) of each plane's stage slice
+  const int srow = tid >> 2, sseg = tid & 3;
+  const int8_t* xsrc = xdig + (size_t)min(t0 + srow, T - 1) * H + 16 * sseg;
+  const int8_t* wsrc = wdig + (size_t)min(e0 + srow, E - 1) * H + 16 * sseg;
+  const size_t xplane = (size_t)T * H, wplane = (size_t)E * H;
+  const int soff = srow * kRS + 16 * sseg;
+
+  // one register set: stage s + 1's digits (loaded during stage s - 1) go into the idle LDS
+  // buffer at the start of stage s, the same registers then take stage s + 2's loads, then the
+  // MFMAs of stage s run; one barrier per stage
+  u32x4 xq[kXD], wq[WD];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int a = 0; a < kXD; ++a) xq[a] = *reinterpret_cast<const u32x4*>(xsrc + a * xplane + k0);
+#pragma unroll
+    for (int a = 0; a < WD; ++a) wq[a] = *reinterpret_cast<const u32x4*>(wsrc + a * wplane + k0);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int a = 0; a < kXD; ++a) *reinterpret_cast<u32x4*>(&sx[buf][a][soff]) = xq[a];
+#pragma unroll
+    for (int a = 0; a < WD; ++a) *reinterpret_cast<u32x4*>(&sw[buf][a][soff]) = wq[a];
+  };
+
+  v16i acc[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) acc[l] = (v16i){};
+  const int ar = (wm * 32 + (lane & 31)) * kRS + 16 * (lane >> 5);
+  const int br = (wn * 32 + (lane & 31)) * kRS + 16 * (lane >> 5);
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < kKC; ks += 32) {
+      v4i a[kXD], bq[WD];
+#pragma unroll
+      for (int p = 0; p < kXD; ++p) a[p] = *reinterpret_cast<const v4i*>(&sx[buf][p][ar + ks]);
+#pragma unroll
+      for (int q = 0; q < WD; ++q) bq[q] = *reinterpret_cast<const v4i*>(&sw[buf][q][br + ks]);
+#pragma unroll
+      for (int p = 0; p < kXD; ++p)
+#pragma unroll
+        for (int q = 0; q < WD; ++q)
+          acc[p + q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[p], bq[q], acc[p + q], 0, 0, 0);
+    }
+  };
+  const int nst = H / kKC;
+  gload(0);
+  lstore(0);
+  if (nst > 1) gload(kKC);
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nst) lstore(buf ^ 1);
+    if (s + 2 < nst) gload((s + 2) * kKC);
+    fence_sched();
+    mma(buf);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds expert e0 + 32 wn + lane % 32 for 16 tokens
+  const int e = e0 + wn * 32 + (lane & 31);
+  const bool e_ok = e < E;
+  const RowMeta mw = wmeta[min(e, E - 1)];
+  const double bval = (bias && e_ok) ? (double)bias[e] : 0.0;
+  uint32_t fail = 0;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = t0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    if (t >= T || !e_ok) continue;
+    const RowMeta mx = meta[t];
+    double v = (double)acc[NL - 1][r], cb = 0.0;
+#pragma unroll
+    for (int l = NL - 2; l >= 0; --l) {
+      v = fma(v, 0x1p-8, (double)acc[l][r]);
+      cb += fabs(v);
+    }
+    const int sc = mx.e + mw.e - 10;
+    const double s = ldexp(v, sc) + bval;
+    const double bound = (mx.dsum * mw.qmax + mx.vmax * mw.dsum) * (1.0 + 0x1p-32) +
+                         ldexp(cb, sc) * 0x1p-52 + fabs(s) * 0x1p-52;
+    uint32_t bits;
+    if (round_bf16_certified(s, bound, &bits)) logits[(size_t)t * E + e] = (uint16_t)bits;
+    else fail |= 1u << r;
+  }
+  // uncertified logits: the wave recomputes each one together (rare)
+  for (;;) {
+    const uint64_t m = __ballot(fail != 0);
+    if (m == 0) break;
+    const int l0 = __builtin_ctzll(m);
+    const int r0 = __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)fail, l0));
+    const int t = t0 + wm * 32 + 8 * (r0 >> 2) + 4 * (l0 >> 5) + (r0 & 3);
+    const int ee = e0 + wn * 32 + (l0 & 31);
+    const double bv = bias ? (double)bias[ee] : 0.0;
+    const uint32_t bits = wave_dd_logit<XDT, WDT>(xv, w, t, ee, H, bv, lane);
+    if (lane == l0) {
+      logits[(size_t)t * E + ee] = (uint16_t)bits;
+      fail &= ~(1u << r0);
+    }
+  }
+}
+
+// scratch: RowMeta[T + E] | x digit planes [kXD][T][H] | router digit planes [WD][E][H]
+inline size_t meta_bytes(int T, int E) { return ((size_t)(T + E) * sizeof(RowMeta) + 255) / 256 * 256; }
+inline size_t xdig_bytes(int T, int H) { return ((size_t)kXD * T * H + 255) / 256 * 256; }
+
+template <int XDT, int WDT>
+void launch(const void* x, const void* w, const float* bias, int T, int H, int E, uint16_t* logits,
+            void* scratch, hipStream_t st) {
+  RowMeta* meta = reinterpret_cast<RowMeta*>(scratch);
+  int8_t* xdig = reinterpret_cast<int8_t*>(scratch) + meta_bytes(T, E);
+  int8_t* wdig = xdig + xdig_bytes(T, H);
+  hipLaunchKernelGGL((k_router_prep<XDT, WDT>), dim3((T + E + 3) / 4), dim3(256), 0, st, x, w, T, H,
+                     E, meta, xdig, wdig);
+  const int nT = (T + 63) / 64, nE = (E + 63) / 64;
+  hipLaunchKernelGGL((k_router_i8<XDT, WDT>), dim3(8 * nE * ((nT + 7) / 8)), dim3(256), 0, st, x, w,
+                     xdig, wdig, meta, bias, T, H, E, logits);
+}
+
+}  // namespace ri8
+}  // namespace moe
+
+using namespace moe;
+
+size_t moe_router_i8_scratch_bytes(int T, int H, int E) {
+  return ri8::meta_bytes(T, E) + ri8::xdig_bytes(T, H) + ((size_t)5 * E * H + 255) / 256 * 256;
+}
+
+bool moe_router_i8_supported(int T, int H, int E) {
+  return T > 256 && H % 512 == 0 && H <= 512 * ri8::kMaxCh && E >= 1;
+}
+
+int moe_launch_router_logits_i8(const void* x, int x_dtype, const void* w, int w_dtype,
+                                const float* bias, int T, int H, int E, uint16_t* logits,
+                                void* scratch, hipStream_t st) {
+  if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32)
+    ri8::launch<MOE_DT_F32, MOE_DT_F32>(x, w, bias, T, H, E, logits, scratch, st);
+  else if (x_dtype == MOE_DT_F32)
+    ri8::launch<MOE_DT_F32, MOE_DT_BF16>(x, w, bias, T, H, E, logits, scratch, st);
+  else if (w_dtype == MOE_DT_F32)
+    ri8::launch<MOE_DT_BF16, MOE_DT_F32>(x, w, bias, T, H, E, logits, scratch, st);
+  else
+    ri8::launch<MOE_DT_BF16, MOE_DT_BF16>(x, w, bias, T, H, E, logits, scratch, st);
+  return moe_check_launch("router_logits_i8");
+}

@@ -106,3 +106,72 @@ def test_router_heap_select_branch(pkg, dev):
     w = torch.zeros(256, 2048, dtype=torch.bfloat16)
     r, got = _check_route(pkg, x.to(dev), w.to(dev), bias.to(dev))
     assert got[0].tolist() == ids_model
+
+
+def _router_f64_path(pkg, x, w, bias, K=8):
+    """moe_router_topk with the logits given and no workspace: R1 stays on the f64 matrix cores."""
+    L = pkg._lib
+    T, H = x.shape
+    E = w.shape[0]
+    dev = x.device
+    lg = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
+    ids = torch.empty(T, K, dtype=torch.int32, device=dev)
+    wf = torch.empty(T, K, dtype=torch.float32, device=dev)
+    wb = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+    xdt = L.MOE_DT_F32 if x.dtype == torch.float32 else L.MOE_DT_BF16
+    wdt = L.MOE_DT_F32 if w.dtype == torch.float32 else L.MOE_DT_BF16
+    p = lambda t: None if t is None else t.data_ptr()
+    rc = L.lib.moe_router_topk(p(x), xdt, p(w), wdt, p(bias), T, H, E, K, p(lg), None, p(ids),
+                               p(wf), p(wb), None, 0, torch.cuda.current_stream(dev).cuda_stream)
+    assert rc == 0
+    return lg, ids
+
+
+@pytest.mark.parametrize("xdt,wdt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.bfloat16), (torch.float32, torch.float32)])
+def test_router_int8_and_f64_matrix_cores_same_bits(pkg, dev, xdt, wdt):
+    """R1 at T = 4096 on the int8 matrix cores (digit-split, certified) and on the f64 ones: the
+    same logits and ids bit for bit, for every x / router width, with a bias."""
+    g = torch.Generator().manual_seed(4242)
+    x = torch.randn(4096, 2048, generator=g).to(xdt).to(dev)
+    w = (torch.randn(256, 2048, generator=g) * 0.02).to(wdt).to(dev)
+    bias = (torch.randn(256, generator=g) * 0.1).to(dev)
+    r = pkg.abi.router_topk(x, w, 8, bias)
+    lg, ids = _router_f64_path(pkg, x, w, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(r["router_logits"].view(torch.int16), lg.view(torch.int16)), \
+        f"{(r['router_logits'] != lg).sum().item()} logits differ"
+    assert torch.equal(r["topk_ids"], ids)
+
+
+@pytest.mark.parametrize("T,E,xdt,wdt", [(333, 200, torch.bfloat16, torch.float32),
+                                         (257, 24, torch.float32, torch.bfloat16),
+                                         (700, 256, torch.bfloat16, torch.bfloat16)])
+def test_router_int8_ragged_and_wide_range(pkg, dev, T, E, xdt, wdt):
+    """The int8 R1 on partial 64-token / 64-expert tiles, with rows whose elements span 2^-40 ..
+    2^3 (so some fall below the digit grid and the certificate, or the double-double recompute,
+    must carry them), against the correctly rounded oracle."""
+    g = torch.Generator().manual_seed(T + 7 * E)
+    x = torch.randn(T, 2048, generator=g) * torch.exp2(-40 * torch.rand(T, 2048, generator=g))
+    w = torch.randn(E, 2048, generator=g) * 0.02 * torch.exp2(-30 * torch.rand(E, 2048, generator=g))
+    x[::5, ::3] *= 8.0
+    bias = torch.randn(E, generator=g) * 0.1
+    x, w = x.to(xdt), w.to(wdt)
+    _check_route(pkg, x.to(dev), w.to(dev), bias.to(dev))
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_router_int8_midpoints_round_to_even(pkg, dev, xdt):
+    """Exact bf16 midpoints and values 2^-40 above them at T = 300 (the int8 R1): the digit sums
+    land on the midpoint, the certificate refuses, and the wave's double-double recompute decides
+    (ties to even; the 2^-40 element, below the x digit grid, rounds up)."""
+    T, H = 300, 2048
+    x = torch.zeros(T, H)
+    x[0::2, 0], x[0::2, 1] = 1.0, 2.0 ** -8
+    x[1::2, 0], x[1::2, 1], x[1::2, 2] = 1.0, 2.0 ** -8, 2.0 ** -40
+    w = torch.zeros(256, H)
+    w[:, 0:3] = 1.0
+    r = pkg.abi.router_topk(x.to(xdt).to(dev), w.to(torch.bfloat16).to(dev), 8)
+    lg = r["router_logits"].cpu().float()
+    assert (lg[0::2] == 1.0).all()
+    assert (lg[1::2] == 1.0 + 2.0 ** -7).all()
