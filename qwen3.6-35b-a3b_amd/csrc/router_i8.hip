@@ -23,9 +23,10 @@
 //   * A logit the bound does not certify is recomputed by its wave in double-double (the whole
 //     wave sums the row in parallel) and rounded from that, ties to even on the midpoint itself.
 //
-// Kernels: k_router_prep (one wave per row: the row metadata for x rows and router rows, and the
-// router rows' digit planes), then k_router_i8 (64 tokens x 64 experts per block; x rows are cut
-// into digits on the fly while staged into LDS, the router digits come from the prep).
+// Kernels: k_router_prep (one wave per row: the row metadata and digit planes of the router rows
+// and of the x rows), then k_router_i8 (64 tokens x 64 experts per block of 8 waves: two waves per
+// 32 x 32 tile, each summing one k half of every 64-wide LDS stage, their int32 partial sums
+// added through LDS at the end; digit planes staged global -> registers -> LDS one stage ahead).
 #include <type_traits>
 
 #include "common.h"
@@ -243,7 +244,7 @@ __device__ uint32_t wave_dd_logit(const void* __restrict__ xv, const void* __res
 // tiles), block = 256 (4 waves, 2 x 2 of 32 x 32). Blocks are dealt to the 8 XCDs round-robin;
 // the nE blocks of one token tile share an XCD, so its x rows are fetched into one L2.
 template <int XDT, int WDT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
             const int8_t* __restrict__ xdig, const int8_t* __restrict__ wdig,
             const RowMeta* __restrict__ meta, const float* __restrict__ bias, int T, int H, int E,
@@ -257,32 +258,44 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   const int tt = xcd + 8 * (jb / nE), et = jb % nE;
   if (tt >= nT) return;
   const int t0 = tt * 64, e0 = et * 64;
+  // 8 waves: wave (kh, q) owns the 32 x 32 tile q (2 x 2) for the k half kh of every stage
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int kh = wv >> 2, q4 = wv & 3;
+  const int wm = q4 >> 1, wn = q4 & 1;
   const RowMeta* wmeta = meta + T;
 
-  // staging role: row tid/4 of the tile, 16 bytes at 16 * (tid % 4) of each plane's stage slice
-  const int srow = tid >> 2, sseg = tid & 3;
-  const int8_t* xsrc = xdig + (size_t)min(t0 + srow, T - 1) * H + 16 * sseg;
-  const int8_t* wsrc = wdig + (size_t)min(e0 + srow, E - 1) * H + 16 * sseg;
-  const size_t xplane = (size_t)T * H, wplane = (size_t)E * H;
+  // staging role: waves 0-3 copy the x planes, waves 4-7 the router planes; row (tid%256)/4 of
+  // the tile, 16 bytes at 16 * (tid % 4) of each plane's stage slice
+  const int st = tid & 255;
+  const int srow = st >> 2, sseg = st & 3;
+  const bool stage_x = kh == 0;
+  const int8_t* src = stage_x ? xdig + (size_t)min(t0 + srow, T - 1) * H + 16 * sseg
+                              : wdig + (size_t)min(e0 + srow, E - 1) * H + 16 * sseg;
+  const size_t plane = stage_x ? (size_t)T * H : (size_t)E * H;
   const int soff = srow * kRS + 16 * sseg;
 
   // one register set: stage s + 1's digits (loaded during stage s - 1) go into the idle LDS
   // buffer at the start of stage s, the same registers then take stage s + 2's loads, then the
   // MFMAs of stage s run; one barrier per stage
-  u32x4 xq[kXD], wq[WD];
+  constexpr int NP = WD > kXD ? WD : kXD;
+  u32x4 q[NP];
   auto gload = [&](int k0) {
+    if (stage_x) {
 #pragma unroll
-    for (int a = 0; a < kXD; ++a) xq[a] = *reinterpret_cast<const u32x4*>(xsrc + a * xplane + k0);
+      for (int a = 0; a < kXD; ++a) q[a] = *reinterpret_cast<const u32x4*>(src + a * plane + k0);
+    } else {
 #pragma unroll
-    for (int a = 0; a < WD; ++a) wq[a] = *reinterpret_cast<const u32x4*>(wsrc + a * wplane + k0);
+      for (int a = 0; a < WD; ++a) q[a] = *reinterpret_cast<const u32x4*>(src + a * plane + k0);
+    }
   };
   auto lstore = [&](int buf) {
+    if (stage_x) {
 #pragma unroll
-    for (int a = 0; a < kXD; ++a) *reinterpret_cast<u32x4*>(&sx[buf][a][soff]) = xq[a];
+      for (int a = 0; a < kXD; ++a) *reinterpret_cast<u32x4*>(&sx[buf][a][soff]) = q[a];
+    } else {
 #pragma unroll
-    for (int a = 0; a < WD; ++a) *reinterpret_cast<u32x4*>(&sw[buf][a][soff]) = wq[a];
+      for (int a = 0; a < WD; ++a) *reinterpret_cast<u32x4*>(&sw[buf][a][soff]) = q[a];
+    }
   };
 
   v16i acc[NL];
@@ -291,8 +304,8 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   const int ar = (wm * 32 + (lane & 31)) * kRS + 16 * (lane >> 5);
   const int br = (wn * 32 + (lane & 31)) * kRS + 16 * (lane >> 5);
   auto mma = [&](int buf) {
-#pragma unroll
-    for (int ks = 0; ks < kKC; ks += 32) {
+    {
+      const int ks = 32 * kh;
       v4i a[kXD], bq[WD];
 #pragma unroll
       for (int p = 0; p < kXD; ++p) a[p] = *reinterpret_cast<const v4i*>(&sx[buf][p][ar + ks]);
@@ -319,7 +332,30 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
     __syncthreads();
   }
 
-  // epilogue: lane holds expert e0 + 32 wn + lane % 32 for 16 tokens
+  // the two k halves meet: wave (kh, q) keeps registers 8 kh .. 8 kh + 7 of every level and
+  // takes the partner's partial sums for them through LDS (integer adds, exact)
+  int32_t* xch = reinterpret_cast<int32_t*>(&sx[0][0][0]);
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    if (kh == 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xch[((q4 * 2 + 0) * 8 + j) * 64 + lane] = acc[l][8 + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xch[((q4 * 2 + 1) * 8 + j) * 64 + lane] = acc[l][j];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[l][j] += xch[((q4 * 2 + 1) * 8 + j) * 64 + lane];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[l][8 + j] += xch[((q4 * 2 + 0) * 8 + j) * 64 + lane];
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds expert e0 + 32 wn + lane % 32 for the 8 tokens of its registers
   const int e = e0 + wn * 32 + (lane & 31);
   const bool e_ok = e < E;
   const RowMeta mw = wmeta[min(e, E - 1)];
@@ -327,6 +363,7 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   uint32_t fail = 0;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
+    if ((r >> 3) != kh) continue;
     const int t = t0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     if (t >= T || !e_ok) continue;
     const RowMeta mx = meta[t];
@@ -374,7 +411,7 @@ void launch(const void* x, const void* w, const float* bias, int T, int H, int E
   hipLaunchKernelGGL((k_router_prep<XDT, WDT>), dim3((T + E + 3) / 4), dim3(256), 0, st, x, w, T, H,
                      E, meta, xdig, wdig);
   const int nT = (T + 63) / 64, nE = (E + 63) / 64;
-  hipLaunchKernelGGL((k_router_i8<XDT, WDT>), dim3(8 * nE * ((nT + 7) / 8)), dim3(256), 0, st, x, w,
+  hipLaunchKernelGGL((k_router_i8<XDT, WDT>), dim3(8 * nE * ((nT + 7) / 8)), dim3(512), 0, st, x, w,
                      xdig, wdig, meta, bias, T, H, E, logits);
 }
 
