@@ -447,6 +447,9 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     return moe_launch_decode_fused(L, st);
   }
   uint16_t* logits = logits_bf16 ? reinterpret_cast<uint16_t*>(logits_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
+  // torch's slot order among equal probabilities only matters to a caller that reads the routing
+  // (ids, weights) or the per-slot expert rows
+  const bool exact_order = topk_ids || topk_w_f32 || topk_w_bf16 || expert_raw;
   int32_t* ids = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w.take((size_t)P * 4));
   float* wf = topk_w_f32 ? topk_w_f32 : reinterpret_cast<float*>(w.take((size_t)P * 4));
   uint16_t* wb = topk_w_bf16 ? reinterpret_cast<uint16_t*>(topk_w_bf16) : reinterpret_cast<uint16_t*>(w.take((size_t)P * 2));
@@ -469,7 +472,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   }
   if (T < kForkMinT) {
     MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, nullptr, 0, st));
-    MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st));
+    MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order));
     MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
     MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
     MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
@@ -495,7 +498,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);
   void* rscr = wr.take(rsb);
   if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, rscr, rsb, st);
-  if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st);
+  if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order);
   if (rc == MOE_OK) rc = moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st);
   if (rc == MOE_OK)
     rc = experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,

@@ -26,7 +26,8 @@ int moe_launch_router_logits_i8(const void* x, int x_dtype, const void* w, int w
                                 const float* bias, int T, int H, int E, uint16_t* logits,
                                 void* scratch, hipStream_t st);
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
-                          float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st);
+                          float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st,
+                          bool exact_order = true);
 
 // sort / permute; ws must hold moe_sort_ws_bytes(P, E) bytes
 size_t moe_sort_ws_bytes(int P, int E);

@@ -360,12 +360,16 @@ __global__ __launch_bounds__(256) void k_router_logits_gemm(
   }
 }
 
+// exact_order = 0 (the block forward when no routing output is asked for) accepts the fast path's
+// slot order when equal probabilities sit only inside the top K: the same experts and weights, and
+// the combine sums in ascending expert id, so the block output is the same bits.
 __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ logits, int T,
                                                    int E, int K, float* __restrict__ probs,
                                                    int32_t* __restrict__ ids,
                                                    float* __restrict__ w_f32,
                                                    uint16_t* __restrict__ w_bf16,
-                                                   int32_t* __restrict__ heap_flag) {
+                                                   int32_t* __restrict__ heap_flag,
+                                                   int exact_order) {
   __shared__ TopkLds s;
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
@@ -378,7 +382,7 @@ __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ 
       if (64 * j + lane < E) probs[(size_t)t * E + 64 * j + lane] = p[j];
   }
   route_select_and_write(s, p, E, K, lane, ids + (size_t)t * K, w_f32 + (size_t)t * K,
-                         w_bf16 + (size_t)t * K, heap_flag);
+                         w_bf16 + (size_t)t * K, heap_flag, exact_order != 0);
 }
 
 }  // namespace moe
@@ -417,8 +421,9 @@ int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dt
 }
 
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
-                          float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st) {
+                          float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st,
+                          bool exact_order) {
   hipLaunchKernelGGL(k_route_topk, dim3(T), dim3(64), 0, st, logits, T, E, K, probs, ids, w_f32,
-                     w_bf16, heap_flag);
+                     w_bf16, heap_flag, exact_order ? 1 : 0);
   return moe_check_launch("route_topk");
 }

@@ -325,3 +325,25 @@ def _graph_replays_match(pkg, lw, x):
         other = pkg.abi.block_forward(x, lw)["combined_out"]
         torch.cuda.synchronize()
         assert torch.equal(other, want), rep
+
+
+@pytest.mark.parametrize("T", [7, 300])
+def test_block_output_independent_of_tie_slot_order(pkg, layer_c0, dev, T):
+    """Router rows in equal pairs, so most tokens have equal probabilities inside their top 8.
+    Without routing outputs the block forward keeps the fast top-k's slot order among them; asked
+    for ids and per-slot expert rows it replays torch's order. The combine sums in ascending expert
+    id with the same weights, so the block output is the same bits; the replayed ids are torch's."""
+    import dataclasses
+    from oracle import moe_oracle as O
+    lw, _ = layer_c0
+    g = torch.Generator().manual_seed(97 + T)
+    half = (torch.randn(128, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    router = torch.cat([half, half])[torch.randperm(256, generator=g)].contiguous().to(dev)
+    lt = dataclasses.replace(lw, router=router)
+    x = pkg.synth.make_input(T, seed=97 + T, device=dev, dtype=torch.bfloat16)
+    a = pkg.abi.block_forward(x, lt)
+    b = pkg.abi.block_forward(x, lt, stages={"topk_ids", "expert_raw"})
+    torch.cuda.synchronize()
+    assert torch.equal(a["combined_out"], b["combined_out"])
+    ref = O.route(x.cpu(), router.cpu(), 8, None)
+    assert torch.equal(b["topk_ids"].cpu().long(), ref["topk_ids"])
