@@ -357,12 +357,15 @@ __device__ __forceinline__ int wave_topk_fast(const float* p, int E, int K, int 
 // R2: softmax over E bf16 logits in f32 (max-subtracted, sum, multiply by the reciprocal — the
 // same form as torch's CPU kernel); lane holds positions lane + 64j.
 __device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lane, float* p) {
+  // clamped loads, all four in flight at once (guarded loads would each wait for the last)
+  uint32_t raw[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) raw[j] = lg[min(64 * j + lane, E - 1)];
   float lv[4];
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    lv[j] = pos < E ? bf16_to_f32(lg[pos]) : -INFINITY;
+    lv[j] = (64 * j + lane) < E ? bf16_to_f32(raw[j]) : -INFINITY;
     m = fmaxf(m, lv[j]);
   }
   m = wave_max_f32(m);
