@@ -62,8 +62,53 @@ __device__ __forceinline__ void w_load4(const void* w, size_t i, double* o) {
 }
 
 // ----------------------------------------------------------------- R1, small T (T <= 256) -------
-// One wave per (expert row, 8-token slice): the row (H bf16) is read once per slice and applied to
-// each of the slice's tokens. grid = (ceil(E/4), ceil(T/8)), block = 256 (4 waves).
+// One wave per (expert row, 8-token slice): the row (H <= 2048) is loaded once into registers,
+// then the slice's tokens go kGemvU at a time with every x load of the group issued before the
+// first use, and the group's wave reductions (dot, |x|^2) interleaved. grid = (ceil(E/4), ceil(T/8)),
+// block = 256 (4 waves). Each logit: f64 dot (products exact), certified bf16 rounding, the
+// double-double recompute where the certificate does not hold.
+constexpr int kGemvCh = 4;                            // 512-wide chunks: H <= 2048
+constexpr int kGemvU = 2;                             // tokens whose loads go out together
+
+template <int DT>
+__device__ __forceinline__ void load8f(const void* p, size_t i, float* o) {
+  if constexpr (DT == MOE_DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = bf16_to_f32(w[k] & 0xFFFFu);
+      o[2 * k + 1] = bf16_to_f32(w[k] >> 16);
+    }
+  }
+}
+
+template <int XDT, int WDT>
+__device__ __noinline__ uint32_t gemv_dd_logit(const void* __restrict__ xv, const void* __restrict__ w,
+                                               int t, int e, int H, int lane, double bval,
+                                               double xsq, double wsq) {
+  // double-double recompute, error-free per lane, then across the wave
+  DD d = {0.0, 0.0};
+  for (int k = lane; k < H; k += 64) {
+    const double xk = (XDT == MOE_DT_F32)
+                          ? (double)reinterpret_cast<const float*>(xv)[(size_t)t * H + k]
+                          : (double)bf16_to_f32(reinterpret_cast<const uint16_t*>(xv)[(size_t)t * H + k]);
+    d = dd_add(d, DD{xk * w_at<WDT>(w, (size_t)e * H + k), 0.0});   // product exact in f64
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    DD other = {__shfl_xor(d.hi, o, 64), __shfl_xor(d.lo, o, 64)};
+    d = dd_add(d, other);
+  }
+  d = dd_add(d, DD{bval, 0.0});
+  const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
+  return round_bf16_dd(d, ddb);
+}
+
 template <int XDT, int WDT>
 __global__ __launch_bounds__(256) void k_router_logits_gemv(
     const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias,
@@ -73,76 +118,63 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
   if (e >= E) return;
   const size_t wr = (size_t)e * H;                    // the row's first element
   const int nchunk = H / 512;                         // 8 weights per lane per chunk
+  float wf[kGemvCh][8];
+#pragma unroll
+  for (int c = 0; c < kGemvCh; ++c)
+    if (c < nchunk) load8f<WDT>(w, wr + c * 512 + lane * 8, wf[c]);
   double wsq = 0.0;
-  for (int c = 0; c < nchunk; ++c) {
-    double wd[8];
-    w_load8<WDT>(w, wr + c * 512 + lane * 8, wd);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wsq = fma(wd[i], wd[i], wsq);
-  }
+  for (int c = 0; c < kGemvCh; ++c)
+    if (c < nchunk) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wsq = fma((double)wf[c][i], (double)wf[c][i], wsq);
+    }
   wsq = wave_sum_f64(wsq);
-  const int t_end = min(T, 8 * (int)blockIdx.y + 8);
-  for (int t = 8 * blockIdx.y; t < t_end; ++t) {
-    double acc = 0.0, xsq = 0.0;
-    for (int c = 0; c < nchunk; ++c) {
-      double wd[8];
-      w_load8<WDT>(w, wr + c * 512 + lane * 8, wd);
-      float xf[8];
-      if (XDT == MOE_DT_F32) {
-        const float* xp = reinterpret_cast<const float*>(xv) + (size_t)t * H + c * 512 + lane * 8;
-        float4 a = *reinterpret_cast<const float4*>(xp);
-        float4 b = *reinterpret_cast<const float4*>(xp + 4);
-        xf[0] = a.x; xf[1] = a.y; xf[2] = a.z; xf[3] = a.w;
-        xf[4] = b.x; xf[5] = b.y; xf[6] = b.z; xf[7] = b.w;
-      } else {
-        const uint16_t* xp = reinterpret_cast<const uint16_t*>(xv) + (size_t)t * H + c * 512 + lane * 8;
-        uint4 a = *reinterpret_cast<const uint4*>(xp);
-        const uint32_t aa[4] = {a.x, a.y, a.z, a.w};
+  const double bval = bias ? (double)bias[e] : 0.0;
+  const int t0 = 8 * (int)blockIdx.y, t_end = min(T, t0 + 8);
+  for (int tb = t0; tb < t_end; tb += kGemvU) {
+    float xf[kGemvU][kGemvCh][8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          xf[2 * i] = bf16_to_f32(aa[i] & 0xFFFFu);
-          xf[2 * i + 1] = bf16_to_f32(aa[i] >> 16);
+    for (int u = 0; u < kGemvU; ++u) {
+      const int t = min(tb + u, t_end - 1);           // a clamped token is computed, not stored
+#pragma unroll
+      for (int c = 0; c < kGemvCh; ++c)
+        if (c < nchunk) load8f<XDT>(xv, (size_t)t * H + c * 512 + lane * 8, xf[u][c]);
+    }
+    double acc[kGemvU], xsq[kGemvU];
+#pragma unroll
+    for (int u = 0; u < kGemvU; ++u) {
+      acc[u] = 0.0;
+      xsq[u] = 0.0;
+#pragma unroll
+      for (int c = 0; c < kGemvCh; ++c)
+        if (c < nchunk) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            acc[u] = fma((double)xf[u][c][i], (double)wf[c][i], acc[u]);
+            xsq[u] = fma((double)xf[u][c][i], (double)xf[u][c][i], xsq[u]);
+          }
         }
-      }
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        acc = fma((double)xf[i], wd[i], acc);
-        xsq = fma((double)xf[i], (double)xf[i], xsq);
+    for (int o = 32; o >= 1; o >>= 1) {
+#pragma unroll
+      for (int u = 0; u < kGemvU; ++u) {
+        acc[u] += __shfl_xor(acc[u], o, 64);
+        xsq[u] += __shfl_xor(xsq[u], o, 64);
       }
     }
-    acc = wave_sum_f64(acc);
-    xsq = wave_sum_f64(xsq);
-    double bval = bias ? (double)bias[e] : 0.0;
-    const double s = acc + bval;
-    const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
-    uint32_t bits;
-    bool ok = round_bf16_certified(s, bound, &bits);
-    if (!ok) {
-      // double-double recompute, error-free per lane, then across the wave
-      DD d = {0.0, 0.0};
-      for (int c = 0; c < nchunk; ++c) {
-        double wd[8];
-        w_load8<WDT>(w, wr + c * 512 + lane * 8, wd);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          double xv_;
-          if (XDT == MOE_DT_F32)
-            xv_ = reinterpret_cast<const float*>(xv)[(size_t)t * H + c * 512 + lane * 8 + i];
-          else
-            xv_ = bf16_to_f32(reinterpret_cast<const uint16_t*>(xv)[(size_t)t * H + c * 512 + lane * 8 + i]);
-          d = dd_add(d, DD{xv_ * wd[i], 0.0});         // product exact in f64
-        }
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        DD other = {__shfl_xor(d.hi, o, 64), __shfl_xor(d.lo, o, 64)};
-        d = dd_add(d, other);
-      }
-      d = dd_add(d, DD{bval, 0.0});
-      const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
-      bits = round_bf16_dd(d, ddb);
+    for (int u = 0; u < kGemvU; ++u) {
+      const int t = tb + u;
+      if (t >= t_end) break;
+      const double s = acc[u] + bval;
+      const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xsq[u]) * sqrt(wsq) + fabs(bval));
+      uint32_t bits;
+      if (!round_bf16_certified(s, bound, &bits))
+        bits = gemv_dd_logit<XDT, WDT>(xv, w, t, e, H, lane, bval, xsq[u], wsq);
+      if (lane == 0) logits[(size_t)t * E + e] = (uint16_t)bits;
     }
-    if (lane == 0) logits[(size_t)t * E + e] = (uint16_t)bits;
   }
 }
 
@@ -392,7 +424,7 @@ using namespace moe;
 template <int XDT, int WDT>
 static void launch_router_logits(const void* x, const void* w, const float* bias, int T, int H,
                                  int E, uint16_t* logits, hipStream_t st) {
-  if (T <= 256) {
+  if (T <= 256 && H <= 512 * kGemvCh) {
     hipLaunchKernelGGL((k_router_logits_gemv<XDT, WDT>), dim3((E + 3) / 4, (T + 7) / 8), dim3(256), 0, st,
                        x, w, bias, T, H, E, logits);
   } else if (H % 64 == 0) {
