@@ -2,8 +2,8 @@
 // 448-452): pairs p = t*K + k ordered by expert id, equal ids in ascending p — the permutation
 // torch.argsort(ids.flatten(), stable=True) returns. Integer work only, so bit-exact by design.
 //
-// P <= 64 (decode): one wave ranks every pair directly.
-// Otherwise: per-chunk histograms -> one-block scan -> per-chunk stable scatter, where ranks
+// P <= 64 (decode): one wave ranks every pair directly. P <= 1024: one block runs the three
+// phases below. Otherwise: per-chunk histograms -> one-block scan -> per-chunk stable scatter, where ranks
 // inside a 256-pair round come from wave-level id matching (8 ballots on the id bits) and a
 // per-wave count table, so no atomics decide any position.
 #include "common.h"
@@ -122,17 +122,14 @@ __global__ __launch_bounds__(256) void k_sort_scan(int32_t* __restrict__ hist, i
   if (e == 0) hit_list[0] = hsum;
 }
 
-// phase 3: stable scatter of each chunk
-__global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int P,
-                                                      int E, const int32_t* __restrict__ start,
-                                                      int32_t* __restrict__ sorted_pairs,
-                                                      int32_t* __restrict__ pair_pos) {
-  __shared__ int run[256];
-  __shared__ int wcnt[4][256];
+// Stable scatter of the pairs [base, base + kChunk) given the start position of the chunk's pairs
+// of every expert (start_row[e]): ranks inside a 256-pair round come from wave-level id matching
+// and per-wave counts, run[e] carries them across rounds. run (LDS, 256 ints) must be zero.
+__device__ void scatter_chunk(const int32_t* __restrict__ ids, int P, int E, int base,
+                              const int32_t* start_row, int32_t* __restrict__ sorted_pairs,
+                              int32_t* __restrict__ pair_pos, int* run, int (*wcnt)[256]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < 256; i += 256) run[i] = 0;
   const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  const int base = blockIdx.x * kChunk;
   for (int r = 0; r < kChunk; r += 256) {
     for (int i = tid; i < 4 * 256; i += 256) (&wcnt[0][0])[i] = 0;
     __syncthreads();
@@ -152,11 +149,10 @@ __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict_
     const bool leader = valid && rank_w == 0;
     if (leader) wcnt[wave][e] = __popcll(peers);
     __syncthreads();
-    int dest = 0;
     if (valid) {
       int before = 0;
       for (int w2 = 0; w2 < wave; ++w2) before += wcnt[w2][e];
-      dest = start[(size_t)blockIdx.x * E + e] + run[e] + before + rank_w;
+      const int dest = start_row[e] + run[e] + before + rank_w;
       sorted_pairs[dest] = p;
       pair_pos[p] = dest;
     }
@@ -164,6 +160,50 @@ __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict_
     if (leader) atomicAdd(&run[e], __popcll(peers));
     __syncthreads();
   }
+}
+
+// phase 3: stable scatter of each chunk
+__global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int P,
+                                                      int E, const int32_t* __restrict__ start,
+                                                      int32_t* __restrict__ sorted_pairs,
+                                                      int32_t* __restrict__ pair_pos) {
+  __shared__ int run[256];
+  __shared__ int wcnt[4][256];
+  run[threadIdx.x] = 0;
+  scatter_chunk(ids, P, E, blockIdx.x * kChunk, start + (size_t)blockIdx.x * E, sorted_pairs,
+                pair_pos, run, wcnt);
+}
+
+// 64 < P <= kChunk: the three phases in one block (histogram, scan, the one chunk's scatter), so
+// a small batch pays one launch instead of three; same positions as the three-kernel form.
+__global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ ids, int P, int E,
+                                                  int32_t* __restrict__ offsets,
+                                                  int32_t* __restrict__ sorted_pairs,
+                                                  int32_t* __restrict__ pair_pos,
+                                                  int32_t* __restrict__ hit_list) {
+  __shared__ int h[256], start[256], tmp[256], run[256];
+  __shared__ int wcnt[4][256];
+  const int e = threadIdx.x;
+  h[e] = 0;
+  run[e] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < P; i += 256) {
+    const int id = ids[i];
+    if (id >= 0 && id < E) atomicAdd(&h[id], 1);
+  }
+  __syncthreads();
+  const int tot = e < E ? h[e] : 0;
+  int tsum;
+  const int base = block_exclusive_scan(tot, tmp, &tsum);
+  start[e] = base;
+  if (e < E) offsets[e] = base;
+  if (e == 0) offsets[E] = tsum;   // == P unless out-of-range ids were dropped
+  int hsum;
+  const int hidx = block_exclusive_scan((e < E && tot > 0) ? 1 : 0, tmp, &hsum);
+  if (e < E && tot > 0) hit_list[1 + hidx] = e;
+  if (e == 0) hit_list[0] = hsum;
+  __syncthreads();
+  scatter_chunk(ids, P, E, 0, start, sorted_pairs, pair_pos, run, wcnt);
 }
 
 // MFMA work list: for every hit expert (ascending) ceil(n_e / BM) tiles of BM sorted rows.
@@ -206,6 +246,11 @@ int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t*
     hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(64), 0, st, ids, P, E, offsets, sorted_pairs,
                        pair_pos, hit_list);
     return moe_check_launch("sort_small");
+  }
+  if (P <= kChunk) {
+    hipLaunchKernelGGL(k_sort_one, dim3(1), dim3(256), 0, st, ids, P, E, offsets, sorted_pairs,
+                       pair_pos, hit_list);
+    return moe_check_launch("sort_one");
   }
   const int nchunks = (P + kChunk - 1) / kChunk;
   int32_t* hist = reinterpret_cast<int32_t*>(ws);

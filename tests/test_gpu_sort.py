@@ -14,8 +14,8 @@ def _ids(T, K, E, seed, zipf):
     return torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32)
 
 
-@pytest.mark.parametrize("T,zipf", [(1, False), (8, False), (9, True), (64, True), (300, False),
-                                    (4096, False), (16384, True)])
+@pytest.mark.parametrize("T,zipf", [(1, False), (8, False), (9, True), (64, True), (128, True),
+                                    (129, False), (300, False), (4096, False), (16384, True)])
 def test_sort_permute_matches_stable_argsort(pkg, dev, T, zipf):
     K, E = 8, 256
     ids = _ids(T, K, E, seed=T, zipf=zipf)
