@@ -178,6 +178,103 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
   }
 }
 
+// ------------------------------------------------- R1, 8 <= T <= 256: f64 MFMA, K split by wave --
+// Block = 8 waves on one tile of 16 tokens x 16 experts; wave w sums k in [w H/8, (w+1) H/8) with
+// v_mfma_f64_16x16x4f64 (A: lane l holds x[t0 + l%16][k], B: W[e0 + l%16][k], k = k0 + 4(l/16) + i
+// for the step's MFMA i; D: lane l, register j holds D[4j + l/16][l%16]). The 8 partial tiles are
+// added through LDS in wave order, so the f64 sum has a fixed order; any order stays inside the
+// certificate's bound 4(H+3) 2^-53 (|x||W_e| + |b|). Logits the bound does not settle are
+// recomputed in double-double by one wave. grid = (ceil(T/16), ceil(E/16)), block = 512.
+template <int XDT, int WDT>
+__global__ __launch_bounds__(512) void k_router_logits_small(
+    const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias,
+    int T, int H, int E, uint16_t* __restrict__ logits) {
+  using d4 = double __attribute__((ext_vector_type(4)));
+  __shared__ double s_d[8][256];
+  __shared__ double s_xsq[8][16], s_wsq[8][16];
+  __shared__ int s_fail[256];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+  const int tr = min(t0 + r, T - 1), er = min(e0 + r, E - 1);   // clamped rows: never stored
+  const int kw = H / 8, kb = wv * kw;
+  d4 acc = {0, 0, 0, 0}, acc2 = acc;                  // two chains of dependent MFMAs
+  double xsq = 0.0, wsq = 0.0;
+#pragma unroll 4
+  for (int k0 = kb; k0 < kb + kw; k0 += 64) {
+    double a[4][4], b[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const size_t kx = (size_t)k0 + 16 * u + 4 * g;
+      if constexpr (XDT == MOE_DT_F32) {
+        const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(xv) + (size_t)tr * H + kx);
+        a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(xv) + (size_t)tr * H + kx);
+        a[u][0] = bf16_to_f32(v.x & 0xFFFFu); a[u][1] = bf16_to_f32(v.x >> 16);
+        a[u][2] = bf16_to_f32(v.y & 0xFFFFu); a[u][3] = bf16_to_f32(v.y >> 16);
+      }
+      w_load4<WDT>(w, (size_t)er * H + kx, b[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (u & 1) acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u][i], b[u][i], acc2, 0, 0, 0);
+        else acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u][i], b[u][i], acc, 0, 0, 0);
+        xsq = fma(a[u][i], a[u][i], xsq);
+        wsq = fma(b[u][i], b[u][i], wsq);
+      }
+  }
+  // row norms over this wave's k range: sum the four lane groups
+  xsq += __shfl_xor(xsq, 16, 64);
+  xsq += __shfl_xor(xsq, 32, 64);
+  wsq += __shfl_xor(wsq, 16, 64);
+  wsq += __shfl_xor(wsq, 32, 64);
+  if (g == 0) { s_xsq[wv][r] = xsq; s_wsq[wv][r] = wsq; }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s_d[wv][16 * (4 * j + g) + r] = acc[j] + acc2[j];
+  __syncthreads();
+  if (tid < 256) {
+    const int tt = tid >> 4, ee = tid & 15;            // D[tt][ee]: token t0 + tt, expert e0 + ee
+    const int t = t0 + tt, e = e0 + ee;
+    int fail = 0;
+    if (t < T && e < E) {
+      double sum = 0.0, xs = 0.0, ws = 0.0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        sum += s_d[q][tid];
+        xs += s_xsq[q][tt];
+        ws += s_wsq[q][ee];
+      }
+      const double bval = bias ? (double)bias[e] : 0.0;
+      const double sv = sum + bval;
+      const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(xs) * sqrt(ws) + fabs(bval));
+      uint32_t bits;
+      if (round_bf16_certified(sv, bound, &bits)) logits[(size_t)t * E + e] = (uint16_t)bits;
+      else fail = 1;
+    }
+    s_fail[tid] = fail;
+  }
+  __syncthreads();
+  // uncertified logits (rare): wave 0 recomputes each in double-double
+  if (wv == 0) {
+    for (int base = 0; base < 256; base += 64) {
+      uint64_t m = __ballot(s_fail[base + lane] != 0);
+      while (m) {
+        const int idx = base + __builtin_ctzll(m);
+        m &= m - 1;
+        const int t = t0 + (idx >> 4), e = e0 + (idx & 15);
+        double xs = 0.0, ws = 0.0;
+        for (int q = 0; q < 8; ++q) { xs += s_xsq[q][idx >> 4]; ws += s_wsq[q][idx & 15]; }
+        const double bval = bias ? (double)bias[e] : 0.0;
+        const uint32_t bits = gemv_dd_logit<XDT, WDT>(xv, w, t, e, H, lane, bval, xs, ws);
+        if (lane == 0) logits[(size_t)t * E + e] = (uint16_t)bits;
+      }
+    }
+  }
+}
+
 // Rare path of the certificate: one logit recomputed sequentially in double-double (each
 // product is exact in f64, TwoSum accumulation), then rounded to bf16.
 template <int XDT, int WDT>
@@ -424,7 +521,10 @@ using namespace moe;
 template <int XDT, int WDT>
 static void launch_router_logits(const void* x, const void* w, const float* bias, int T, int H,
                                  int E, uint16_t* logits, hipStream_t st) {
-  if (T <= 256 && H <= 512 * kGemvCh) {
+  if (T >= 8 && T <= 256 && H % 512 == 0) {
+    hipLaunchKernelGGL((k_router_logits_small<XDT, WDT>), dim3((T + 15) / 16, (E + 15) / 16), dim3(512), 0,
+                       st, x, w, bias, T, H, E, logits);
+  } else if (T <= 256 && H <= 512 * kGemvCh) {
     hipLaunchKernelGGL((k_router_logits_gemv<XDT, WDT>), dim3((E + 3) / 4, (T + 7) / 8), dim3(256), 0, st,
                        x, w, bias, T, H, E, logits);
   } else if (H % 64 == 0) {
