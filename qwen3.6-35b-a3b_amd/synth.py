@@ -92,7 +92,8 @@ def make_norm_weight(seed: int, device="cuda", hidden: int = 2048, std: float = 
 
 
 def decode_active_bytes(lw: LayerWeights) -> int:
-    """Bytes of the 8 routed + 1 shared active experts per token-layer (20,447,232)."""
+    """Bytes of the 8 routed + 1 shared active experts per token-layer (20,447,232 for Q4_K experts
+    and a bf16 shared expert at H = 2048, I = I_s = 512)."""
     return lw.top_k * lw.routed_bytes_per_expert() + lw.shared_bytes()
 
 
