@@ -110,7 +110,8 @@ int moe_sort_permute(const int32_t *topk_ids, int T, int K, int E, int32_t *expe
  * ffn_up_exps). down_q: [E][H rows][I/256 blocks]. y [T*K, H] f32 in sorted-pair order
  * (expert_raw before the routing weight). path: GEMV = fused dequant + f32 GEMV (decode),
  * MFMA / MFMA_BF16 = tiles dequantised to f16 / bf16 in LDS, contracted on MFMA (prefill);
- * AUTO picks GEMV for T <= 16 with Q4_K gate_up, MFMA otherwise. */
+ * AUTO picks GEMV for T <= 6 with Q4_K gate_up and Q4_K / Q5_K / Q6_K down, MFMA otherwise.
+ * Formats the chosen path cannot read are refused before anything is queued. */
 int moe_experts(const void *x, int x_dtype, const void *gate_up_q, const void *up_q, int gate_up_fmt,
                 const void *down_q, int down_fmt, const int32_t *expert_offsets,
                 const int32_t *sorted_pairs, const int32_t *hit_list, int T, int H, int I, int E,

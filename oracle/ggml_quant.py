@@ -31,6 +31,7 @@ Q6K_BYTES = 210      # 128 (ql) + 64 (qh) + 16 (int8 scales) + 2 (d, at byte 208
 GGML_Q4_K = 12
 GGML_Q5_K = 13
 GGML_Q6_K = 14
+GGML_BF16 = 30                       # plain bf16 rows (ggml type id)
 BLOCK_BYTES = {GGML_Q4_K: Q4K_BYTES, GGML_Q5_K: Q5K_BYTES, GGML_Q6_K: Q6K_BYTES}
 
 
@@ -129,6 +130,10 @@ def dequant(buf, fmt: int, n_elts: int) -> np.ndarray:
         return dequant_q6k(buf, n_elts)
     if fmt == GGML_Q5_K:
         return dequant_q5k(buf, n_elts)
+    if fmt == GGML_BF16:
+        # plain bf16 rows (ggml type 30): each 16-bit pattern is the top half of an f32
+        u = np.frombuffer(np.ascontiguousarray(buf).tobytes(), dtype=np.uint16, count=n_elts)
+        return (u.astype(np.uint32) << 16).view(np.float32)
     raise NotImplementedError(f"no decoder for ggml type {fmt}")
 
 

@@ -125,6 +125,22 @@ def round_f64_to_bf16(v: np.ndarray) -> np.ndarray:
     return np.round(v / q) * q          # v/q and the product are exact; np.round is half-even
 
 
+def midpoint_distance(s: np.ndarray) -> np.ndarray:
+    """Distance from each f64 value to the nearest bf16 rounding midpoint (0 where s is 0: a
+    zero sum is always recomputed exactly). Inside a binade the midpoints sit half a quantum q
+    from the bf16 grid; just above a power of two 2^e (|s| < 2^e + q) the quantum below 2^e is
+    q/2, so the midpoint 2^e - q/4 may be the nearer one. Below 2^-126 (qe = -133 on both sides)
+    the quantum does not change."""
+    a = np.abs(s)
+    q = _bf16_quantum(s)
+    r = a / q                                    # exact (division by a power of two)
+    fl = np.floor(r)
+    d = np.abs((r - fl) - 0.5)
+    at_pow2 = (fl == 128.0) & (q > 2.0 ** -133)
+    d = np.where(at_pow2, np.minimum(d, (r - fl) + 0.25), d)
+    return np.where(a > 0, d * q, 0.0)
+
+
 def r1_logits(x: torch.Tensor, w_router: torch.Tensor, bias: torch.Tensor | None = None):
     """R1, correctly rounded: returns (logits bf16 [T,E], n_exact_recomputes)."""
     xd = x.detach().double().numpy()
@@ -140,10 +156,7 @@ def r1_logits(x: torch.Tensor, w_router: torch.Tensor, bias: torch.Tensor | None
     # |f64 result - exact| <= gamma_n * sum|p|, and the computed `a` is itself within gamma_n;
     # a factor 4 covers both with room to spare.
     bound = 4.0 * (n + 2) * U64 * a
-    q = _bf16_quantum(s)
-    r = s / q
-    frac = r - np.floor(r)
-    near = np.abs(frac - 0.5) * q <= bound
+    near = midpoint_distance(s) <= bound
     out = round_f64_to_bf16(s)
     idx = np.argwhere(near)
     for t, e in idx:
@@ -186,14 +199,31 @@ def experts_and_combine(x: torch.Tensor, ids: torch.Tensor, w_bf16: torch.Tensor
         tok, slot = torch.where(ids == e)
         gu, dn = lw.expert_f32(e)
         raw[tok, slot] = expert_apply(xf[tok], gu, dn)
+    return {"expert_raw": raw, "routed_sum": routed_combine(raw, ids, w_bf16)}
+
+
+def routed_combine(raw: torch.Tensor, ids: torch.Tensor, w_bf16: torch.Tensor) -> torch.Tensor:
+    """routed[t] = sum over the token's K slots in ascending expert id of f32(w_bf16[t,k]) *
+    raw[t,k], each product rounded to f32 before its add (speccheck/moe_ref.py:452-476: the
+    expert_asc order, the cast-before weight, `prod = raw * w; acc += prod`)."""
+    T, K, H = raw.shape
     w = w_bf16.to(torch.float32)
     order = torch.argsort(ids, dim=-1, stable=True)
     acc = torch.zeros(T, H, dtype=torch.float32)
+    ar = torch.arange(T)
     for j in range(K):
         k = order[:, j]
-        ar = torch.arange(T)
-        acc += raw[ar, k] * w[ar, k][:, None]
-    return {"expert_raw": raw, "routed_sum": acc}
+        prod = raw[ar, k] * w[ar, k][:, None]
+        acc = acc + prod
+    return acc
+
+
+def final_add(routed: torch.Tensor, gate_prob: torch.Tensor, shared_raw: torch.Tensor,
+              residual: torch.Tensor | None = None) -> torch.Tensor:
+    """combined = routed + gate_prob * shared_raw (speccheck/moe_ref.py:514-517), then
+    x = x1 + combined (engine/m3_forward.py:737); every op rounded to f32 on its own."""
+    combined = routed + gate_prob.reshape(-1, 1) * shared_raw
+    return combined if residual is None else residual + combined
 
 
 def shared_expert(x: torch.Tensor, lw: LayerWeights) -> dict:
@@ -218,7 +248,7 @@ def moe_block(x: torch.Tensor, lw: LayerWeights, top_k: int = 8) -> dict:
     out.update(r)
     out.update(e)
     out.update(s)
-    out["combined_out"] = e["routed_sum"] + s["shared_out"]
+    out["combined_out"] = final_add(e["routed_sum"], s["shared_gate_prob"], s["shared_raw"])
     return out
 
 
@@ -241,15 +271,29 @@ def residual_step(x1: torch.Tensor, lw: LayerWeights, norm_w: torch.Tensor, eps:
     """The decoder layer's MoE half (engine/m3_forward.py:732-737): h = rmsnorm_a(x1, w);
     x = x1 + moe_block(h). Returns moe_block's stages (on h) plus "x_out"."""
     st = moe_block(rmsnorm_a(x1, norm_w, eps), lw, top_k)
-    st["x_out"] = x1.float() + st["combined_out"]
+    st["x_out"] = final_add(st["routed_sum"], st["shared_gate_prob"], st["shared_raw"], x1.float())
     return st
 
 
+def ulp_of(v: float) -> float:
+    """The width of one bf16 step above |v| (speccheck/moe_ref.py:551-567): 2^(floor(log2|v|) - 7),
+    bf16 having 7 explicit mantissa bits; 0.0 at zero and for non-finite v."""
+    v = abs(float(v))
+    if v == 0 or not math.isfinite(v):
+        return 0.0
+    m, e = math.frexp(v)                 # v = m 2^e, 0.5 <= m < 1: floor(log2 v) = e - 1, exactly
+    return math.ldexp(1.0, e - 1 - 7)
+
+
 def metrics(a: torch.Tensor, b: torch.Tensor, name: str = "") -> dict:
-    """speccheck/moe_ref.py:578-630 comparator fields (max_abs, max_abs_over_scale, 1-cos, ndiff);
-    refuses non-finite input and an all-zero reference."""
+    """speccheck/moe_ref.py:578-630 comparator fields (max_abs, max_abs_over_scale, mean_abs,
+    1-cos, ndiff, n_gt_1ulp / n_gt_100ulp against one bf16 step at the reference's max |value|).
+    Refuses a shape or dtype mismatch (both sides are widened to f64 explicitly, so a mixed pair
+    would otherwise compare quietly), non-finite input, an all-zero reference and a zero norm."""
     if a.shape != b.shape:
         raise AssertionError(f"{name}: shape {tuple(a.shape)} vs {tuple(b.shape)}")
+    if a.dtype != b.dtype:
+        raise AssertionError(f"{name}: dtype {a.dtype} vs {b.dtype}")
     x = a.detach().to(torch.float64).flatten()
     y = b.detach().to(torch.float64).flatten()
     if not (torch.isfinite(x).all() and torch.isfinite(y).all()):
@@ -259,11 +303,16 @@ def metrics(a: torch.Tensor, b: torch.Tensor, name: str = "") -> dict:
         raise AssertionError(f"{name}: the reference side is all zero")
     diff = (x - y).abs()
     denom = (x.norm() * y.norm()).item()
-    cos = (x @ y).item() / denom if denom else float("nan")
-    return {"name": name, "n": int(x.numel()), "max_abs": diff.max().item(),
-            "max_abs_over_scale": diff.max().item() / scale,
+    if denom == 0:
+        raise AssertionError(f"{name}: zero-norm side; cos is undefined")
+    cos = (x @ y).item() / denom
+    ulp_ref = ulp_of(scale)
+    return {"name": name, "dtype": str(a.dtype), "n": int(x.numel()), "max_abs": diff.max().item(),
+            "max_abs_over_scale": diff.max().item() / scale, "mean_abs": diff.mean().item(),
             "one_minus_cos": max(0.0, 1.0 - cos), "ndiff": int((diff > 0).sum().item()),
-            "ref_absmax": scale}
+            "n_gt_1ulp": int((diff > ulp_ref).sum().item()),
+            "n_gt_100ulp": int((diff > 100 * ulp_ref).sum().item()),
+            "ref_absmax": scale, "ulp_of_refmax": ulp_ref}
 
 
 def from_device(lw) -> LayerWeights:

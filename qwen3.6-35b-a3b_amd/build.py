@@ -54,7 +54,24 @@ def build(verbose: bool = False) -> Path:
     if p.returncode != 0:
         raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
     os.replace(tmp, OUT)
+    build_hostcheck()
     return OUT
+
+
+HOSTCHECK = PKG / "libmoe_hostcheck.so"
+
+
+def build_hostcheck() -> Path:
+    """libmoe_hostcheck.so: host-callable builds of device helpers (csrc/hostcheck/) that the CPU
+    tests check without a GPU. Test infrastructure; the product library does not link it."""
+    src = CSRC / "hostcheck" / "hostcheck.hip"
+    tmp = HOSTCHECK.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, "-shared", "-o", str(tmp), str(src)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("hostcheck build failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, HOSTCHECK)
+    return HOSTCHECK
 
 
 if __name__ == "__main__":

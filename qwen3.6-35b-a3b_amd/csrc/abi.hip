@@ -43,10 +43,11 @@ static int check_geom(int T, int H, int I, int E, int K, const char* who) {
   return MOE_OK;
 }
 
-static int pick_path(int path, int T, int gate_up_fmt) {
+static int pick_path(int path, int T, int gate_up_fmt, int down_fmt) {
   if (path == MOE_PATH_GEMV_MULTI) return MOE_PATH_GEMV;
   if (path == MOE_PATH_GEMV || path == MOE_PATH_MFMA || path == MOE_PATH_MFMA_BF16) return path;
-  if (gate_up_fmt != MOE_FMT_Q4_K) return MOE_PATH_MFMA;
+  // the GEMV kernels read Q4_K gate_up and GGUF-block down only
+  if (gate_up_fmt != MOE_FMT_Q4_K || down_fmt == MOE_FMT_BF16) return MOE_PATH_MFMA;
   // measured crossover (block at 2..24 tokens, the shared expert on the second stream from 7):
   // the GEMV path reads every hit expert once per token group, the MFMA path once per tile
   return T <= 6 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
@@ -201,7 +202,7 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                         int E, int K, int path, float* y, MoeWs& w, hipStream_t st) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
-  path = pick_path(path, T, gu_fmt);
+  path = pick_path(path, T, gu_fmt, dn_fmt);
   if (path == MOE_PATH_GEMV) {
     float* S = reinterpret_cast<float*>(w.take((size_t)P * I * 4));
     if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
@@ -243,6 +244,17 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
   return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, opb, y, st);
 }
 
+// the formats the resolved routed path reads; checked before any launch is queued
+static int check_path_fmt(int rpath, int gu_fmt, int dn_fmt, const char* who) {
+  if (rpath == MOE_PATH_GEMV && gu_fmt != MOE_FMT_Q4_K)
+    return moe_set_error(MOE_E_FORMAT, "%s: the GEMV path reads Q4_K gate_up only", who);
+  if (rpath == MOE_PATH_GEMV && dn_fmt == MOE_FMT_BF16)
+    return moe_set_error(MOE_E_FORMAT, "%s: the GEMV path reads Q4_K / Q5_K / Q6_K down only", who);
+  if (rpath == MOE_PATH_MFMA_BF16 && dn_fmt == MOE_FMT_Q5_K)
+    return moe_set_error(MOE_E_FORMAT, "%s: Q5_K down runs on the GEMV and MFMA (f16) paths", who);
+  return MOE_OK;
+}
+
 static int check_wfmt(int gu_fmt, int dn_fmt, const void* gu, const void* up, const void* dn, const char* who) {
   if (gu_fmt != MOE_FMT_Q4_K && gu_fmt != MOE_FMT_Q6_K && gu_fmt != MOE_FMT_BF16)
     return moe_set_error(MOE_E_FORMAT, "%s: unsupported gate_up format %d", who, gu_fmt);
@@ -282,8 +294,7 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, const void* u
   if (x_dtype != MOE_DT_F32 && x_dtype != MOE_DT_BF16) return moe_set_error(MOE_E_ARG, "moe_experts: bad x_dtype %d", x_dtype);
   MOE_TRY(check_geom(T, H, I, E, K, "moe_experts"));
   MOE_TRY(check_wfmt(gate_up_fmt, down_fmt, gate_up_q, up_q, down_q, "moe_experts"));
-  if (path == MOE_PATH_GEMV && gate_up_fmt != MOE_FMT_Q4_K) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K gate_up only");
-  if (path == MOE_PATH_GEMV && down_fmt == MOE_FMT_BF16) return moe_set_error(MOE_E_FORMAT, "moe_experts: the GEMV path reads Q4_K / Q5_K / Q6_K down only");
+  MOE_TRY(check_path_fmt(pick_path(path, T, gate_up_fmt, down_fmt), gate_up_fmt, down_fmt, "moe_experts"));
   if (!aligned16(x)) return moe_set_error(MOE_E_ARG, "moe_experts: x must be 16-byte aligned");
   MoeWs w{reinterpret_cast<char*>(ws), ws ? ws_bytes : 0};
   w.take(kSyncBytes);
@@ -399,7 +410,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   const int P = T * K;
   MoeWs w{reinterpret_cast<char*>(ws), ws_bytes};
   int* sync = reinterpret_cast<int*>(w.take(kSyncBytes));
-  const int rpath = pick_path(path, T, gate_up_fmt);
+  const int rpath = pick_path(path, T, gate_up_fmt, down_fmt);
+  MOE_TRY(check_path_fmt(rpath, gate_up_fmt, down_fmt, "moe_block_forward"));
   const bool decode = T == 1 && K == 8 && rpath == MOE_PATH_GEMV && gate_up_fmt == MOE_FMT_Q4_K &&
                       (down_fmt == MOE_FMT_Q4_K || down_fmt == MOE_FMT_Q5_K || down_fmt == MOE_FMT_Q6_K) &&
                       I_s % 128 == 0 && E % 4 == 0;

@@ -2,7 +2,8 @@
 // speccheck/moe_ref.py:452-476, 516-518; engine/block_forward.py:664-667, 680):
 //   routed[t,h] = sum over the token's K experts in ascending expert id of
 //                 f32(w_bf16[t, rank]) * y[pair_pos[t*K + rank], h]       (f32, fixed order)
-//   out[t,h]    = routed[t,h] + gate_prob[t] * shared_raw[t,h]
+//   out[t,h]    = residual[t,h] + (routed[t,h] + gate_prob[t] * shared_raw[t,h])
+// every product and sum rounded to f32 on its own (comb_madd / comb_out, common.h)
 // The weight is reached through the rank (slot) the expert holds, never through its id.
 #include "common.h"
 #include "moe_internal.h"
@@ -51,13 +52,13 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
     const int k = s_order[j];
     const int pos = s_pos[k];
     const float v = pos >= 0 ? y[(size_t)pos * H + h] : 0.0f;   // dropped (out-of-range) id
-    acc += s_w[k] * v;
+    acc = comb_madd(acc, s_w[k], v);
     if (expert_raw) expert_raw[((size_t)t * K + k) * H + h] = v;
   }
-  const float sh = gate_prob[t] * shared_raw[(size_t)t * H + h];
+  const float gp = gate_prob[t], sr = shared_raw[(size_t)t * H + h];
   if (routed_sum) routed_sum[(size_t)t * H + h] = acc;
-  if (shared_out) shared_out[(size_t)t * H + h] = sh;
-  out[(size_t)t * H + h] = (residual ? residual[(size_t)t * H + h] : 0.0f) + acc + sh;
+  if (shared_out) shared_out[(size_t)t * H + h] = gp * sr;
+  out[(size_t)t * H + h] = comb_out(residual ? residual[(size_t)t * H + h] : 0.0f, acc, gp, sr);
 }
 
 // Same sums, four columns per thread (H % 4 == 0) and a compile-time K: the K expert rows are
@@ -111,10 +112,10 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ y,
 #pragma unroll
   for (int j = 0; j < KK; ++j) {
     const float w = s_w[j];
-    acc.x += w * v[j].x;
-    acc.y += w * v[j].y;
-    acc.z += w * v[j].z;
-    acc.w += w * v[j].w;
+    acc.x = comb_madd(acc.x, w, v[j].x);
+    acc.y = comb_madd(acc.y, w, v[j].y);
+    acc.z = comb_madd(acc.z, w, v[j].z);
+    acc.w = comb_madd(acc.w, w, v[j].w);
     if (expert_raw)
       *reinterpret_cast<float4*>(expert_raw + ((size_t)t * KK + s_slot[j]) * H + h) = v[j];
   }
@@ -122,7 +123,8 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ y,
   if (routed_sum) *reinterpret_cast<float4*>(routed_sum + o) = acc;
   if (shared_out) *reinterpret_cast<float4*>(shared_out + o) = sh;
   *reinterpret_cast<float4*>(out + o) =
-      make_float4(rs.x + acc.x + sh.x, rs.y + acc.y + sh.y, rs.z + acc.z + sh.z, rs.w + acc.w + sh.w);
+      make_float4(comb_out(rs.x, acc.x, gp, sr.x), comb_out(rs.y, acc.y, gp, sr.y),
+                  comb_out(rs.z, acc.z, gp, sr.z), comb_out(rs.w, acc.w, gp, sr.w));
 }
 
 }  // namespace moe

@@ -90,6 +90,24 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 
 __device__ __forceinline__ float silu_f32(float z) { return z / (1.0f + __expf(-z)); }
 
+// ------------------------------------------------------------------- the combine's roundings --
+// The block's final sums round every product and every sum to f32 on its own, as the reference's
+// torch ops do (speccheck/moe_ref.py:466-474: prod = raw * w, then acc += prod;
+// engine/m3_forward.py:464, 475, 737): out = x1 + (routed + gate * shared_raw). The contraction
+// pragma keeps the compiler from fusing a product into the following add (an FMA rounds once).
+// acc + w * v with the product rounded first
+__device__ __forceinline__ float comb_madd(float acc, float w, float v) {
+#pragma clang fp contract(off)
+  const float p = w * v;
+  return acc + p;
+}
+// residual + (routed + gate * shared_raw), the residual NaN-free zero when absent
+__device__ __forceinline__ float comb_out(float resid, float routed, float gate, float sraw) {
+#pragma clang fp contract(off)
+  const float sh = gate * sraw;
+  return resid + (routed + sh);
+}
+
 // ----------------------------------------------------------------------------- Q4_K element --
 // 144-byte super-block: f16 d | f16 dmin | 12 B packed 6-bit (sc, m) x 8 | 128 B nibbles.
 // get_scale_min_k4 (tools/gguf_reader.py:165-175), with the 12 scale bytes held as 3 dwords

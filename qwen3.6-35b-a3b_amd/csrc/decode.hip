@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void k_dec_down_combine(DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int k = order[j];
-      acc += bf16_to_f32(a.w_bf16[k]) * ys[r][k];
+      acc = comb_madd(acc, bf16_to_f32(a.w_bf16[k]), ys[r][k]);
     }
     const float sh = a.gate_prob[0] * a.shared_raw[h];
     if (a.routed_sum) a.routed_sum[h] = acc;
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void k_dec_down_combine(DecodeArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) a.expert_raw[(size_t)k * a.H + h] = ys[r][k];
     }
-    a.out[h] = (a.residual ? a.residual[h] : 0.0f) + acc + sh;
+    a.out[h] = comb_out(a.residual ? a.residual[h] : 0.0f, acc, a.gate_prob[0], a.shared_raw[h]);
   }
 }
 

@@ -763,15 +763,14 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
       for (int q = 0; q < K; ++q) {
         const int k = s_order[q];
-        acc += s_w[k] * s_comb[0][k][t];
+        acc = comb_madd(acc, s_w[k], s_comb[0][k][t]);
       }
       float shr = 0.0f;
 #pragma unroll
       for (int q = 0; q < kXcd; ++q) shr += s_comb[1][q][t];
-      const float sh = s_gate * shr;
       if (a.routed_sum) a.routed_sum[h] = acc;
-      if (a.shared_out) a.shared_out[h] = sh;
-      a.out[h] = resid + acc + sh;
+      if (a.shared_out) a.shared_out[h] = s_gate * shr;
+      a.out[h] = comb_out(resid, acc, s_gate, shr);
     }
     // this role's launch count, for the next launch
     if (t == 0) astore(a.sync + kRoleEpoch + kPer * x + r, (int)epoch);

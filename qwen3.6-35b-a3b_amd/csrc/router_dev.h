@@ -21,10 +21,11 @@ __device__ __forceinline__ DD dd_add(DD a, DD b) {
 }
 
 // exponent e with 2^e <= |v| < 2^(e+1), v != 0, v finite
-__device__ __forceinline__ int exp2_floor(double v) { return ilogb(v); }
+__host__ __device__ __forceinline__ int exp2_floor(double v) { return ilogb(v); }
 
-// Round the f64 value s (|s - exact| <= bound) to bf16. Returns false if not certified.
-__device__ __forceinline__ bool round_bf16_certified(double s, double bound, uint32_t* out) {
+// Round the f64 value s (|s - exact| <= bound) to bf16. Returns false if not certified, i.e. if a
+// bf16 rounding midpoint lies within `bound` of s. (Host-callable, so the host tests can check it.)
+__host__ __device__ __forceinline__ bool round_bf16_certified(double s, double bound, uint32_t* out) {
   if (s == 0.0) {
     if (bound > 0.0) {
       // the exact value may be a tiny non-zero: certify only if every value within the bound
@@ -39,12 +40,18 @@ __device__ __forceinline__ bool round_bf16_certified(double s, double bound, uin
   const int qe = max(e - 7, -133);
   const double r = ldexp(a, -qe);                     // exact
   const double fl = floor(r);
-  const double dist = fabs((r - fl) - 0.5);          // in units of the quantum, exact
+  double dist = fabs((r - fl) - 0.5);                // in units of the quantum, exact
+  // just above a power of two (fl == 128) the quantum below 2^e is half as wide, so the nearest
+  // midpoint may be 2^e - q/4, at (r - 128) + 1/4 quanta, rather than 2^e + q/2; in the subnormal
+  // range (qe == -133 below and above 2^e) the quantum does not change
+  if (fl == 128.0 && qe > -133) dist = fmin(dist, (r - fl) + 0.25);
   if (ldexp(dist, qe) <= bound) return false;
   const double rounded = ldexp(rint(r), qe);          // rint: ties-to-even
   float f = (float)rounded;                           // exact (or inf on overflow)
   if (s < 0) f = -f;
-  *out = __float_as_uint(f) >> 16;
+  uint32_t fb;
+  __builtin_memcpy(&fb, &f, 4);
+  *out = fb >> 16;
   return true;
 }
 
@@ -60,15 +67,22 @@ __device__ uint32_t round_bf16_dd(DD v, double ddbound) {
   const int qe = max(exp2_floor(a) - 7, -133);
   const double r = ldexp(a, -qe);
   const double fl = floor(r);
-  const double mid_abs = ldexp(fl + 0.5, qe);
+  // the nearest midpoint: fl + 1/2, or 2^e - q/4 (127.75 quanta) just above a power of two
+  const bool below_pow2 = fl == 128.0 && qe > -133 && (r - fl) + 0.25 < fabs((r - fl) - 0.5);
+  const double mq = below_pow2 ? 127.75 : fl + 0.5;
+  // its two neighbours in quanta (127.5 = the largest bf16 below 2^e) and whether the upper
+  // one is the even one (2^e is; so is fl + 1 when fl is odd)
+  const double lo_n = below_pow2 ? 127.5 : fl, hi_n = below_pow2 ? 128.0 : fl + 1.0;
+  const bool hi_even = below_pow2 || fmod(fl, 2.0) != 0.0;
+  const double mid_abs = ldexp(mq, qe);
   const double mid = (sref < 0) ? -mid_abs : mid_abs;
   const double diff = (v.hi - mid) + v.lo;            // hi - mid is exact (close values)
   double n;                                           // magnitude in quanta after rounding
   if (fabs(diff) <= ddbound) {
-    n = (fmod(fl, 2.0) == 0.0) ? fl : fl + 1.0;       // tie: to even
+    n = hi_even ? hi_n : lo_n;                        // tie: to even
   } else {
     const bool above = (sref < 0) ? (diff < 0) : (diff > 0);
-    n = above ? fl + 1.0 : fl;
+    n = above ? hi_n : lo_n;
   }
   float f = (float)ldexp(n, qe);
   if (sref < 0) f = -f;

@@ -33,7 +33,8 @@ FMT_BF16 = 30
 FMT_Q8_0 = 8
 Q8_0_BYTES = 34                      # f16 d + 32 x int8, per 32 elements
 # bytes per 256 elements
-BLOCK_BYTES = {FMT_Q4_K: Q4K_BYTES, FMT_Q5_K: Q5K_BYTES, FMT_Q6_K: Q6K_BYTES, FMT_Q8_0: 8 * Q8_0_BYTES}
+BLOCK_BYTES = {FMT_Q4_K: Q4K_BYTES, FMT_Q5_K: Q5K_BYTES, FMT_Q6_K: Q6K_BYTES, FMT_Q8_0: 8 * Q8_0_BYTES,
+               FMT_BF16: 2 * QK_K}
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
@@ -142,6 +143,11 @@ def _q8_0_rows(w: torch.Tensor) -> torch.Tensor:
     return out.reshape(rows, nb * Q8_0_BYTES)
 
 
+def _bf16_rows(w: torch.Tensor) -> torch.Tensor:
+    """Plain bf16 rows (RNE) as their little-endian bytes: the BF16 weight records."""
+    return w.to(torch.bfloat16).contiguous().view(torch.uint8).reshape(w.shape[0], -1)
+
+
 def quantize(w, fmt: int, chunk_rows: int = 16384) -> torch.Tensor:
     """float[rows, cols] (torch or numpy; cols % 256 == 0) -> uint8[rows, row_bytes(fmt, cols)]
     on the same device as `w`."""
@@ -149,7 +155,8 @@ def quantize(w, fmt: int, chunk_rows: int = 16384) -> torch.Tensor:
         w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float32))
     if w.dim() != 2 or w.shape[1] % QK_K:
         raise ValueError(f"expected [rows, cols] with cols % 256 == 0, got {tuple(w.shape)}")
-    fn = {FMT_Q4_K: _q4k_rows, FMT_Q5_K: _q5k_rows, FMT_Q6_K: _q6k_rows, FMT_Q8_0: _q8_0_rows}.get(fmt)
+    fn = {FMT_Q4_K: _q4k_rows, FMT_Q5_K: _q5k_rows, FMT_Q6_K: _q6k_rows, FMT_Q8_0: _q8_0_rows,
+          FMT_BF16: _bf16_rows}.get(fmt)
     if fn is None:
         raise ValueError(f"unsupported format {fmt}")
     rows = w.shape[0]

@@ -110,3 +110,70 @@ def test_combine_is_ascending_expert_order_with_rank_weights():
     w_by_id = torch.gather(w, 1, (r["topk_ids"] % K))
     wrong = (raw * w_by_id[..., None]).double().sum(1)
     assert (wrong - want).abs().max() > 1e-4
+
+
+def _silu64(z: torch.Tensor) -> torch.Tensor:
+    """silu(z) = z / (1 + e^-z) (moe_gather_kernels.h:514), evaluated in f64 from its definition."""
+    return z / (1.0 + torch.exp(-z))
+
+
+def test_shared_expert_matches_one_hot_closed_form():
+    """x = e_j (speccheck/moe_ref.py:480-495): gate x = W_sg[:, j], up x = W_su[:, j], so
+    shared_raw = W_sd @ (silu(W_sg[:, j]) * W_su[:, j]) and gate_prob = sigmoid(w_sg_scalar[j])."""
+    lw = _layer(9)
+    for j in (0, 37, H - 1):
+        x = torch.zeros(1, H)
+        x[0, j] = 1.0
+        s = O.shared_expert(x, lw)
+        g = lw.shared_gate.double()[:, j]
+        u = lw.shared_up.double()[:, j]
+        want = lw.shared_down.double() @ (_silu64(g) * u)
+        assert torch.allclose(s["shared_raw"][0].double(), want, rtol=1e-5, atol=1e-7)
+        p = 1.0 / (1.0 + torch.exp(-lw.shared_scalar_gate.double()[0, j]))
+        assert abs(s["shared_gate_prob"].item() - p.item()) <= 2e-7
+        # negative controls: silu on the up projection, or the gate and up rows exchanged
+        wrong = lw.shared_down.double() @ (g * _silu64(u))
+        assert (wrong - want).abs().max() > 1e-4
+        assert (s["shared_raw"][0].double() - wrong).abs().max() > 1e-4
+
+
+def test_shared_expert_two_hot_is_not_linear_in_x():
+    """silu makes the expert nonlinear: x = e_i + e_j is not the sum of the one-hot outputs, and the
+    closed form silu(g_i + g_j) * (u_i + u_j) is what the oracle computes."""
+    lw = _layer(10)
+    i, j = 5, 200
+    x = torch.zeros(1, H)
+    x[0, i] = 1.0
+    x[0, j] = 1.0
+    s = O.shared_expert(x, lw)["shared_raw"][0].double()
+    g = lw.shared_gate.double()[:, i] + lw.shared_gate.double()[:, j]
+    u = lw.shared_up.double()[:, i] + lw.shared_up.double()[:, j]
+    want = lw.shared_down.double() @ (_silu64(g) * u)
+    assert torch.allclose(s, want, rtol=1e-5, atol=1e-7)
+
+
+def test_metrics_fields_and_refusals():
+    """The comparator (speccheck/moe_ref.py:578-630): n_gt_1ulp counts against one bf16 step at
+    the reference's max |value|, and mismatched dtypes, non-finite values and an all-zero
+    reference are refused."""
+    import pytest
+
+    assert O.ulp_of(1.0) == 2.0 ** -7
+    assert O.ulp_of(3.0) == 2.0 ** -6
+    assert O.ulp_of(0.75) == 2.0 ** -8
+    assert O.ulp_of(-2.0) == 2.0 ** -6
+    assert O.ulp_of(0.0) == 0.0 and O.ulp_of(float("inf")) == 0.0
+    ref = torch.tensor([1.0, -0.5, 0.25, 1.5])        # max |ref| = 1.5: one step = 2^-7
+    got = ref + torch.tensor([0.0, 2.0 ** -8, 2.0 ** -6, 0.5])
+    m = O.metrics(got, ref, name="t")
+    assert m["ulp_of_refmax"] == 2.0 ** -7
+    assert m["ndiff"] == 3 and m["n_gt_1ulp"] == 2 and m["n_gt_100ulp"] == 0
+    assert m["max_abs"] == 0.5 and m["max_abs_over_scale"] == 0.5 / 1.5
+    with pytest.raises(AssertionError, match="dtype"):
+        O.metrics(got.double(), ref)
+    with pytest.raises(AssertionError, match="shape"):
+        O.metrics(got[:3], ref)
+    with pytest.raises(AssertionError, match="non-finite"):
+        O.metrics(torch.tensor([float("nan"), 0.0, 0.0, 1.0]), ref)
+    with pytest.raises(AssertionError, match="all zero"):
+        O.metrics(got, torch.zeros(4))
