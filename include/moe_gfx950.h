@@ -225,6 +225,27 @@ int moe_block_forward_prefetch(const void *x, int x_dtype, int T, int H, int I, 
                                float *expert_raw, void *ws, size_t ws_bytes, void *stream,
                                const moe_next_layer *next);
 
+/* moe_block_forward_w for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Same arguments,
+ * outputs, limits and errors as moe_block_forward_w, without (ws, ws_bytes): the scratch is a
+ * static device array of MOE_NOALLOC_SCRATCH_BYTES inside the library, one per device, held until
+ * the process ends. A step needing more scratch than that (moe_workspace_bytes(T, ...) >
+ * MOE_NOALLOC_SCRATCH_BYTES: above MOE_NOALLOC_MAX_T tokens at the model's geometry) is refused
+ * with MOE_E_WORKSPACE before anything is queued. The call allocates nothing: no hipMalloc, no
+ * stream or event (the shared expert runs on `stream`, where moe_block_forward_w would fork a
+ * second stream from 7 tokens on; the bits are the same). The first call on a device clears the
+ * array's sync words with a fill launch on `stream`. Every call on one device shares that device's
+ * array: calls that overlap on one GPU (two streams, two threads) race and must be ordered by
+ * the caller. */
+#define MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define MOE_NOALLOC_MAX_T 120  /* the largest T whose moe_workspace_bytes fits, at H=2048 I=512 E=256 K=8 I_s=512 */
+int moe_block_forward_w_noalloc(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                                const moe_layer_weights *w, float norm_eps, int path,
+                                const float *residual, float *out, void *logits_bf16,
+                                int32_t *topk_ids, void *topk_w_bf16, float *topk_w_f32,
+                                float *routed_sum, float *shared_out, float *gate_prob,
+                                float *expert_raw, void *stream, const moe_layer_weights *next);
+
 /* Untied lm_head GEMV: logits[b, j] = sum_k h[b, k] * W[row_j, k] in f32 for b < B (1..8) and
  * j < n_rows, with row_j = j (dense: row_ids NULL, n_rows <= V) or row_j = row_ids[j] (gather; an
  * id outside [0, V) gives NaN for that output). h: [B, H] f32 or bf16 (h_dtype); W: V rows of H

@@ -34,6 +34,9 @@ MOE_PATH_MFMA_BF16 = 3
 MOE_PATH_GEMV_MULTI = 4
 # every workspace starts with this many bytes of device-side sync words
 SYNC_BYTES = 512 * 1024
+# moe_block_forward_w_noalloc's static scratch (include/moe_gfx950.h)
+NOALLOC_SCRATCH_BYTES = 16 << 20
+NOALLOC_MAX_T = 120
 
 
 
@@ -84,6 +87,10 @@ SIGNATURES = {
     "moe_block_forward_w": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(LayerWeightsC),
                                  ctypes.c_float, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                  _VP, _VP, _SZ, _VP, ctypes.POINTER(LayerWeightsC)]),
+    "moe_block_forward_w_noalloc": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I,
+                                         ctypes.POINTER(LayerWeightsC), ctypes.c_float, _I, _VP,
+                                         _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                                         ctypes.POINTER(LayerWeightsC)]),
     "moe_workspace_init": (_I, [_VP, _SZ, _VP]),
     "moe_lm_head": (_I, [_VP, _I, _I, _I, _VP, _I, _I64, _VP, _I64, _VP, _VP]),
 }

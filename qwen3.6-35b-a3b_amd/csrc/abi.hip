@@ -378,7 +378,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
                               int32_t* topk_ids, void* topk_w_bf16, float* topk_w_f32,
                               float* routed_sum, float* shared_out, float* gate_prob,
                               float* expert_raw, void* ws, size_t ws_bytes, void* stream,
-                              const moe_layer_weights* next) {
+                              const moe_layer_weights* next, bool allow_fork = true) {
   const void* w_router = Wt.w_router;
   const float* logit_bias = Wt.logit_bias;
   const void* gate_up_q = Wt.gate_q;
@@ -482,7 +482,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
     MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
   }
-  if (T < kForkMinT) {
+  if (T < kForkMinT || !allow_fork) {
     MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, nullptr, 0, st));
     MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order));
     MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
@@ -583,6 +583,70 @@ int moe_block_forward_w(const void* x, int x_dtype, int T, int H, int I, int E, 
   return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, *w, norm_eps, path, residual, out, logits_bf16,
                             topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob,
                             expert_raw, ws, ws_bytes, stream, next);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ the allocation-free entry --
+// moe_block_forward_w_noalloc's scratch: one array per device (each GPU the library runs on holds
+// its own copy until the process ends). Host code never passes `scratch` itself to a kernel (its
+// name is a host-side stand-in there): the device address comes from hipGetSymbolAddress, once
+// per device, on that device's first call, and is kept per device.
+static __device__ __align__(256) unsigned char scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+struct ScratchDev {
+  void* ptr = nullptr;      // the device's copy of `scratch`
+  bool zeroed = false;      // its sync words cleared (stream-ordered before the first use)
+};
+static ScratchDev g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_for_device(hipStream_t st, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return moe_set_error(MOE_E_HIP, "moe_block_forward_w_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchDev& d = g_scratch[dev];
+  if (!d.ptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return moe_set_error(MOE_E_HIP, "moe_block_forward_w_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                           dev, hipGetErrorString(e));
+    d.ptr = p;
+  }
+  if (!d.zeroed) {
+    // the sync words must start at zero; every later call leaves them valid for the next
+    MOE_TRY(moe_launch_zero_words(reinterpret_cast<int*>(d.ptr), (int)(kSyncBytes / 4), st));
+    d.zeroed = true;
+  }
+  *out = d.ptr;
+  return MOE_OK;
+}
+
+extern "C" {
+
+int moe_block_forward_w_noalloc(const void* x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
+                                const moe_layer_weights* w, float norm_eps, int path, const float* residual,
+                                float* out, void* logits_bf16, int32_t* topk_ids, void* topk_w_bf16,
+                                float* topk_w_f32, float* routed_sum, float* shared_out, float* gate_prob,
+                                float* expert_raw, void* stream, const moe_layer_weights* next) {
+  if (!w) return moe_set_error(MOE_E_ARG, "moe_block_forward_w_noalloc: NULL weights");
+  MOE_TRY(check_geom(T, H, I, E, K, "moe_block_forward_w_noalloc"));
+  const size_t need = moe_workspace_bytes(T, H, I, E, K, I_s);
+  if (need > (size_t)MOE_NOALLOC_SCRATCH_BYTES)
+    return moe_set_error(MOE_E_WORKSPACE,
+                         "moe_block_forward_w_noalloc: a %d-token step needs %zu scratch bytes, the static "
+                         "scratch holds %zu (at most %d tokens at H=2048, I=512, E=256, K=8, I_s=512)",
+                         T, need, (size_t)MOE_NOALLOC_SCRATCH_BYTES, MOE_NOALLOC_MAX_T);
+  hipStream_t st = (hipStream_t)stream;
+  void* ws = nullptr;
+  MOE_TRY(scratch_for_device(st, &ws));
+  // one stream: the shared expert runs on the caller's stream (the fork's second stream and
+  // events would be created on first use)
+  return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, *w, norm_eps, path, residual, out, logits_bf16,
+                            topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob,
+                            expert_raw, ws, (size_t)MOE_NOALLOC_SCRATCH_BYTES, stream, next, false);
 }
 
 int moe_lm_head(const void* h, int h_dtype, int B, int H, const void* w, int w_fmt, int64_t V,
