@@ -2,9 +2,13 @@
  *
  * Every data pointer is a DEVICE pointer owned by the caller (for example a torch tensor's
  * data_ptr()); `stream` is a hipStream_t passed as void*. Every call is asynchronous on `stream`,
- * allocates nothing, frees nothing and never synchronises the host; scratch memory comes in
- * through (ws, ws_bytes). Routing values never travel to the host (specification/11-moe-block.md
- * §11.7: the block is computable with zero host-visible routing values).
+ * allocates no device memory, frees nothing and never synchronises the host; scratch memory
+ * comes in through (ws, ws_bytes). One exception to "creates nothing": the first
+ * moe_block_forward* call of 7 or more tokens on a device creates that device's second stream (default
+ * priority, non-blocking) and two events, kept until the process ends, on which the shared expert
+ * runs beside the routed path (moe_block_forward_w_noalloc never does). Routing values never
+ * travel to the host (specification/11-moe-block.md §11.7: the block is computable with zero
+ * host-visible routing values).
  *
  * Return value: MOE_OK (0) or a negative MOE_E_* code; moe_last_error() then returns a
  * thread-local description. Nothing throws across the ABI. Results are deterministic: no float
@@ -259,7 +263,23 @@ int moe_block_forward_w_noalloc(const void *x, int x_dtype, int T, int H, int I,
 int moe_lm_head(const void *h, int h_dtype, int B, int H, const void *w, int w_fmt, int64_t V,
                 const int32_t *row_ids, int64_t n_rows, float *logits, void *stream);
 
-/* Zero the workspace's device-side sync words (its first 512 KiB: error bits, the single-launch
+/* The workspace's status word, stream-ordered: *status (a device int32 the caller owns) receives
+ * the bits recorded since the last call, and the word is cleared. Bit MOE_STATUS_SPIN_TIMEOUT: a
+ * bounded wait of the single-launch decode layer gave up (its workgroups were not all co-resident,
+ * or not placed on the XCDs round robin as it assumes); the output rows of every workgroup that
+ * gave up are NaN and the rest of that call's outputs are unspecified. No host synchronisation:
+ * read *status after the stream reaches it. No counterpart in the reference (its device work ran
+ * in fresh processes and reported through their exit status, engine/device_arm.py:417-463). */
+#define MOE_STATUS_WORD 3              /* int32 index of the status word in the workspace */
+#define MOE_STATUS_SPIN_TIMEOUT 1
+/* Test hook: while the workspace's int32 word MOE_TEST_HOOK_WORD is non-zero, every bounded wait
+ * of the single-launch decode layer completes as usual and then reports a timeout, so a caller's
+ * handling of the status and the NaN rows can be exercised without a real timeout. Zero in normal
+ * use (moe_workspace_init clears it). */
+#define MOE_TEST_HOOK_WORD 4
+int moe_workspace_status(void *ws, size_t ws_bytes, int32_t *status, void *stream);
+
+/* Zero the workspace's device-side sync words (its first 512 KiB: status bits, the single-launch
  * decode layer's per-role launch counts and its two exchange buffers; one short fill launch).
  * Call once after allocating a workspace, before its first use by moe_block_forward /
  * moe_experts / moe_shared_expert / moe_router_topk; a workspace zeroed by other means is the

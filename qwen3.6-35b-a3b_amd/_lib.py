@@ -37,6 +37,10 @@ SYNC_BYTES = 512 * 1024
 # moe_block_forward_w_noalloc's static scratch (include/moe_gfx950.h)
 NOALLOC_SCRATCH_BYTES = 16 << 20
 NOALLOC_MAX_T = 120
+# the workspace's status word and test-hook word (int32 indices), and the status bit
+STATUS_WORD = 3
+TEST_HOOK_WORD = 4
+STATUS_SPIN_TIMEOUT = 1
 
 
 
@@ -92,6 +96,7 @@ SIGNATURES = {
                                          _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                          ctypes.POINTER(LayerWeightsC)]),
     "moe_workspace_init": (_I, [_VP, _SZ, _VP]),
+    "moe_workspace_status": (_I, [_VP, _SZ, _VP, _VP]),
     "moe_lm_head": (_I, [_VP, _I, _I, _I, _VP, _I, _I64, _VP, _I64, _VP, _VP]),
 }
 

@@ -71,14 +71,20 @@ def _xdt(x: torch.Tensor) -> int:
 _WS_CACHE: dict = {}
 
 
+def _ws_key(device: torch.device):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return idx, torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream
+
+
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached scratch buffer of at least nbytes on `device` (allocated by torch, not the library)."""
-    key = (device.index if device.index is not None else torch.cuda.current_device())
+    """A cached scratch buffer of at least nbytes for (device, the current stream), allocated by
+    torch (not the library) and initialised on that stream. Calls that share a workspace must be
+    ordered on one stream, so each stream gets its own."""
+    key = _ws_key(device)
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _check(L.lib.moe_workspace_init(_p(buf), buf.numel(),
-                                        ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)),
+        _check(L.lib.moe_workspace_init(_p(buf), buf.numel(), ctypes.c_void_p(key[1])),
                "workspace_init")
         _WS_CACHE[key] = buf
     return buf
@@ -88,16 +94,45 @@ def workspace_bytes(T: int, H: int, I: int, E: int, K: int, I_s: int) -> int:
     return int(L.lib.moe_workspace_bytes(T, H, I, E, K, I_s))
 
 
-def device_error_bits(device) -> int:
-    """The workspace's device-side error word of the single-launch decode layer: bit 0, a bounded
-    spin timed out (its workgroups were not all co-resident, or not placed on the XCDs round
-    robin as the single-launch decode layer assumes). Zero when every launch ran as designed.
-    Reading it synchronises."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
+def workspace_status(device) -> int:
+    """moe_workspace_status of the current stream's workspace on `device`: the status bits since the
+    last read (bit MOE_STATUS_SPIN_TIMEOUT: a bounded wait of the single-launch decode layer gave
+    up, and the rows of the workgroups that gave up are NaN), then cleared. 0 when no workspace
+    exists yet. Stream-ordered in the library; this helper then synchronises to return the value."""
+    key = _ws_key(device)
     buf = _WS_CACHE.get(key)
     if buf is None:
         return 0
-    return int(buf[:16].view(torch.int32)[3].item())
+    out = torch.empty(1, dtype=torch.int32, device=device)
+    _check(L.lib.moe_workspace_status(_p(buf), buf.numel(), _p(out), ctypes.c_void_p(key[1])),
+           "workspace_status")
+    return int(out.item())
+
+
+def set_test_hook(device, on: bool) -> None:
+    """Sets the current stream's workspace's test-hook word: while on, every bounded wait of the
+    single-launch decode layer reports a timeout after completing (include/moe_gfx950.h)."""
+    buf = workspace(device, L.SYNC_BYTES)
+    buf[4 * L.TEST_HOOK_WORD:4 * L.TEST_HOOK_WORD + 4].view(torch.int32).fill_(1 if on else 0)
+
+
+def device_error_bits(device) -> int:
+    """The status bits of every workspace this module holds on `device`, OR-ed, each read and
+    cleared (moe_workspace_status); 0 when every launch since the last read ran as designed.
+    Synchronises the device first, so work on any stream (graph replays included) is counted."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    torch.cuda.synchronize(idx)
+    st = ctypes.c_void_p(torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream)
+    bufs = [b for (d, _), b in _WS_CACHE.items() if d == idx]
+    if not bufs:
+        return 0
+    out = torch.zeros(len(bufs), dtype=torch.int32, device=device)
+    for i, buf in enumerate(bufs):
+        _check(L.lib.moe_workspace_status(_p(buf), buf.numel(), _p(out[i:i + 1]), st), "workspace_status")
+    bits = 0
+    for v in out.tolist():
+        bits |= int(v)
+    return bits
 
 
 # ---------------------------------------------------------------------------------- entry points

@@ -665,6 +665,12 @@ int moe_lm_head(const void* h, int h_dtype, int B, int H, const void* w, int w_f
                             (hipStream_t)stream);
 }
 
+int moe_workspace_status(void* ws, size_t ws_bytes, int32_t* status, void* stream) {
+  if (!ws || ws_bytes < kSyncBytes) return moe_set_error(MOE_E_ARG, "moe_workspace_status: workspace smaller than %zu bytes", kSyncBytes);
+  if (!status || (reinterpret_cast<uintptr_t>(status) & 3u)) return moe_set_error(MOE_E_ARG, "moe_workspace_status: status must be an aligned int32 pointer");
+  return moe_launch_take_status(reinterpret_cast<int*>(ws) + MOE_STATUS_WORD, status, (hipStream_t)stream);
+}
+
 int moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {
   if (!ws || ws_bytes < kSyncBytes) return moe_set_error(MOE_E_ARG, "moe_workspace_init: workspace smaller than %zu bytes", kSyncBytes);
   return moe_launch_zero_words(reinterpret_cast<int*>(ws), (int)(kSyncBytes / 4), (hipStream_t)stream);

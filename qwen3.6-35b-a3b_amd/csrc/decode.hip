@@ -334,6 +334,11 @@ __global__ void k_zero_words(int* p, int n) {
   if (i < n) p[i] = 0;
 }
 
+// the status word, read and cleared in one device-scope exchange
+__global__ void k_take_status(int* word, int32_t* out) {
+  if (threadIdx.x == 0) out[0] = atomicExch(word, 0);
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -341,6 +346,11 @@ using namespace moe;
 int moe_launch_zero_words(int* p, int n, hipStream_t st) {
   hipLaunchKernelGGL(k_zero_words, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
   return moe_check_launch("zero_words");
+}
+
+int moe_launch_take_status(int* word, int32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_take_status, dim3(1), dim3(64), 0, st, word, out);
+  return moe_check_launch("take_status");
 }
 
 int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st) {

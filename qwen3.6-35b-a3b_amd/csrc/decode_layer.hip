@@ -42,6 +42,9 @@
 // store) and writes it back incremented at the end, so no launch starts or ends on a contended
 // atomic. Every spin is bounded: on a timeout the workgroup records an error bit and carries on
 // (no hang).
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "moe_internal.h"
 #include "router_dev.h"
@@ -56,11 +59,30 @@ constexpr int kThreads = 512;           // 8 waves
 constexpr int kSpinLimit = 1 << 20;     // polls (each a memory round trip) before giving up
 constexpr int kOccPad = 5120;           // uint4s of LDS that keep the grid at one workgroup per CU
 // sync words (int32 index into the workspace's first kSyncBytes)
-constexpr int kErrWord = 3;             // error bits
+constexpr int kErrWord = MOE_STATUS_WORD;   // status bits (moe_workspace_status)
+constexpr int kHookWord = MOE_TEST_HOOK_WORD; // test hook: non-zero = every wait reports a timeout
 constexpr int kRoleEpoch = 114688;      // [xcd][kPer]: launches run by role (x, r), past the exchange
 
-// error bits (sync word 3)
-constexpr int kErrSpin = 1;             // a bounded wait timed out
+// status bits (sync word kErrWord)
+constexpr int kErrSpin = MOE_STATUS_SPIN_TIMEOUT;   // a bounded wait timed out
+
+// What a bounded wait does when it gives up: the status bit for the caller, and this workgroup's
+// LDS flag, which poisons the output rows the workgroup writes (NaN) at the end. With the test
+// hook set, every wait completes as usual and then reports a timeout, so the reporting path runs
+// on valid data and every workgroup still exits normally.
+struct Spin {
+  int* err;       // the workspace's status word
+  int* bad;       // this workgroup's flag (LDS)
+  int force;      // the test hook's value
+  __device__ __forceinline__ void give_up() const {
+    atomicOr(err, kErrSpin);
+    *bad = 1;
+  }
+  // called after each wait: report a forced timeout
+  __device__ __forceinline__ void done() const {
+    if (force) give_up();
+  }
+};
 
 struct LayerArgs {
   const void* x;
@@ -133,31 +155,15 @@ __device__ __forceinline__ uint4 xload4(__amdgpu_buffer_rsrc_t r, int off) {
 }
 __device__ __forceinline__ bool xfull(uint4 v) { return v.x && v.y && v.z && v.w; }
 
-// N words p[j * stride]: every missing word is loaded again, in parallel, until all are written
-template <int N>
-__device__ __forceinline__ void xwait(uint32_t* p, int stride, int* err, uint32_t* v) {
-#pragma unroll
-  for (int j = 0; j < N; ++j) v[j] = xload(p + j * stride);
-  for (int spins = 0;; ++spins) {
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < N; ++j) ok = ok && v[j] != 0u;
-    if (ok) return;
-    if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); return; }
-    __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-    for (int j = 0; j < N; ++j)
-      if (v[j] == 0u) v[j] = xload(p + j * stride);
-  }
-}
 // one 16-byte group at byte offset `off` of the buffer, same protocol
-__device__ __forceinline__ uint4 xwait4(__amdgpu_buffer_rsrc_t r, int off, int* err) {
+__device__ __forceinline__ uint4 xwait4(__amdgpu_buffer_rsrc_t r, int off, const Spin& sp) {
   uint4 v = xload4(r, off);
   for (int spins = 0; !xfull(v); ++spins) {
-    if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); break; }
+    if (spins >= kSpinLimit) { sp.give_up(); break; }
     __builtin_amdgcn_s_sleep(1);
     v = xload4(r, off);
   }
+  sp.done();
   return v;
 }
 
@@ -238,13 +244,14 @@ __device__ __forceinline__ uint4 lload4(__amdgpu_buffer_rsrc_t r, int off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ uint4 lwait4(__amdgpu_buffer_rsrc_t r, int off, int* err) {
+__device__ __forceinline__ uint4 lwait4(__amdgpu_buffer_rsrc_t r, int off, const Spin& sp) {
   uint4 v = lload4(r, off);
   for (int spins = 0; !xfull(v); ++spins) {
-    if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); break; }
+    if (spins >= kSpinLimit) { sp.give_up(); break; }
     __builtin_amdgcn_s_sleep(1);
     v = lload4(r, off);
   }
+  sp.done();
   return v;
 }
 
@@ -337,7 +344,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ float s_comb[2][K][8];      // [y | shared partial][slot | xcd][row]
   __shared__ float s_gate;
   __shared__ double s_red[2][kThreads / 64];
-  __shared__ int s_role[1];
+  __shared__ int s_role[2];               // the role's launch count, the test hook
+  __shared__ int s_bad;                   // a wait of this workgroup gave up
   __shared__ uint4 s_occ[kOccPad];
   // Q8_0 shared rows staged for the lanes' block reads: waves 5-6 their gate and up rows (2176 B
   // each, dwords [1088 (wave - 5), +1088)), wave 4 the 64 rows' 68-byte slices of this XCD
@@ -356,8 +364,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   // first, the input row and every routing-independent weight this role uses right behind it
   const int x = (int)blockIdx.x & (kXcd - 1), r = (int)blockIdx.x >> 3;
   const int j = kPer * x + r;            // combine rows [8j, 8j+8)
-  int ep = 0;
-  if (t == 0) ep = aload(a.sync + kRoleEpoch + kPer * x + r);
+  int ep = 0, hook = 0;
+  if (t == 0) {
+    ep = aload(a.sync + kRoleEpoch + kPer * x + r);
+    hook = aload(a.sync + kHookWord);
+  }
   float4 xin;
   if (XDT == MOE_DT_F32) {
     xin = reinterpret_cast<const float4*>(a.x)[t];
@@ -401,13 +412,18 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     sa = wave_sum_f64(sa);
     if (lane == 0) { s_red[0][wave] = ss; s_red[1][wave] = sa; }
   }
-  if (t == 0) s_role[0] = ep;
+  if (t == 0) {
+    s_role[0] = ep;
+    s_role[1] = hook;
+    s_bad = 0;
+  }
   // the LDS footprint keeps one workgroup per CU; this never-true branch keeps the array
   const bool never = a.out == reinterpret_cast<float*>(a.sync);
   if (never) s_occ[t] = make_uint4(t, 0, 0, 0);
   __syncthreads();
   if (never) atomicOr(err, (int)s_occ[t ^ 1].x);
   const uint32_t epoch = (uint32_t)s_role[0] + 1u;
+  const Spin sp{err, &s_bad, s_role[1]};
   // Q8_0 shared rows (34-byte blocks, 2-byte aligned; a row's block pairs are 4-byte aligned),
   // requested as contiguous bytes and staged through LDS (s_q8) just before use: waves 5-6 the gate
   // and up rows of their intermediate row (16-byte loads), wave 4 the 64 shared-down rows'
@@ -560,12 +576,21 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     for (int spins = 0;; ++spins) {
       const bool ok = lw[0] && lw[1] && lw[2] && lw[3];
       if (ok) break;
-      if (spins >= kSpinLimit) { atomicOr(err, kErrSpin); break; }
+      if (spins >= kSpinLimit) {
+        // a logit that never arrived counts as the lowest finite bf16 (-3.39e38), so no NaN
+        // reaches the selection, whose indices stay in range whatever the values
+        sp.give_up();
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (lw[q] == 0u) lw[q] = ~0xFF7Fu;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (lw[q] == 0u) lw[q] = lload(xr, 4 * (XW_LOG + 256 * x + lane + 64 * q));
     }
+    sp.done();
     uint32_t lb[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) lb[q] = ~lw[q] & 0xFFFFu;
@@ -594,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     // meanwhile: the shared-down partial over this XCD's 64 shared activations, rows
     // h = 64r + (lane >> 3) + 8q, published to the combining workgroups (agent scope)
     {
-      const uint4 v = lane < ISX / 4 ? lwait4(xr, 4 * (XW_SSH + ISX * x) + 16 * lane, err) : make_uint4(0, 0, 0, 0);
+      const uint4 v = lane < ISX / 4 ? lwait4(xr, 4 * (XW_SSH + ISX * x) + 16 * lane, sp) : make_uint4(0, 0, 0, 0);
       if (lane < ISX / 4)
         reinterpret_cast<float4*>(s_sh)[lane] = make_float4(xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w));
     }
@@ -690,7 +715,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 
   // ------------------------------------------------------------------------------ phase 3 --
   if (t < I / 4) {
-    const uint4 v = lwait4(xr, 4 * (XW_SR + I * x) + 16 * t, err);
+    const uint4 v = lwait4(xr, 4 * (XW_SR + I * x) + 16 * t, sp);
     reinterpret_cast<float4*>(s_k)[t] = make_float4(xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w));
   }
   __syncthreads();
@@ -752,7 +777,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     // y[k][8j..8j+7] for the 8 slots and the 8 XCDs' shared partials (two 16-byte groups each)
     if (t < 32) {
       const int k = t >> 2, kind = (t >> 1) & 1, half = t & 1;
-      const uint4 v = xwait4(xr, 4 * ((kind ? XW_SHP : XW_Y) + H * k + 8 * j) + 16 * half, err);
+      const uint4 v = xwait4(xr, 4 * ((kind ? XW_SHP : XW_Y) + H * k + 8 * j) + 16 * half, sp);
       float* o = &s_comb[kind][k][4 * half];
       o[0] = xdec(v.x); o[1] = xdec(v.y); o[2] = xdec(v.z); o[3] = xdec(v.w);
     }
@@ -768,9 +793,12 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       float shr = 0.0f;
 #pragma unroll
       for (int q = 0; q < kXcd; ++q) shr += s_comb[1][q][t];
-      if (a.routed_sum) a.routed_sum[h] = acc;
-      if (a.shared_out) a.shared_out[h] = s_gate * shr;
-      a.out[h] = comb_out(resid, acc, s_gate, shr);
+      // a wait of this workgroup gave up: its rows are NaN (the status word says so too)
+      const bool bad = s_bad != 0;
+      const float nan = __builtin_nanf("");
+      if (a.routed_sum) a.routed_sum[h] = bad ? nan : acc;
+      if (a.shared_out) a.shared_out[h] = bad ? nan : s_gate * shr;
+      a.out[h] = bad ? nan : comb_out(resid, acc, s_gate, shr);
     }
     // this role's launch count, for the next launch
     if (t == 0) astore(a.sync + kRoleEpoch + kPer * x + r, (int)epoch);
@@ -782,12 +810,17 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 using namespace moe;
 
 bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, int dn_fmt) {
-  static int ncu = -1;
+  // the CU count of the current device, cached per device (0: unknown, -1 not yet asked)
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> ncu_cache[kMaxDev];
+  static std::once_flag once;
+  std::call_once(once, [] { for (auto& c : ncu_cache) c.store(-1); });
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+  int ncu = ncu_cache[dev].load();
   if (ncu < 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      ncu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) ncu = 0;
+    ncu_cache[dev].store(ncu);
   }
   // 8 XCDs with at least 32 CUs each (MI355X: exactly 32)
   return ncu >= kG && ncu % kXcd == 0 && H == 2048 && I == 512 && E == 256 && K == 8 &&

@@ -138,6 +138,8 @@ int moe_launch_decode_fused(const MoeDecodeLaunch& L, hipStream_t st);
 int moe_launch_rmsnorm(const void* x, int x_dtype, int T, int H, const float* w, float eps,
                        float* out, hipStream_t st);
 int moe_launch_zero_words(int* p, int n, hipStream_t st);
+// *out = *word; *word = 0 (one device-scope exchange)
+int moe_launch_take_status(int* word, int32_t* out, hipStream_t st);
 
 // The first kSyncBytes of every workspace hold the library's device-side sync words (block
 // tickets, the decode layer's epoch, arrival counter and per-XCD tickets, its two exchange
