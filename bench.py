@@ -517,7 +517,9 @@ def main():
     # ---------------------------------------------------------------- prefill, config 3
     prefill = {}
     if not args.no_prefill:
-        prefill = prefill_c3(torch, synth, abi, layers[0], dev, args.prefill_steps)
+        lwp = synth.make_layer(seed=2, device=dev)              # config 3's seed
+        prefill = prefill_c3(torch, synth, abi, lwp, dev, args.prefill_steps)
+        del lwp
 
     # ---------------------------------------------------------------- prefill, config 4
     c4 = {} if args.no_c4 else prefill_c4(torch, pkg, dev, args.prefill_steps)

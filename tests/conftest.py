@@ -37,6 +37,15 @@ def layer_c0(pkg, dev):
 
 
 @pytest.fixture(scope="session")
+def layer_c3(pkg, dev):
+    """BASELINE config 3 weights: seed 2, Q4_K gate_up and down, uniform routing."""
+    from oracle import moe_oracle as O
+    lw = pkg.synth.make_layer(seed=2, device=dev)
+    torch.cuda.synchronize()
+    return lw, O.from_device(lw)
+
+
+@pytest.fixture(scope="session")
 def layer_zipf(pkg, dev):
     """BASELINE config 2 weights: seed 1, Zipf(1.1)-skewed router bias."""
     from oracle import moe_oracle as O

@@ -40,10 +40,10 @@ def test_c2_batched_decode_zipf(pkg, layer_zipf, dev):
         _compare(st, ref, tag=f"c2 path={path}")
 
 
-def test_c3_prefill_sampled_rows(pkg, layer_c0, dev):
-    """T = 4096 bf16 activations on the MFMA path; the block is row-independent, so the oracle
-    checks a seeded sample of 192 rows of the full-size run."""
-    lw, ow = layer_c0
+def test_c3_prefill_sampled_rows(pkg, layer_c3, dev):
+    """T = 4096 bf16 activations on the MFMA path (config 3: seed 2 weights and input); the block
+    is row-independent, so the oracle checks a seeded sample of 192 rows of the full-size run."""
+    lw, ow = layer_c3
     x = pkg.synth.make_input(4096, seed=2, device=dev, dtype=torch.bfloat16)
     st = pkg.block.moe_block(x, lw, pkg.load_geometry())
     rows = torch.randperm(4096, generator=torch.Generator().manual_seed(2))[:192]
