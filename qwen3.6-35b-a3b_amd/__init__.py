@@ -7,7 +7,7 @@ The directory name is not a Python identifier; load it with
                                            submodule_search_locations=["<repo>/qwen3.6-35b-a3b_amd"])
 (`__graft_entry__.load_package()` does exactly this).
 """
-from . import _lib, quant, weights, synth  # noqa: F401
+from . import _lib, quant, weights, synth, gguf  # noqa: F401
 from . import abi, block  # noqa: F401
 from .abi import Refused  # noqa: F401
 from .weights import LayerWeights, load_geometry  # noqa: F401
