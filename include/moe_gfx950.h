@@ -187,7 +187,7 @@ typedef struct moe_layer_weights {
  * optional next-layer hint (next: as moe_block_forward_prefetch, the router rows and norm weight of
  * a bf16-router next layer). Same outputs, limits and errors as moe_block_forward. The
  * single-launch decode layer takes a bf16 or f32 router and scalar gate, Q4_K gate/up (fused or
- * split) and Q4_K or Q5_K down; Q6_K down runs the three-launch decode path at T = 1. The next
+ * split), Q4_K, Q5_K or Q6_K down, and a bf16 or Q8_0 shared expert. The next
  * layer's router rows (bf16 or f32) and norm weight are the L2 warm-up hint.
  * Replaces engine/m3_forward.py:430-476 and engine/block_forward.py:670-681 on the policy-A
  * weights (engine/block_forward.py:211-231). */

@@ -326,8 +326,67 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
   return true;
 }
 
+// 32-bit word at a 2-byte-aligned byte offset of an LDS region (4-byte-aligned base): the two
+// dwords around it, realigned
+__device__ __forceinline__ uint32_t lds_u32_at(const uint32_t* base, int off) {
+  const int i = off >> 2, sh = off & 3;
+  return __builtin_amdgcn_alignbyte(base[i + 1], base[i], sh);
+}
+
+// Q6_K (210-byte block, 2-byte aligned in LDS at byte `blk` of `lds`): 64 of its elements against
+// the activations a[0..64): half g, planes k = 2m and 2m + 1, every l in [0, 32) —
+// e = 128 g + 32 k + l, q = (ql[64g + 32(k&1) + l] >> 4(k>>1)) & 15 | ((qh[32g + l] >> 2k) & 3) << 4,
+// value d * sc[8g + 2k + (l>>4)] * (q - 32) (tools/gguf_reader.py:299-322), summed as
+// d * sc * (sum a q - 32 sum a) per 16-element run.
+__device__ __forceinline__ float q6k_lane64_dot(const uint32_t* lds, int blk, int g, int m, const float* a) {
+  const int sh = blk & 3;
+  uint32_t ql[16], qh[8];
+  {
+    const int o = (blk + 64 * g) >> 2;
+    uint32_t w[17];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) w[i] = lds[o + i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ql[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+  }
+  {
+    const int o = (blk + 128 + 32 * g) >> 2;
+    uint32_t w[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w[i] = lds[o + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qh[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+  }
+  const uint32_t scw = lds_u32_at(lds, blk + 192 + 8 * g + 4 * m);
+  const uint32_t dw = lds[(blk + 208) >> 2] >> (8 * ((blk + 208) & 3));
+  const float d = f16_to_f32(dw & 0xFFFFu);
+  const uint32_t shl = 4u * (uint32_t)m;
+  float acc = 0.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t shh = 4u * (uint32_t)m + 2u * (uint32_t)h;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float dq = 0.0f, sa = 0.0f;
+#pragma unroll
+      for (int l = 16 * u; l < 16 * u + 16; ++l) {
+        const uint32_t qlb = ql[(32 * h + l) >> 2] >> (8 * (l & 3));
+        const uint32_t qhb = qh[l >> 2] >> (8 * (l & 3));
+        const float q = (float)(((qlb >> shl) & 15u) | (((qhb >> shh) & 3u) << 4));
+        const float av = a[32 * h + l];
+        dq = fmaf(av, q, dq);
+        sa += av;
+      }
+      const float sc = (float)(int8_t)(scw >> (8 * (2 * h + u)));
+      acc += d * sc * (dq - 32.0f * sa);
+    }
+  }
+  return acc;
+}
+
 // XDT: input x width; RDT: router row width (bf16, or f32 as the shipped artifact's ffn_gate_inp);
-// DFMT: routed down format (Q4_K, or Q5_K as the artifact's ffn_down_exps in 37 of 40 layers);
+// DFMT: routed down format (Q4_K, Q5_K as the artifact's ffn_down_exps in 37 of 40 layers, or
+// Q6_K as in its other 3, whose 2-byte-aligned 210-byte blocks are staged through LDS);
 // SFMT: shared-expert rows (bf16, or Q8_0 as the artifact's ffn_*_shexp)
 template <int XDT, int RDT, int DFMT, int SFMT>
 __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
@@ -399,8 +458,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   }
   // waves 5-6: shared gate row wx[0..3], up row wx[4..7]; wave 7: the scalar gate row wx[0..3];
   // wave 4: shared-down rows 64r + (lane >> 3) + 8q at cols 64x + 8 (lane & 7), q = 0..7
-  // the logit bias, read unconditionally (a device zero when there is none) after the weights
-  const float bias_e = *(a.bias ? a.bias + 8 * r + wave : &kZeroBias);
+  // the logit bias, read unconditionally (a device zero when there is none) after the weights, as
+  // a global-address-space load: a flat load outstanding would make the compiler wait for every
+  // earlier load (the router rows) before the first use of x
+  typedef const __attribute__((address_space(1))) float gfloat;
+  const float bias_e = *(gfloat*)(a.bias ? a.bias + 8 * r + wave : &kZeroBias);
   const float resid = (t < 8 && a.residual) ? a.residual[8 * j + t] : 0.0f;
   // norm: r = f32(1 / sqrt(mean(x^2) + eps)) in f64 (every square exact, one final rounding);
   // xl1 >= |input|_1 for the router's error bound, from sum |x_j nw_j| (exact products)
@@ -615,9 +677,78 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
         if (a.w_bf16_out) a.w_bf16_out[lane] = s_wb[lane];
       }
     }
-  } else if (wave == 4) {
-    // meanwhile: the shared-down partial over this XCD's 64 shared activations, rows
-    // h = 64r + (lane >> 3) + 8q, published to the combining workgroups (agent scope)
+  }
+  __syncthreads();
+  const int e = s_ids[x];
+  // phase-3 weights: down rows h = 64 r + 2 (t >> 4) + pass of expert e; 16 lanes per row,
+  // lane: super-block b = l16 >> 3, 16-byte nibble chunk c = l16 & 7 (requested with phase 2's)
+  // Q4_K: header + nibble chunk (two loads); Q5_K: also the chunk's 16 qh bytes (tools/gguf_reader.py:271-296)
+  constexpr int kDB = DFMT == MOE_FMT_Q6_K ? 210 : DFMT == MOE_FMT_Q5_K ? 176 : 144;
+  constexpr int kDQs = DFMT == MOE_FMT_Q5_K ? 48 : 16;
+  constexpr size_t drowb = (I / 256) * kDB;
+  // Q6_K: the workgroup's 64 down rows are one 16-byte-aligned run of 64 * 420 bytes, loaded as
+  // uint4 (4 per thread, the index clamped so no load sits in a branch) and staged in s_occ
+  constexpr int kQ6U4 = 64 * (int)drowb / 16;
+  static_assert(DFMT != MOE_FMT_Q6_K || (kQ6U4 <= 4 * kThreads && 4 * kThreads <= kOccPad), "Q6_K staging");
+  uint4 dh[2], dq[2], dqh[2];
+  uint4 d60, d61, d62, d63;              // named, not an array: a loop-indexed array goes to LDS
+  {
+    // routed gate/up: intermediate rows i0, i0+1 (gate and up) per wave
+    const int i0 = 16 * r + 2 * wave;
+    const int b = lane >> 3, c = lane & 7, gq = c >> 1, l0 = 16 * (c & 1);
+    constexpr size_t rowb = (H / 256) * 144;
+    const uint8_t* gbase = a.gu + (size_t)e * a.gu_estride;
+    const uint8_t* ubase = a.gu_up + (size_t)e * a.gu_estride;
+    uint4 hdr[4], qs[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint8_t* p = ((q & 1) ? ubase : gbase) + (size_t)(i0 + (q >> 1)) * rowb + (size_t)b * 144;
+      hdr[q] = *reinterpret_cast<const uint4*>(p);
+      qs[q] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
+    }
+    if (DFMT == MOE_FMT_Q6_K) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.dn + ((size_t)e * H + 64 * r) * drowb);
+      d60 = src[t];
+      d61 = src[min(t + kThreads, kQ6U4 - 1)];
+      d62 = src[min(t + 2 * kThreads, kQ6U4 - 1)];
+      d63 = src[min(t + 3 * kThreads, kQ6U4 - 1)];
+    } else {
+      const int db = l16 >> 3, dc = l16 & 7;
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass) {
+        const int h = 64 * r + 2 * (t >> 4) + pass;
+        const uint8_t* p = a.dn + ((size_t)e * H + h) * drowb + (size_t)db * kDB;
+        dh[pass] = *reinterpret_cast<const uint4*>(p);
+        dq[pass] = *reinterpret_cast<const uint4*>(p + kDQs + 16 * dc);
+        if (DFMT == MOE_FMT_Q5_K) dqh[pass] = *reinterpret_cast<const uint4*>(p + 16 + 16 * (dc & 1));
+      }
+    }
+    float xl[16], xh[16];
+    {
+      const float* xp = s_x + 256 * b + 64 * gq + l0;
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        const float4 u0 = *reinterpret_cast<const float4*>(xp + i);
+        const float4 u1 = *reinterpret_cast<const float4*>(xp + 32 + i);
+        xl[i] = u0.x; xl[i + 1] = u0.y; xl[i + 2] = u0.z; xl[i + 3] = u0.w;
+        xh[i] = u1.x; xh[i + 1] = u1.y; xh[i + 2] = u1.z; xh[i + 3] = u1.w;
+      }
+    }
+    float sxl = 0.0f, sxh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { sxl += xl[i]; sxh += xh[i]; }
+    float acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = wave_sum_f32(q4k_chunk_dot(hdr[q], qs[q], gq, xl, xh, sxl, sxh));
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (lane == q) lstore(xr, 4 * (XW_SR + I * x + i0 + q), xenc(silu_f32(acc[2 * q]) * acc[2 * q + 1]));
+  }
+
+  // wave 4, while waves 0-1 wait for the slot's activations: the shared-down partial over this
+  // XCD's 64 shared activations (ready since phase 1), rows h = 64r + (lane >> 3) + 8q, published
+  // to the combining workgroups (agent scope); off the routing's path to the expert loads
+  if (wave == 4) {
     {
       const uint4 v = lane < ISX / 4 ? lwait4(xr, 4 * (XW_SSH + ISX * x) + 16 * lane, sp) : make_uint4(0, 0, 0, 0);
       if (lane < ISX / 4)
@@ -657,69 +788,34 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       acc += dpp_f32<0x141>(acc);        // sum over the 8 lanes of the row
       if ((lane & 7) == 0) xstore(xb + XW_SHP + H * x + 64 * r + (lane >> 3) + 8 * q, xenc(acc));
     }
-  }
-  __syncthreads();
-  const int e = s_ids[x];
-  // phase-3 weights: down rows h = 64 r + 2 (t >> 4) + pass of expert e; 16 lanes per row,
-  // lane: super-block b = l16 >> 3, 16-byte nibble chunk c = l16 & 7 (requested with phase 2's)
-  // Q4_K: header + nibble chunk (two loads); Q5_K: also the chunk's 16 qh bytes (tools/gguf_reader.py:271-296)
-  constexpr int kDB = DFMT == MOE_FMT_Q5_K ? 176 : 144, kDQs = DFMT == MOE_FMT_Q5_K ? 48 : 16;
-  constexpr size_t drowb = (I / 256) * kDB;
-  uint4 dh[2], dq[2], dqh[2];
-  {
-    // routed gate/up: intermediate rows i0, i0+1 (gate and up) per wave
-    const int i0 = 16 * r + 2 * wave;
-    const int b = lane >> 3, c = lane & 7, gq = c >> 1, l0 = 16 * (c & 1);
-    constexpr size_t rowb = (H / 256) * 144;
-    const uint8_t* gbase = a.gu + (size_t)e * a.gu_estride;
-    const uint8_t* ubase = a.gu_up + (size_t)e * a.gu_estride;
-    uint4 hdr[4], qs[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint8_t* p = ((q & 1) ? ubase : gbase) + (size_t)(i0 + (q >> 1)) * rowb + (size_t)b * 144;
-      hdr[q] = *reinterpret_cast<const uint4*>(p);
-      qs[q] = *reinterpret_cast<const uint4*>(p + 16 + 16 * c);
     }
-    {
-      const int db = l16 >> 3, dc = l16 & 7;
-#pragma unroll
-      for (int pass = 0; pass < 2; ++pass) {
-        const int h = 64 * r + 2 * (t >> 4) + pass;
-        const uint8_t* p = a.dn + ((size_t)e * H + h) * drowb + (size_t)db * kDB;
-        dh[pass] = *reinterpret_cast<const uint4*>(p);
-        dq[pass] = *reinterpret_cast<const uint4*>(p + kDQs + 16 * dc);
-        if (DFMT == MOE_FMT_Q5_K) dqh[pass] = *reinterpret_cast<const uint4*>(p + 16 + 16 * (dc & 1));
-      }
-    }
-    float xl[16], xh[16];
-    {
-      const float* xp = s_x + 256 * b + 64 * gq + l0;
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const float4 u0 = *reinterpret_cast<const float4*>(xp + i);
-        const float4 u1 = *reinterpret_cast<const float4*>(xp + 32 + i);
-        xl[i] = u0.x; xl[i + 1] = u0.y; xl[i + 2] = u0.z; xl[i + 3] = u0.w;
-        xh[i] = u1.x; xh[i + 1] = u1.y; xh[i + 2] = u1.z; xh[i + 3] = u1.w;
-      }
-    }
-    float sxl = 0.0f, sxh = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { sxl += xl[i]; sxh += xh[i]; }
-    float acc[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = wave_sum_f32(q4k_chunk_dot(hdr[q], qs[q], gq, xl, xh, sxl, sxh));
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      if (lane == q) lstore(xr, 4 * (XW_SR + I * x + i0 + q), xenc(silu_f32(acc[2 * q]) * acc[2 * q + 1]));
-  }
 
   // ------------------------------------------------------------------------------ phase 3 --
+  if (DFMT == MOE_FMT_Q6_K) {
+    s_occ[t] = d60;
+    s_occ[t + kThreads] = d61;
+    s_occ[t + 2 * kThreads] = d62;
+    s_occ[t + 3 * kThreads] = d63;
+  }
   if (t < I / 4) {
     const uint4 v = lwait4(xr, 4 * (XW_SR + I * x) + 16 * t, sp);
     reinterpret_cast<float4*>(s_k)[t] = make_float4(xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w));
   }
   __syncthreads();
-  {
+  if (DFMT == MOE_FMT_Q6_K) {
+    // down row 64r + (t >> 3): 8 lanes per row, 64 elements each, from the staged rows
+    const int rho = t >> 3, s8 = t & 7, b = s8 >> 2, g = (s8 >> 1) & 1, m = s8 & 1;
+    float v = q6k_lane64_dot(reinterpret_cast<const uint32_t*>(s_occ), (int)drowb * rho + kDB * b, g, m,
+                             s_k + 256 * b + 128 * g + 64 * m);
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);              // the 8 lanes of the row
+    if (s8 == 0) {
+      const int h = 64 * r + rho;
+      xstore(xb + XW_Y + H * x + h, xenc(v));
+      if (a.expert_raw) a.expert_raw[(size_t)x * H + h] = v;
+    }
+  } else {
     const int b = l16 >> 3, c = l16 & 7, gq = c >> 1, l0 = 16 * (c & 1);
     const float* sp = s_k + 256 * b + 64 * gq + l0;
     float xl[16], xh[16], sxl = 0.0f, sxh = 0.0f;
@@ -824,7 +920,8 @@ bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, 
   }
   // 8 XCDs with at least 32 CUs each (MI355X: exactly 32)
   return ncu >= kG && ncu % kXcd == 0 && H == 2048 && I == 512 && E == 256 && K == 8 &&
-         Is == 512 && gu_fmt == MOE_FMT_Q4_K && (dn_fmt == MOE_FMT_Q4_K || dn_fmt == MOE_FMT_Q5_K);
+         Is == 512 && gu_fmt == MOE_FMT_Q4_K &&
+         (dn_fmt == MOE_FMT_Q4_K || dn_fmt == MOE_FMT_Q5_K || dn_fmt == MOE_FMT_Q6_K);
 }
 
 namespace {
@@ -833,6 +930,8 @@ template <int XDT, int RDT, int SFMT>
 void launch_layer_sfmt(int dn_fmt, const LayerArgs& a, hipStream_t st) {
   if (dn_fmt == MOE_FMT_Q5_K)
     hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q5_K, SFMT>), dim3(kG), dim3(kThreads), 0, st, a);
+  else if (dn_fmt == MOE_FMT_Q6_K)
+    hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q6_K, SFMT>), dim3(kG), dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL((k_dec_layer<XDT, RDT, MOE_FMT_Q4_K, SFMT>), dim3(kG), dim3(kThreads), 0, st, a);
 }

@@ -347,3 +347,28 @@ def test_block_output_independent_of_tie_slot_order(pkg, layer_c0, dev, T):
     assert torch.equal(a["combined_out"], b["combined_out"])
     ref = O.route(x.cpu(), router.cpu(), 8, None)
     assert torch.equal(b["topk_ids"].cpu().long(), ref["topk_ids"])
+
+
+@pytest.mark.parametrize("fmt", ["q5k", "q6k"])
+def test_decode_single_launch_q5k_q6k_down(pkg, layer_q5k, layer_q6k, dev, fmt):
+    """Q5_K and Q6_K down (the artifact's widths) in the single-launch decode layer, with the
+    post-attention norm and residual fused: routing bit-exact vs the oracle on 16 tokens and the
+    same results as the three-launch path within the block bars."""
+    lw, ow = layer_q5k if fmt == "q5k" else layer_q6k
+    L = pkg._lib
+    w = pkg.synth.make_norm_weight(seed=61, device=dev)
+    xs = pkg.synth.make_input(16, seed=60, device=dev)
+    ref = O.residual_step(xs.cpu(), ow, w.cpu(), 1e-6)
+    outs = {}
+    for path in (L.MOE_PATH_GEMV, L.MOE_PATH_GEMV_MULTI):
+        got, ids = [], []
+        for i in range(16):
+            x1 = xs[i:i + 1].contiguous()
+            st = pkg.abi.block_forward(x1, lw, path=path, stages={"topk_ids"}, residual=x1, norm_w=w)
+            got.append(st["combined_out"])
+            ids.append(st["topk_ids"])
+        torch.cuda.synchronize()
+        assert torch.equal(torch.cat(ids).cpu().long(), ref["topk_ids"]), (fmt, path)
+        outs[path] = torch.cat(got)
+        assert_close(outs[path], ref["x_out"], f"{fmt} decode path {path}")
+    assert pkg.abi.device_error_bits(dev) == 0
