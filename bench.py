@@ -24,6 +24,8 @@ Usage:
   python bench.py --pmc [--no-hint]          short decode workload + copy calibration (for rocprofv3 --pmc)
   python bench.py --pmc-summary DF DW [DFH DWH]   traffic summary (markdown) from --pmc runs
   python bench.py --stats-summary DIR [CMD]   kernel table (markdown) from rocprofv3 --kernel-trace --stats
+  python bench.py --pmc-prefill               config-3 prefill workload (for rocprofv3 --pmc passes)
+  python bench.py --pmc-prefill-summary DIR_A DIR_T   MFMA counter summary (markdown) of the GEMMs
 """
 from __future__ import annotations
 
@@ -82,6 +84,10 @@ def parse():
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="DIR_FETCH DIR_WRITE of --pmc --no-hint runs [then of --pmc runs]")
     ap.add_argument("--stats-summary", nargs="+", metavar="DIR [CMD]")
+    ap.add_argument("--pmc-prefill", action="store_true",
+                    help="config-3 prefill steps only, untimed (what the MFMA counter passes profile)")
+    ap.add_argument("--pmc-prefill-summary", nargs=2, metavar=("DIR_PMC", "DIR_TRACE"),
+                    help="MFMA counter summary from a --pmc run and a --kernel-trace run of --pmc-prefill")
     return ap.parse_args()
 
 
@@ -247,6 +253,87 @@ def stats_summary(d: str, cmd: str) -> str:
     return "\n".join(out) + "\n"
 
 
+PREFILL_PMC = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_BUSY_CU_CYCLES",
+               "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_LDS", "GRBM_GUI_ACTIVE"]
+PREFILL_KERNELS = {"k_gemm4_gateup": 137438953472.0, "k_gemm4_down": 68719476736.0}   # FLOP per launch at T = 4096
+N_CU, N_SIMD = 256, 4
+
+
+def pmc_prefill_summary(dir_pmc: str, dir_trace: str) -> str:
+    """Markdown summary of the config-3 grouped GEMMs from one rocprofv3 --pmc pass (PREFILL_PMC)
+    and one --kernel-trace pass of `bench.py --pmc-prefill`: medians per dispatch of each counter,
+    the f16 MFMA FLOPs the counters count (MOPS x 512) against the algorithmic FLOPs, and two
+    utilisations: achieved = counted FLOPs / kernel duration / 2.5 PFLOP/s, and MFMA busy =
+    SQ_VALU_MFMA_BUSY_CYCLES / (SQ_BUSY_CU_CYCLES x 4 SIMDs)."""
+    import statistics
+    per = {c: _per_dispatch(dir_pmc, c) for c in PREFILL_PMC}
+    files = glob.glob(os.path.join(dir_trace, "**", "*kernel_stats.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_stats.csv under {dir_trace}")
+    dur = {}
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                dur[r["Name"]] = float(r["AverageNs"])
+    lines = [
+        "# Config-3 prefill grouped GEMMs: MFMA counters (rocprofv3 --pmc)", "",
+        "Commands (GPU box, repo root):", "",
+        "    rocprofv3 --pmc " + " ".join(PREFILL_PMC) + " --kernel-include-regex 'k_gemm4' "
+        "--output-format csv -d /tmp/ppmc -o p -- python3 bench.py --pmc-prefill",
+        "    rocprofv3 --kernel-trace --stats --kernel-include-regex 'k_gemm4' --output-format csv "
+        "-d /tmp/ptr -o t -- python3 bench.py --pmc-prefill",
+        "    python3 bench.py --pmc-prefill-summary /tmp/ppmc /tmp/ptr", "",
+        "Per dispatch (median over the run's dispatches). FLOP(counted) = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512",
+        "(it includes the zero rows of partly filled row tiles); issued = FLOP(counted) / average kernel",
+        "duration; algorithmic = FLOP(algorithmic) / average kernel duration; % of peak uses 2.5 PFLOP/s",
+        "(dense f16/bf16);",
+        f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (SQ_BUSY_CU_CYCLES x {N_SIMD}).", "",
+        "| kernel | dispatches | avg us | FLOP algorithmic | FLOP counted | algorithmic TFLOP/s | algorithmic % "
+        "of peak | issued TFLOP/s | MFMA busy % | SQ_WAIT_ANY / SQ_WAVE_CYCLES | LDS bank conflicts / LDS insts |",
+        "|---|---|---|---|---|---|---|---|---|---|---|"]
+    out = {}
+    for kname, flop_alg in PREFILL_KERNELS.items():
+        med = {}
+        for c in PREFILL_PMC:
+            ks = [k for k in per[c] if kname in k]
+            if not ks:
+                raise SystemExit(f"no {kname} dispatch with counter {c}")
+            med[c] = statistics.median(v for k in ks for v in per[c][k])
+        n = sum(len(per[PREFILL_PMC[0]][k]) for k in per[PREFILL_PMC[0]] if kname in k)
+        us = statistics.median(v for k, v in dur.items() if kname in k) / 1e3
+        flop = med["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0
+        tf = flop / (us * 1e-6) / 1e12
+        tfa = flop_alg / (us * 1e-6) / 1e12
+        busy = med["SQ_VALU_MFMA_BUSY_CYCLES"] / max(med["SQ_BUSY_CU_CYCLES"] * N_SIMD, 1.0)
+        wait = med["SQ_WAIT_ANY"] / max(med["SQ_WAVE_CYCLES"], 1.0)
+        conf = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_INSTS_LDS"], 1.0)
+        out[kname] = dict(us=us, tflops=tfa, frac=tfa / BF16_PEAK_TFLOPS, issued_tflops=tf, busy=busy)
+        lines.append(f"| {kname} | {n} | {us:.1f} | {flop_alg:.4g} | {flop:.4g} | {tfa:.0f} | "
+                     f"{100 * tfa / BF16_PEAK_TFLOPS:.1f} | {tf:.0f} | {100 * busy:.1f} | {wait:.3f} | {conf:.2f} |")
+    lines += ["", "Raw medians per dispatch:", "", "| kernel | " + " | ".join(PREFILL_PMC) + " |",
+              "|---|" + "---|" * len(PREFILL_PMC)]
+    for kname in PREFILL_KERNELS:
+        vals = []
+        for c in PREFILL_PMC:
+            vals.append(statistics.median(v for k in per[c] if kname in k for v in per[c][k]))
+        lines.append(f"| {kname} | " + " | ".join(f"{v:.4g}" for v in vals) + " |")
+    lines += ["", "prefill_gemm_summary: " + json.dumps({k: {kk: round(vv, 4) for kk, vv in v.items()}
+                                                       for k, v in out.items()})]
+    return "\n".join(lines) + "\n"
+
+
+PREFILL_PMC_SUMMARY = ROOT / "profiles" / "prefill_c3_pmc.md"
+
+
+def committed_prefill_pmc():
+    """The GEMMs' counter figures from the committed summary (or None)."""
+    try:
+        m = re.search(r"prefill_gemm_summary:\s*(\{.*\})", PREFILL_PMC_SUMMARY.read_text())
+        return json.loads(m.group(1)) if m else None
+    except (OSError, ValueError):
+        return None
+
+
 def committed_traffic():
     try:
         m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", TRAFFIC_SUMMARY.read_text())
@@ -393,6 +480,9 @@ def main():
             raise SystemExit("--pmc-summary takes DIR_FETCH DIR_WRITE [DIR_FETCH_HINT DIR_WRITE_HINT]")
         print(pmc_summary(*args.pmc_summary), end="")
         return
+    if args.pmc_prefill_summary:
+        print(pmc_prefill_summary(*args.pmc_prefill_summary), end="")
+        return
     if args.stats_summary:
         d = args.stats_summary[0]
         print(stats_summary(d, " ".join(args.stats_summary[1:]) or "(not given)"), end="")
@@ -420,6 +510,16 @@ def main():
     if args.lm_head_only:
         r = lm_head_bench(torch, pkg, dev)
         print(json.dumps({k: round(v, 3) for k, v in r.items()}), flush=True)
+        return
+
+    if args.pmc_prefill:
+        lwp = synth.make_layer(seed=2, device=dev)
+        xp = synth.make_input(4096, seed=2, device=dev, dtype=torch.bfloat16)
+        outp = torch.empty(4096, 2048, dtype=torch.float32, device=dev)
+        for _ in range(3):
+            abi.block_forward(xp, lwp, out=outp)
+        torch.cuda.synchronize()
+        log("pmc prefill workload done: 3 config-3 blocks")
         return
 
     if args.prefill_only:
@@ -568,6 +668,7 @@ def main():
                      "traffic": traffic, "kernel": DECODE_KERNEL,
                      "bytes_per_launch": active, "avg_us": round(ms_k * 1000, 3)},
         "cpu_baseline": cpu,
+        "prefill_gemm_counters": committed_prefill_pmc(),
     }
     result.update(c2)
     result.update({k: round(v, 3) for k, v in art.items()})

@@ -3,9 +3,10 @@
 // torch.argsort(ids.flatten(), stable=True) returns. Integer work only, so bit-exact by design.
 //
 // P <= 64 (decode): one wave ranks every pair directly. P <= 1024: one block runs the three
-// phases below. Otherwise: per-chunk histograms -> one-block scan -> per-chunk stable scatter, where ranks
-// inside a 256-pair round come from wave-level id matching (8 ballots on the id bits) and a
-// per-wave count table, so no atomics decide any position.
+// phases below. Otherwise two launches: per-chunk histograms, then per chunk one block that sums
+// the histograms itself (totals, scan, its own chunk's start positions) and scatters its chunk
+// stably, where ranks inside a 256-pair round come from wave-level id matching (8 ballots on the
+// id bits) and a per-wave count table, so no atomics decide any position.
 #include "common.h"
 #include "moe_internal.h"
 
@@ -94,34 +95,6 @@ __device__ int block_exclusive_scan(int v, int* tmp, int* total) {
   return incl - v;
 }
 
-// phase 2 (one block): expert totals, offsets, hit list; hist[c][e] becomes the start position of
-// chunk c's pairs of expert e.
-__global__ __launch_bounds__(256) void k_sort_scan(int32_t* __restrict__ hist, int nchunks, int P,
-                                                   int E, int32_t* __restrict__ offsets,
-                                                   int32_t* __restrict__ hit_list) {
-  __shared__ int tmp[256];
-  const int e = threadIdx.x;
-  int tot = 0;
-  if (e < E)
-    for (int c = 0; c < nchunks; ++c) tot += hist[(size_t)c * E + e];
-  int tsum;
-  const int base = block_exclusive_scan(e < E ? tot : 0, tmp, &tsum);
-  if (e < E) {
-    offsets[e] = base;
-    int run = base;
-    for (int c = 0; c < nchunks; ++c) {
-      const int v = hist[(size_t)c * E + e];
-      hist[(size_t)c * E + e] = run;
-      run += v;
-    }
-  }
-  if (e == 0) offsets[E] = tsum;   // == P unless out-of-range ids were dropped
-  int hsum;
-  const int hidx = block_exclusive_scan((e < E && tot > 0) ? 1 : 0, tmp, &hsum);
-  if (e < E && tot > 0) hit_list[1 + hidx] = e;
-  if (e == 0) hit_list[0] = hsum;
-}
-
 // Stable scatter of the pairs [base, base + kChunk) given the start position of the chunk's pairs
 // of every expert (start_row[e]): ranks inside a 256-pair round come from wave-level id matching
 // and per-wave counts, run[e] carries them across rounds. run (LDS, 256 ints) must be zero.
@@ -162,16 +135,49 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, int P, int E, int
   }
 }
 
-// phase 3: stable scatter of each chunk
-__global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int P,
-                                                      int E, const int32_t* __restrict__ start,
-                                                      int32_t* __restrict__ sorted_pairs,
-                                                      int32_t* __restrict__ pair_pos) {
-  __shared__ int run[256];
+// phases 2 and 3 in one launch: every block sums the chunk histograms itself (expert totals and
+// its own chunk's prefix; 4 loads in flight per step), scans the totals, and scatters its chunk;
+// block 0 also writes the offsets and the hit list. hist[c][e] is only read.
+__global__ __launch_bounds__(256) void k_sort_scan_scatter(const int32_t* __restrict__ ids, int P, int E,
+                                                           const int32_t* __restrict__ hist, int nchunks,
+                                                           int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ sorted_pairs,
+                                                           int32_t* __restrict__ pair_pos,
+                                                           int32_t* __restrict__ hit_list) {
+  __shared__ int start[256], tmp[256], run[256];
   __shared__ int wcnt[4][256];
-  run[threadIdx.x] = 0;
-  scatter_chunk(ids, P, E, blockIdx.x * kChunk, start + (size_t)blockIdx.x * E, sorted_pairs,
-                pair_pos, run, wcnt);
+  const int e = threadIdx.x, c0 = blockIdx.x;
+  run[e] = 0;
+  int tot = 0, pre = 0;
+  if (e < E) {
+    int c = 0;
+    for (; c + 4 <= nchunks; c += 4) {
+      const int v0 = hist[(size_t)c * E + e], v1 = hist[(size_t)(c + 1) * E + e];
+      const int v2 = hist[(size_t)(c + 2) * E + e], v3 = hist[(size_t)(c + 3) * E + e];
+      tot += v0 + v1 + v2 + v3;
+      pre += (c < c0 ? v0 : 0) + (c + 1 < c0 ? v1 : 0) + (c + 2 < c0 ? v2 : 0) + (c + 3 < c0 ? v3 : 0);
+    }
+    for (; c < nchunks; ++c) {
+      const int v = hist[(size_t)c * E + e];
+      tot += v;
+      pre += c < c0 ? v : 0;
+    }
+  }
+  int tsum;
+  const int base = block_exclusive_scan(e < E ? tot : 0, tmp, &tsum);
+  start[e] = base + pre;
+  if (c0 == 0) {
+    if (e < E) offsets[e] = base;
+    if (e == 0) offsets[E] = tsum;   // == P unless out-of-range ids were dropped
+  }
+  int hsum;
+  const int hidx = block_exclusive_scan((e < E && tot > 0) ? 1 : 0, tmp, &hsum);
+  if (c0 == 0) {
+    if (e < E && tot > 0) hit_list[1 + hidx] = e;
+    if (e == 0) hit_list[0] = hsum;
+  }
+  __syncthreads();
+  scatter_chunk(ids, P, E, c0 * kChunk, start, sorted_pairs, pair_pos, run, wcnt);
 }
 
 // 64 < P <= kChunk: the three phases in one block (histogram, scan, the one chunk's scatter), so
@@ -255,9 +261,8 @@ int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t*
   const int nchunks = (P + kChunk - 1) / kChunk;
   int32_t* hist = reinterpret_cast<int32_t*>(ws);
   hipLaunchKernelGGL(k_sort_hist, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist);
-  hipLaunchKernelGGL(k_sort_scan, dim3(1), dim3(256), 0, st, hist, nchunks, P, E, offsets, hit_list);
-  hipLaunchKernelGGL(k_sort_scatter, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, sorted_pairs,
-                     pair_pos);
+  hipLaunchKernelGGL(k_sort_scan_scatter, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, nchunks,
+                     offsets, sorted_pairs, pair_pos, hit_list);
   return moe_check_launch("sort");
 }
 
