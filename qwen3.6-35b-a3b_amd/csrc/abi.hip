@@ -228,13 +228,14 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
       MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
       x16 = c;
     }
-    if (gu_fmt == MOE_FMT_Q4_K)
+    // gemm4's persistent item stream needs two super-blocks per item (H, I >= 512)
+    if (gu_fmt == MOE_FMT_Q4_K && H >= 512)
       MOE_TRY(moe_launch_gemm4_gateup(x16, gate, up, estride, tiles, max_tiles, offsets, sorted_pairs,
                                       K, H, I, S, st));
     else
       MOE_TRY(moe_launch_gemm3_gateup(x16, gate, up, gu_fmt, estride, tiles, max_tiles, T, offsets,
                                       sorted_pairs, K, H, I, S, st));
-    if (dn_fmt == MOE_FMT_Q4_K)
+    if (dn_fmt == MOE_FMT_Q4_K && I >= 512)
       return moe_launch_gemm4_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, st);
     return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, st);
   }

@@ -1,22 +1,33 @@
 // Prefill-path grouped GEMM for Q4_K experts with the weight decode in the MFMA waves
 // (gfx950, v_mfma_f32_32x32x16_f16, f32 accumulation).
 //
-// Work: one tile of up to 160 sorted (token, slot) rows of one expert (k_build_tiles, 160-row
-// tiles) times one 256-row weight slab per block (gate_up: 128 gate + the matching 128 up rows;
-// down: 256 rows), tiles dealt to XCDs so the slabs of one tile share its activation rows in L2.
-// Block = 8 waves:
-//   producers (waves 4..7) only move bytes. Raw Q4_K super-blocks (256 K, 144 B per row) go to an
-//     LDS ring of two super-blocks, nine lanes per row so a load instruction covers seven whole
-//     rows; f16 activation rows go to an LDS ring of four 64-wide K steps (eight lanes per
-//     128-byte row segment, 16-byte chunks XOR-swizzled by row so fragment reads spread over
-//     the banks). Both are requested four steps / one super-block ahead in registers.
-//   consumers (waves 0..3) read their two 32-row weight groups' raw nibbles and scales from LDS,
-//     decode them in registers straight into MFMA B fragments, and run the MFMAs; each owns all
-//     160 rows x (32 gate + 32 up) columns (gate_up) or 64 columns (down). The decode is VALU
-//     work that issues while the wave's earlier MFMAs execute.
-// One barrier per K step hands the rings over. The decode arithmetic and the k order of every
-// MFMA equal gemm3.hip's (q * f16(d sc) + f16(-dmin m) on the f16 mantissa trick), so both give
-// the same bits.
+// Work item: one tile of up to 160 sorted (token, slot) rows of one expert (k_build_tiles,
+// 160-row tiles, largest first) times one 256-row weight slab (gate_up: 128 gate + the matching
+// 128 up rows; down: 256 rows). The grid is persistent: two blocks per CU, block b serving XCD
+// b % 8 and taking that XCD's items (tiles x, x + 8, ... times the slabs) with stride
+// gridDim.x / 8, so the slabs of one tile run side by side on one XCD and share its rows in L2.
+//
+// Block = 4 waves (one per SIMD) and 80 KB of LDS, so each SIMD runs two independent waves: one
+// block's MFMAs cover the other's waits. Operands reach LDS by direct global->LDS loads
+// (global_load_lds_dwordx4, no registers): every wave issues its share of the next K step's
+// activation chunks, of the raw nibble bytes three steps ahead and of the next super-block's
+// 16-byte headers, and waits for its own loads with explicit vmcnt counts before the step's
+// barrier. The K steps of consecutive items form one stream: the last super-block of an item
+// issues the next item's first loads, so an item's epilogue runs while the next one's operands
+// arrive. LDS rings:
+//   A[2]:  f16 activations of one 64-wide K step, 160 rows x 128 B, 16-byte chunk c of row m at
+//          chunk c ^ swz(m) (swz(m) = (m ^ m >> 1) & 7, so the fragment reads of 8 or 16 lanes
+//          hit distinct banks under either a 32- or a 64-bank layout);
+//   Q[4]:  the 32 nibble bytes of one K step for 256 weight rows, half h of row n at h ^ bit;
+//   Hd[2]: the 16-byte header (d, dmin, 12 scale bytes) of one super-block for 256 rows.
+// Each wave owns all 160 rows x (32 gate + 32 up) columns (gate_up) or 64 columns (down), reads
+// its rows' raw bytes and headers from LDS, decodes them in registers straight into MFMA B
+// fragments (q * f16(d sc) + f16(-dmin m) on the f16 mantissa trick) and runs the MFMAs.
+// k order inside a K step: lane half h takes nibble bytes 16h..16h+15 of the step, so substep
+// ss covers k = 32 (ss >> 1) + 16 h + 8 (ss & 1) + 0..7 and the activation fragments follow.
+// Results leave through raw buffer stores whose descriptor ends at the tile's last row, so rows
+// past it are dropped by the hardware (the whole offset is in the VGPR operand: the range check
+// does not cover the SGPR offset) and every wave issues the same number of stores.
 #include "common.h"
 #include "moe_internal.h"
 
@@ -30,16 +41,44 @@ namespace g4 {
 
 constexpr int kBM = MOE_GEMM3_BM;       // 160 activation rows per tile
 constexpr int kMG = kBM / 32;           // MFMA row groups
-constexpr int kBN = 256;                // weight rows per block
+constexpr int kBN = 256;                // weight rows per item
 constexpr int kSBB = 144;               // bytes per Q4_K super-block row (256 K)
-constexpr int kAR = 4;                  // activation ring depth (K steps of 64)
+constexpr int kQR = 4;                  // raw nibble ring depth (K steps)
 constexpr int kXcd = 8;
-constexpr int kChunks = kBN * kSBB / 16 / 256;   // 9 raw 16-byte chunks per producer thread
+constexpr int kWaves = 4;
+constexpr int kBlocksPerCu = 2;
+constexpr int kAI = kBM * 8 / 64 / kWaves;   // A loads per wave per K step (5)
+constexpr int kQI = kBN * 2 / 64 / kWaves;   // nibble loads per wave per K step (2)
+static_assert(kAI == 5 && kQI == 2 && kBN / 64 == kWaves, "load split assumes 160 x 256 items");
 
 struct Smem {
-  uint8_t B[2][kBN * kSBB];             // 2 x 36 KB raw super-blocks
-  uint16_t A[kAR][kBM * 64];            // 4 x 20 KB f16, chunk c of row r at c ^ (r & 7)
+  uint8_t A[2][kBM * 128];
+  uint8_t Q[kQR][kBN * 32];
+  uint8_t Hd[2][kBN * 16];
 };
+static_assert(sizeof(Smem) * kBlocksPerCu <= 160 * 1024, "two blocks per CU");
+
+__device__ __forceinline__ int a_swz(int m) { return (m ^ (m >> 1)) & 7; }
+__device__ __forceinline__ int q_swz(int n) { return ((n >> 2) ^ (n >> 3)) & 1; }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+
+// 16 bytes per lane from base + off to LDS bytes [lds + 16 lane, +16). Issued as inline asm so
+// that the compiler does not wait for it before unrelated LDS reads; the caller waits with
+// explicit vmcnt counts (vector memory operations complete in issue order).
+__device__ __forceinline__ void dma16(uint32_t off, const void* base, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory");
+}
+// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
 __device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
@@ -65,7 +104,7 @@ __device__ __forceinline__ uint32_t q4_pair(uint32_t w, uint32_t sel, f16x2_t ds
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, ds, ndm));
 }
 
-// 8 bytes of nibbles (w0, w1) -> the 8 f16 of one B fragment (low or high nibbles, k order)
+// 8 bytes of nibbles (w0, w1) -> the 8 f16 of one B fragment (low or high nibbles, byte order)
 template <bool HIGH>
 __device__ __forceinline__ uint4 q4_frag(uint32_t w0, uint32_t w1, f16x2_t ds, f16x2_t ndm) {
   return make_uint4(q4_pair<HIGH>(w0, 0x0C010C00u, ds, ndm), q4_pair<HIGH>(w0, 0x0C030C02u, ds, ndm),
@@ -73,7 +112,7 @@ __device__ __forceinline__ uint4 q4_frag(uint32_t w0, uint32_t w1, f16x2_t ds, f
 }
 
 // scale and negated min of sub-block j of a super-block header as f16 pairs (get_scale_min_k4,
-// tools/gguf_reader.py:165-175; d * sc and dmin * m rounded to f16 once, as the LDS decode does)
+// tools/gguf_reader.py:165-175; d * sc and dmin * m rounded to f16 once)
 __device__ __forceinline__ void q4_scales(uint4 hdr, int j, f16x2_t& ds, f16x2_t& ndm) {
   uint32_t sc, m;
   q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
@@ -83,289 +122,448 @@ __device__ __forceinline__ void q4_scales(uint4 hdr, int j, f16x2_t& ds, f16x2_t
   ndm = (f16x2_t){n, n};
 }
 
-__device__ __forceinline__ int tile_rows(const int32_t* tiles, const int32_t* offsets, int ncol,
-                                         int& e, int& m0, int& mend, int& col) {
+// ------------------------------------------------------------------------------- items --
+struct Item {
+  int e, m0, mend, col;
+};
+
+// Item q of this block's XCD: tile x + 8 (q / ncol), slab q % ncol. False past the list.
+__device__ __forceinline__ bool get_item(const int32_t* __restrict__ tiles,
+                                         const int32_t* __restrict__ offsets, int q, int ncol,
+                                         Item& it) {
+  const int x = blockIdx.x % kXcd;
   const int count = tiles[0];
-  const int per = (count + kXcd - 1) / kXcd;
-  const int xcd = blockIdx.x % kXcd, slot = blockIdx.x / kXcd;
-  const int tl = slot / ncol;
-  col = slot % ncol;
-  const int tile = xcd * per + tl;
-  if (tl >= per || tile >= count) return 0;
-  e = tiles[1 + 2 * tile];
-  m0 = tiles[2 + 2 * tile];
-  mend = min(m0 + kBM, offsets[e + 1]);
-  return 1;
+  const int ntx = count > x ? (count - x + kXcd - 1) / kXcd : 0;
+  if (q >= ntx * ncol) return false;
+  const int t = x + kXcd * (q / ncol);
+  it.col = q % ncol;
+  it.e = tiles[1 + 2 * t];
+  it.m0 = tiles[2 + 2 * t];
+  it.mend = min(it.m0 + kBM, offsets[it.e + 1]);
+  return true;
 }
 
-// ------------------------------------------------------------------------------- producer --
-// Thread p (0..255). Raw chunk q = 256 i + p (i < 9) of a super-block slab is row q / 9, bytes
-// 16 (q % 9) .. +16 of that row's super-block; it lands at LDS byte 16 q. Activation chunk
-// p & 7 of rows (p >> 3) + 32 i (i < 5) of a K step lands at chunk (p & 7) ^ (row & 7).
-struct Producer {
-  const uint8_t* wsrc[kChunks];         // each raw chunk's bytes in super-block 0 of its row
-  const uint16_t* arow[kMG];            // activation row starts
-  uint4 braw[kChunks];                  // one super-block's chunks in flight
-  uint4 areg[kAR][kMG];                 // kAR K steps of activation chunks in flight
-  int p;
+// Load geometry. Wave w, lane l: its j-th load of a ring slot covers the slot's 16-byte units
+// 64 (w + 4 j) + l.
+//   A unit u: tile row u >> 3, chunk (u & 7) ^ a_swz(row) of that row's 64 K of the step.
+//   Q unit u: weight row u >> 1, logical half (u & 1) ^ q_swz(row) of the step's 32 nibble bytes.
+//   Hd unit u: weight row u (one load per wave).
+struct Lane {
+  uint32_t qoff[kQI];                   // byte offset of Q load j from its base (sb 0, step 0)
+  uint32_t hoff;                        // byte offset of the Hd load from its base
+  uint32_t la, lq, lh;                  // LDS address of this wave's first unit in slot 0
+};
+// the thread index through an empty asm: derived lane constants are recomputed where they are
+// used instead of being kept (or spilled) across the item loop
+__device__ __forceinline__ int tid_fresh() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+// A load j of wave w, lane l: tile row and the chunk's byte offset within the row (t = thread)
+__device__ __forceinline__ int a_row(int t, int j) { return (t + 256 * j) >> 3; }
+__device__ __forceinline__ uint32_t a_chunk(int t, int j) {
+  const int u = t + 256 * j;
+  return 16u * (uint32_t)((u & 7) ^ a_swz(u >> 3));
+}
 
-  __device__ __forceinline__ void load_b(int sb, int i0, int i1) {
+// per-item addresses: uniform bases, per-lane A row offsets
+struct Addr {
+  const uint8_t* qb[kQI];               // Q load j's base; the Hd load of waves 0, 1 uses qb[0],
+  const uint8_t* ab;                    // of waves 2, 3 qb[kQI - 1]
+  uint32_t aoff[kAI];
+};
+
+__device__ __forceinline__ void ld_a(const Lane& ln, const Addr& ad, int slot, int ks) {
+  const uint8_t* b = ad.ab + (size_t)ks * 128;
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i)
-      if (i >= i0 && i < i1) braw[i] = *reinterpret_cast<const uint4*>(wsrc[i] + sb * kSBB);
+  for (int j = 0; j < kAI; ++j) dma16(ad.aoff[j], b, ln.la + slot * (kBM * 128) + j * 4096);
+}
+__device__ __forceinline__ void ld_q(const Lane& ln, const Addr& ad, int slot, int ks) {
+  const int off = (ks >> 2) * kSBB + 32 * (ks & 3);
+#pragma unroll
+  for (int j = 0; j < kQI; ++j) dma16(ln.qoff[j], ad.qb[j] + off, ln.lq + slot * (kBN * 32) + j * 4096);
+}
+__device__ __forceinline__ void ld_h(const Lane& ln, const Addr& ad, int slot, int sb) {
+  const uint8_t* hb = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7) ? ad.qb[kQI - 1] : ad.qb[0];
+  dma16(ln.hoff, hb + sb * kSBB, ln.lh + slot * (kBN * 16));
+}
+
+__device__ __forceinline__ void lane_common(Lane& ln, Smem& sm, int wave, int lane) {
+  (void)lane;
+  ln.la = lds_addr(sm.A[0]) + 1024 * wave;
+  ln.lq = lds_addr(sm.Q[0]) + 1024 * wave;
+  ln.lh = lds_addr(sm.Hd[0]) + 1024 * wave;
+}
+
+// a value the compiler cannot see through: what derives from it is not hoisted out of the loop
+// that produces it
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// keeps values computed before this point (and the waits for their loads) ahead of what follows
+__device__ __forceinline__ void pin(const uint32_t (&v)[kAI]) {
+  asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]));
+}
+
+// ------------------------------------------------------------------------------- modes --
+struct GateUp {
+  const uint16_t* x16;
+  const uint8_t *wg, *wu;
+  size_t estride, rowb;
+  const int32_t* sorted_pairs;
+  int K, H, I;
+  uint16_t* S;
+  static constexpr int kStores = kMG * 16;          // per wave per item
+  __device__ int nk() const { return H / 64; }
+  __device__ int ncol() const { return I / 128; }
+  __device__ int n0(int wave) const { return 32 * wave; }
+  __device__ int n1(int wave) const { return 128 + 32 * wave; }
+  __device__ void lane_init(Lane& ln, int wave, int lane) const {
+    // Q load 0 covers gate rows 32 w + l / 2, load 1 the up rows 128 + 32 w + l / 2
+#pragma unroll
+    for (int j = 0; j < kQI; ++j) {
+      const int u = 64 * (wave + kWaves * j) + lane, n = u >> 1;
+      ln.qoff[j] = (uint32_t)((n & 127) * rowb) + 16u + 16u * (uint32_t)((u & 1) ^ q_swz(n));
+    }
+    ln.hoff = (uint32_t)(((64 * wave + lane) & 127) * rowb);
   }
-  __device__ __forceinline__ void store_b(uint8_t* Bs, int i0, int i1) const {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i)
-      if (i >= i0 && i < i1) *reinterpret_cast<uint4*>(Bs + 16 * (256 * i + p)) = braw[i];
+  __device__ void bases(Addr& ad, const Item& it, int wave) const {
+    const uint8_t* g = wg + (size_t)it.e * estride + (size_t)it.col * 128 * rowb;
+    const uint8_t* u = wu + (size_t)it.e * estride + (size_t)it.col * 128 * rowb;
+    ad.qb[0] = g;
+    ad.qb[1] = u;
+    ad.ab = reinterpret_cast<const uint8_t*>(x16);
   }
-  template <int R>
-  __device__ __forceinline__ void load_a(int ks) {
+  // stage 1: the rows' token ids (raw, held in aoff); stage 2: byte offsets
+  __device__ void rows1(Addr& ad, const Item& it, const Lane&) const {
+    const int t = tid_fresh();
 #pragma unroll
-    for (int i = 0; i < kMG; ++i)
-      areg[R][i] = *reinterpret_cast<const uint4*>(arow[i] + 64 * ks + 8 * (p & 7));
+    for (int j = 0; j < kAI; ++j) ad.aoff[j] = (uint32_t)sorted_pairs[min(it.m0 + a_row(t, j), it.mend - 1)];
   }
-  template <int R>
-  __device__ __forceinline__ void store_a(uint16_t* As) const {
+  __device__ void rows2(Addr& ad, const Lane&) const {
+    const int t = tid_fresh();
 #pragma unroll
-    for (int i = 0; i < kMG; ++i) {
-      const int row = (p >> 3) + 32 * i;
-      *reinterpret_cast<uint4*>(As + row * 64 + 8 * ((p & 7) ^ (row & 7))) = areg[R][i];
+    for (int j = 0; j < kAI; ++j) ad.aoff[j] = (ad.aoff[j] / (uint32_t)K) * (uint32_t)H * 2u + a_chunk(t, j);
+  }
+  __device__ void epilogue(const Item& it, int wave, int lane, const f32x16_t (&acc)[kMG][2]) const {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        S + (size_t)it.m0 * I, 0, (it.mend - it.m0) * I * 2, 0x00020000);
+    // row 32 mg + 8 (r >> 2) + 4 h + (r & 3), column n: lane part + uniform row part
+    const int rs2 = opaque(I * 2);
+    const int lane_off = (4 * (lane >> 5) * I + it.col * 128 + 32 * wave + (lane & 31)) * 2;
+#pragma unroll
+    for (int mg = 0; mg < kMG; ++mg) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int vo = lane_off + (32 * mg + 8 * rq) * rs2;
+#pragma unroll
+        for (int r3 = 0; r3 < 4; ++r3) {
+          const int r = 4 * rq + r3;
+          const float g = acc[mg][0][r];
+          float v = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * acc[mg][1][r];
+          v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v), rs,
+                                                vo + r3 * rs2, 0, 0);
+        }
+      }
     }
   }
 };
 
-// chunks of the next super-block stored at step s of the current one (9 = 3 + 2 + 2 + 2)
-__device__ __forceinline__ int chunk_lo(int s) { return s == 0 ? 0 : 1 + 2 * s; }
-__device__ __forceinline__ int chunk_hi(int s) { return 3 + 2 * s; }
-
-// Step ks = 4 sb + s: consumers read A[s] and B[sb & 1]. The producer stores step ks + 3's
-// activations into A[(s + 3) % 4] (set (s + 3) % 4, then reloads it with step ks + 7) and part s
-// of super-block sb + 1 into B[(sb + 1) & 1] (then reloads those registers from sb + 2).
-template <int S>
-__device__ __forceinline__ void pstep(Producer& pr, int sb, int nk, int nsb, Smem& sm) {
-  const int ks = 4 * sb + S;
-  pr.store_a<(S + 3) % 4>(sm.A[(S + 3) % 4]);
-  pr.store_b(sm.B[(sb + 1) & 1], chunk_lo(S), chunk_hi(S));
-  pr.load_a<(S + 3) % 4>(min(ks + 7, nk - 1));
-  pr.load_b(min(sb + 2, nsb - 1), chunk_lo(S), chunk_hi(S));
-  __syncthreads();
-}
-
-__device__ __forceinline__ void produce(Producer& pr, int nk, Smem& sm) {
-  const int nsb = nk / 4;
-  // prologue: super-block 0 and steps 0..2 in LDS; super-block 1 and steps 3..6 in registers
-  pr.load_b(0, 0, kChunks);
-  pr.load_a<0>(0);
-  pr.load_a<1>(min(1, nk - 1));
-  pr.load_a<2>(min(2, nk - 1));
-  pr.store_b(sm.B[0], 0, kChunks);
-  pr.store_a<0>(sm.A[0]);
-  pr.store_a<1>(sm.A[1]);
-  pr.store_a<2>(sm.A[2]);
-  pr.load_b(min(1, nsb - 1), 0, kChunks);
-  pr.load_a<3>(min(3, nk - 1));
-  pr.load_a<0>(min(4, nk - 1));
-  pr.load_a<1>(min(5, nk - 1));
-  pr.load_a<2>(min(6, nk - 1));
-  __syncthreads();
-  for (int sb = 0; sb < nsb; ++sb) {
-    pstep<0>(pr, sb, nk, nsb, sm);
-    pstep<1>(pr, sb, nk, nsb, sm);
-    pstep<2>(pr, sb, nk, nsb, sm);
-    pstep<3>(pr, sb, nk, nsb, sm);
+struct Down {
+  const uint16_t* S;
+  const uint8_t* wd;
+  size_t estride, rowb;
+  int H, I;
+  float* y;
+  static constexpr int kStores = kMG * 32;
+  __device__ int nk() const { return I / 64; }
+  __device__ int ncol() const { return H / kBN; }
+  __device__ int n0(int wave) const { return 64 * wave; }
+  __device__ int n1(int wave) const { return 64 * wave + 32; }
+  __device__ void lane_init(Lane& ln, int wave, int lane) const {
+#pragma unroll
+    for (int j = 0; j < kQI; ++j) {
+      const int u = 64 * (wave + kWaves * j) + lane, n = u >> 1;
+      ln.qoff[j] = (uint32_t)(n * rowb) + 16u + 16u * (uint32_t)((u & 1) ^ q_swz(n));
+    }
+    ln.hoff = (uint32_t)((64 * wave + lane) * rowb);
   }
-}
-
-// ------------------------------------------------------------------------------- consumer --
-// Consumer lane l: weight rows n0 + l % 32 (group 0) and n1 + l % 32 (group 1) of the slab, half
-// h = l / 32 of every 16-wide MFMA k substep. In step s of a super-block the lane needs bytes
-// [8h, 8h+8) and [16 + 8h, +8) of the row's 32-byte nibble group s: substep 0 = low nibbles of the
-// first, 1 = low of the second, 2 = high of the first, 3 = high of the second (elements
-// 16 ss + 8h .. +8, the natural k order).
-template <int NG>
-__device__ __forceinline__ void consume(int nk, int n0, int n1, Smem& sm, f32x16_t (&acc)[kMG][2]) {
-  const int lane = threadIdx.x & 63;
-  const int h = lane >> 5, r = lane & 31;
-  const int nsb = nk / 4;
-  __syncthreads();
-  for (int sb = 0; sb < nsb; ++sb) {
-    const uint8_t* Bs = sm.B[sb & 1];
-    const uint8_t* rg0 = Bs + (n0 + r) * kSBB;
-    const uint8_t* rg1 = Bs + (n1 + r) * kSBB;
-    const uint4 hdr0 = *reinterpret_cast<const uint4*>(rg0);
-    const uint4 hdr1 = *reinterpret_cast<const uint4*>(rg1);
+  __device__ void bases(Addr& ad, const Item& it, int) const {
+    const uint8_t* w = wd + (size_t)it.e * estride + (size_t)it.col * kBN * rowb;
+    ad.qb[0] = w;
+    ad.qb[1] = w;
+    ad.ab = reinterpret_cast<const uint8_t*>(S + (size_t)it.m0 * I);
+  }
+  __device__ void rows1(Addr&, const Item&, const Lane&) const {}
+  __device__ void rows2_item(Addr& ad, const Item& it, const Lane&) const {
+    const int last = it.mend - it.m0 - 1;
+    const int t = tid_fresh();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint2 a0 = *reinterpret_cast<const uint2*>(rg0 + 16 + 32 * s + 8 * h);
-      const uint2 b0 = *reinterpret_cast<const uint2*>(rg0 + 32 + 32 * s + 8 * h);
-      const uint2 a1 = *reinterpret_cast<const uint2*>(rg1 + 16 + 32 * s + 8 * h);
-      const uint2 b1 = *reinterpret_cast<const uint2*>(rg1 + 32 + 32 * s + 8 * h);
-      f16x2_t ds0l, nd0l, ds0h, nd0h, ds1l, nd1l, ds1h, nd1h;
-      q4_scales(hdr0, 2 * s, ds0l, nd0l);
-      q4_scales(hdr0, 2 * s + 1, ds0h, nd0h);
-      q4_scales(hdr1, 2 * s, ds1l, nd1l);
-      q4_scales(hdr1, 2 * s + 1, ds1h, nd1h);
-      const uint16_t* As = sm.A[s];
-      // software pipeline over the 4 substeps: substep ss + 1's A fragments are requested and its
-      // B fragments decoded while substep ss's MFMAs run
-      auto decode = [&](int ss, uint4& bg, uint4& bu) {
-        if (ss == 0) { bg = q4_frag<false>(a0.x, a0.y, ds0l, nd0l); bu = q4_frag<false>(a1.x, a1.y, ds1l, nd1l); }
-        else if (ss == 1) { bg = q4_frag<false>(b0.x, b0.y, ds0l, nd0l); bu = q4_frag<false>(b1.x, b1.y, ds1l, nd1l); }
-        else if (ss == 2) { bg = q4_frag<true>(a0.x, a0.y, ds0h, nd0h); bu = q4_frag<true>(a1.x, a1.y, ds1h, nd1h); }
-        else { bg = q4_frag<true>(b0.x, b0.y, ds0h, nd0h); bu = q4_frag<true>(b1.x, b1.y, ds1h, nd1h); }
-      };
-      auto afrag = [&](int ss, uint4 (&a)[NG]) {
+    for (int j = 0; j < kAI; ++j) ad.aoff[j] = (uint32_t)min(a_row(t, j), last) * (uint32_t)I * 2u + a_chunk(t, j);
+  }
+  __device__ void epilogue(const Item& it, int wave, int lane, const f32x16_t (&acc)[kMG][2]) const {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        y + (size_t)it.m0 * H, 0, (it.mend - it.m0) * H * 4, 0x00020000);
+    const int rs4 = opaque(H * 4);
+    const int lane_off = (4 * (lane >> 5) * H + it.col * kBN + 64 * wave + (lane & 31)) * 4;
 #pragma unroll
-        for (int mg = 0; mg < NG; ++mg) {
-          const int row = 32 * mg + r;
-          a[mg] = *reinterpret_cast<const uint4*>(As + row * 64 + 8 * ((2 * ss + h) ^ (row & 7)));
-        }
-      };
-      uint4 ac[NG], an[NG], bgc, buc, bgn, bun;
-      afrag(0, ac);
-      decode(0, bgc, buc);
+    for (int mg = 0; mg < kMG; ++mg) {
 #pragma unroll
-      for (int ss = 0; ss < 4; ++ss) {
-        if (ss < 3) {
-          afrag(ss + 1, an);
-          decode(ss + 1, bgn, bun);
-        }
+      for (int rq = 0; rq < 4; ++rq) {
+        const int vo = lane_off + (32 * mg + 8 * rq) * rs4;
 #pragma unroll
-        for (int mg = 0; mg < NG; ++mg) {
-          acc[mg][0] = mfma(ac[mg], bgc, acc[mg][0]);
-          acc[mg][1] = mfma(ac[mg], buc, acc[mg][1]);
-        }
-        if (ss < 3) {
-#pragma unroll
-          for (int mg = 0; mg < NG; ++mg) ac[mg] = an[mg];
-          bgc = bgn;
-          buc = bun;
+        for (int r3 = 0; r3 < 4; ++r3) {
+          const int r = 4 * rq + r3;
+          // the builtin's data operand is an integer: pass the bits, not the value (copied out of
+          // the vector first: a bit cast of the vector element itself read element 0 here)
+          const float v0 = acc[mg][0][r], v1 = acc[mg][1][r];
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v0), rs, vo + r3 * rs4, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v1), rs, vo + r3 * rs4 + 128, 0, 0);
         }
       }
-      __syncthreads();
     }
   }
+};
+
+__device__ __forceinline__ void rows_all(const GateUp& md, Addr& ad, const Item& it, const Lane& ln) {
+  md.rows1(ad, it, ln);
+  md.rows2(ad, ln);
+}
+__device__ __forceinline__ void rows_all(const Down& md, Addr& ad, const Item& it, const Lane& ln) {
+  md.rows2_item(ad, it, ln);
+}
+// next item's A row offsets in two stages (loads issued in step 1, consumed in step 2)
+__device__ __forceinline__ void rows_stage1(const GateUp& md, Addr& ad, const Item& it, const Lane& ln) {
+  md.rows1(ad, it, ln);
+}
+__device__ __forceinline__ void rows_stage2(const GateUp& md, Addr& ad, const Item&, const Lane& ln) {
+  md.rows2(ad, ln);
+}
+__device__ __forceinline__ void rows_stage1(const Down&, Addr&, const Item&, const Lane&) {}
+__device__ __forceinline__ void rows_stage2(const Down& md, Addr& ad, const Item& it, const Lane& ln) {
+  md.rows2_item(ad, it, ln);
 }
 
-__device__ __forceinline__ void consume_n(int ng, int nk, int n0, int n1, Smem& sm,
-                                          f32x16_t (&acc)[kMG][2]) {
-  if (ng >= 5) consume<5>(nk, n0, n1, sm, acc);
-  else if (ng == 4) consume<4>(nk, n0, n1, sm, acc);
-  else if (ng == 3) consume<3>(nk, n0, n1, sm, acc);
-  else if (ng == 2) consume<2>(nk, n0, n1, sm, acc);
-  else consume<1>(nk, n0, n1, sm, acc);
+// ------------------------------------------------------------------------------- one item --
+// Step ks (super-block sb = ks / 4, s = ks % 4) of the item reads A[ks & 1], Q[ks % 4] and
+// Hd[(hp + sb) & 1]. After the step's barrier the wave issues A of step ks + 1, Q of step ks + 3
+// and (s == 0) Hd of super-block sb + 1, each into the slot step ks - 1 (super-block sb - 1)
+// used; in the last super-block those are the next item's steps 0..2 and super-block 0 (or, with
+// no next item, clamped repeats of this item's last ones, into slots nothing reads again), so
+// every step issues the same loads and the vmcnt counts are constants.
+// Lane l: weight rows n0 + l % 32 (group 0) and n1 + l % 32 (group 1); half h = l / 32.
+template <int NG, class M>
+__device__ __forceinline__ void run_item(const M& md, const Lane& ln, const Addr& ca, Addr& na,
+                                         const Item& nx, bool has_next, bool first, int hp, int n0,
+                                         int n1, Smem& sm, f32x16_t (&acc)[kMG][2]) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int nk = md.nk(), nsb = nk / 4;
+  int aoff[4];
+#pragma unroll
+  for (int ss = 0; ss < 4; ++ss)
+    aoff[ss] = 16 * (8 * r + ((4 * (ss >> 1) + 2 * h + (ss & 1)) ^ a_swz(r)));
+  const int qo0 = 16 * (2 * (n0 + r) + (h ^ q_swz(r)));
+  const int qo1 = 16 * (2 * (n1 + r) + (h ^ q_swz(r)));
+  auto step = [&](int sb, int s, bool first_sb, bool last) {
+    const int ks = 4 * sb + s;
+    // wait for this wave's loads of step ks (A was issued last in step ks - 1, then its Q and,
+    // after s == 0, Hd; before an item's first step: the previous item's epilogue stores)
+    if (first_sb && s == 0) {
+      if (!first) wait_vm<(kQI + M::kStores < 63 ? kQI + M::kStores : 63)>();
+    } else if (s == 1) {
+      wait_vm<kQI + 1>();
+    } else {
+      wait_vm<kQI>();
+    }
+    __syncthreads();
+    // the next item's row offsets: loads issued in step 1 (after its loads), consumed here, ahead
+    // of this step's loads (with no next item they describe the current one and go unused)
+    if (first_sb && s == 2) {
+      rows_stage2(md, na, nx, ln);
+      pin(na.aoff);
+    }
+    if (!last) {
+      ld_a(ln, ca, (s + 1) & 1, ks + 1);
+      ld_q(ln, ca, (s + 3) & 3, min(ks + 3, nk - 1));
+      if (s == 0) ld_h(ln, ca, (hp + sb + 1) & 1, sb + 1);
+    } else if (has_next) {
+      if (s == 3) ld_a(ln, na, 0, 0); else ld_a(ln, ca, (s + 1) & 1, ks + 1);
+      if (s == 0) ld_q(ln, ca, 3, nk - 1); else ld_q(ln, na, s - 1, s - 1);
+      if (s == 0) ld_h(ln, na, (hp + nsb) & 1, 0);
+    } else {
+      ld_a(ln, ca, (s + 1) & 1, min(ks + 1, nk - 1));
+      ld_q(ln, ca, (s + 3) & 3, nk - 1);
+      if (s == 0) ld_h(ln, ca, (hp + nsb) & 1, nsb - 1);
+    }
+    if (first_sb && s == 1) rows_stage1(md, na, nx, ln);
+    const uint8_t* As = sm.A[s & 1];
+    const uint8_t* Qs = sm.Q[s];
+    // the super-block's headers stay in their slot for its four steps: read them every step
+    const uint8_t* Hs = sm.Hd[(hp + sb) & 1];
+    const uint4 hdr0 = *reinterpret_cast<const uint4*>(Hs + 16 * (n0 + r));
+    const uint4 hdr1 = *reinterpret_cast<const uint4*>(Hs + 16 * (n1 + r));
+    const uint4 q0 = *reinterpret_cast<const uint4*>(Qs + qo0);
+    const uint4 q1 = *reinterpret_cast<const uint4*>(Qs + qo1);
+    f16x2_t ds0l, nd0l, ds0h, nd0h, ds1l, nd1l, ds1h, nd1h;
+    q4_scales(hdr0, 2 * s, ds0l, nd0l);
+    q4_scales(hdr0, 2 * s + 1, ds0h, nd0h);
+    q4_scales(hdr1, 2 * s, ds1l, nd1l);
+    q4_scales(hdr1, 2 * s + 1, ds1h, nd1h);
+    auto decode = [&](int ss, uint4& bg, uint4& bu) {
+      if (ss == 0) { bg = q4_frag<false>(q0.x, q0.y, ds0l, nd0l); bu = q4_frag<false>(q1.x, q1.y, ds1l, nd1l); }
+      else if (ss == 1) { bg = q4_frag<false>(q0.z, q0.w, ds0l, nd0l); bu = q4_frag<false>(q1.z, q1.w, ds1l, nd1l); }
+      else if (ss == 2) { bg = q4_frag<true>(q0.x, q0.y, ds0h, nd0h); bu = q4_frag<true>(q1.x, q1.y, ds1h, nd1h); }
+      else { bg = q4_frag<true>(q0.z, q0.w, ds0h, nd0h); bu = q4_frag<true>(q1.z, q1.w, ds1h, nd1h); }
+    };
+    auto afrag = [&](int ss, uint4 (&a)[NG]) {
+#pragma unroll
+      for (int mg = 0; mg < NG; ++mg) a[mg] = *reinterpret_cast<const uint4*>(As + aoff[ss] + 4096 * mg);
+    };
+    // one set of A and B fragments: substep ss + 1's are read and decoded into the same
+    // registers once substep ss's MFMAs have issued (an MFMA holds its operands from issue)
+    uint4 ac[NG], bg, bu;
+    afrag(0, ac);
+    decode(0, bg, bu);
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+#pragma unroll
+      for (int mg = 0; mg < NG; ++mg) {
+        acc[mg][0] = mfma(ac[mg], bg, acc[mg][0]);
+        acc[mg][1] = mfma(ac[mg], bu, acc[mg][1]);
+      }
+      if (ss < 3) {
+        afrag(ss + 1, ac);
+        decode(ss + 1, bg, bu);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < 4; ++s) step(0, s, true, false);
+  for (int sb = 1; sb < nsb - 1; ++sb) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) step(sb, s, false, false);
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) step(nsb - 1, s, false, true);
+}
+
+template <class M>
+__device__ __forceinline__ void run_n(int ng, const M& md, const Lane& ln, const Addr& ca, Addr& na,
+                                      const Item& nx, bool has_next, bool first, int hp, int n0,
+                                      int n1, Smem& sm, f32x16_t (&acc)[kMG][2]) {
+  if (ng >= 5) run_item<5>(md, ln, ca, na, nx, has_next, first, hp, n0, n1, sm, acc);
+  else if (ng == 4) run_item<4>(md, ln, ca, na, nx, has_next, first, hp, n0, n1, sm, acc);
+  else if (ng == 3) run_item<3>(md, ln, ca, na, nx, has_next, first, hp, n0, n1, sm, acc);
+  else if (ng == 2) run_item<2>(md, ln, ca, na, nx, has_next, first, hp, n0, n1, sm, acc);
+  else run_item<1>(md, ln, ca, na, nx, has_next, first, hp, n0, n1, sm, acc);
+}
+
+// The block's items in order; the first one's operands are loaded up front, every later one's
+// by the previous item's last super-block.
+template <class M>
+__device__ __forceinline__ void persistent(const M& md, const int32_t* __restrict__ tiles,
+                                           const int32_t* __restrict__ offsets, Smem& sm) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int stride = gridDim.x / kXcd;
+  const int ncol = md.ncol(), nsb = md.nk() / 4;
+  int q = blockIdx.x / kXcd;
+  Item cur;
+  if (!get_item(tiles, offsets, q, ncol, cur)) return;
+  Lane ln;
+  lane_common(ln, sm, wave, lane);
+  md.lane_init(ln, wave, lane);
+  Addr ca;
+  md.bases(ca, cur, wave);
+  rows_all(md, ca, cur, ln);
+  // step 0's operands first; steps 1 and 2's nibbles may still be in flight at step 0
+  ld_h(ln, ca, 0, 0);
+  ld_q(ln, ca, 0, 0);
+  ld_a(ln, ca, 0, 0);
+#pragma unroll
+  for (int j = 1; j < kQR - 1; ++j) ld_q(ln, ca, j, j);
+  wait_vm<(kQR - 2) * kQI>();
+  int hp = 0;
+  bool first = true;
+  for (;;) {
+    Item nx;
+    const bool has_next = get_item(tiles, offsets, q + stride, ncol, nx);
+    if (!has_next) nx = cur;
+    Addr na;
+    md.bases(na, nx, wave);
+    f32x16_t acc[kMG][2];
+#pragma unroll
+    for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
+    const int ng = __builtin_amdgcn_readfirstlane((cur.mend - cur.m0 + 31) >> 5);
+    run_n(ng, md, ln, ca, na, nx, has_next, first, hp, md.n0(wave), md.n1(wave), sm, acc);
+    md.epilogue(cur, wave, lane, acc);
+    if (!has_next) break;
+    cur = nx;
+    ca = na;
+    hp = (hp + nsb) & 1;
+    q += stride;
+    first = false;
+  }
+  // no load may still be writing this block's LDS when its waves exit
+  wait_vm<0>();
 }
 
 }  // namespace g4
 
-// ----------------------------------------------------------------------------------- gate/up --
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm4_gateup(
+// ----------------------------------------------------------------------------------- kernels --
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm4_gateup(
     const uint16_t* __restrict__ x16, const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
     size_t estride, const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_pairs, int K, int H, int I, uint16_t* __restrict__ S) {
   using namespace g4;
   __shared__ __attribute__((aligned(16))) Smem sm;
-  int e, m0, mend, col;
-  if (!tile_rows(tiles, offsets, I / 128, e, m0, mend, col)) return;
-  const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int nk = H / 64;
-  if (wave >= 4) {
-    Producer pr;
-    pr.p = t - 256;
-    const size_t rowb = (size_t)(H / 256) * kSBB;
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int q = 256 * i + pr.p, row = q / 9;
-      pr.wsrc[i] = (row < 128 ? wg : wu) + (size_t)e * estride + (size_t)(col * 128 + (row & 127)) * rowb +
-                   16 * (q % 9);
-    }
-#pragma unroll
-    for (int i = 0; i < kMG; ++i) {
-      const int m = min(m0 + (pr.p >> 3) + 32 * i, mend - 1);
-      pr.arow[i] = x16 + (size_t)(sorted_pairs[m] / K) * H;
-    }
-    produce(pr, nk, sm);
-    return;
-  }
-  f32x16_t acc[kMG][2];
-#pragma unroll
-  for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
-  const int ng = __builtin_amdgcn_readfirstlane((mend - m0 + 31) >> 5);
-  consume_n(ng, nk, 32 * wave, 128 + 32 * wave, sm, acc);
-  const int n = col * 128 + 32 * wave + (lane & 31), h = lane >> 5;
-#pragma unroll
-  for (int mg = 0; mg < kMG; ++mg) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (mm < mend) {
-        float v = silu_f32(acc[mg][0][r]) * acc[mg][1][r];
-        v = fminf(fmaxf(v, -65504.0f), 65504.0f);
-        S[(size_t)mm * I + n] = __builtin_bit_cast(uint16_t, (_Float16)v);
-      }
-    }
-  }
+  const GateUp md{x16, wg, wu, estride, (size_t)(H / 256) * kSBB, sorted_pairs, K, H, I, S};
+  persistent(md, tiles, offsets, sm);
 }
 
-// -------------------------------------------------------------------------------------- down --
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm4_down(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm4_down(
     const uint16_t* __restrict__ S, const uint8_t* __restrict__ wd, size_t estride,
     const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets, int H, int I,
     float* __restrict__ y) {
   using namespace g4;
   __shared__ __attribute__((aligned(16))) Smem sm;
-  int e, m0, mend, col;
-  if (!tile_rows(tiles, offsets, H / kBN, e, m0, mend, col)) return;
-  const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int nk = I / 64;
-  if (wave >= 4) {
-    Producer pr;
-    pr.p = t - 256;
-    const size_t rowb = (size_t)(I / 256) * kSBB;
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int q = 256 * i + pr.p, row = q / 9;
-      pr.wsrc[i] = wd + (size_t)e * estride + (size_t)(col * kBN + row) * rowb + 16 * (q % 9);
-    }
-#pragma unroll
-    for (int i = 0; i < kMG; ++i) pr.arow[i] = S + (size_t)min(m0 + (pr.p >> 3) + 32 * i, mend - 1) * I;
-    produce(pr, nk, sm);
-    return;
-  }
-  f32x16_t acc[kMG][2];
-#pragma unroll
-  for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
-  const int ng = __builtin_amdgcn_readfirstlane((mend - m0 + 31) >> 5);
-  consume_n(ng, nk, 64 * wave, 64 * wave + 32, sm, acc);
-  const int nb = col * kBN + 64 * wave + (lane & 31), h = lane >> 5;
-#pragma unroll
-  for (int mg = 0; mg < kMG; ++mg) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (mm < mend) {
-        y[(size_t)mm * H + nb] = acc[mg][0][r];
-        y[(size_t)mm * H + nb + 32] = acc[mg][1][r];
-      }
-    }
-  }
+  const Down md{S, wd, estride, (size_t)(I / 256) * kSBB, H, I, y};
+  persistent(md, tiles, offsets, sm);
 }
 
 }  // namespace moe
 
 using namespace moe;
 
+static int persistent_grid(int max_tiles, int ncol) {
+  static int n_cu = 0;
+  if (!n_cu) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      n_cu = n;
+    else
+      n_cu = 256;
+  }
+  const int per_xcd_items = (max_tiles + g4::kXcd - 1) / g4::kXcd * ncol;
+  const int per_xcd_slots = (n_cu * g4::kBlocksPerCu + g4::kXcd - 1) / g4::kXcd;
+  return g4::kXcd * (per_xcd_items < per_xcd_slots ? per_xcd_items : per_xcd_slots);
+}
+
 int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
                             size_t expert_stride, const int32_t* tiles, int max_tiles,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
                             int I, uint16_t* S, hipStream_t st) {
-  if (H % 256 || I % 128)
-    return moe_set_error(MOE_E_UNSUPPORTED, "gemm4 gate_up needs H %% 256 == 0, I %% 128 == 0");
-  const dim3 grid(g4::kXcd * ((max_tiles + g4::kXcd - 1) / g4::kXcd) * (I / 128));
-  hipLaunchKernelGGL(k_gemm4_gateup, grid, dim3(512), 0, st, x16, reinterpret_cast<const uint8_t*>(w_gate),
+  if (H % 256 || H < 512 || I % 128)
+    return moe_set_error(MOE_E_UNSUPPORTED, "gemm4 gate_up needs H %% 256 == 0, H >= 512, I %% 128 == 0");
+  const dim3 grid(persistent_grid(max_tiles, I / 128));
+  hipLaunchKernelGGL(k_gemm4_gateup, grid, dim3(256), 0, st, x16, reinterpret_cast<const uint8_t*>(w_gate),
                      reinterpret_cast<const uint8_t*>(w_up), expert_stride, tiles, offsets, sorted_pairs,
                      K, H, I, S);
   return moe_check_launch("gemm4_gateup");
@@ -374,10 +572,10 @@ int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void*
 int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
                           float* y, hipStream_t st) {
-  if (H % g4::kBN || I % 256)
-    return moe_set_error(MOE_E_UNSUPPORTED, "gemm4 down needs H %% 256 == 0, I %% 256 == 0");
-  const dim3 grid(g4::kXcd * ((max_tiles + g4::kXcd - 1) / g4::kXcd) * (H / g4::kBN));
-  hipLaunchKernelGGL(k_gemm4_down, grid, dim3(512), 0, st, S, reinterpret_cast<const uint8_t*>(w_down),
+  if (H % g4::kBN || I % 256 || I < 512)
+    return moe_set_error(MOE_E_UNSUPPORTED, "gemm4 down needs H %% 256 == 0, I %% 256 == 0, I >= 512");
+  const dim3 grid(persistent_grid(max_tiles, H / g4::kBN));
+  hipLaunchKernelGGL(k_gemm4_down, grid, dim3(256), 0, st, S, reinterpret_cast<const uint8_t*>(w_down),
                      expert_stride, tiles, offsets, H, I, y);
   return moe_check_launch("gemm4_down");
 }

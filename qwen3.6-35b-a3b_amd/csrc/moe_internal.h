@@ -57,9 +57,10 @@ int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t
                           const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
                           int H, int I, float* y, hipStream_t st);
 
-// gemm4.hip: Q4_K gate_up and down with the weight decode in the MFMA waves (producers move raw
-// super-blocks and f16 activations into LDS); same tiles (MOE_GEMM3_BM rows), arguments and
-// results as the gemm3 launchers for Q4_K.
+// gemm4.hip: Q4_K gate_up and down with the weight decode in the MFMA waves (persistent grid,
+// direct global->LDS operand loads, two blocks per CU); same tiles (MOE_GEMM3_BM rows),
+// arguments and results as the gemm3 launchers for Q4_K, within f32 rounding (another k order).
+// Needs H >= 512 (gate_up) and I >= 512 (down).
 int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
                             size_t expert_stride, const int32_t* tiles, int max_tiles,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,

@@ -212,27 +212,37 @@ __global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ id
   scatter_chunk(ids, P, E, 0, start, sorted_pairs, pair_pos, run, wcnt);
 }
 
-// MFMA work list: for every hit expert (ascending) ceil(n_e / BM) tiles of BM sorted rows.
+// MFMA work list: for every hit expert ceil(n_e / BM) tiles of BM sorted rows, listed by
+// decreasing 32-row group count (full tiles first, then the experts' partial last tiles; within a
+// group count by ascending expert), so that the work a grid takes up last is the smallest.
 __global__ __launch_bounds__(256) void k_build_tiles(const int32_t* __restrict__ offsets,
                                                      const int32_t* __restrict__ hit_list,
                                                      int32_t* __restrict__ tiles, int bm) {
   __shared__ int tmp[256];
   const int nhit = hit_list[0];
+  const int ngmax = (bm + 31) / 32;
   int written = 0;
-  for (int h0 = 0; h0 < nhit; h0 += 256) {
-    const int h = h0 + threadIdx.x;
-    int e = 0, n = 0;
-    if (h < nhit) {
-      e = hit_list[1 + h];
-      n = (offsets[e + 1] - offsets[e] + bm - 1) / bm;
+  for (int g = ngmax; g >= 1; --g) {
+    for (int h0 = 0; h0 < nhit; h0 += 256) {
+      const int h = h0 + threadIdx.x;
+      int e = 0, nfull = 0, rem = 0, n = 0;
+      if (h < nhit) {
+        e = hit_list[1 + h];
+        const int rows = offsets[e + 1] - offsets[e];
+        nfull = rows / bm;
+        rem = rows - nfull * bm;
+        // full tiles have ngmax groups; the remainder tile ceil(rem / 32)
+        n = (g == ngmax ? nfull : 0) + ((rem > 0 && (rem + 31) / 32 == g) ? 1 : 0);
+      }
+      int tot;
+      const int pre = block_exclusive_scan(n, tmp, &tot);
+      for (int i = 0; i < n; ++i) {
+        const int ti = (g == ngmax && i < nfull) ? i : nfull;   // tile index within the expert
+        tiles[1 + 2 * (written + pre + i)] = e;
+        tiles[2 + 2 * (written + pre + i)] = offsets[e] + ti * bm;
+      }
+      written += tot;
     }
-    int tot;
-    const int pre = block_exclusive_scan(n, tmp, &tot);
-    for (int i = 0; i < n; ++i) {
-      tiles[1 + 2 * (written + pre + i)] = e;
-      tiles[2 + 2 * (written + pre + i)] = offsets[e] + i * bm;
-    }
-    written += tot;
   }
   if (threadIdx.x == 0) tiles[0] = written;
 }
