@@ -318,6 +318,17 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
   uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
   if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
   MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
+  // bf16 shared weights on the f16 MFMA path: the dense 128-row kernels
+  if (path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && moe_gemm5_supports(H, Is)) {
+    if (!x16) {
+      uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+      if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+      MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+      x16 = c;
+    }
+    MOE_TRY(moe_launch_gemm5_gateup(x16, wg, wu, T, H, Is, s, st));
+    return moe_launch_gemm5_down(s, wd, T, H, Is, shared_raw, st);
+  }
   // Q8_0 shared weights take the 160-row f16 kernels on either MFMA path
   if ((path == MOE_PATH_MFMA || sfmt == MOE_FMT_Q8_0) && H % 256 == 0 && Is % 256 == 0) {
     if (!x16) {

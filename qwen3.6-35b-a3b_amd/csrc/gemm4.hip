@@ -30,6 +30,7 @@
 // does not cover the SGPR offset) and every wave issues the same number of stores.
 #include "common.h"
 #include "moe_internal.h"
+#include "lds_dma.h"
 
 namespace moe {
 
@@ -38,6 +39,11 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace g4 {
+
+using dma::lds_addr;
+using dma::opaque;
+using dma::tid_fresh;
+using dma::wait_vm;
 
 constexpr int kBM = MOE_GEMM3_BM;       // 160 activation rows per tile
 constexpr int kMG = kBM / 32;           // MFMA row groups
@@ -60,25 +66,6 @@ static_assert(sizeof(Smem) * kBlocksPerCu <= 160 * 1024, "two blocks per CU");
 
 __device__ __forceinline__ int a_swz(int m) { return (m ^ (m >> 1)) & 7; }
 __device__ __forceinline__ int q_swz(int n) { return ((n >> 2) ^ (n >> 3)) & 1; }
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
-}
-
-// 16 bytes per lane from base + off to LDS bytes [lds + 16 lane, +16). Issued as inline asm so
-// that the compiler does not wait for it before unrelated LDS reads; the caller waits with
-// explicit vmcnt counts (vector memory operations complete in issue order).
-__device__ __forceinline__ void dma16(uint32_t off, const void* base, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-               : "memory");
-}
-// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding: vmcnt bits 3:0 and 15:14)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
 
 __device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
@@ -153,13 +140,6 @@ struct Lane {
   uint32_t hoff;                        // byte offset of the Hd load from its base
   uint32_t la, lq, lh;                  // LDS address of this wave's first unit in slot 0
 };
-// the thread index through an empty asm: derived lane constants are recomputed where they are
-// used instead of being kept (or spilled) across the item loop
-__device__ __forceinline__ int tid_fresh() {
-  int t = (int)threadIdx.x;
-  asm volatile("" : "+v"(t));
-  return t;
-}
 // A load j of wave w, lane l: tile row and the chunk's byte offset within the row (t = thread)
 __device__ __forceinline__ int a_row(int t, int j) { return (t + 256 * j) >> 3; }
 __device__ __forceinline__ uint32_t a_chunk(int t, int j) {
@@ -177,16 +157,16 @@ struct Addr {
 __device__ __forceinline__ void ld_a(const Lane& ln, const Addr& ad, int slot, int ks) {
   const uint8_t* b = ad.ab + (size_t)ks * 128;
 #pragma unroll
-  for (int j = 0; j < kAI; ++j) dma16(ad.aoff[j], b, ln.la + slot * (kBM * 128) + j * 4096);
+  for (int j = 0; j < kAI; ++j) dma::load16(ad.aoff[j], b, ln.la + slot * (kBM * 128) + j * 4096);
 }
 __device__ __forceinline__ void ld_q(const Lane& ln, const Addr& ad, int slot, int ks) {
   const int off = (ks >> 2) * kSBB + 32 * (ks & 3);
 #pragma unroll
-  for (int j = 0; j < kQI; ++j) dma16(ln.qoff[j], ad.qb[j] + off, ln.lq + slot * (kBN * 32) + j * 4096);
+  for (int j = 0; j < kQI; ++j) dma::load16(ln.qoff[j], ad.qb[j] + off, ln.lq + slot * (kBN * 32) + j * 4096);
 }
 __device__ __forceinline__ void ld_h(const Lane& ln, const Addr& ad, int slot, int sb) {
   const uint8_t* hb = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7) ? ad.qb[kQI - 1] : ad.qb[0];
-  dma16(ln.hoff, hb + sb * kSBB, ln.lh + slot * (kBN * 16));
+  dma::load16(ln.hoff, hb + sb * kSBB, ln.lh + slot * (kBN * 16));
 }
 
 __device__ __forceinline__ void lane_common(Lane& ln, Smem& sm, int wave, int lane) {
@@ -194,13 +174,6 @@ __device__ __forceinline__ void lane_common(Lane& ln, Smem& sm, int wave, int la
   ln.la = lds_addr(sm.A[0]) + 1024 * wave;
   ln.lq = lds_addr(sm.Q[0]) + 1024 * wave;
   ln.lh = lds_addr(sm.Hd[0]) + 1024 * wave;
-}
-
-// a value the compiler cannot see through: what derives from it is not hoisted out of the loop
-// that produces it
-__device__ __forceinline__ int opaque(int v) {
-  asm volatile("" : "+s"(v));
-  return v;
 }
 
 // keeps values computed before this point (and the waits for their loads) ahead of what follows
@@ -249,8 +222,7 @@ struct GateUp {
     for (int j = 0; j < kAI; ++j) ad.aoff[j] = (ad.aoff[j] / (uint32_t)K) * (uint32_t)H * 2u + a_chunk(t, j);
   }
   __device__ void epilogue(const Item& it, int wave, int lane, const f32x16_t (&acc)[kMG][2]) const {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        S + (size_t)it.m0 * I, 0, (it.mend - it.m0) * I * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = dma::rsrc(S + (size_t)it.m0 * I, (it.mend - it.m0) * I * 2);
     // row 32 mg + 8 (r >> 2) + 4 h + (r & 3), column n: lane part + uniform row part
     const int rs2 = opaque(I * 2);
     const int lane_off = (4 * (lane >> 5) * I + it.col * 128 + 32 * wave + (lane & 31)) * 2;
@@ -306,8 +278,7 @@ struct Down {
     for (int j = 0; j < kAI; ++j) ad.aoff[j] = (uint32_t)min(a_row(t, j), last) * (uint32_t)I * 2u + a_chunk(t, j);
   }
   __device__ void epilogue(const Item& it, int wave, int lane, const f32x16_t (&acc)[kMG][2]) const {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        y + (size_t)it.m0 * H, 0, (it.mend - it.m0) * H * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = dma::rsrc(y + (size_t)it.m0 * H, (it.mend - it.m0) * H * 4);
     const int rs4 = opaque(H * 4);
     const int lane_off = (4 * (lane >> 5) * H + it.col * kBN + 64 * wave + (lane & 31)) * 4;
 #pragma unroll

@@ -57,6 +57,14 @@ int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t
                           const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
                           int H, int I, float* y, hipStream_t st);
 
+// gemm5.hip: the shared expert's dense GEMMs over all T rows with bf16 weights (f16 MFMA, f32
+// accumulation): gate/up -> S = SiLU(gate) * up (f16 [T, I_s]), down -> y (f32 [T, H]).
+bool moe_gemm5_supports(int H, int Is);
+int moe_launch_gemm5_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int T, int H,
+                            int Is, uint16_t* S, hipStream_t st);
+int moe_launch_gemm5_down(const uint16_t* S, const void* w_down, int T, int H, int Is, float* y,
+                          hipStream_t st);
+
 // gemm4.hip: Q4_K gate_up and down with the weight decode in the MFMA waves (persistent grid,
 // direct global->LDS operand loads, two blocks per CU); same tiles (MOE_GEMM3_BM rows),
 // arguments and results as the gemm3 launchers for Q4_K, within f32 rounding (another k order).

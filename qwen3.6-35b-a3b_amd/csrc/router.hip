@@ -514,6 +514,57 @@ __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ 
                          w_bf16 + (size_t)t * K, heap_flag, exact_order != 0);
 }
 
+// E = 256, K = 8, many tokens: one wave per token, four per block. The fast path settles a token
+// (32-bit keys, rank r's id and weight written by lane r); a token it cannot settle (a tie at the
+// K-th place, or any tie when the caller reads the slot order) is marked by ids[t][0] = -1 and
+// left to k_route_replay8, so the slow exact replay runs in its own launch instead of beside three
+// fast waves on its SIMD.
+__global__ __launch_bounds__(256) void k_route_topk8(const uint16_t* __restrict__ logits, int T,
+                                                     float* __restrict__ probs,
+                                                     int32_t* __restrict__ ids,
+                                                     float* __restrict__ w_f32,
+                                                     uint16_t* __restrict__ w_bf16,
+                                                     int exact_order) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= T) return;
+  float p[4];
+  route_softmax(logits + (size_t)t * 256, 256, lane, p);
+  if (probs) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) probs[(size_t)t * 256 + 64 * j + lane] = p[j];
+  }
+  int my_id;
+  float my_val, tot;
+  const int code = wave_topk32<8>(p, lane, my_id, my_val, tot);
+  const bool replay = code == 2 || (code == 1 && exact_order);
+  if (replay) {
+    if (lane == 0) ids[(size_t)t * 8] = -1;
+  } else if (lane < 8) {
+    const float wv = my_val / tot;
+    ids[(size_t)t * 8 + lane] = my_id;
+    w_f32[(size_t)t * 8 + lane] = wv;
+    w_bf16[(size_t)t * 8 + lane] = (uint16_t)f32_to_bf16(wv);
+  }
+}
+
+// The exact replay of torch's CPU topk for the tokens k_route_topk8 marked; every other wave
+// returns at once.
+__global__ __launch_bounds__(256) void k_route_replay8(const uint16_t* __restrict__ logits, int T,
+                                                       int32_t* __restrict__ ids,
+                                                       float* __restrict__ w_f32,
+                                                       uint16_t* __restrict__ w_bf16,
+                                                       int32_t* __restrict__ heap_flag) {
+  __shared__ TopkLds s[4];
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T || ids[(size_t)t * 8] != -1) return;
+  float p[4];
+  route_softmax(logits + (size_t)t * 256, 256, lane, p);
+  route_replay_and_write(s[wave], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
+                         w_bf16 + (size_t)t * 8, heap_flag);
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -555,6 +606,13 @@ int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dt
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
                           float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st,
                           bool exact_order) {
+  if (E == 256 && K == 8 && T >= 16) {
+    const dim3 grid((T + 3) / 4);
+    hipLaunchKernelGGL(k_route_topk8, grid, dim3(256), 0, st, logits, T, probs, ids, w_f32, w_bf16,
+                       exact_order ? 1 : 0);
+    hipLaunchKernelGGL(k_route_replay8, grid, dim3(256), 0, st, logits, T, ids, w_f32, w_bf16, heap_flag);
+    return moe_check_launch("route_topk");
+  }
   hipLaunchKernelGGL(k_route_topk, dim3(T), dim3(64), 0, st, logits, T, E, K, probs, ids, w_f32,
                      w_bf16, heap_flag, exact_order ? 1 : 0);
   return moe_check_launch("route_topk");
