@@ -195,11 +195,22 @@ int moe_sort_permute(const int32_t* topk_ids, int T, int K, int E, int32_t* expe
 
 // x16: the rows already in f16 (the MFMA paths' activation operand), or NULL to convert here
 // gate / up: the routed gate and up rows of expert e at gate + e * estride and up + e * estride
+// rows per MFMA tile of the grouped-GEMM path experts_impl takes (0: a GEMV path)
+static int mfma_tile_rows(int path, int T, int H, int I, int gu_fmt, int dn_fmt) {
+  path = pick_path(path, T, gu_fmt, dn_fmt);
+  if (path == MOE_PATH_GEMV) return 0;
+  const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_down_supports(dn_fmt) &&
+                  H % 256 == 0 && I % 256 == 0;
+  return v2 ? MOE_GEMM3_BM : MOE_GEMM_BM;
+}
+
+// tiles_pre: the tile list of mfma_tile_rows(...) rows, already built (NULL: built here)
 static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const void* gate,
                         const void* up, size_t estride, int gu_fmt,
                         const void* dn, int dn_fmt, const int32_t* offsets,
                         const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
-                        int E, int K, int path, float* y, MoeWs& w, hipStream_t st) {
+                        int E, int K, int path, float* y, MoeWs& w, hipStream_t st,
+                        const int32_t* tiles_pre = nullptr) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
   path = pick_path(path, T, gu_fmt, dn_fmt);
@@ -217,10 +228,15 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                   H % 256 == 0 && I % 256 == 0;
   const int bm = v2 ? MOE_GEMM3_BM : MOE_GEMM_BM;
   const int max_tiles = moe_max_mtiles(P, E, bm);
-  int32_t* tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
+  const int32_t* tiles = tiles_pre;
+  if (!tiles) {
+    int32_t* t = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
+    if (!t) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+    MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, t, st, bm));
+    tiles = t;
+  }
   uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
-  if (!tiles || !S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
-  MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, bm));
+  if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
   if (v2) {
     if (!x16) {
       uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
@@ -487,6 +503,13 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   float* gp = gate_prob ? gate_prob : reinterpret_cast<float*>(w.take((size_t)T * 4));
   if (!logits || !ids || !wf || !wb || !offsets || !sorted || !pos || !hits || !y || !sraw || !gp)
     return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+  // the grouped GEMMs' tile list, built by the sort
+  const int bm = mfma_tile_rows(path, T, H, I, gate_up_fmt, down_fmt);
+  int32_t* tiles = nullptr;
+  if (bm) {
+    tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * moe_max_mtiles(P, E, bm)) * 4));
+    if (!tiles) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+  }
   // the MFMA path's f16 activation operand, converted once for the shared and routed GEMMs
   uint16_t* x16 = nullptr;
   if (rpath == MOE_PATH_MFMA) {
@@ -497,12 +520,12 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   if (T < kForkMinT || !allow_fork) {
     MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, nullptr, 0, st));
     MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order));
-    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st));
+    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
     MoeWs w2 = w;   // the shared expert's scratch is dead before the experts' is taken
     MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
                         Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w2, st));
     MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets, sorted,
-                         hits, T, H, I, E, K, path, y, w, st));
+                         hits, T, H, I, E, K, path, y, w, st, tiles));
     return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                               shared_out, expert_raw, st);
   }
@@ -523,12 +546,15 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   void* rscr = wr.take(rsb);
   if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, rscr, rsb, st);
   if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order);
-  if (rc == MOE_OK) rc = moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st);
-  if (rc == MOE_OK)
-    rc = experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
-                      sorted, hits, T, H, I, E, K, path, y, w, st);
+  if (rc == MOE_OK) rc = moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm);
+  // joined before the routed GEMMs: their persistent grids take every CU and each block owns a
+  // fixed share of the items, so a block kept waiting by a still-running shared-expert kernel
+  // would stretch the whole grid
   if (hipEventRecord(f->join, f->s) != hipSuccess || hipStreamWaitEvent(st, f->join, 0) != hipSuccess)
     return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot join the shared-expert stream");
+  if (rc == MOE_OK)
+    rc = experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
+                      sorted, hits, T, H, I, E, K, path, y, w, st, tiles);
   if (rc != MOE_OK) return rc;
   return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                             shared_out, expert_raw, st);

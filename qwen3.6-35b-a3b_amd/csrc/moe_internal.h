@@ -29,10 +29,12 @@ int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* pr
                           float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st,
                           bool exact_order = true);
 
-// sort / permute; ws must hold moe_sort_ws_bytes(P, E) bytes
+// sort / permute; ws must hold moe_sort_ws_bytes(P, E) bytes. tiles != NULL: also the MFMA tile
+// list of bm-row tiles (moe_launch_build_tiles' result), built inside the sort where it can be.
 size_t moe_sort_ws_bytes(int P, int E);
 int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t* sorted_pairs,
-                    int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st);
+                    int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st,
+                    int32_t* tiles = nullptr, int bm = 0);
 
 // MFMA tile list: [count, (expert, row0) x count], rows per tile = bm (MOE_GEMM_BM for gemm.hip,
 // MOE_GEMM3_BM for gemm3.hip)

@@ -60,9 +60,12 @@ __global__ __launch_bounds__(64) void k_sort_small(const int32_t* __restrict__ i
   }
 }
 
-// phase 1: histogram of each chunk -> hist[chunk][E]
+// row stride (ints) of the chunk histograms: hist[e][c], rows padded to 16 bytes
+__host__ __device__ inline int hist_stride(int nchunks) { return (nchunks + 3) & ~3; }
+
+// phase 1: histogram of each chunk -> hist[e][chunk] (an expert's counts contiguous)
 __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ ids, int P, int E,
-                                                   int32_t* __restrict__ hist) {
+                                                   int32_t* __restrict__ hist, int hs) {
   __shared__ int h[256];
   for (int i = threadIdx.x; i < E; i += 256) h[i] = 0;
   __syncthreads();
@@ -75,7 +78,11 @@ __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ i
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < E; i += 256) hist[(size_t)blockIdx.x * E + i] = h[i];
+  for (int i = threadIdx.x; i < E; i += 256) hist[(size_t)i * hs + blockIdx.x] = h[i];
+  // the row padding reads as zero
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < E; i += 256)
+      for (int c = gridDim.x; c < hs; ++c) hist[(size_t)i * hs + c] = 0;
 }
 
 // block-wide exclusive scan of one int per thread (256 threads)
@@ -135,32 +142,91 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, int P, int E, int
   }
 }
 
+// exclusive scan of a 64-bit value over a 256-thread block (wave shuffles, then the four wave
+// totals); *total gets the block sum
+__device__ uint64_t block_exclusive_scan64(uint64_t v, uint64_t* tmp, uint64_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t n = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += n;
+  }
+  if (lane == 63) tmp[wave] = incl;
+  __syncthreads();
+  uint64_t base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    base += w < wave ? tmp[w] : 0;
+    tot += tmp[w];
+  }
+  *total = tot;
+  __syncthreads();
+  return base + incl - v;
+}
+
+// Largest tile count the one-scan builder takes (12-bit fields of a 64-bit scan)
+constexpr int kTilesPacked = 4095;
+
+// MFMA work list from the per-expert row counts (thread e of a 256-thread block holds expert e's
+// rows and first sorted row): ceil(rows / bm) tiles of bm rows per expert, listed by decreasing
+// 32-row group count (full tiles first, then the experts' partial last tiles; within a group
+// count by ascending expert, an expert's full tiles before its partial one), so that the work a
+// grid takes up last is the smallest. One 64-bit scan carries the five per-group-count prefix
+// counts (12 bits each). Needs bm <= 160 and at most kTilesPacked tiles.
+__device__ void build_tiles_block(int rows, int first_row, int e, int bm, int32_t* __restrict__ tiles,
+                                  uint64_t* tmp) {
+  const int ngmax = (bm + 31) / 32;
+  const int nfull = rows / bm, rem = rows - nfull * bm;
+  const int grem = rem > 0 ? (rem + 31) / 32 : 0;
+  const uint64_t packed = ((uint64_t)nfull << (12 * (ngmax - 1))) + (grem ? (1ull << (12 * (grem - 1))) : 0ull);
+  uint64_t tot;
+  const uint64_t pre = block_exclusive_scan64(packed, tmp, &tot);
+  auto field = [](uint64_t v, int g) { return (int)((v >> (12 * (g - 1))) & 4095u); };
+  int start[6] = {0, 0, 0, 0, 0, 0};   // start[g]: first position of the tiles with g groups
+  int acc = 0;
+  for (int g = ngmax; g >= 1; --g) {
+    start[g] = acc;
+    acc += field(tot, g);
+  }
+  const int p_full = start[ngmax] + field(pre, ngmax);
+  for (int i = 0; i < nfull; ++i) {
+    tiles[1 + 2 * (p_full + i)] = e;
+    tiles[2 + 2 * (p_full + i)] = first_row + i * bm;
+  }
+  if (grem) {
+    const int p = start[grem] + field(pre, grem) + (grem == ngmax ? nfull : 0);
+    tiles[1 + 2 * p] = e;
+    tiles[2 + 2 * p] = first_row + nfull * bm;
+  }
+  if (threadIdx.x == 0) tiles[0] = acc;
+}
+
 // phases 2 and 3 in one launch: every block sums the chunk histograms itself (expert totals and
-// its own chunk's prefix; 4 loads in flight per step), scans the totals, and scatters its chunk;
-// block 0 also writes the offsets and the hit list. hist[c][e] is only read.
+// its own chunk's prefix, 16-byte loads of an expert's contiguous counts), scans the totals, and
+// scatters its chunk; block 0 also writes the offsets, the hit list and (tiles != NULL) the MFMA
+// tile list of bm-row tiles. hist is only read.
 __global__ __launch_bounds__(256) void k_sort_scan_scatter(const int32_t* __restrict__ ids, int P, int E,
-                                                           const int32_t* __restrict__ hist, int nchunks,
+                                                           const int32_t* __restrict__ hist, int hs,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ sorted_pairs,
                                                            int32_t* __restrict__ pair_pos,
-                                                           int32_t* __restrict__ hit_list) {
+                                                           int32_t* __restrict__ hit_list,
+                                                           int32_t* __restrict__ tiles, int bm) {
   __shared__ int start[256], tmp[256], run[256];
   __shared__ int wcnt[4][256];
+  __shared__ uint64_t tmp64[4];
   const int e = threadIdx.x, c0 = blockIdx.x;
   run[e] = 0;
   int tot = 0, pre = 0;
   if (e < E) {
-    int c = 0;
-    for (; c + 4 <= nchunks; c += 4) {
-      const int v0 = hist[(size_t)c * E + e], v1 = hist[(size_t)(c + 1) * E + e];
-      const int v2 = hist[(size_t)(c + 2) * E + e], v3 = hist[(size_t)(c + 3) * E + e];
-      tot += v0 + v1 + v2 + v3;
-      pre += (c < c0 ? v0 : 0) + (c + 1 < c0 ? v1 : 0) + (c + 2 < c0 ? v2 : 0) + (c + 3 < c0 ? v3 : 0);
-    }
-    for (; c < nchunks; ++c) {
-      const int v = hist[(size_t)c * E + e];
-      tot += v;
-      pre += c < c0 ? v : 0;
+    const int4* row = reinterpret_cast<const int4*>(hist + (size_t)e * hs);
+#pragma unroll 8
+    for (int q = 0; q < hs / 4; ++q) {
+      const int4 v = row[q];
+      const int c = 4 * q;
+      tot += v.x + v.y + v.z + v.w;
+      pre += (c < c0 ? v.x : 0) + (c + 1 < c0 ? v.y : 0) + (c + 2 < c0 ? v.z : 0) + (c + 3 < c0 ? v.w : 0);
     }
   }
   int tsum;
@@ -175,6 +241,7 @@ __global__ __launch_bounds__(256) void k_sort_scan_scatter(const int32_t* __rest
   if (c0 == 0) {
     if (e < E && tot > 0) hit_list[1 + hidx] = e;
     if (e == 0) hit_list[0] = hsum;
+    if (tiles) build_tiles_block(e < E ? tot : 0, base, e, bm, tiles, tmp64);
   }
   __syncthreads();
   scatter_chunk(ids, P, E, c0 * kChunk, start, sorted_pairs, pair_pos, run, wcnt);
@@ -210,6 +277,16 @@ __global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ id
   if (e == 0) hit_list[0] = hsum;
   __syncthreads();
   scatter_chunk(ids, P, E, 0, start, sorted_pairs, pair_pos, run, wcnt);
+}
+
+// the tile list of build_tiles_block from the expert offsets (E <= 256), one scan
+__global__ __launch_bounds__(256) void k_build_tiles_packed(const int32_t* __restrict__ offsets, int E,
+                                                            int32_t* __restrict__ tiles, int bm) {
+  __shared__ uint64_t tmp64[4];
+  const int e = threadIdx.x;
+  const int first = e < E ? offsets[e] : 0;
+  const int rows = e < E ? offsets[e + 1] - first : 0;
+  build_tiles_block(rows, first, e, bm, tiles, tmp64);
 }
 
 // MFMA work list: for every hit expert ceil(n_e / BM) tiles of BM sorted rows, listed by
@@ -253,26 +330,28 @@ using namespace moe;
 
 size_t moe_sort_ws_bytes(int P, int E) {
   const size_t nchunks = (size_t)(P + kChunk - 1) / kChunk;
-  return (nchunks * E * sizeof(int32_t) + 255) & ~size_t(255);
+  return ((size_t)hist_stride((int)nchunks) * E * sizeof(int32_t) + 255) & ~size_t(255);
 }
 
 int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t* sorted_pairs,
-                    int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st) {
+                    int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st,
+                    int32_t* tiles, int bm) {
+  const bool fuse_tiles = tiles && P > kChunk && E <= 256 && bm <= 160 &&
+                          moe_max_mtiles(P, E, bm) <= kTilesPacked;
   if (P <= 64) {
     hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(64), 0, st, ids, P, E, offsets, sorted_pairs,
                        pair_pos, hit_list);
-    return moe_check_launch("sort_small");
-  }
-  if (P <= kChunk) {
+  } else if (P <= kChunk) {
     hipLaunchKernelGGL(k_sort_one, dim3(1), dim3(256), 0, st, ids, P, E, offsets, sorted_pairs,
                        pair_pos, hit_list);
-    return moe_check_launch("sort_one");
+  } else {
+    const int nchunks = (P + kChunk - 1) / kChunk, hs = hist_stride(nchunks);
+    int32_t* hist = reinterpret_cast<int32_t*>(ws);
+    hipLaunchKernelGGL(k_sort_hist, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, hs);
+    hipLaunchKernelGGL(k_sort_scan_scatter, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, hs,
+                       offsets, sorted_pairs, pair_pos, hit_list, fuse_tiles ? tiles : nullptr, bm);
   }
-  const int nchunks = (P + kChunk - 1) / kChunk;
-  int32_t* hist = reinterpret_cast<int32_t*>(ws);
-  hipLaunchKernelGGL(k_sort_hist, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist);
-  hipLaunchKernelGGL(k_sort_scan_scatter, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, nchunks,
-                     offsets, sorted_pairs, pair_pos, hit_list);
+  if (tiles && !fuse_tiles) return moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, bm);
   return moe_check_launch("sort");
 }
 
@@ -283,8 +362,9 @@ int moe_max_mtiles(int P, int E, int bm) {
 
 int moe_launch_build_tiles(const int32_t* offsets, const int32_t* hit_list, int E, int P,
                            int32_t* tiles, hipStream_t st, int bm) {
-  (void)E;
-  (void)P;
-  hipLaunchKernelGGL(k_build_tiles, dim3(1), dim3(256), 0, st, offsets, hit_list, tiles, bm);
+  if (E <= 256 && bm <= 160 && moe_max_mtiles(P, E, bm) <= kTilesPacked)
+    hipLaunchKernelGGL(k_build_tiles_packed, dim3(1), dim3(256), 0, st, offsets, E, tiles, bm);
+  else
+    hipLaunchKernelGGL(k_build_tiles, dim3(1), dim3(256), 0, st, offsets, hit_list, tiles, bm);
   return moe_check_launch("build_tiles");
 }

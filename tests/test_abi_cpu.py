@@ -125,8 +125,9 @@ def test_refusals_happen_on_the_host(pkg):
     assert lib.moe_workspace_init(p, 16, None) == pkg._lib.MOE_E_ARG
     # the sort's scratch starts after the sync words: a workspace that only holds the scratch
     # itself is too small
+    # 512 KiB + 256 experts x 1 chunk count padded to 4 x 4 B
     rc = lib.moe_sort_permute(p, 16, 8, 256, p, p, p, p, p, 4096, None)
-    assert rc == pkg._lib.MOE_E_WORKSPACE and b"525312" in lib.moe_last_error()   # 512 KiB + 256 x 4 B
+    assert rc == pkg._lib.MOE_E_WORKSPACE and b"528384" in lib.moe_last_error()
 
 
 def test_product_path_never_imports_the_oracle():
