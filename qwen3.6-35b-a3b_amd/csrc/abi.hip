@@ -195,22 +195,37 @@ int moe_sort_permute(const int32_t* topk_ids, int T, int K, int E, int32_t* expe
 
 // x16: the rows already in f16 (the MFMA paths' activation operand), or NULL to convert here
 // gate / up: the routed gate and up rows of expert e at gate + e * estride and up + e * estride
-// rows per MFMA tile of the grouped-GEMM path experts_impl takes (0: a GEMV path)
+// the 160-row kernels for both GEMMs (gemm3 / gemm4)
+static bool mfma_v2(int path, int H, int I, int gu_fmt, int dn_fmt) {
+  return path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_down_supports(dn_fmt) &&
+         H % 256 == 0 && I % 256 == 0;
+}
+// Q4_K gate_up on gemm4 while the down format has no 160-row kernel (Q6_K): the down GEMM then
+// runs on gemm.hip's 64-row tiles
+static bool mfma_gu4_mixed(int path, int H, int I, int gu_fmt, int dn_fmt) {
+  return path == MOE_PATH_MFMA && gu_fmt == MOE_FMT_Q4_K && H >= 512 && H % 256 == 0 && I % 128 == 0 &&
+         !mfma_v2(path, H, I, gu_fmt, dn_fmt);
+}
+
+// rows per MFMA tile of the first grouped GEMM experts_impl runs (0: a GEMV path)
 static int mfma_tile_rows(int path, int T, int H, int I, int gu_fmt, int dn_fmt) {
   path = pick_path(path, T, gu_fmt, dn_fmt);
   if (path == MOE_PATH_GEMV) return 0;
-  const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_down_supports(dn_fmt) &&
-                  H % 256 == 0 && I % 256 == 0;
-  return v2 ? MOE_GEMM3_BM : MOE_GEMM_BM;
+  return (mfma_v2(path, H, I, gu_fmt, dn_fmt) || mfma_gu4_mixed(path, H, I, gu_fmt, dn_fmt)) ? MOE_GEMM3_BM
+                                                                                           : MOE_GEMM_BM;
 }
 
-// tiles_pre: the tile list of mfma_tile_rows(...) rows, already built (NULL: built here)
+// ints of a tile-list buffer that holds the list of either tile height
+static size_t tile_list_ints(int P, int E) { return 1 + 2 * (size_t)moe_max_mtiles(P, E, MOE_GEMM_BM); }
+
+// tiles_pre: the tile list of mfma_tile_rows(...) rows, already built in a buffer of
+// tile_list_ints(P, E) ints (NULL: built here)
 static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const void* gate,
                         const void* up, size_t estride, int gu_fmt,
                         const void* dn, int dn_fmt, const int32_t* offsets,
                         const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
                         int E, int K, int path, float* y, MoeWs& w, hipStream_t st,
-                        const int32_t* tiles_pre = nullptr) {
+                        int32_t* tiles_pre = nullptr) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
   path = pick_path(path, T, gu_fmt, dn_fmt);
@@ -224,19 +239,32 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                       : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
   if (dn_fmt == MOE_FMT_Q5_K && path == MOE_PATH_MFMA_BF16)
     return moe_set_error(MOE_E_FORMAT, "moe_experts: Q5_K down runs on the GEMV and MFMA (f16) paths");
-  const bool v2 = path == MOE_PATH_MFMA && moe_gemm3_supports(gu_fmt) && moe_gemm3_down_supports(dn_fmt) &&
-                  H % 256 == 0 && I % 256 == 0;
-  const int bm = v2 ? MOE_GEMM3_BM : MOE_GEMM_BM;
+  const bool v2 = mfma_v2(path, H, I, gu_fmt, dn_fmt);
+  const bool gu4 = mfma_gu4_mixed(path, H, I, gu_fmt, dn_fmt);
+  const int bm = (v2 || gu4) ? MOE_GEMM3_BM : MOE_GEMM_BM;
   const int max_tiles = moe_max_mtiles(P, E, bm);
-  const int32_t* tiles = tiles_pre;
+  int32_t* tiles = tiles_pre;
   if (!tiles) {
-    int32_t* t = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * max_tiles) * 4));
-    if (!t) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
-    MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, t, st, bm));
-    tiles = t;
+    tiles = reinterpret_cast<int32_t*>(w.take(tile_list_ints(P, E) * 4));
+    if (!tiles) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+    MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, bm));
   }
   uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
   if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+  if (gu4) {
+    if (!x16) {
+      uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+      if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
+      MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+      x16 = c;
+    }
+    MOE_TRY(moe_launch_gemm4_gateup(x16, gate, up, estride, tiles, max_tiles, offsets, sorted_pairs,
+                                    K, H, I, S, st));
+    // the down GEMM's 64-row list replaces the 160-row one in the same buffer (stream order)
+    MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, MOE_GEMM_BM));
+    return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, moe_max_mtiles(P, E, MOE_GEMM_BM), T,
+                                offsets, H, I, 0, y, st);
+  }
   if (v2) {
     if (!x16) {
       uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
@@ -507,7 +535,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   const int bm = mfma_tile_rows(path, T, H, I, gate_up_fmt, down_fmt);
   int32_t* tiles = nullptr;
   if (bm) {
-    tiles = reinterpret_cast<int32_t*>(w.take((size_t)(1 + 2 * moe_max_mtiles(P, E, bm)) * 4));
+    tiles = reinterpret_cast<int32_t*>(w.take(tile_list_ints(P, E) * 4));
     if (!tiles) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
   }
   // the MFMA path's f16 activation operand, converted once for the shared and routed GEMMs
