@@ -104,10 +104,15 @@ def time_stream(fn, n: int, torch, stream=None) -> float:
 
 
 def capture(torch, fn):
-    """fn's launches captured into a HIP graph on a side stream."""
+    """fn's launches captured into a HIP graph on a side stream. One eager run on that stream
+    first: the library's per-stream workspace is then created (and initialised) outside the
+    graph, so its one-time initialisation is not replayed with every step."""
     g = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        fn()
+    cap.synchronize()
     with torch.cuda.stream(cap):
         with torch.cuda.graph(g, stream=cap):
             fn()

@@ -17,9 +17,10 @@
 //     2^(Ex+Ew-10) (exact) and the bias is added. The distance to the exact sum x . w + b is at most
 //       sum|x^-x| max|w^| + max|x| sum|w^-w|        (the rows' rounding to the digit grid)
 //     + 2^-52 (sum of the Horner partials' magnitudes) 2^(Ex+Ew-10) + 2^-52 |s|  (f64 roundings),
-//     and that bound certifies the bf16 rounding exactly as the f64 kernels' bound does. x uses
-//     D = 4 digits (exact for elements within 2^21 of the row maximum), bf16 router rows D = 4,
-//     f32 router rows D = 5 (exact within 2^13); what is left over is rare and bounded.
+//     and that bound certifies the bf16 rounding exactly as the f64 kernels' bound does. bf16
+//     rows (x or router) use D = 3 digits (S = 21: a bf16 element is on the grid when within 2^14
+//     of its row maximum), f32 x rows D = 4 (within 2^6), f32 router rows D = 5 (within 2^14);
+//     what is left over is rare and bounded.
 //   * A logit the bound does not certify is recomputed by its wave in double-double (the whole
 //     wave sums the row in parallel) and rounded from that, ties to even on the midpoint itself.
 //
@@ -36,13 +37,14 @@
 namespace moe {
 namespace ri8 {
 
-constexpr int kXD = 4;                 // digits per x element
-constexpr int kXS = 8 * kXD - 3;       // x scale exponent S
+constexpr int kXDMax = 4;              // digits per x element, at most (scratch sizing)
 constexpr int kKC = 64;                // k per LDS stage
 constexpr int kRS = 80;                // LDS row stride (bytes): 16-byte slots of 8 rows distinct
 constexpr int kMaxCh = 8;              // prep: 8-element chunks per lane, so H <= 4096
 
-template <int WDT> struct WDig { static constexpr int D = (WDT == MOE_DT_F32) ? 5 : 4; };
+template <int XDT> struct XDig { static constexpr int D = (XDT == MOE_DT_F32) ? 4 : 3; };
+template <int WDT> struct WDig { static constexpr int D = (WDT == MOE_DT_F32) ? 5 : 3; };
+static_assert(XDig<MOE_DT_F32>::D <= kXDMax && XDig<MOE_DT_BF16>::D <= kXDMax, "x digit planes");
 
 struct alignas(32) RowMeta {
   int e;          // row exponent E (0 for an all-zero row)
@@ -139,7 +141,7 @@ __device__ __forceinline__ void store_digits8(const double* n8, int8_t* dst, siz
 }
 
 // One wave per row: rows 0..E-1 are the router rows (D = WD; planes [WD][E][H] in wdig), rows
-// E..E+T-1 the x rows (D = kXD; planes [kXD][T][H] in xdig); the metadata goes to meta[t] for
+// E..E+T-1 the x rows (D = XD; planes [XD][T][H] in xdig); the metadata goes to meta[t] for
 // x rows and meta[T + e] for router rows. The router rows come first so that their longer
 // digit work starts with the launch. grid = ceil((T+E)/4), block = 256.
 template <int RD, int DT>
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(256) void k_router_prep(const void* __restrict__ xv
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T + E) return;
   if (row < E) prep_row<WDig<WDT>::D, WDT>(w, row, E, H, lane, meta + T + row, wdig);
-  else prep_row<kXD, XDT>(xv, row - E, T, H, lane, meta + (row - E), xdig);
+  else prep_row<XDig<XDT>::D, XDT>(xv, row - E, T, H, lane, meta + (row - E), xdig);
 }
 
 // ------------------------------------------------------------------------------ digit GEMM --
@@ -250,8 +252,9 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
             const RowMeta* __restrict__ meta, const float* __restrict__ bias, int T, int H, int E,
             uint16_t* __restrict__ logits) {
   constexpr int WD = WDig<WDT>::D;
-  constexpr int NL = kXD + WD - 1;                  // accumulator levels
-  __shared__ __attribute__((aligned(16))) int8_t sx[2][kXD][64 * kRS];
+  constexpr int XD = XDig<XDT>::D;
+  constexpr int NL = XD + WD - 1;                  // accumulator levels
+  __shared__ __attribute__((aligned(16))) int8_t sx[2][XD][64 * kRS];
   __shared__ __attribute__((aligned(16))) int8_t sw[2][WD][64 * kRS];
   const int nT = (T + 63) / 64, nE = (E + 63) / 64;
   const int b = blockIdx.x, xcd = b & 7, jb = b >> 3;
@@ -277,12 +280,12 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   // one register set: stage s + 1's digits (loaded during stage s - 1) go into the idle LDS
   // buffer at the start of stage s, the same registers then take stage s + 2's loads, then the
   // MFMAs of stage s run; one barrier per stage
-  constexpr int NP = WD > kXD ? WD : kXD;
+  constexpr int NP = WD > XD ? WD : XD;
   u32x4 q[NP];
   auto gload = [&](int k0) {
     if (stage_x) {
 #pragma unroll
-      for (int a = 0; a < kXD; ++a) q[a] = *reinterpret_cast<const u32x4*>(src + a * plane + k0);
+      for (int a = 0; a < XD; ++a) q[a] = *reinterpret_cast<const u32x4*>(src + a * plane + k0);
     } else {
 #pragma unroll
       for (int a = 0; a < WD; ++a) q[a] = *reinterpret_cast<const u32x4*>(src + a * plane + k0);
@@ -291,7 +294,7 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   auto lstore = [&](int buf) {
     if (stage_x) {
 #pragma unroll
-      for (int a = 0; a < kXD; ++a) *reinterpret_cast<u32x4*>(&sx[buf][a][soff]) = q[a];
+      for (int a = 0; a < XD; ++a) *reinterpret_cast<u32x4*>(&sx[buf][a][soff]) = q[a];
     } else {
 #pragma unroll
       for (int a = 0; a < WD; ++a) *reinterpret_cast<u32x4*>(&sw[buf][a][soff]) = q[a];
@@ -306,13 +309,13 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   auto mma = [&](int buf) {
     {
       const int ks = 32 * kh;
-      v4i a[kXD], bq[WD];
+      v4i a[XD], bq[WD];
 #pragma unroll
-      for (int p = 0; p < kXD; ++p) a[p] = *reinterpret_cast<const v4i*>(&sx[buf][p][ar + ks]);
+      for (int p = 0; p < XD; ++p) a[p] = *reinterpret_cast<const v4i*>(&sx[buf][p][ar + ks]);
 #pragma unroll
       for (int q = 0; q < WD; ++q) bq[q] = *reinterpret_cast<const v4i*>(&sw[buf][q][br + ks]);
 #pragma unroll
-      for (int p = 0; p < kXD; ++p)
+      for (int p = 0; p < XD; ++p)
 #pragma unroll
         for (int q = 0; q < WD; ++q)
           acc[p + q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[p], bq[q], acc[p + q], 0, 0, 0);
@@ -398,9 +401,10 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   }
 }
 
-// scratch: RowMeta[T + E] | x digit planes [kXD][T][H] | router digit planes [WD][E][H]
+// scratch: RowMeta[T + E] | x digit planes [XD][T][H] | router digit planes [WD][E][H] (sized
+// for the most digits)
 inline size_t meta_bytes(int T, int E) { return ((size_t)(T + E) * sizeof(RowMeta) + 255) / 256 * 256; }
-inline size_t xdig_bytes(int T, int H) { return ((size_t)kXD * T * H + 255) / 256 * 256; }
+inline size_t xdig_bytes(int T, int H) { return ((size_t)kXDMax * T * H + 255) / 256 * 256; }
 
 template <int XDT, int WDT>
 void launch(const void* x, const void* w, const float* bias, int T, int H, int E, uint16_t* logits,
