@@ -184,25 +184,51 @@ __device__ void q_heap_select(TopkLds& s, int lo, int mid, int hi) {
   }
 }
 
-// Unguarded Hoare partition of [a, b) around the pivot at a-1, done by the whole wave.
-__device__ int wave_partition(TopkLds& s, int a, int b, int lane) {
-  const float pv = s.v[a - 1];
+// ---- torch CPU topk(values, k) for k*64 > n: nth_element(k-1) then sort of the first k-1 ----
+// (libstdc++ introselect: median-of-three pivot to the front, unguarded Hoare partition, until at
+// most 3 elements remain or the depth limit 2 floor(log2 n) sends it to heap-select; then the
+// insertion sorts). The partition rounds run on registers: lane l holds positions l + 64 j.
+// value (or id bits) at position p: register p >> 6 (wave-uniform) of lane p & 63
+__device__ __forceinline__ uint32_t reg_at(const uint32_t (&r)[4], int p) {
+  // four reads and scalar selects: no branches
+  const int l = p & 63, j = p >> 6;
+  const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)r[0], l);
+  const uint32_t x1 = (uint32_t)__builtin_amdgcn_readlane((int)r[1], l);
+  const uint32_t x2 = (uint32_t)__builtin_amdgcn_readlane((int)r[2], l);
+  const uint32_t x3 = (uint32_t)__builtin_amdgcn_readlane((int)r[3], l);
+  const uint32_t lo = (j & 1) ? x1 : x0, hi = (j & 1) ? x3 : x2;
+  return (j & 2) ? hi : lo;
+}
+
+// One unguarded Hoare partition of [a, b) around pv (the pivot, at a - 1), by rank pairing: the
+// i-th stop of the left scan (an A position, !(v > pv)) trades places with the i-th stop of the
+// right scan (a B position, !(pv > v)) while it lies to the left of it, which is the sequence of
+// swaps the sequential scans make. Partners meet through LDS slots indexed by the rank, with no
+// position lookup. Returns the cut, min(A[M], B[M-1], b) for M swaps.
+__device__ int reg_partition(TopkLds& s, uint32_t (&v)[4], uint32_t (&id)[4], int a, int b, float pv,
+                             int lane) {
   const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
   const uint64_t gt = (lane == 63) ? 0ull : ((~0ull) << (lane + 1));
+  // registers holding positions of [a, b) (wave-uniform): the others are skipped
+  const int j0 = a >> 6, j1 = (b - 1) >> 6;
   bool isA[4], isB[4];
   uint64_t mA[4], mB[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    isA[j] = isB[j] = false;
+    mA[j] = mB[j] = 0ull;
+    if (j < j0 || j > j1) continue;
     const int pos = 64 * j + lane;
     const bool in = pos >= a && pos < b;
-    const float v = in ? s.v[pos] : 0.0f;
-    isA[j] = in && !(v > pv);
-    isB[j] = in && !(pv > v);
+    const float x = __uint_as_float(v[j]);
+    isA[j] = in && !(x > pv);
+    isB[j] = in && !(pv > x);
     mA[j] = __ballot(isA[j]);
     mB[j] = __ballot(isB[j]);
   }
   int cA[5], cB[5];
-  cA[0] = 0; cB[0] = 0;
+  cA[0] = 0;
+  cB[0] = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     cA[j + 1] = cA[j] + __popcll(mA[j]);
@@ -218,83 +244,119 @@ __device__ int wave_partition(TopkLds& s, int a, int b, int lane) {
     rankB[j] = (totB - cB[j + 1]) + __popcll(mB[j] & gt);    // # B positions > pos
     swA[j] = isA[j] && rankB[j] > rankA[j];
     swB[j] = isB[j] && rankA[j] > rankB[j];
-    M += __popcll(__ballot(swA[j]));
+    if (j >= j0 && j <= j1) M += __popcll(__ballot(swA[j]));
   }
-  if (lane == 0) { s.cell[0] = 0x7FFFFFFF; s.cell[1] = 0x7FFFFFFF; }
-  wave_sync();
+  // A[M] and B[M-1]: the positions holding those ranks (none: past the range)
+  int cut = b;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    if (swA[j]) s.pa[rankA[j]] = pos;
-    if (swB[j]) s.pb[rankB[j]] = pos;
-    if (isA[j] && rankA[j] == M) s.cell[0] = pos;            // A[M]
-    if (isB[j] && rankB[j] == M - 1) s.cell[1] = pos;        // B[M-1]
+    if (j < j0 || j > j1) continue;
+    const uint64_t fa = __ballot(isA[j] && rankA[j] == M);
+    const uint64_t fb = __ballot(isB[j] && rankB[j] == M - 1);
+    if (fa) cut = min(cut, 64 * j + (int)__builtin_ctzll(fa));
+    if (fb) cut = min(cut, 64 * j + (int)__builtin_ctzll(fb));
   }
-  wave_sync();
-  float nv[4];
-  int ni[4];
+  if (M > 0) {
+    // the rank slots: swapping A of rank r -> v[r] / i[r], swapping B of rank r -> pa[r] / pb[r]
+    // (r < M <= 128). Every lane of a register in range stores and loads: the others use slot
+    // 128 + lane, which no rank reaches.
+    const int dummy = 128 + lane;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int partner = -1;
-    if (swA[j]) partner = s.pb[rankA[j]];
-    if (swB[j]) partner = s.pa[rankB[j]];
-    if (partner >= 0) { nv[j] = s.v[partner]; ni[j] = s.i[partner]; }
-  }
-  // min(A[M], B[M-1]); the median-of-three guarantees A[0] exists, the clamp only keeps a broken
-  // invariant from indexing outside the range
-  const int cut = min(min(s.cell[0], s.cell[1]), b);
-  wave_sync();
+    for (int j = 0; j < 4; ++j) {
+      if (j < j0 || j > j1) continue;
+      const int ia = swA[j] ? rankA[j] : dummy;
+      const int ib = swB[j] ? rankB[j] : dummy;
+      s.v[ia] = __uint_as_float(v[j]);
+      s.i[ia] = (int)id[j];
+      s.pa[ib] = (int)v[j];
+      s.pb[ib] = (int)id[j];
+    }
+    wave_sync();
+    uint32_t na[4], nia[4], nb[4], nib[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (swA[j] || swB[j]) { s.v[64 * j + lane] = nv[j]; s.i[64 * j + lane] = ni[j]; }
+    for (int j = 0; j < 4; ++j) {
+      if (j < j0 || j > j1) continue;
+      const int ra = swA[j] ? rankA[j] : dummy;
+      const int rb = swB[j] ? rankB[j] : dummy;
+      na[j] = (uint32_t)s.pa[ra];
+      nia[j] = (uint32_t)s.pb[ra];
+      nb[j] = __float_as_uint(s.v[rb]);
+      nib[j] = (uint32_t)s.i[rb];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < j0 || j > j1) continue;
+      v[j] = swA[j] ? na[j] : (swB[j] ? nb[j] : v[j]);
+      id[j] = swA[j] ? nia[j] : (swB[j] ? nib[j] : id[j]);
+    }
+    wave_sync();
   }
-  wave_sync();
   return cut;
 }
 
-// torch CPU topk(values, k) for k*64 > n: nth_element(k-1) then sort of the first k-1.
+// p holds the n values (lane + 64 j); the array goes to s.v / s.i (positions 0..n-1) when the
+// rounds end, for the heap-select fallback and the final insertion sorts, which run on LDS.
 // Returns 1 if the heap-select branch ran (reported for tests), 0 otherwise.
-__device__ int wave_torch_topk(TopkLds& s, int n, int k, int lane) {
+__device__ int wave_torch_topk_reg(TopkLds& s, const float* p, int n, int k, int lane) {
+  uint32_t v[4], id[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = __float_as_uint(p[j]);
+    id[j] = (uint32_t)(64 * j + lane);
+  }
   int lo = 0, hi = n;
   const int nth = k - 1;
   int depth = 2 * (31 - __clz(n));
-  int heap = 0;
+  bool deep = false;
   while (hi - lo > 3) {
-    if (depth == 0) {
-      if (lane == 0) {
-        q_heap_select(s, lo, nth + 1, hi);
-        qswap(s, lo, nth);
-      }
-      wave_sync();
-      heap = 1;
-      break;
-    }
+    if (depth == 0) { deep = true; break; }
     --depth;
     const int mid = lo + (hi - lo) / 2;
-    {
-      // move_median_to_first(lo, lo+1, mid, hi-1): the three candidates read in parallel
-      const int a = lo + 1, b = mid, c = hi - 1;
-      const float cand = s.v[lane == 0 ? a : (lane == 1 ? b : c)];
-      const float va = readlane_f32(cand, 0), vb = readlane_f32(cand, 1), vc = readlane_f32(cand, 2);
-      int pick;
-      if (va > vb) {
-        if (vb > vc) pick = b;
-        else if (va > vc) pick = c;
-        else pick = a;
-      } else if (va > vc) pick = a;
-      else if (vb > vc) pick = c;
-      else pick = b;
-      if (lane == 0) qswap(s, lo, pick);
+    // move_median_to_first(lo, lo+1, mid, hi-1)
+    const int a = lo + 1, b = mid, c = hi - 1;
+    const float va = __uint_as_float(reg_at(v, a)), vb = __uint_as_float(reg_at(v, b));
+    const float vc = __uint_as_float(reg_at(v, c));
+    int pick;
+    if (va > vb) {
+      if (vb > vc) pick = b;
+      else if (va > vc) pick = c;
+      else pick = a;
+    } else if (va > vc) pick = a;
+    else if (vb > vc) pick = c;
+    else pick = b;
+    const uint32_t vlo = reg_at(v, lo), ilo = reg_at(id, lo);
+    const uint32_t vpk = reg_at(v, pick), ipk = reg_at(id, pick);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = 64 * j + lane;
+      const bool at_lo = pos == lo, at_pk = pos == pick;
+      v[j] = at_lo ? vpk : (at_pk ? vlo : v[j]);
+      id[j] = at_lo ? ipk : (at_pk ? ilo : id[j]);
     }
-    wave_sync();
-    const int cut = wave_partition(s, lo + 1, hi, lane);
+    const int cut = reg_partition(s, v, id, lo + 1, hi, __uint_as_float(vpk), lane);
     if (cut <= nth) lo = cut;
     else hi = cut;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int pos = 64 * j + lane;
+    if (pos < n) { s.v[pos] = __uint_as_float(v[j]); s.i[pos] = (int)id[j]; }
+  }
+  wave_sync();
+  int heap = 0;
+  if (deep) {
+    if (lane == 0) {
+      q_heap_select(s, lo, nth + 1, hi);
+      qswap(s, lo, nth);
+    }
+    wave_sync();
+    heap = 1;
   }
   if (!heap) wave_stable_sort_small(s, lo, hi - lo, lane);
   wave_stable_sort_small(s, 0, k - 1, lane);
   return heap;
 }
+
 
 
 // 64-bit unsigned wave max, every lane ends with the maximum (DPP inside rows, readlane across)
@@ -401,13 +463,7 @@ __device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lan
 __device__ __forceinline__ void route_replay_and_write(TopkLds& s, const float* p, int E, int K,
                                                        int lane, int32_t* ids, float* w_f32,
                                                        uint16_t* w_bf16, int32_t* heap_flag) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pos = 64 * j + lane;
-    if (pos < E) { s.v[pos] = p[j]; s.i[pos] = pos; }
-  }
-  wave_sync();
-  const int heap = wave_torch_topk(s, E, K, lane);
+  const int heap = wave_torch_topk_reg(s, p, E, K, lane);
   if (lane == 0) {
     float tot = 0.0f;
     for (int k = 0; k < K; ++k) tot += s.v[k];
