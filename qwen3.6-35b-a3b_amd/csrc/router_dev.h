@@ -23,20 +23,17 @@ __device__ __forceinline__ DD dd_add(DD a, DD b) {
 // exponent e with 2^e <= |v| < 2^(e+1), v != 0, v finite
 __host__ __device__ __forceinline__ int exp2_floor(double v) { return ilogb(v); }
 
-// Round the f64 value s (|s - exact| <= bound) to bf16. Returns false if not certified, i.e. if a
-// bf16 rounding midpoint lies within `bound` of s. (Host-callable, so the host tests can check it.)
-__host__ __device__ __forceinline__ bool round_bf16_certified(double s, double bound, uint32_t* out) {
-  if (s == 0.0) {
-    if (bound > 0.0) {
-      // the exact value may be a tiny non-zero: certify only if every value within the bound
-      // rounds to zero, i.e. the bound is below half the smallest bf16 subnormal
-      if (bound >= ldexp(1.0, -134)) return false;
-    }
-    *out = 0u;
-    return true;
-  }
+// The bf16 rounding of the f64 value s (|s - exact| <= bound) into bits, and whether it is
+// certified, i.e. no bf16 rounding midpoint lies within `bound` of s. Straight-line (selects, no early exits or
+// conditional writes), so that a wave finishing many logits interleaves their dependency chains.
+// bits is the bf16 rounding of s whether or not it is certified.
+__host__ __device__ __forceinline__ bool round_bf16_sel(double s, double bound, uint32_t& bits) {
   const double a = fabs(s);
-  const int e = exp2_floor(a);
+  const bool zero = a == 0.0;
+  // zero: certified only if every value within the bound rounds to zero, i.e. the bound is below
+  // half the smallest bf16 subnormal (the exact value may be a tiny non-zero)
+  const bool ok_zero = !(bound > 0.0 && bound >= 0x1p-134);
+  const int e = zero ? 0 : exp2_floor(a);
   const int qe = max(e - 7, -133);
   const double r = ldexp(a, -qe);                     // exact
   const double fl = floor(r);
@@ -44,15 +41,23 @@ __host__ __device__ __forceinline__ bool round_bf16_certified(double s, double b
   // just above a power of two (fl == 128) the quantum below 2^e is half as wide, so the nearest
   // midpoint may be 2^e - q/4, at (r - 128) + 1/4 quanta, rather than 2^e + q/2; in the subnormal
   // range (qe == -133 below and above 2^e) the quantum does not change
-  if (fl == 128.0 && qe > -133) dist = fmin(dist, (r - fl) + 0.25);
-  if (ldexp(dist, qe) <= bound) return false;
+  dist = (fl == 128.0 && qe > -133) ? fmin(dist, (r - fl) + 0.25) : dist;
   const double rounded = ldexp(rint(r), qe);          // rint: ties-to-even
   float f = (float)rounded;                           // exact (or inf on overflow)
-  if (s < 0) f = -f;
+  f = s < 0 ? -f : f;
   uint32_t fb;
   __builtin_memcpy(&fb, &f, 4);
-  *out = fb >> 16;
-  return true;
+  bits = zero ? 0u : fb >> 16;
+  return zero ? ok_zero : !(ldexp(dist, qe) <= bound);
+}
+
+// round_bf16_sel with the bits written only when certified. (Host-callable, so the host tests can
+// check it.)
+__host__ __device__ __forceinline__ bool round_bf16_certified(double s, double bound, uint32_t* out) {
+  uint32_t bits;
+  const bool ok = round_bf16_sel(s, bound, bits);
+  if (ok) *out = bits;
+  return ok;
 }
 
 // Decide the bf16 rounding of hi+lo (double-double) whose error is below ddbound.

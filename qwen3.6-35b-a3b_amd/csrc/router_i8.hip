@@ -28,9 +28,11 @@
 // and of the x rows), then k_router_i8 (64 tokens x 64 experts per block of 8 waves: two waves per
 // 32 x 32 tile, each summing one k half of every 64-wide LDS stage, their int32 partial sums
 // added through LDS at the end; digit planes staged global -> registers -> LDS one stage ahead).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
+#include "lds_dma.h"
 #include "moe_internal.h"
 #include "router_dev.h"
 
@@ -59,6 +61,20 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // type uint4 are left as allocas, which the backend then places in LDS)
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Three digits on both sides (bf16 x, bf16 router rows): the digit planes are stored
+// fragment-tiled, so that every MFMA operand (32 rows x 32 k of one plane, lane l holding row
+// l % 32, k 16 (l / 32) .. + 15) is one contiguous kilobyte with lane l's 16 bytes at 16 l,
+// operands ordered [row group r / 32][k chunk k / 32][digit]. Row groups run to a multiple of 64
+// rows; the rows past T (or E) are never written and their sums never stored.
+constexpr int kTD = 3;
+template <int XDT, int WDT> constexpr bool tiled() {
+  return XDig<XDT>::D == kTD && WDig<WDT>::D == kTD;
+}
+__host__ __device__ __forceinline__ size_t tiled_off(int r, int k, int C) {
+  const size_t frag = ((size_t)(r >> 5) * C + (k >> 5)) * kTD;
+  return (frag << 10) + ((size_t)((((k >> 4) & 1) << 5) | (r & 31)) << 4) + (k & 15);
+}
 
 template <int DT>
 __device__ __forceinline__ float elt(const void* p, size_t i) {
@@ -144,7 +160,7 @@ __device__ __forceinline__ void store_digits8(const double* n8, int8_t* dst, siz
 // E..E+T-1 the x rows (D = XD; planes [XD][T][H] in xdig); the metadata goes to meta[t] for
 // x rows and meta[T + e] for router rows. The router rows come first so that their longer
 // digit work starts with the launch. grid = ceil((T+E)/4), block = 256.
-template <int RD, int DT>
+template <int RD, int DT, bool TILED>
 __device__ __forceinline__ void prep_row(const void* __restrict__ base, int r, int nrows, int H,
                                          int lane, RowMeta* __restrict__ m_out,
                                          int8_t* __restrict__ dig) {
@@ -180,7 +196,9 @@ __device__ __forceinline__ void prep_row(const void* __restrict__ base, int r, i
       qmax = fmax(qmax, fabs(n));
       n8[j] = n;
     }
-    store_digits8<RD>(n8, dig + off + (size_t)(c * 64 + lane) * 8, plane);
+    const int k = (c * 64 + lane) * 8;
+    if constexpr (TILED) store_digits8<RD>(n8, dig + tiled_off(r, k, H >> 5), 1024);
+    else store_digits8<RD>(n8, dig + off + k, plane);
   }
   dsum = wave_sum_f64(dsum);
   qmax = wave_max_f64(qmax);
@@ -204,8 +222,9 @@ __global__ __launch_bounds__(256) void k_router_prep(const void* __restrict__ xv
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T + E) return;
-  if (row < E) prep_row<WDig<WDT>::D, WDT>(w, row, E, H, lane, meta + T + row, wdig);
-  else prep_row<XDig<XDT>::D, XDT>(xv, row - E, T, H, lane, meta + (row - E), xdig);
+  constexpr bool kTiled = tiled<XDT, WDT>();
+  if (row < E) prep_row<WDig<WDT>::D, WDT, kTiled>(w, row, E, H, lane, meta + T + row, wdig);
+  else prep_row<XDig<XDT>::D, XDT, kTiled>(xv, row - E, T, H, lane, meta + (row - E), xdig);
 }
 
 // ------------------------------------------------------------------------------ digit GEMM --
@@ -216,30 +235,116 @@ __device__ __forceinline__ void fence_sched() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// One wave recomputes logit (t, e) in double-double: lane l sums k = l, l+64, ... (every x*W
-// product is exact in f64), the partial sums meet in a butterfly; bound as logit_dd_recompute's.
+// One wave recomputes logit (t, e) in double-double: lane l sums k = 512 c + 8 l .. + 7 over the
+// H / 512 chunks c (every x*W product is exact in f64) into four interleaved double-doubles, all
+// of its elements loaded before the first add (the chunk index clamped, so the loads do not
+// depend on H); the partial sums then meet in a butterfly. Bound as logit_dd_recompute's (at most
+// H + 64 double-double adds on any path, whatever their order).
 template <int XDT, int WDT>
 __device__ uint32_t wave_dd_logit(const void* __restrict__ xv, const void* __restrict__ w, int t,
                                   int e, int H, double bval, int lane) {
-  DD d = {0.0, 0.0};
-  double xsq = 0.0, wsq = 0.0;
-  for (int k = lane; k < H; k += 64) {
-    const double xk = elt<XDT>(xv, (size_t)t * H + k);
-    const double wk = elt<WDT>(w, (size_t)e * H + k);
-    d = dd_add(d, DD{xk * wk, 0.0});
-    xsq = fma(xk, xk, xsq);
-    wsq = fma(wk, wk, wsq);
+  const int nch = H / 512;
+  float xa[kMaxCh][8], wa[kMaxCh][8];
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const size_t k = (size_t)(min(c, nch - 1) * 64 + lane) * 8;
+    load8<XDT>(xv, (size_t)t * H + k, xa[c]);
+    load8<WDT>(w, (size_t)e * H + k, wa[c]);
   }
+  DD d[4] = {{0.0, 0.0}, {0.0, 0.0}, {0.0, 0.0}, {0.0, 0.0}};
+  double xsq = 0.0, wsq = 0.0;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    if (c >= nch) break;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const double xk = xa[c][j], wk = wa[c][j];
+      d[j & 3] = dd_add(d[j & 3], DD{xk * wk, 0.0});
+      xsq = fma(xk, xk, xsq);
+      wsq = fma(wk, wk, wsq);
+    }
+  }
+  DD s = dd_add(dd_add(d[0], d[1]), dd_add(d[2], d[3]));
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
-    const DD p = {__shfl_xor(d.hi, o, 64), __shfl_xor(d.lo, o, 64)};
-    d = dd_add(d, p);
+    const DD p = {__shfl_xor(s.hi, o, 64), __shfl_xor(s.lo, o, 64)};
+    s = dd_add(s, p);
     xsq += __shfl_xor(xsq, o, 64);
     wsq += __shfl_xor(wsq, o, 64);
   }
-  d = dd_add(d, DD{bval, 0.0});
+  s = dd_add(s, DD{bval, 0.0});
   const double ddb = (double)(H + 64) * 0x1p-104 * 16.0 * (sqrt(xsq) * sqrt(wsq) + fabs(bval));
-  return round_bf16_dd(d, ddb);
+  return round_bf16_dd(s, ddb);
+}
+
+// Row metadata of a block's 64 tokens (from t0) and 64 experts (from e0) into LDS (indices
+// clamped; rows past T or E are never finished). Read after the block's next barrier.
+__device__ __forceinline__ void stage_meta(RowMeta* sm, const RowMeta* __restrict__ meta, int t0,
+                                           int e0, int T, int E, int tid) {
+  if (tid < 64) sm[tid] = meta[min(t0 + tid, T - 1)];
+  else if (tid < 128) sm[tid] = meta[T + min(e0 + tid - 64, E - 1)];
+}
+
+// The certified bf16 logits of one wave's 32 x 32 tile from its exact level sums (level l =
+// the digit pairs a + b = l): register r of lane l holds token tb + 8 (r / 4) + 4 (l / 32) + r % 4
+// and expert eb + l % 32; registers [r0, r1) are this wave's to finish. xm / wm: the row metadata
+// of the block's tokens t0 .. t0 + 63 and experts e0 .. e0 + 63 (in LDS, tb - t0 and eb - e0 the
+// tile's offsets in them). A logit the bound does not certify is recomputed by the whole wave in
+// double-double (rare).
+template <int XDT, int WDT, int NL>
+__device__ __forceinline__ void finish_tile(const v16i (&acc)[NL], int r0, int r1, int t0, int tl,
+                                            int e0, int el, const RowMeta* xm, const RowMeta* wm,
+                                            const void* __restrict__ xv,
+                                            const void* __restrict__ w,
+                                            const float* __restrict__ bias, int T, int H, int E,
+                                            int lane, uint16_t* __restrict__ logits) {
+  const int tb = t0 + tl, eb = e0 + el;
+  const int e = eb + (lane & 31);
+  const bool e_ok = e < E;
+  const RowMeta mw = wm[el + (lane & 31)];
+  const double bval = (bias && e_ok) ? (double)bias[e] : 0.0;
+  // every register's chain is computed first (no branches) so that the wave interleaves them;
+  // the stores follow
+  uint32_t fail = 0, okm = 0, bits[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int tr = tl + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    const int t = t0 + tr;
+    const bool live = r >= r0 && r < r1 && t < T && e_ok;
+    const RowMeta mx = xm[tr];
+    double v = (double)acc[NL - 1][r], cb = 0.0;
+#pragma unroll
+    for (int l = NL - 2; l >= 0; --l) {
+      v = fma(v, 0x1p-8, (double)acc[l][r]);
+      cb += fabs(v);
+    }
+    const int sc = mx.e + mw.e - 10;
+    const double s = ldexp(v, sc) + bval;
+    const double bound = (mx.dsum * mw.qmax + mx.vmax * mw.dsum) * (1.0 + 0x1p-32) +
+                         ldexp(cb, sc) * 0x1p-52 + fabs(s) * 0x1p-52;
+    const bool ok = round_bf16_sel(s, bound, bits[r]);
+    okm |= (live && ok) ? 1u << r : 0u;
+    fail |= (live && !ok) ? 1u << r : 0u;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = t0 + tl + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    if (okm >> r & 1) logits[(size_t)t * E + e] = (uint16_t)bits[r];
+  }
+  for (;;) {
+    const uint64_t m = __ballot(fail != 0);
+    if (m == 0) break;
+    const int l0 = __builtin_ctzll(m);
+    const int r = __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)fail, l0));
+    const int t = tb + 8 * (r >> 2) + 4 * (l0 >> 5) + (r & 3);
+    const int ee = eb + (l0 & 31);
+    const double bv = bias ? (double)bias[ee] : 0.0;
+    const uint32_t bits = wave_dd_logit<XDT, WDT>(xv, w, t, ee, H, bv, lane);
+    if (lane == l0) {
+      logits[(size_t)t * E + ee] = (uint16_t)bits;
+      fail &= ~(1u << r);
+    }
+  }
 }
 
 // grid = 8 * nE * ceil(nT / 8) blocks (nT = ceil(T/64) token tiles, nE = ceil(E/64) expert
@@ -256,6 +361,7 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   constexpr int NL = XD + WD - 1;                  // accumulator levels
   __shared__ __attribute__((aligned(16))) int8_t sx[2][XD][64 * kRS];
   __shared__ __attribute__((aligned(16))) int8_t sw[2][WD][64 * kRS];
+  __shared__ RowMeta smeta[128];
   const int nT = (T + 63) / 64, nE = (E + 63) / 64;
   const int b = blockIdx.x, xcd = b & 7, jb = b >> 3;
   const int tt = xcd + 8 * (jb / nE), et = jb % nE;
@@ -263,10 +369,9 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
   const int t0 = tt * 64, e0 = et * 64;
   // 8 waves: wave (kh, q) owns the 32 x 32 tile q (2 x 2) for the k half kh of every stage
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  stage_meta(smeta, meta, t0, e0, T, E, tid);
   const int kh = wv >> 2, q4 = wv & 3;
   const int wm = q4 >> 1, wn = q4 & 1;
-  const RowMeta* wmeta = meta + T;
-
   // staging role: waves 0-3 copy the x planes, waves 4-7 the router planes; row (tid%256)/4 of
   // the tile, 16 bytes at 16 * (tid % 4) of each plane's stage slice
   const int st = tid & 255;
@@ -358,53 +463,128 @@ k_router_i8(const void* __restrict__ xv, const void* __restrict__ w,
     __syncthreads();
   }
 
-  // epilogue: lane holds expert e0 + 32 wn + lane % 32 for the 8 tokens of its registers
-  const int e = e0 + wn * 32 + (lane & 31);
-  const bool e_ok = e < E;
-  const RowMeta mw = wmeta[min(e, E - 1)];
-  const double bval = (bias && e_ok) ? (double)bias[e] : 0.0;
-  uint32_t fail = 0;
+  finish_tile<XDT, WDT, NL>(acc, 8 * kh, 8 * kh + 8, t0, wm * 32, e0, wn * 32, smeta, smeta + 64, xv,
+                            w, bias, T, H, E, lane, logits);
+}
+
+// Tiled operands (bf16 x, bf16 router rows): grid as k_router_i8's, block = 256 (4 waves, one
+// per SIMD; no LDS in the main loop). Wave (kh, n) = (w / 2, w % 2) sums the k chunks kh,
+// kh + 2, ... of the block's 64 tokens x experts 32 n .. 32 n + 31 (two 32 x 32 tiles), its
+// operands streamed straight into registers, nine kilobyte operands per chunk with two chunks in
+// flight (the x operands are fetched by both waves of a k half, the second time from L1). The
+// two k halves then meet through LDS: each wave keeps the tile of token half kh and hands the
+// other one to its partner (w ^ 2); integer adds, exact.
+template <int XDT, int WDT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+k_router_i8t(const void* __restrict__ xv, const void* __restrict__ w,
+             const int8_t* __restrict__ xdig, const int8_t* __restrict__ wdig,
+             const RowMeta* __restrict__ meta, const float* __restrict__ bias, int T, int H, int E,
+             uint16_t* __restrict__ logits) {
+  static_assert(tiled<XDT, WDT>(), "three digits on both sides");
+  constexpr int D = kTD, NL = 2 * D - 1;
+  constexpr int kOps = 3 * D;                             // operands per chunk
+  __shared__ __attribute__((aligned(16))) u32x4 xch[4][NL][4][64];
+  __shared__ RowMeta smeta[128];
+  const int nT = (T + 63) / 64, nE = (E + 63) / 64;
+  const int b = blockIdx.x, xcd = b & 7, jb = b >> 3;
+  const int tt = xcd + 8 * (jb / nE), et = jb % nE;
+  if (tt >= nT) return;
+  stage_meta(smeta, meta, 64 * tt, 64 * et, T, E, threadIdx.x);
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kh = wv >> 1, cg = wv & 1;
+  const int C = H >> 5;                                   // k chunks
+  const uint32_t gb = (uint32_t)C * D * 1024;             // bytes per 32-row group
+  const auto rx = dma::rsrc(xdig, (int)(2u * nT * gb));
+  const auto rw = dma::rsrc(wdig, (int)(2u * nE * gb));
+  // local tile j covers token half j ^ kh: tile 0 is the one this wave keeps
+  const uint32_t xo0 = (2u * tt + kh) * gb, xo1 = (2u * tt + (kh ^ 1)) * gb;
+  const uint32_t wo = (2u * et + cg) * gb;
+  const uint32_t voff = 16u * lane;
+  // operands of chunk c: x tile 0 digits 0..2, x tile 1 digits 0..2, expert digits 0..2
+  auto load = [&](u32x4 (&g)[kOps], int c) {
+    const uint32_t co = (uint32_t)c * (D * 1024);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    if ((r >> 3) != kh) continue;
-    const int t = t0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    if (t >= T || !e_ok) continue;
-    const RowMeta mx = meta[t];
-    double v = (double)acc[NL - 1][r], cb = 0.0;
+    for (int a = 0; a < D; ++a) {
+      g[a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, voff, xo0 + co + a * 1024, 0));
+      g[D + a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, voff, xo1 + co + a * 1024, 0));
+      g[2 * D + a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, voff, wo + co + a * 1024, 0));
+    }
+  };
+  v16i acc[2][NL];
 #pragma unroll
-    for (int l = NL - 2; l >= 0; --l) {
-      v = fma(v, 0x1p-8, (double)acc[l][r]);
-      cb += fabs(v);
-    }
-    const int sc = mx.e + mw.e - 10;
-    const double s = ldexp(v, sc) + bval;
-    const double bound = (mx.dsum * mw.qmax + mx.vmax * mw.dsum) * (1.0 + 0x1p-32) +
-                         ldexp(cb, sc) * 0x1p-52 + fabs(s) * 0x1p-52;
-    uint32_t bits;
-    if (round_bf16_certified(s, bound, &bits)) logits[(size_t)t * E + e] = (uint16_t)bits;
-    else fail |= 1u << r;
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int l = 0; l < NL; ++l) acc[j][l] = (v16i){};
+  auto mma = [&](const u32x4 (&g)[kOps]) {
+#pragma unroll
+    for (int a = 0; a < D; ++a)
+#pragma unroll
+      for (int c = 0; c < D; ++c)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[j][a + c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              __builtin_bit_cast(v4i, g[D * j + a]), __builtin_bit_cast(v4i, g[2 * D + c]),
+              acc[j][a + c], 0, 0, 0);
+  };
+  const int n = C >> 1;                                   // chunks per wave (a multiple of 8)
+  // three chunks in flight: chunk i + 3 is loaded into the registers chunk i has just freed. The
+  // fences keep each chunk's loads behind those MFMAs (the scheduler would otherwise gather the
+  // loads and wait for all of them at once); the loads past the last chunk repeat it (in bounds,
+  // unused) so every step waits for the same count.
+  u32x4 f0[kOps], f1[kOps], f2[kOps];
+  load(f0, kh);
+  fence_sched();
+  load(f1, kh + 2);
+  fence_sched();
+  load(f2, kh + 4);
+  fence_sched();
+  auto step = [&](u32x4 (&g)[kOps], int i) {
+    if (i < n) mma(g);
+    fence_sched();
+    load(g, kh + 2 * min(i + 3, n - 1));
+    fence_sched();
+  };
+  for (int i = 0; i < n; i += 3) {
+    step(f0, i);
+    step(f1, i + 1);
+    step(f2, i + 2);
   }
-  // uncertified logits: the wave recomputes each one together (rare)
-  for (;;) {
-    const uint64_t m = __ballot(fail != 0);
-    if (m == 0) break;
-    const int l0 = __builtin_ctzll(m);
-    const int r0 = __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)fail, l0));
-    const int t = t0 + wm * 32 + 8 * (r0 >> 2) + 4 * (l0 >> 5) + (r0 & 3);
-    const int ee = e0 + wn * 32 + (l0 & 31);
-    const double bv = bias ? (double)bias[ee] : 0.0;
-    const uint32_t bits = wave_dd_logit<XDT, WDT>(xv, w, t, ee, H, bv, lane);
-    if (lane == l0) {
-      logits[(size_t)t * E + ee] = (uint16_t)bits;
-      fail &= ~(1u << r0);
+
+  // the partner (other k half, same experts) takes tile 1, which is its tile 0
+#pragma unroll
+  for (int l = 0; l < NL; ++l)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      xch[wv][l][q][lane] = (u32x4){(unsigned)acc[1][l][4 * q], (unsigned)acc[1][l][4 * q + 1],
+                                    (unsigned)acc[1][l][4 * q + 2], (unsigned)acc[1][l][4 * q + 3]};
+  __syncthreads();
+#pragma unroll
+  for (int l = 0; l < NL; ++l)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 v = xch[wv ^ 2][l][q][lane];
+      acc[0][l][4 * q] += (int)v.x;
+      acc[0][l][4 * q + 1] += (int)v.y;
+      acc[0][l][4 * q + 2] += (int)v.z;
+      acc[0][l][4 * q + 3] += (int)v.w;
     }
-  }
+  finish_tile<XDT, WDT, NL>(acc[0], 0, 16, 64 * tt, 32 * kh, 64 * et, 32 * cg, smeta, smeta + 64, xv,
+                            w, bias, T, H, E, lane, logits);
 }
 
 // scratch: RowMeta[T + E] | x digit planes [XD][T][H] | router digit planes [WD][E][H] (sized
 // for the most digits)
 inline size_t meta_bytes(int T, int E) { return ((size_t)(T + E) * sizeof(RowMeta) + 255) / 256 * 256; }
-inline size_t xdig_bytes(int T, int H) { return ((size_t)kXDMax * T * H + 255) / 256 * 256; }
+inline size_t pad64(int n) { return (size_t)(n + 63) / 64 * 64; }
+inline size_t xdig_bytes(int T, int H) {
+  const size_t n = std::max((size_t)kXDMax * T, kTD * pad64(T)) * H;
+  return (n + 255) / 256 * 256;
+}
+inline size_t wdig_bytes(int E, int H) {
+  const size_t n = std::max((size_t)WDig<MOE_DT_F32>::D * E, kTD * pad64(E)) * H;
+  return (n + 255) / 256 * 256;
+}
 
 template <int XDT, int WDT>
 void launch(const void* x, const void* w, const float* bias, int T, int H, int E, uint16_t* logits,
@@ -415,8 +595,12 @@ void launch(const void* x, const void* w, const float* bias, int T, int H, int E
   hipLaunchKernelGGL((k_router_prep<XDT, WDT>), dim3((T + E + 3) / 4), dim3(256), 0, st, x, w, T, H,
                      E, meta, xdig, wdig);
   const int nT = (T + 63) / 64, nE = (E + 63) / 64;
-  hipLaunchKernelGGL((k_router_i8<XDT, WDT>), dim3(8 * nE * ((nT + 7) / 8)), dim3(512), 0, st, x, w,
-                     xdig, wdig, meta, bias, T, H, E, logits);
+  if constexpr (tiled<XDT, WDT>())
+    hipLaunchKernelGGL((k_router_i8t<XDT, WDT>), dim3(8 * nE * ((nT + 7) / 8)), dim3(256), 0, st, x,
+                       w, xdig, wdig, meta, bias, T, H, E, logits);
+  else
+    hipLaunchKernelGGL((k_router_i8<XDT, WDT>), dim3(8 * nE * ((nT + 7) / 8)), dim3(512), 0, st, x,
+                       w, xdig, wdig, meta, bias, T, H, E, logits);
 }
 
 }  // namespace ri8
@@ -425,7 +609,7 @@ void launch(const void* x, const void* w, const float* bias, int T, int H, int E
 using namespace moe;
 
 size_t moe_router_i8_scratch_bytes(int T, int H, int E) {
-  return ri8::meta_bytes(T, E) + ri8::xdig_bytes(T, H) + ((size_t)5 * E * H + 255) / 256 * 256;
+  return ri8::meta_bytes(T, E) + ri8::xdig_bytes(T, H) + ri8::wdig_bytes(E, H);
 }
 
 bool moe_router_i8_supported(int T, int H, int E) {

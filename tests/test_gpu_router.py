@@ -146,7 +146,9 @@ def test_router_int8_and_f64_matrix_cores_same_bits(pkg, dev, xdt, wdt):
 
 @pytest.mark.parametrize("T,E,xdt,wdt", [(333, 200, torch.bfloat16, torch.float32),
                                          (257, 24, torch.float32, torch.bfloat16),
-                                         (700, 256, torch.bfloat16, torch.bfloat16)])
+                                         (700, 256, torch.bfloat16, torch.bfloat16),
+                                         (333, 200, torch.bfloat16, torch.bfloat16),
+                                         (1100, 24, torch.bfloat16, torch.bfloat16)])
 def test_router_int8_ragged_and_wide_range(pkg, dev, T, E, xdt, wdt):
     """The int8 R1 on partial 64-token / 64-expert tiles, with rows whose elements span 2^-40 ..
     2^3 (so some fall below the digit grid and the certificate, or the double-double recompute,
