@@ -215,6 +215,13 @@ static int mfma_tile_rows(int path, int T, int H, int I, int gu_fmt, int dn_fmt)
                                                                                            : MOE_GEMM_BM;
 }
 
+// the routed down GEMM writes its rows as f16 (the block forward's combine operand: half the
+// bytes written and read back) on the gemm3 / gemm4 path with the combine's K == 8 kernel
+static bool y16_rows(int path, int T, int H, int I, int K, int gu_fmt, int dn_fmt) {
+  path = pick_path(path, T, gu_fmt, dn_fmt);
+  return path != MOE_PATH_GEMV && mfma_v2(path, H, I, gu_fmt, dn_fmt) && K == 8 && H % 4 == 0;
+}
+
 // ints of a tile-list buffer that holds the list of either tile height
 static size_t tile_list_ints(int P, int E) { return 1 + 2 * (size_t)moe_max_mtiles(P, E, MOE_GEMM_BM); }
 
@@ -224,16 +231,19 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                         const void* up, size_t estride, int gu_fmt,
                         const void* dn, int dn_fmt, const int32_t* offsets,
                         const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
-                        int E, int K, int path, float* y, MoeWs& w, hipStream_t st,
-                        int32_t* tiles_pre = nullptr) {
+                        int E, int K, int path, void* y, MoeWs& w, hipStream_t st,
+                        int32_t* tiles_pre = nullptr, int y16 = 0) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
+  if (y16 && !y16_rows(path, T, H, I, K, gu_fmt, dn_fmt))
+    return moe_set_error(MOE_E_UNSUPPORTED, "moe_experts: f16 expert rows need the gemm3/gemm4 MFMA path");
   path = pick_path(path, T, gu_fmt, dn_fmt);
+  float* yf = reinterpret_cast<float*>(y);
   if (path == MOE_PATH_GEMV) {
     float* S = reinterpret_cast<float*>(w.take((size_t)P * I * 4));
     if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
     MOE_TRY(moe_launch_gemv_gateup(x, x_dtype, gate, up, estride, gu_fmt, offsets, sorted_pairs, hit_list, max_hits, H, I, K, S, st));
-    return moe_launch_gemv_down(S, dn, dn_fmt, offsets, hit_list, max_hits, H, I, y, st);
+    return moe_launch_gemv_down(S, dn, dn_fmt, offsets, hit_list, max_hits, H, I, yf, st);
   }
   const size_t dn_row = dn_fmt == MOE_FMT_Q4_K ? (size_t)I / 256 * 144 : dn_fmt == MOE_FMT_Q5_K ? (size_t)I / 256 * 176
                       : dn_fmt == MOE_FMT_Q6_K ? (size_t)I / 256 * 210 : (size_t)I * 2;
@@ -263,7 +273,7 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
     // the down GEMM's 64-row list replaces the 160-row one in the same buffer (stream order)
     MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, MOE_GEMM_BM));
     return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, moe_max_mtiles(P, E, MOE_GEMM_BM), T,
-                                offsets, H, I, 0, y, st);
+                                offsets, H, I, 0, yf, st);
   }
   if (v2) {
     if (!x16) {
@@ -280,13 +290,13 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
       MOE_TRY(moe_launch_gemm3_gateup(x16, gate, up, gu_fmt, estride, tiles, max_tiles, T, offsets,
                                       sorted_pairs, K, H, I, S, st));
     if (dn_fmt == MOE_FMT_Q4_K && I >= 512)
-      return moe_launch_gemm4_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, st);
-    return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, st);
+      return moe_launch_gemm4_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st);
+    return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, y16, st);
   }
   const int opb = path == MOE_PATH_MFMA_BF16;
   MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, gate, up, gu_fmt, estride, tiles, max_tiles, T, offsets,
                                  sorted_pairs, K, H, I, opb, S, st));
-  return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, opb, y, st);
+  return moe_launch_gemm_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, opb, yf, st);
 }
 
 // the formats the resolved routed path reads; checked before any launch is queued
@@ -382,7 +392,7 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
       x16 = c;
     }
     MOE_TRY(moe_launch_gemm3_gateup(x16, wg, wu, sfmt, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, s, st));
-    return moe_launch_gemm3_down(s, wd, sfmt, 0, nullptr, 0, T, nullptr, H, Is, shared_raw, st);
+    return moe_launch_gemm3_down(s, wd, sfmt, 0, nullptr, 0, T, nullptr, H, Is, shared_raw, 0, st);
   }
   if (sfmt != MOE_FMT_BF16)
     return moe_set_error(MOE_E_UNSUPPORTED, "moe_shared_expert: Q8_0 shared weights need H and I_s multiples of 256 on the MFMA paths");
@@ -423,7 +433,7 @@ int moe_combine(const float* y, const int32_t* pair_pos, const int32_t* topk_ids
   if (!y || !pair_pos || !topk_ids || !w_bf16 || !shared_raw || !gate_prob || !out)
     return moe_set_error(MOE_E_ARG, "moe_combine: NULL pointer");
   if (T < 1 || K < 1 || K > 16 || H < 1) return moe_set_error(MOE_E_ARG, "moe_combine: bad shape");
-  return moe_launch_combine(y, pair_pos, topk_ids, reinterpret_cast<const uint16_t*>(w_bf16),
+  return moe_launch_combine(y, 0, pair_pos, topk_ids, reinterpret_cast<const uint16_t*>(w_bf16),
                             shared_raw, gate_prob, nullptr, T, K, H, out, routed_sum, shared_out,
                             expert_raw, (hipStream_t)stream);
 }
@@ -526,7 +536,9 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   int32_t* pos = reinterpret_cast<int32_t*>(w.take((size_t)P * 4));
   int32_t* hits = reinterpret_cast<int32_t*>(w.take((size_t)(E + 1) * 4));
   void* sort_ws = w.take(moe_sort_ws_bytes(P, E));
-  float* y = reinterpret_cast<float*>(w.take((size_t)P * H * 4));
+  // the per-slot expert rows: f16 where the down GEMM can write them so
+  const int y16 = y16_rows(path, T, H, I, K, gate_up_fmt, down_fmt) ? 1 : 0;
+  void* y = w.take((size_t)P * H * (y16 ? 2 : 4));
   float* sraw = reinterpret_cast<float*>(w.take((size_t)T * H * 4));
   float* gp = gate_prob ? gate_prob : reinterpret_cast<float*>(w.take((size_t)T * 4));
   if (!logits || !ids || !wf || !wb || !offsets || !sorted || !pos || !hits || !y || !sraw || !gp)
@@ -553,8 +565,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     MOE_TRY(shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
                         Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w2, st));
     MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets, sorted,
-                         hits, T, H, I, E, K, path, y, w, st, tiles));
-    return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
+                         hits, T, H, I, E, K, path, y, w, st, tiles, y16));
+    return moe_launch_combine(y, y16, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                               shared_out, expert_raw, st);
   }
   // the shared expert on the second stream, its scratch taken before (and disjoint from) the
@@ -582,9 +594,9 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot join the shared-expert stream");
   if (rc == MOE_OK)
     rc = experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
-                      sorted, hits, T, H, I, E, K, path, y, w, st, tiles);
+                      sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16);
   if (rc != MOE_OK) return rc;
-  return moe_launch_combine(y, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
+  return moe_launch_combine(y, y16, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                             shared_out, expert_raw, st);
 }
 

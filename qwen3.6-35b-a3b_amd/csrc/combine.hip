@@ -65,8 +65,8 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
 // all in flight before the first add, and the ascending-id order comes from per-slot ranks
 // (ids within a token are distinct; equal ids would keep slot order) instead of a serial sort.
 // grid = (T, ceil(H / 1024)), block = 256.
-template <int KK>
-__global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ y,
+template <int KK, bool Y16>
+__global__ __launch_bounds__(256) void k_combine4(const void* __restrict__ y,
                                                   const int32_t* __restrict__ pair_pos,
                                                   const int32_t* __restrict__ ids,
                                                   const uint16_t* __restrict__ w_bf16,
@@ -101,8 +101,15 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ y,
 #pragma unroll
   for (int j = 0; j < KK; ++j) {
     const int pos = s_pos[j];
-    v[j] = pos >= 0 ? *reinterpret_cast<const float4*>(y + (size_t)pos * H + h)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);       // dropped (out-of-range) id
+    if (pos < 0) {
+      v[j] = make_float4(0.f, 0.f, 0.f, 0.f);                // dropped (out-of-range) id
+    } else if constexpr (Y16) {
+      const uint2 q = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(y) + (size_t)pos * H + h);
+      v[j] = make_float4(f16_to_f32(q.x & 0xFFFFu), f16_to_f32(q.x >> 16), f16_to_f32(q.y & 0xFFFFu),
+                         f16_to_f32(q.y >> 16));
+    } else {
+      v[j] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(y) + (size_t)pos * H + h);
+    }
   }
   const size_t o = (size_t)t * H + h;
   const float4 sr = *reinterpret_cast<const float4*>(shared_raw + o);
@@ -131,20 +138,30 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ y,
 
 using namespace moe;
 
-int moe_launch_combine(const float* y, const int32_t* pair_pos, const int32_t* ids,
+int moe_launch_combine(const void* y, int y16, const int32_t* pair_pos, const int32_t* ids,
                        const uint16_t* w_bf16, const float* shared_raw, const float* gate_prob,
                        const float* residual, int T, int K, int H, float* out, float* routed_sum,
                        float* shared_out, float* expert_raw, hipStream_t st) {
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (y16) {
+    // the block forward's f16 rows (its MFMA down GEMMs), always with K == 8 and H % 4 == 0
+    if (K != 8 || H % 4 || !a16(y) || !a16(shared_raw) || !a16(residual) || !a16(out) ||
+        !a16(routed_sum) || !a16(shared_out) || !a16(expert_raw))
+      return moe_set_error(MOE_E_UNSUPPORTED, "combine: f16 expert rows need K == 8, H %% 4 == 0 and 16-byte aligned rows");
+    dim3 grid(T, (H + 1023) / 1024);
+    hipLaunchKernelGGL((k_combine4<8, true>), grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16,
+                       shared_raw, gate_prob, residual, T, H, out, routed_sum, shared_out, expert_raw);
+    return moe_check_launch("combine");
+  }
   if (K == 8 && H % 4 == 0 && a16(y) && a16(shared_raw) && a16(residual) && a16(out) &&
       a16(routed_sum) && a16(shared_out) && a16(expert_raw)) {
     dim3 grid(T, (H + 1023) / 1024);
-    hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16, shared_raw,
-                       gate_prob, residual, T, H, out, routed_sum, shared_out, expert_raw);
+    hipLaunchKernelGGL((k_combine4<8, false>), grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16,
+                       shared_raw, gate_prob, residual, T, H, out, routed_sum, shared_out, expert_raw);
     return moe_check_launch("combine");
   }
   dim3 grid(T, (H + 255) / 256);
-  hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16, shared_raw,
+  hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, st, reinterpret_cast<const float*>(y), pair_pos, ids, w_bf16, shared_raw,
                      gate_prob, residual, T, K, H, out, routed_sum, shared_out, expert_raw);
   return moe_check_launch("combine");
 }

@@ -193,6 +193,81 @@ struct WRaw<MOE_FMT_BF16> {
   }
 };
 
+// Q6_K (210-byte super-blocks: ql[128] low nibbles, qh[64] 2-bit highs, 16 int8 scales, f16 d).
+// Element l + 32 g of half hf (l < 32, g < 4) is d * sc[8 hf + l / 16 + 2 g] * (q - 32), q =
+// nibble g / 2 of ql[64 hf + l + 32 (g % 2)] | (bits 2 g, 2 g + 1 of qh[32 hf + l]) << 4. A 64-wide
+// K step is g = 2 gp, 2 gp + 1 of one half: its element s takes nibble gp of ql byte 64 hf + s,
+// qh byte 32 hf + s % 32 (bits 4 gp + 2 (s / 32)) and scale 8 hf + 4 gp + s / 16. Super-blocks
+// start on even bytes only, so each piece is read as the aligned dwords that cover it (never past
+// its last byte) and shifted into place by 0 or 2 bytes (alignbyte) at decode. Mantissa trick as
+// Q5_K's with two high bits: under 0x6400 they go to mantissa bits 4-5 (1024 + q), under 0x5400
+// (high nibble) to bits 8-9 (64 + q); one packed subtract leaves q - 32 exactly and one packed
+// multiply by f16(d * sc) rounds once.
+template <bool HIGH>
+__device__ __forceinline__ uint32_t q6_pair(uint32_t w, uint32_t h, uint32_t sel, uint32_t hs,
+                                            f16x2_t ds) {
+  const uint32_t p = __builtin_amdgcn_perm(0u, w, sel);
+  const uint32_t hp = __builtin_amdgcn_perm(0u, h, sel) >> hs;
+  const uint32_t magic = HIGH ? and_or_s(p, 0x00F000F0u, 0x54005400u) | ((hp << 8) & 0x03000300u)
+                              : and_or_s(p, 0x000F000Fu, 0x64006400u) | ((hp << 4) & 0x00300030u);
+  const _Float16 off = HIGH ? (_Float16)96.0f : (_Float16)1056.0f;
+  const f16x2_t q = __builtin_bit_cast(f16x2_t, magic) - (f16x2_t){off, off};
+  return __builtin_bit_cast(uint32_t, q * ds);
+}
+
+template <>
+struct WRaw<MOE_FMT_Q6_K> {
+  uint32_t ql[17], qh[9], sc[2], d, sh;
+  __device__ __forceinline__ void load(const uint8_t* row, int k0) {
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 210;
+    const int q = (k0 >> 6) & 3, hf = q >> 1, gp = q & 1;
+    sh = (uint32_t)(reinterpret_cast<uintptr_t>(b) & 3u);        // 0 or 2
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(b - sh);
+    const int x = sh ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ql[i] = a[16 * hf + i];
+    ql[16] = a[16 * hf + 15 + x];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qh[i] = a[32 + 8 * hf + i];
+    qh[8] = a[32 + 8 * hf + 7 + x];
+    sc[0] = a[48 + 2 * hf + gp];
+    sc[1] = a[48 + 2 * hf + gp + x];
+    d = *reinterpret_cast<const uint16_t*>(b + 208);
+  }
+  // 64 f16 in k order into dst (LDS row, 128 B)
+  __device__ __forceinline__ void decode(int k0, uint16_t* dst) const {
+    const int gp = (k0 >> 6) & 1;
+    uint32_t w[16], h[8];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = __builtin_amdgcn_alignbyte(ql[i + 1], ql[i], sh);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = __builtin_amdgcn_alignbyte(qh[i + 1], qh[i], sh);
+    const uint32_t scw = __builtin_amdgcn_alignbyte(sc[1], sc[0], sh);
+    const float df = f16_to_f32(d);
+    uint32_t o[32];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {                  // 16 elements of scale j
+      const _Float16 dsj = (_Float16)(df * (float)(int8_t)(scw >> (8 * j)));
+      const f16x2_t ds = {dsj, dsj};
+      const uint32_t hs = 4u * (uint32_t)gp + 2u * (uint32_t)(j >> 1);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {                // dword m of the group: elements 16 j + 4 m ..
+        const uint32_t wv = w[4 * j + m], hv = h[(4 * j + m) & 7];
+        if (gp) {
+          o[8 * j + 2 * m] = q6_pair<true>(wv, hv, 0x0C010C00u, hs, ds);
+          o[8 * j + 2 * m + 1] = q6_pair<true>(wv, hv, 0x0C030C02u, hs, ds);
+        } else {
+          o[8 * j + 2 * m] = q6_pair<false>(wv, hv, 0x0C010C00u, hs, ds);
+          o[8 * j + 2 * m + 1] = q6_pair<false>(wv, hv, 0x0C030C02u, hs, ds);
+        }
+      }
+    }
+    uint4* dd = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dd[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+  }
+};
+
 // Q8_0 (the shipped artifact's shared expert, ffn_*_shexp): a 64-wide K step is one pair of
 // blocks (f16 d + 32 x int8 each, 68 B, 4-byte aligned in a row of an even block count). Each
 // quant becomes an exact f16 through the mantissa trick on its sign-flipped byte (1024 + q + 128
@@ -230,6 +305,7 @@ struct WRaw<MOE_FMT_Q8_0> {
 __device__ __forceinline__ size_t row_bytes(int fmt, int cols) {
   return fmt == MOE_FMT_Q4_K ? (size_t)(cols / 256) * 144
        : fmt == MOE_FMT_Q5_K ? (size_t)(cols / 256) * 176
+       : fmt == MOE_FMT_Q6_K ? (size_t)(cols / 256) * 210
        : fmt == MOE_FMT_Q8_0 ? (size_t)(cols / 32) * 34 : (size_t)cols * 2;
 }
 
@@ -288,12 +364,12 @@ struct PSet {
 // stores step ks + 1 (set (ks + 1) % kD) into the other buffer and requests step ks + kD into the
 // set it just freed, so each request has kD - 1 steps to land. kD is even and divides the step
 // count (H / 64 = 32 for gate_up, I / 64 = 8 for down), so set and buffer indices are compile-time.
-// Q4_K sets are 28 registers and Q5_K 40 (4 deep); bf16 sets 48 (2 deep, within the
+// Q4_K sets are 28 registers and Q5_K 40 (4 deep); bf16 sets 48 and Q6_K 50 (2 deep, within the
 // 256-register budget).
 template <int WFMT>
 __device__ __forceinline__ void produce(int nk, const ARows& asrc, const uint8_t* wrow, int p,
                                         Smem& sm) {
-  constexpr int kD = (WFMT == MOE_FMT_BF16 || WFMT == MOE_FMT_Q8_0) ? 2 : 4;
+  constexpr int kD = (WFMT == MOE_FMT_BF16 || WFMT == MOE_FMT_Q8_0 || WFMT == MOE_FMT_Q6_K) ? 2 : 4;
   PSet<WFMT> s[kD];
 #pragma unroll
   for (int i = 0; i < kD; ++i) s[i].load(wrow, asrc, min(i, nk - 1) * kBK, p);
@@ -403,11 +479,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // -------------------------------------------------------------------------------------- down --
-template <int WFMT>
+// Y16: rows out as f16 (saturated to +-65504) instead of f32
+template <int WFMT, bool Y16>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3_down(
     const uint16_t* __restrict__ S, const uint8_t* __restrict__ wd, size_t estride,
     const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets, int H, int I, int T,
-    float* __restrict__ y) {
+    void* __restrict__ y) {
   using namespace g3;
   __shared__ __attribute__((aligned(16))) Smem sm;
   int e, m0, mend, col;
@@ -436,8 +513,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int r = 0; r < 16; ++r) {
       const int mm = m0 + 32 * mg + 8 * (r >> 2) + 4 * h + (r & 3);
       if (mm < mend) {
-        y[(size_t)mm * H + nb] = acc[mg][0][r];
-        y[(size_t)mm * H + nb + 32] = acc[mg][1][r];
+        const float v0 = acc[mg][0][r], v1 = acc[mg][1][r];
+        if constexpr (Y16) {
+          uint16_t* yh = reinterpret_cast<uint16_t*>(y) + (size_t)mm * H + nb;
+          yh[0] = __builtin_bit_cast(uint16_t, (_Float16)fminf(fmaxf(v0, -65504.0f), 65504.0f));
+          yh[32] = __builtin_bit_cast(uint16_t, (_Float16)fminf(fmaxf(v1, -65504.0f), 65504.0f));
+        } else {
+          float* yf = reinterpret_cast<float*>(y) + (size_t)mm * H + nb;
+          yf[0] = v0;
+          yf[32] = v1;
+        }
       }
     }
   }
@@ -477,7 +562,7 @@ using namespace moe;
 
 bool moe_gemm3_supports(int fmt) { return fmt == MOE_FMT_Q4_K || fmt == MOE_FMT_BF16; }
 bool moe_gemm3_down_supports(int fmt) {
-  return fmt == MOE_FMT_Q4_K || fmt == MOE_FMT_Q5_K || fmt == MOE_FMT_BF16;
+  return fmt == MOE_FMT_Q4_K || fmt == MOE_FMT_Q5_K || fmt == MOE_FMT_Q6_K || fmt == MOE_FMT_BF16;
 }
 
 int moe_launch_to_f16(const void* x, int x_dtype, size_t n, uint16_t* out, hipStream_t st) {
@@ -515,21 +600,23 @@ int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void*
 
 int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
-                          int H, int I, float* y, hipStream_t st) {
+                          int H, int I, void* y, int y16, hipStream_t st) {
   if (H % g3::kBN || I % 256)
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm3 down needs H %% 256 == 0, I %% 256 == 0");
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_down);
   const int ntile = tiles ? max_tiles : (T + g3::kBM - 1) / g3::kBM;
   const dim3 grid(g3::kXcd * ((ntile + g3::kXcd - 1) / g3::kXcd) * (H / g3::kBN));
-  if (fmt == MOE_FMT_Q4_K)
-    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q4_K>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
-  else if (fmt == MOE_FMT_Q5_K)
-    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q5_K>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
-  else if (fmt == MOE_FMT_BF16)
-    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_BF16>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
-  else if (fmt == MOE_FMT_Q8_0)
-    hipLaunchKernelGGL(k_gemm3_down<MOE_FMT_Q8_0>, grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);
-  else
-    return moe_set_error(MOE_E_FORMAT, "gemm3 down: unsupported format %d", fmt);
+#define MOE_G3D(F)                                                                                 \
+  do {                                                                                             \
+    if (y16) hipLaunchKernelGGL((k_gemm3_down<F, true>), grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y); \
+    else hipLaunchKernelGGL((k_gemm3_down<F, false>), grid, dim3(512), 0, st, S, w, expert_stride, tiles, offsets, H, I, T, y);    \
+  } while (0)
+  if (fmt == MOE_FMT_Q4_K) MOE_G3D(MOE_FMT_Q4_K);
+  else if (fmt == MOE_FMT_Q5_K) MOE_G3D(MOE_FMT_Q5_K);
+  else if (fmt == MOE_FMT_Q6_K) MOE_G3D(MOE_FMT_Q6_K);
+  else if (fmt == MOE_FMT_BF16) MOE_G3D(MOE_FMT_BF16);
+  else if (fmt == MOE_FMT_Q8_0) MOE_G3D(MOE_FMT_Q8_0);
+  else return moe_set_error(MOE_E_FORMAT, "gemm3 down: unsupported format %d", fmt);
+#undef MOE_G3D
   return moe_check_launch("gemm3_down");
 }

@@ -245,13 +245,16 @@ struct GateUp {
   }
 };
 
+// Y16: the rows leave as f16 (saturated to +-65504, the combine's operand in the block forward)
+// instead of f32.
+template <bool Y16>
 struct Down {
   const uint16_t* S;
   const uint8_t* wd;
   size_t estride, rowb;
   int H, I;
-  float* y;
-  static constexpr int kStores = kMG * 32;
+  void* y;
+  static constexpr int kStores = kMG * 32;          // per wave per item (b32 or b16 stores alike)
   __device__ int nk() const { return I / 64; }
   __device__ int ncol() const { return H / kBN; }
   __device__ int n0(int wave) const { return 64 * wave; }
@@ -278,22 +281,33 @@ struct Down {
     for (int j = 0; j < kAI; ++j) ad.aoff[j] = (uint32_t)min(a_row(t, j), last) * (uint32_t)I * 2u + a_chunk(t, j);
   }
   __device__ void epilogue(const Item& it, int wave, int lane, const f32x16_t (&acc)[kMG][2]) const {
-    const __amdgpu_buffer_rsrc_t rs = dma::rsrc(y + (size_t)it.m0 * H, (it.mend - it.m0) * H * 4);
-    const int rs4 = opaque(H * 4);
-    const int lane_off = (4 * (lane >> 5) * H + it.col * kBN + 64 * wave + (lane & 31)) * 4;
+    constexpr int kB = Y16 ? 2 : 4;                   // bytes per element
+    char* yb = reinterpret_cast<char*>(y) + (size_t)it.m0 * H * kB;
+    const __amdgpu_buffer_rsrc_t rs = dma::rsrc(yb, (it.mend - it.m0) * H * kB);
+    const int rsb = opaque(H * kB);
+    const int lane_off = (4 * (lane >> 5) * H + it.col * kBN + 64 * wave + (lane & 31)) * kB;
 #pragma unroll
     for (int mg = 0; mg < kMG; ++mg) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const int vo = lane_off + (32 * mg + 8 * rq) * rs4;
+        const int vo = lane_off + (32 * mg + 8 * rq) * rsb;
 #pragma unroll
         for (int r3 = 0; r3 < 4; ++r3) {
           const int r = 4 * rq + r3;
-          // the builtin's data operand is an integer: pass the bits, not the value (copied out of
+          // the builtins' data operand is an integer: pass the bits, not the value (copied out of
           // the vector first: a bit cast of the vector element itself read element 0 here)
-          const float v0 = acc[mg][0][r], v1 = acc[mg][1][r];
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v0), rs, vo + r3 * rs4, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v1), rs, vo + r3 * rs4 + 128, 0, 0);
+          float v0 = acc[mg][0][r], v1 = acc[mg][1][r];
+          if constexpr (Y16) {
+            v0 = fminf(fmaxf(v0, -65504.0f), 65504.0f);
+            v1 = fminf(fmaxf(v1, -65504.0f), 65504.0f);
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v0), rs,
+                                                  vo + r3 * rsb, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v1), rs,
+                                                  vo + r3 * rsb + 64, 0, 0);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v0), rs, vo + r3 * rsb, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v1), rs, vo + r3 * rsb + 128, 0, 0);
+          }
         }
       }
     }
@@ -304,7 +318,8 @@ __device__ __forceinline__ void rows_all(const GateUp& md, Addr& ad, const Item&
   md.rows1(ad, it, ln);
   md.rows2(ad, ln);
 }
-__device__ __forceinline__ void rows_all(const Down& md, Addr& ad, const Item& it, const Lane& ln) {
+template <bool Y16>
+__device__ __forceinline__ void rows_all(const Down<Y16>& md, Addr& ad, const Item& it, const Lane& ln) {
   md.rows2_item(ad, it, ln);
 }
 // next item's A row offsets in two stages (loads issued in step 1, consumed in step 2)
@@ -314,8 +329,10 @@ __device__ __forceinline__ void rows_stage1(const GateUp& md, Addr& ad, const It
 __device__ __forceinline__ void rows_stage2(const GateUp& md, Addr& ad, const Item&, const Lane& ln) {
   md.rows2(ad, ln);
 }
-__device__ __forceinline__ void rows_stage1(const Down&, Addr&, const Item&, const Lane&) {}
-__device__ __forceinline__ void rows_stage2(const Down& md, Addr& ad, const Item& it, const Lane& ln) {
+template <bool Y16>
+__device__ __forceinline__ void rows_stage1(const Down<Y16>&, Addr&, const Item&, const Lane&) {}
+template <bool Y16>
+__device__ __forceinline__ void rows_stage2(const Down<Y16>& md, Addr& ad, const Item& it, const Lane& ln) {
   md.rows2_item(ad, it, ln);
 }
 
@@ -498,13 +515,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   persistent(md, tiles, offsets, sm);
 }
 
+template <bool Y16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm4_down(
     const uint16_t* __restrict__ S, const uint8_t* __restrict__ wd, size_t estride,
     const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets, int H, int I,
-    float* __restrict__ y) {
+    void* __restrict__ y) {
   using namespace g4;
   __shared__ __attribute__((aligned(16))) Smem sm;
-  const Down md{S, wd, estride, (size_t)(I / 256) * kSBB, H, I, y};
+  const Down<Y16> md{S, wd, estride, (size_t)(I / 256) * kSBB, H, I, y};
   persistent(md, tiles, offsets, sm);
 }
 
@@ -542,11 +560,15 @@ int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void*
 
 int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
-                          float* y, hipStream_t st) {
+                          void* y, int y16, hipStream_t st) {
   if (H % g4::kBN || I % 256 || I < 512)
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm4 down needs H %% 256 == 0, I %% 256 == 0, I >= 512");
   const dim3 grid(persistent_grid(max_tiles, H / g4::kBN));
-  hipLaunchKernelGGL(k_gemm4_down, grid, dim3(256), 0, st, S, reinterpret_cast<const uint8_t*>(w_down),
-                     expert_stride, tiles, offsets, H, I, y);
+  if (y16)
+    hipLaunchKernelGGL(k_gemm4_down<true>, grid, dim3(256), 0, st, S, reinterpret_cast<const uint8_t*>(w_down),
+                       expert_stride, tiles, offsets, H, I, y);
+  else
+    hipLaunchKernelGGL(k_gemm4_down<false>, grid, dim3(256), 0, st, S, reinterpret_cast<const uint8_t*>(w_down),
+                       expert_stride, tiles, offsets, H, I, y);
   return moe_check_launch("gemm4_down");
 }

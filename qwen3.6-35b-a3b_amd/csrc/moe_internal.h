@@ -55,9 +55,10 @@ int moe_launch_gemm3_gateup(const uint16_t* x16, const void* w_gate, const void*
                             size_t expert_stride, const int32_t* tiles, int max_tiles, int T,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
                             int I, uint16_t* S, hipStream_t st);
+// y: f32 rows, or f16 rows (saturated) when y16
 int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
-                          int H, int I, float* y, hipStream_t st);
+                          int H, int I, void* y, int y16, hipStream_t st);
 
 // gemm5.hip: the shared expert's dense GEMMs over all T rows with bf16 weights (f16 MFMA, f32
 // accumulation): gate/up -> S = SiLU(gate) * up (f16 [T, I_s]), down -> y (f32 [T, H]).
@@ -77,7 +78,7 @@ int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void*
                             int I, uint16_t* S, hipStream_t st);
 int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
-                          float* y, hipStream_t st);
+                          void* y, int y16, hipStream_t st);
 
 // decode GEMV path: S [P, I] f32 (sorted order), then y [P, H] f32
 int moe_launch_gemv_gateup(const void* x, int x_dtype, const void* gate, const void* up, size_t estride,
@@ -108,7 +109,8 @@ int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int gate
                            float* gate_prob, hipStream_t st);
 
 // combine
-int moe_launch_combine(const float* y, const int32_t* pair_pos, const int32_t* ids,
+// y: the per-slot expert rows, f32 or (y16) f16
+int moe_launch_combine(const void* y, int y16, const int32_t* pair_pos, const int32_t* ids,
                        const uint16_t* w_bf16, const float* shared_raw, const float* gate_prob,
                        const float* residual, int T, int K, int H, float* out, float* routed_sum,
                        float* shared_out, float* expert_raw, hipStream_t st);
