@@ -54,12 +54,13 @@ static int pick_path(int path, int T, int gate_up_fmt, int down_fmt) {
 }
 
 // The grouped paths' shared expert depends on x alone, so from kForkMinT tokens on it runs on a
-// library-owned second stream of the device (default priority, non-blocking) beside the router,
-// sort and routed GEMMs, and the caller's stream waits for it before the combine: its kernels
-// (few workgroups) then fill CUs the routed GEMMs leave idle. The fork and join are events, so
-// the pattern is legal under graph capture. One mutex serialises the enqueue sequence, because
-// the stream and its two events are shared by every call on the device.
-// below kForkMinT the event round trip costs more than the overlap returns (measured: 2 tokens
+// library-owned second stream of the device (default priority, non-blocking) beside the router
+// and the sort, whose small grids leave most CUs idle; the caller's stream waits for it before
+// the routed GEMMs (their persistent grids take every CU). With bf16 rows the shared GEMMs read x
+// itself and the routed GEMMs' f16 copy of x is made on that stream after them. The fork and join
+// are events, so the pattern is legal under graph capture. One mutex serialises the enqueue
+// sequence, because the stream and its two events are shared by every call on the device.
+// Below kForkMinT the event round trip costs more than the overlap returns (measured: 2 tokens
 // 53 -> 90 us with the fork, 8 tokens 124 -> 116, 64 tokens 184 -> 126)
 constexpr int kForkMinT = 7;
 constexpr int kMaxDevices = 64;
@@ -372,15 +373,19 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
   uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
   if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
   MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
-  // bf16 shared weights on the f16 MFMA path: the dense 128-row kernels
+  // bf16 shared weights on the MFMA path: the dense 128-row kernels, on bf16 rows as they are
   if (path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && moe_gemm5_supports(H, Is)) {
-    if (!x16) {
-      uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
-      if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
-      MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
-      x16 = c;
+    if (x_dtype == MOE_DT_BF16) {
+      MOE_TRY(moe_launch_gemm5_gateup(x, 1, wg, wu, T, H, Is, s, st));
+    } else {
+      if (!x16) {
+        uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+        if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+        MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+        x16 = c;
+      }
+      MOE_TRY(moe_launch_gemm5_gateup(x16, 0, wg, wu, T, H, Is, s, st));
     }
-    MOE_TRY(moe_launch_gemm5_gateup(x16, wg, wu, T, H, Is, s, st));
     return moe_launch_gemm5_down(s, wd, T, H, Is, shared_raw, st);
   }
   // Q8_0 shared weights take the 160-row f16 kernels on either MFMA path
@@ -550,14 +555,19 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     tiles = reinterpret_cast<int32_t*>(w.take(tile_list_ints(P, E) * 4));
     if (!tiles) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
   }
-  // the MFMA path's f16 activation operand, converted once for the shared and routed GEMMs
+  // the MFMA path's f16 activation operand, converted once for the shared and routed GEMMs;
+  // with bf16 rows and the shared expert forked, the shared GEMMs read the rows as they are and
+  // the conversion runs on the shared expert's stream after them (off the router's path)
+  const bool fork = T >= kForkMinT && allow_fork;
   uint16_t* x16 = nullptr;
+  bool x16_late = false;
   if (rpath == MOE_PATH_MFMA) {
     x16 = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
     if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
-    MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
+    x16_late = fork && x_dtype == MOE_DT_BF16 && Wt.shared_fmt == MOE_FMT_BF16;
+    if (!x16_late) MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
   }
-  if (T < kForkMinT || !allow_fork) {
+  if (!fork) {
     MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, nullptr, 0, st));
     MOE_TRY(moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order));
     MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
@@ -577,9 +587,9 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   MOE_TRY(fork_res(f));
   if (hipEventRecord(f->fork, st) != hipSuccess || hipStreamWaitEvent(f->s, f->fork, 0) != hipSuccess)
     return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot fork the shared-expert stream");
-  const int rc_sh = shared_impl(x, x_dtype, x16, ws_gate, ws_up, ws_down, Wt.shared_fmt, ws_scalar_gate,
-                                Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s);
-  int rc = rc_sh;
+  int rc = shared_impl(x, x_dtype, x16_late ? nullptr : x16, ws_gate, ws_up, ws_down, Wt.shared_fmt,
+                       ws_scalar_gate, Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s);
+  if (rc == MOE_OK && x16_late) rc = moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, f->s);
   // the router's scratch is dead before the experts take theirs (same stream)
   MoeWs wr = w;
   const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);

@@ -1,20 +1,24 @@
-// Prefill-path shared expert: dense GEMMs over all T token rows with bf16 weights (gfx950,
-// v_mfma_f32_32x32x16_f16, f32 accumulation): gate/up with SiLU(gate) * up fused into the
-// epilogue (f16 rows, the down GEMM's operand), then down (f32 rows).
+// Prefill-path shared expert: dense GEMMs over all T token rows with bf16 weights (gfx950, f32
+// accumulation): gate/up with SiLU(gate) * up fused into the epilogue (f16 rows, the down GEMM's
+// operand), then down (f32 rows).
 //
 // Work: one block per (128-row token tile, 256-row weight slab) item (gate_up: 128 gate + the
 // matching 128 up rows; down: 256 rows); the slabs of a tile are adjacent block indices so they
-// run side by side and share the tile's rows in L2. Block = 4 waves and 72 KB of LDS (two blocks
-// per CU). Per 32-wide K step every wave issues 2 activation and 4 weight direct global->LDS loads
+// run side by side and share the tile's rows in L2. Block = 8 waves (two per SIMD) and 144 KB of
+// LDS. Per 64-wide K step every wave issues 2 activation and 4 weight direct global->LDS loads
 // (16 bytes per lane) two steps ahead into 3-deep rings, and waits for its own loads with an
 // explicit vmcnt count before the step's barrier:
-//   A[3]: f16 activations, 128 rows x 64 B, 16-byte chunk c of row m at chunk c ^ swz(m);
-//   B[3]: bf16 weights, 256 rows x 64 B, the same swizzle by weight row;
-// swz(m) = ((m >> 1) ^ (m >> 2)) & 3, so the fragment reads of 8 or 16 lanes hit distinct banks
-// under either a 32- or a 64-bank layout. Wave w owns all 128 rows x (32 gate + 32 up) columns
-// 32 w.. of the slab (gate_up) or 64 columns (down). B fragments are converted bf16 -> f16 in
-// registers: exact for |w| >= 2^-17 (and up to 65504); below, the f16 subnormal rounding moves a
-// weight by at most 2^-25. Results leave through raw buffer stores clipped at row T.
+//   A[3]: activations, 128 rows x 128 B, 16-byte chunk c of row m at chunk c ^ swz(m);
+//   B[3]: bf16 weights, 256 rows x 128 B, the same swizzle by weight row;
+// swz(m) = (m ^ (m >> 1)) & 7, so the fragment reads of 8 or 16 lanes hit distinct banks under
+// either a 32- or a 64-bank layout. Wave w owns token rows 64 (w / 4) .. + 63 (two MFMA row
+// groups) x (32 gate + 32 up) columns 32 (w % 4) .. of the slab (gate_up) or 64 columns 64 (w % 4)
+// .. (down).
+// Operands: gate/up on bf16 activations runs v_mfma_f32_32x32x16_bf16 on the rows and weights as
+// they are (every product exact, f32 sums). Otherwise (f16 activations: converted f32 rows, or
+// the f16 SiLU rows of down) v_mfma_f32_32x32x16_f16 with the weight fragments converted bf16 ->
+// f16 in registers: exact for |w| >= 2^-17 (and up to 65504); below, the f16 subnormal rounding
+// moves a weight by at most 2^-25. Results leave through raw buffer stores clipped at row T.
 #include "common.h"
 #include "moe_internal.h"
 #include "lds_dma.h"
@@ -22,6 +26,7 @@
 namespace moe {
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace g5 {
@@ -31,26 +36,30 @@ using dma::opaque;
 using dma::wait_vm;
 
 constexpr int kBM = 128;                // token rows per item
-constexpr int kMG = kBM / 32;           // MFMA row groups
 constexpr int kBN = 256;                // weight rows per item
-constexpr int kBK = 32;                 // K per step
+constexpr int kBK = 64;                 // K per step
 constexpr int kR = 3;                   // ring depth (steps)
-constexpr int kWaves = 4;
-constexpr int kAI = kBM * 4 / 64 / kWaves;   // A loads per wave per step (2)
-constexpr int kBI = kBN * 4 / 64 / kWaves;   // B loads per wave per step (4)
+constexpr int kWaves = 8;
+constexpr int kAI = kBM * 8 / 64 / kWaves;   // A loads per wave per step (2)
+constexpr int kBI = kBN * 8 / 64 / kWaves;   // B loads per wave per step (4)
 static_assert(kAI == 2 && kBI == 4, "load split assumes 128 x 256 items");
 
 struct Smem {
-  uint8_t A[kR][kBM * 64];
-  uint8_t B[kR][kBN * 64];
+  uint8_t A[kR][kBM * 128];
+  uint8_t B[kR][kBN * 128];
 };
-static_assert(sizeof(Smem) * 2 <= 160 * 1024, "two blocks per CU");
+static_assert(sizeof(Smem) <= 160 * 1024, "one block per CU");
 
-__device__ __forceinline__ int swz(int m) { return ((m >> 1) ^ (m >> 2)) & 3; }
+__device__ __forceinline__ int swz(int m) { return (m ^ (m >> 1)) & 7; }
 
+template <bool BF>
 __device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                               __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
 // 8 bf16 (16 bytes, element order kept) -> 8 f16, round to nearest even
@@ -64,51 +73,55 @@ __device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w) {
                     bf16x2_to_f16x2(w.w));
 }
 
-// One item: rows [m0, m0 + rows) of A (row length K elements) against the 256 weight rows whose
-// first bytes are wrow(n) (n < 128: base g, else base u, each + (n & 127) * K * 2). Lane l of
-// wave w: weight rows n0 + l % 32 (group 0) and n1 + l % 32 (group 1), half h = l / 32 of every
-// 16-wide MFMA k substep.
-template <class Epi>
+// One item: rows [m0, m0 + rows) of A (row length K elements, 2 bytes each) against the 256
+// weight rows n (n < 128: base g, else base u, each + (n & 127) * K * 2). Lane l of wave w: token
+// rows 64 (w / 4) + 32 mg + ..., weight rows n0 + l % 32 (group 0) and n1 + l % 32 (group 1), half
+// h = l / 32 of every 16-wide MFMA k substep. BF: bf16 A on the bf16 MFMA; else f16 A with the
+// weights converted.
+template <bool BF, class Epi>
 __device__ __forceinline__ void item(const uint8_t* abase, int rows, int K, const uint8_t* g,
                                      const uint8_t* u, int n0, int n1, Smem& sm, const Epi& epi) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, r = lane & 31;
+  const int rh = wave >> 2;
   const int nk = K / kBK;
-  // load geometry: load j of wave w covers the slot's 16-byte units 64 (w + 4 j) + l
+  // load geometry: load j of wave w covers the slot's 16-byte units 64 (w + 8 j) + l, unit u =
+  // row u >> 3, physical chunk u & 7 (logical chunk (u & 7) ^ swz(row))
   uint32_t aoff[kAI], boff[kBI];
   const uint8_t* bb[kBI];
 #pragma unroll
   for (int j = 0; j < kAI; ++j) {
-    const int uu = 64 * (wave + kWaves * j) + lane, m = uu >> 2;
-    aoff[j] = ((uint32_t)min(m, rows - 1) * (uint32_t)K + 8u * (uint32_t)((uu & 3) ^ swz(m))) * 2u;
+    const int uu = 64 * (wave + kWaves * j) + lane, m = uu >> 3;
+    aoff[j] = (uint32_t)min(m, rows - 1) * (uint32_t)K * 2u + 16u * (uint32_t)((uu & 7) ^ swz(m));
   }
 #pragma unroll
   for (int j = 0; j < kBI; ++j) {
-    const int uu = 64 * (wave + kWaves * j) + lane, n = uu >> 2;
-    boff[j] = ((uint32_t)(n & 127) * (uint32_t)K + 8u * (uint32_t)((uu & 3) ^ swz(n))) * 2u;
+    const int uu = 64 * (wave + kWaves * j) + lane, n = uu >> 3;
+    boff[j] = (uint32_t)(n & 127) * (uint32_t)K * 2u + 16u * (uint32_t)((uu & 7) ^ swz(n));
     bb[j] = j < 2 ? g : u;   // rows 0..127 from g, 128..255 from u
   }
   const uint32_t la = lds_addr(sm.A[0]) + 1024 * wave, lb = lds_addr(sm.B[0]) + 1024 * wave;
   auto issue = [&](int slot, int ks) {
 #pragma unroll
     for (int j = 0; j < kAI; ++j)
-      dma::load16(aoff[j], abase + (size_t)ks * 64, la + slot * (kBM * 64) + j * 4096);
+      dma::load16(aoff[j], abase + (size_t)ks * 128, la + slot * (kBM * 128) + j * 8192);
 #pragma unroll
     for (int j = 0; j < kBI; ++j)
-      dma::load16(boff[j], bb[j] + (size_t)ks * 64, lb + slot * (kBN * 64) + j * 4096);
+      dma::load16(boff[j], bb[j] + (size_t)ks * 128, lb + slot * (kBN * 128) + j * 8192);
   };
-  f32x16_t acc[kMG][2];
+  f32x16_t acc[2][2];
 #pragma unroll
-  for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
-  // per-lane LDS byte offsets of the A fragment of substep ss (row group 0; 64-byte rows, so row
-  // group mg adds 32 * 64 mg) and the B rows
-  int ao[2], bo0[2], bo1[2];
+  for (int mg = 0; mg < 2; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
+  // per-lane LDS byte offsets of substep ss's fragments (rows 64 rh + 32 mg + r, n0 + r, n1 + r:
+  // the swizzle of each is swz(r), the row bases being multiples of 32)
+  int ao[4], bo0[4], bo1[4];
 #pragma unroll
-  for (int ss = 0; ss < 2; ++ss) {
-    ao[ss] = 16 * (4 * r + ((2 * ss + h) ^ swz(r)));
-    bo0[ss] = 16 * (4 * (n0 + r) + ((2 * ss + h) ^ swz(r)));
-    bo1[ss] = 16 * (4 * (n1 + r) + ((2 * ss + h) ^ swz(r)));
+  for (int ss = 0; ss < 4; ++ss) {
+    const int c = 16 * ((2 * ss + h) ^ swz(r));
+    ao[ss] = 128 * (64 * rh + r) + c;
+    bo0[ss] = 128 * (n0 + r) + c;
+    bo1[ss] = 128 * (n1 + r) + c;
   }
   issue(0, 0);
   issue(1, min(1, nk - 1));
@@ -123,46 +136,47 @@ __device__ __forceinline__ void item(const uint8_t* abase, int rows, int K, cons
     const uint8_t* As = sm.A[slot];
     const uint8_t* Bs = sm.B[slot];
 #pragma unroll
-    for (int ss = 0; ss < 2; ++ss) {
-      uint4 a[kMG];
-#pragma unroll
-      for (int mg = 0; mg < kMG; ++mg) a[mg] = *reinterpret_cast<const uint4*>(As + ao[ss] + 32 * 64 * mg);
-      const uint4 bg = bf16x8_to_f16(*reinterpret_cast<const uint4*>(Bs + bo0[ss]));
-      const uint4 bu = bf16x8_to_f16(*reinterpret_cast<const uint4*>(Bs + bo1[ss]));
-#pragma unroll
-      for (int mg = 0; mg < kMG; ++mg) {
-        acc[mg][0] = mfma(a[mg], bg, acc[mg][0]);
-        acc[mg][1] = mfma(a[mg], bu, acc[mg][1]);
+    for (int ss = 0; ss < 4; ++ss) {
+      const uint4 a0 = *reinterpret_cast<const uint4*>(As + ao[ss]);
+      const uint4 a1 = *reinterpret_cast<const uint4*>(As + ao[ss] + 128 * 32);
+      uint4 bg = *reinterpret_cast<const uint4*>(Bs + bo0[ss]);
+      uint4 bu = *reinterpret_cast<const uint4*>(Bs + bo1[ss]);
+      if constexpr (!BF) {
+        bg = bf16x8_to_f16(bg);
+        bu = bf16x8_to_f16(bu);
       }
+      acc[0][0] = mfma<BF>(a0, bg, acc[0][0]);
+      acc[0][1] = mfma<BF>(a0, bu, acc[0][1]);
+      acc[1][0] = mfma<BF>(a1, bg, acc[1][0]);
+      acc[1][1] = mfma<BF>(a1, bu, acc[1][1]);
     }
     slot = slot == 2 ? 0 : slot + 1;
   }
   // no load may still be writing this block's LDS when its waves exit
   wait_vm<0>();
-  epi(acc, wave, lane);
+  epi(acc, rh, lane);
 }
 
-}  // namespace g5
-
-// gate/up: x16 [T, H] f16, w_gate / w_up [I_s, H] bf16 -> S [T, I_s] f16 = SiLU(gate) * up
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm5_gateup(
-    const uint16_t* __restrict__ x16, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
-    int T, int H, int Is, uint16_t* __restrict__ S) {
-  using namespace g5;
-  __shared__ __attribute__((aligned(16))) Smem sm;
+// gate/up: A [T, H] (bf16 rows when BF, else f16), w_gate / w_up [I_s, H] bf16 -> S [T, I_s] f16
+// = SiLU(gate) * up
+template <bool BF>
+__device__ __forceinline__ void gateup(const uint16_t* __restrict__ a, const uint16_t* __restrict__ wg,
+                                       const uint16_t* __restrict__ wu, int T, int H, int Is,
+                                       uint16_t* __restrict__ S, Smem& sm) {
   const int ncol = Is / 128;
   const int m0 = (blockIdx.x / ncol) * kBM, col = blockIdx.x % ncol;
   if (m0 >= T) return;
   const int rows = min(kBM, T - m0);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cq = wave & 3;
   const uint8_t* g = reinterpret_cast<const uint8_t*>(wg + (size_t)col * 128 * H);
   const uint8_t* u = reinterpret_cast<const uint8_t*>(wu + (size_t)col * 128 * H);
-  auto epi = [&](const f32x16_t (&acc)[kMG][2], int w, int lane) {
+  auto epi = [&](const f32x16_t (&acc)[2][2], int rh, int lane) {
     const __amdgpu_buffer_rsrc_t rs = dma::rsrc(S + (size_t)m0 * Is, rows * Is * 2);
     const int rs2 = opaque(Is * 2);
-    const int lane_off = (4 * (lane >> 5) * Is + col * 128 + 32 * w + (lane & 31)) * 2;
+    const int lane_off = ((64 * rh + 4 * (lane >> 5)) * Is + col * 128 + 32 * cq + (lane & 31)) * 2;
 #pragma unroll
-    for (int mg = 0; mg < kMG; ++mg) {
+    for (int mg = 0; mg < 2; ++mg) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int vo = lane_off + (32 * mg + 8 * rq) * rs2;
@@ -177,11 +191,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
-  item(reinterpret_cast<const uint8_t*>(x16 + (size_t)m0 * H), rows, H, g, u, 32 * wave, 128 + 32 * wave, sm, epi);
+  item<BF>(reinterpret_cast<const uint8_t*>(a + (size_t)m0 * H), rows, H, g, u, 32 * cq,
+           128 + 32 * cq, sm, epi);
+}
+
+}  // namespace g5
+
+template <bool BF>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm5_gateup(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
+    int T, int H, int Is, uint16_t* __restrict__ S) {
+  __shared__ __attribute__((aligned(16))) g5::Smem sm;
+  g5::gateup<BF>(a, wg, wu, T, H, Is, S, sm);
 }
 
 // down: S [T, I_s] f16, w_down [H, I_s] bf16 -> y [T, H] f32
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm5_down(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm5_down(
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ wd, int T, int H, int Is,
     float* __restrict__ y) {
   using namespace g5;
@@ -191,14 +216,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (m0 >= T) return;
   const int rows = min(kBM, T - m0);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cq = wave & 3;
   const uint8_t* w0 = reinterpret_cast<const uint8_t*>(wd + (size_t)col * kBN * Is);
   const uint8_t* w1 = reinterpret_cast<const uint8_t*>(wd + ((size_t)col * kBN + 128) * Is);
-  auto epi = [&](const f32x16_t (&acc)[kMG][2], int w, int lane) {
+  auto epi = [&](const f32x16_t (&acc)[2][2], int rh, int lane) {
     const __amdgpu_buffer_rsrc_t rs = dma::rsrc(y + (size_t)m0 * H, rows * H * 4);
     const int rs4 = opaque(H * 4);
-    const int lane_off = (4 * (lane >> 5) * H + col * kBN + 64 * w + (lane & 31)) * 4;
+    const int lane_off = ((64 * rh + 4 * (lane >> 5)) * H + col * kBN + 64 * cq + (lane & 31)) * 4;
 #pragma unroll
-    for (int mg = 0; mg < kMG; ++mg) {
+    for (int mg = 0; mg < 2; ++mg) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int vo = lane_off + (32 * mg + 8 * rq) * rs4;
@@ -213,7 +239,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
-  item(reinterpret_cast<const uint8_t*>(S + (size_t)m0 * Is), rows, Is, w0, w1, 64 * wave, 64 * wave + 32, sm, epi);
+  item<false>(reinterpret_cast<const uint8_t*>(S + (size_t)m0 * Is), rows, Is, w0, w1, 64 * cq,
+              64 * cq + 32, sm, epi);
 }
 
 }  // namespace moe
@@ -224,15 +251,20 @@ bool moe_gemm5_supports(int H, int Is) {
   return H % 256 == 0 && Is % 128 == 0 && Is % g5::kBK == 0 && Is >= 64;
 }
 
-int moe_launch_gemm5_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int T, int H,
-                            int Is, uint16_t* S, hipStream_t st) {
+int moe_launch_gemm5_gateup(const void* a, int a_bf16, const void* w_gate, const void* w_up, int T,
+                            int H, int Is, uint16_t* S, hipStream_t st) {
   if (!moe_gemm5_supports(H, Is))
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm5 gate_up needs H %% 256 == 0, I_s %% 128 == 0");
   if ((size_t)g5::kBM * Is * 4 > 0x7FFFFFFFu || (size_t)g5::kBM * H * 4 > 0x7FFFFFFFu)
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm5: a tile's rows exceed 31-bit buffer offsets");
   const dim3 grid(((T + g5::kBM - 1) / g5::kBM) * (Is / 128));
-  hipLaunchKernelGGL(k_gemm5_gateup, grid, dim3(256), 0, st, x16, reinterpret_cast<const uint16_t*>(w_gate),
-                     reinterpret_cast<const uint16_t*>(w_up), T, H, Is, S);
+  const uint16_t* ap = reinterpret_cast<const uint16_t*>(a);
+  const uint16_t* g = reinterpret_cast<const uint16_t*>(w_gate);
+  const uint16_t* u = reinterpret_cast<const uint16_t*>(w_up);
+  if (a_bf16)
+    hipLaunchKernelGGL(k_gemm5_gateup<true>, grid, dim3(512), 0, st, ap, g, u, T, H, Is, S);
+  else
+    hipLaunchKernelGGL(k_gemm5_gateup<false>, grid, dim3(512), 0, st, ap, g, u, T, H, Is, S);
   return moe_check_launch("gemm5_gateup");
 }
 
@@ -241,7 +273,7 @@ int moe_launch_gemm5_down(const uint16_t* S, const void* w_down, int T, int H, i
   if (!moe_gemm5_supports(H, Is))
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm5 down needs H %% 256 == 0, I_s %% 128 == 0");
   const dim3 grid(((T + g5::kBM - 1) / g5::kBM) * (H / g5::kBN));
-  hipLaunchKernelGGL(k_gemm5_down, grid, dim3(256), 0, st, S, reinterpret_cast<const uint16_t*>(w_down),
+  hipLaunchKernelGGL(k_gemm5_down, grid, dim3(512), 0, st, S, reinterpret_cast<const uint16_t*>(w_down),
                      T, H, Is, y);
   return moe_check_launch("gemm5_down");
 }

@@ -60,11 +60,12 @@ int moe_launch_gemm3_down(const uint16_t* S, const void* w_down, int fmt, size_t
                           const int32_t* tiles, int max_tiles, int T, const int32_t* offsets,
                           int H, int I, void* y, int y16, hipStream_t st);
 
-// gemm5.hip: the shared expert's dense GEMMs over all T rows with bf16 weights (f16 MFMA, f32
-// accumulation): gate/up -> S = SiLU(gate) * up (f16 [T, I_s]), down -> y (f32 [T, H]).
+// gemm5.hip: the shared expert's dense GEMMs over all T rows with bf16 weights (f32
+// accumulation): gate/up -> S = SiLU(gate) * up (f16 [T, I_s]) from bf16 rows a (a_bf16, bf16
+// MFMA) or f16 rows, down -> y (f32 [T, H]).
 bool moe_gemm5_supports(int H, int Is);
-int moe_launch_gemm5_gateup(const uint16_t* x16, const void* w_gate, const void* w_up, int T, int H,
-                            int Is, uint16_t* S, hipStream_t st);
+int moe_launch_gemm5_gateup(const void* a, int a_bf16, const void* w_gate, const void* w_up, int T,
+                            int H, int Is, uint16_t* S, hipStream_t st);
 int moe_launch_gemm5_down(const uint16_t* S, const void* w_down, int T, int H, int Is, float* y,
                           hipStream_t st);
 
