@@ -428,6 +428,72 @@ def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
             "prefill_tflops": tflops, "prefill_mfma_util": tflops / BF16_PEAK_TFLOPS}
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baselines(torch, synth, lw_dec, x0, lw_pf, dev, seconds: float):
+    """The reference's CPU path timed on this host (oracle port, BASELINE.md's plan): config-1
+    decode tokens through one layer with every host thread and with one thread (each layer-token
+    dequantizes its 8 selected experts), and config 3's 4096-token prefill block (every used
+    expert dequantized once, grouped F.linear). Bounded samples; the decode figures are best-of
+    per-token times' mean over the sample, the prefill one a single timed block after a warm-up
+    call on 64 tokens."""
+    from oracle import moe_oracle as O
+    ncpu = os.cpu_count() or 1
+    model = cpu_model()
+    ow = O.from_device(lw_dec)
+
+    def decode(threads: int, budget: float):
+        torch.set_num_threads(threads)
+        xc = x0.cpu()
+        n, t_cpu, per = 0, 0.0, []
+        t_start = time.time()
+        while time.time() - t_start < budget:
+            t1 = time.perf_counter()
+            res = O.moe_block(xc, ow)
+            dt = time.perf_counter() - t1
+            t_cpu += dt
+            per.append(dt)
+            xc = synth.rms_normalize(xc + res["combined_out"])
+            n += 1
+        per.sort()
+        return {"value": round(t_cpu / n * 1e6, 1), "unit": "us/token/layer",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"{n} sequential decode tokens through one config-1 layer: oracle "
+                          "dequant of the 8 selected Q4_K experts + f32 F.linear + shared expert "
+                          f"(os.cpu_count()={ncpu}, {model}; per-token min "
+                          f"{per[0] * 1e6:.0f} us, median {per[len(per) // 2] * 1e6:.0f} us)"}
+
+    cpu = decode(ncpu, seconds)
+    log(f"cpu baseline: {cpu['value']:.0f} us/token/layer, {cpu['cores']} threads")
+    cpu1 = decode(1, max(4.0, seconds / 2))
+    log(f"cpu baseline, 1 thread: {cpu1['value']:.0f} us/token/layer")
+    cpu_pf = None
+    if lw_pf is not None:
+        torch.set_num_threads(ncpu)
+        owp = O.from_device(lw_pf)
+        xp = synth.make_input(4096, seed=2, device=dev, dtype=torch.bfloat16).cpu()
+        O.moe_block(xp[:64], owp)                               # warm-up (allocator, threads)
+        t1 = time.perf_counter()
+        O.moe_block(xp, owp)
+        dt = time.perf_counter() - t1
+        cpu_pf = {"value": round(4096 / dt, 1), "unit": "tok/s", "cores": torch.get_num_threads(),
+                  "kind": "port",
+                  "sample": f"config 3's 4096-token block once: oracle R1-R5, every used Q4_K expert "
+                            f"dequantized once, grouped f32 F.linear, shared expert ({dt:.2f} s; "
+                            f"os.cpu_count()={ncpu}, {model})"}
+        log(f"cpu baseline, prefill: {cpu_pf['value']:.0f} tok/s ({dt:.2f} s for 4096 tokens)")
+    torch.set_num_threads(ncpu)
+    return cpu, cpu1, cpu_pf
+
+
 def prefill_c4(torch, pkg, dev, steps: int, n_layers: int = 40) -> dict:
     """Config 4: T = 16384 bf16 tokens, Q4_K gate_up + Q6_K down, Zipf(1.1) routing, the step
     rotating over 40 resident layer instances (each step one block on the next instance)."""
@@ -621,10 +687,10 @@ def main():
 
     # ---------------------------------------------------------------- prefill, config 3
     prefill = {}
+    lwp = None
     if not args.no_prefill:
         lwp = synth.make_layer(seed=2, device=dev)              # config 3's seed
         prefill = prefill_c3(torch, synth, abi, lwp, dev, args.prefill_steps)
-        del lwp
 
     # ---------------------------------------------------------------- prefill, config 4
     c4 = {} if args.no_c4 else prefill_c4(torch, pkg, dev, args.prefill_steps)
@@ -633,26 +699,10 @@ def main():
     lmh = lm_head_bench(torch, pkg, dev) if not args.no_lm_head else {}
 
     # ---------------------------------------------------------------- CPU baseline
-    cpu = None
+    cpu, cpu1, cpu_pf = None, None, None
     if not args.no_cpu:
-        from oracle import moe_oracle as O
-        torch.set_num_threads(os.cpu_count() or 1)
-        ow = O.from_device(layers[0])
-        xc = x0.cpu()
-        n, t_cpu = 0, 0.0
-        t_start = time.time()
-        while time.time() - t_start < args.cpu_seconds:
-            t1 = time.perf_counter()
-            res = O.moe_block(xc, ow)
-            t_cpu += time.perf_counter() - t1
-            xc = synth.rms_normalize(xc + res["combined_out"])
-            n += 1
-        cpu = {"value": round(t_cpu / n * 1e6, 1), "unit": "us/token/layer",
-               "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"{n} sequential decode tokens through one config-1 layer: oracle "
-                         "dequant of the 8 selected Q4_K experts + f32 F.linear + shared expert "
-                         f"(os.cpu_count()={os.cpu_count()})"}
-        log(f"cpu baseline: {cpu['value']:.0f} us/token/layer over {n} tokens, {cpu['cores']} threads")
+        cpu, cpu1, cpu_pf = cpu_baselines(torch, synth, layers[0], x0, lwp, dev, args.cpu_seconds)
+    del lwp
 
     result = {
         "metric": "MoE-layer us/token + HBM GB/s at bs=1 (Q4_K); prefill tok/s at 4096 tokens",
@@ -673,6 +723,8 @@ def main():
                      "traffic": traffic, "kernel": DECODE_KERNEL,
                      "bytes_per_launch": active, "avg_us": round(ms_k * 1000, 3)},
         "cpu_baseline": cpu,
+        "cpu_baseline_1thread": cpu1,
+        "cpu_baseline_prefill": cpu_pf,
         "prefill_gemm_counters": committed_prefill_pmc(),
     }
     result.update(c2)

@@ -74,5 +74,40 @@ def build_hostcheck() -> Path:
     return HOSTCHECK
 
 
+ASAN_LIB = PKG / "libmoe_gfx950_asan.so"
+
+
+def asan_runtime() -> Path:
+    """The ROCm clang's AddressSanitizer runtime (to preload into a process that loads ASAN_LIB)."""
+    clang = Path(HIPCC).resolve().parent.parent / "llvm" / "bin" / "clang"
+    p = subprocess.run([str(clang) if clang.exists() else "clang",
+                        "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    return Path(p.stdout.strip())
+
+
+def build_asan() -> Path:
+    """libmoe_gfx950_asan.so: the library with abi.hip (every entry point's argument checks and
+    workspace carving) compiled for the host with AddressSanitizer, linked with the other objects
+    of build(). Test infrastructure for the CPU tier; the device code is the same as the product's."""
+    bdir = CSRC / "_build"
+    others = [bdir / (s.stem + ".o") for s in sorted(CSRC.glob("*.hip")) if s.stem != "abi"]
+    if not all(o.exists() for o in others):
+        build()
+    obj = bdir / "abi_asan.o"
+    cmd = [HIPCC, *FLAGS, "-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host",
+           "-fno-omit-frame-pointer", "-c", str(CSRC / "abi.hip"), "-o", str(obj)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("asan compile failed:\n" + p.stdout + p.stderr)
+    tmp = ASAN_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+           "-shared-libasan", "-o", str(tmp), *map(str, others), str(obj)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("asan link failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, ASAN_LIB)
+    return ASAN_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
