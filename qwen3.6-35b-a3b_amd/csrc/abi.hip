@@ -361,9 +361,19 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, const void* u
                       sorted_pairs, hit_list, T, H, I, E, K, path, y, w, (hipStream_t)stream);
 }
 
-static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const void* wg,
+// The small-T shared-expert kernels (narrow slabs, K split over the waves) up to this many tokens;
+// above it the 128 x 256 items keep every CU busy and reuse each weight tile over 128 rows.
+constexpr int kSharedSkinnyMaxT = 256;
+static bool shared_skinny(int path, int sfmt, int T, int H, int Is) {
+  return path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && T <= kSharedSkinnyMaxT && moe_gemm5s_supports(H, Is);
+}
+
+// x16: the f16 rows of x when the caller already has them (else NULL); x16_make: where to write
+// them for the caller (NULL: not wanted), made by the shared expert's own kernels where they can
+static int shared_body(const void* x, int x_dtype, const uint16_t* x16, const void* wg,
                        const void* wu, const void* wd, int sfmt, const void* wsg, int gate_dtype, int T, int H,
-                       int Is, int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st) {
+                       int Is, int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st,
+                       uint16_t* x16_make, bool& made) {
   if (path == MOE_PATH_AUTO) path = T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
   if (path == MOE_PATH_GEMV || path == MOE_PATH_GEMV_MULTI) {
     float* s = reinterpret_cast<float*>(w.take((size_t)T * Is * 4));
@@ -372,6 +382,11 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
   }
   uint16_t* s = reinterpret_cast<uint16_t*>(w.take((size_t)T * Is * 2));
   if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+  if (shared_skinny(path, sfmt, T, H, Is)) {
+    MOE_TRY(moe_launch_gemm5s_gateup(x, x_dtype, wg, wu, wsg, gate_dtype, T, H, Is, s, gate_prob, x16_make, st));
+    made = x16_make != nullptr;
+    return moe_launch_gemm5s_down(s, wd, T, H, Is, shared_raw, st);
+  }
   MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
   // bf16 shared weights on the MFMA path: the dense 128-row kernels, on bf16 rows as they are
   if (path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && moe_gemm5_supports(H, Is)) {
@@ -379,9 +394,10 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
       MOE_TRY(moe_launch_gemm5_gateup(x, 1, wg, wu, T, H, Is, s, st));
     } else {
       if (!x16) {
-        uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+        uint16_t* c = x16_make ? x16_make : reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
         if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
         MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+        made = c == x16_make;
         x16 = c;
       }
       MOE_TRY(moe_launch_gemm5_gateup(x16, 0, wg, wu, T, H, Is, s, st));
@@ -391,9 +407,10 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
   // Q8_0 shared weights take the 160-row f16 kernels on either MFMA path
   if ((path == MOE_PATH_MFMA || sfmt == MOE_FMT_Q8_0) && H % 256 == 0 && Is % 256 == 0) {
     if (!x16) {
-      uint16_t* c = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+      uint16_t* c = x16_make ? x16_make : reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
       if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
       MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+      made = c == x16_make;
       x16 = c;
     }
     MOE_TRY(moe_launch_gemm3_gateup(x16, wg, wu, sfmt, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, s, st));
@@ -404,6 +421,17 @@ static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const vo
   const int opb = path == MOE_PATH_MFMA_BF16;
   MOE_TRY(moe_launch_gemm_gateup(x, x_dtype, wg, wu, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, nullptr, 1, H, Is, opb, s, st));
   return moe_launch_gemm_down(s, wd, MOE_FMT_BF16, 0, nullptr, 0, T, nullptr, H, Is, opb, shared_raw, st);
+}
+
+static int shared_impl(const void* x, int x_dtype, const uint16_t* x16, const void* wg,
+                       const void* wu, const void* wd, int sfmt, const void* wsg, int gate_dtype, int T, int H,
+                       int Is, int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st,
+                       uint16_t* x16_make = nullptr) {
+  bool made = false;
+  MOE_TRY(shared_body(x, x_dtype, x16, wg, wu, wd, sfmt, wsg, gate_dtype, T, H, Is, path, shared_raw,
+                      gate_prob, w, st, x16_make, made));
+  if (x16_make && !made) return moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16_make, st);
+  return MOE_OK;
 }
 
 static int check_shared_fmt(int shared_fmt, int gate_dtype, const char* who) {
@@ -564,7 +592,9 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   if (rpath == MOE_PATH_MFMA) {
     x16 = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
     if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
-    x16_late = fork && x_dtype == MOE_DT_BF16 && Wt.shared_fmt == MOE_FMT_BF16;
+    // made on the shared expert's stream: beside (or after) its GEMMs, off the router's path
+    x16_late = fork && Wt.shared_fmt == MOE_FMT_BF16 &&
+               (x_dtype == MOE_DT_BF16 || shared_skinny(path, Wt.shared_fmt, T, H, I_s));
     if (!x16_late) MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
   }
   if (!fork) {
@@ -588,8 +618,8 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   if (hipEventRecord(f->fork, st) != hipSuccess || hipStreamWaitEvent(f->s, f->fork, 0) != hipSuccess)
     return moe_set_error(MOE_E_HIP, "moe_block_forward: cannot fork the shared-expert stream");
   int rc = shared_impl(x, x_dtype, x16_late ? nullptr : x16, ws_gate, ws_up, ws_down, Wt.shared_fmt,
-                       ws_scalar_gate, Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s);
-  if (rc == MOE_OK && x16_late) rc = moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, f->s);
+                       ws_scalar_gate, Wt.scalar_gate_dtype, T, H, I_s, path, sraw, gp, w, f->s,
+                       x16_late ? x16 : nullptr);
   // the router's scratch is dead before the experts take theirs (same stream)
   MoeWs wr = w;
   const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);

@@ -69,6 +69,15 @@ int moe_launch_gemm5_gateup(const void* a, int a_bf16, const void* w_gate, const
 int moe_launch_gemm5_down(const uint16_t* S, const void* w_down, int T, int H, int Is, float* y,
                           hipStream_t st);
 
+// gemm5.hip, small T: one block per (64-row tile, narrow weight slab), K split over the waves.
+// gate_up also writes gate_prob (sigmoid(x . wsg), NULL: skipped) and x16 (f16(x), NULL: skipped)
+bool moe_gemm5s_supports(int H, int Is);
+int moe_launch_gemm5s_gateup(const void* x, int x_dtype, const void* w_gate, const void* w_up,
+                             const void* wsg, int gate_dtype, int T, int H, int Is, uint16_t* S,
+                             float* gate_prob, uint16_t* x16, hipStream_t st);
+int moe_launch_gemm5s_down(const uint16_t* S, const void* w_down, int T, int H, int Is, float* y,
+                           hipStream_t st);
+
 // gemm4.hip: Q4_K gate_up and down with the weight decode in the MFMA waves (persistent grid,
 // direct global->LDS operand loads, two blocks per CU); same tiles (MOE_GEMM3_BM rows),
 // arguments and results as the gemm3 launchers for Q4_K, within f32 rounding (another k order).

@@ -516,14 +516,17 @@ __global__ __launch_bounds__(64) void k_route_topk(const uint16_t* __restrict__ 
 
 // E = 256, K = 8, many tokens: one wave per token, four per block. The fast path settles a token
 // (32-bit keys, rank r's id and weight written by lane r); a token it cannot settle (a tie at the
-// K-th place, or any tie when the caller reads the slot order) is marked by ids[t][0] = -1 and
-// left to k_route_replay8, so the slow exact replay runs in its own launch instead of beside three
-// fast waves on its SIMD.
+// K-th place, or any tie when the caller reads the slot order) is replayed exactly by its wave
+// (FUSED: up to a few hundred tokens, where the launch the replay would otherwise take costs more
+// than it saves), or marked by ids[t][0] = -1 and left to k_route_replay8, so that with many
+// tokens the slow replays run in their own launch instead of beside three fast waves on a SIMD.
+template <bool FUSED>
 __global__ __launch_bounds__(256) void k_route_topk8(const uint16_t* __restrict__ logits, int T,
                                                      float* __restrict__ probs,
                                                      int32_t* __restrict__ ids,
                                                      float* __restrict__ w_f32,
                                                      uint16_t* __restrict__ w_bf16,
+                                                     int32_t* __restrict__ heap_flag,
                                                      int exact_order) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
@@ -539,7 +542,13 @@ __global__ __launch_bounds__(256) void k_route_topk8(const uint16_t* __restrict_
   const int code = wave_topk32<8>(p, lane, my_id, my_val, tot);
   const bool replay = code == 2 || (code == 1 && exact_order);
   if (replay) {
-    if (lane == 0) ids[(size_t)t * 8] = -1;
+    if constexpr (FUSED) {
+      __shared__ TopkLds s[4];
+      route_replay_and_write(s[threadIdx.x >> 6], p, 256, 8, lane, ids + (size_t)t * 8,
+                             w_f32 + (size_t)t * 8, w_bf16 + (size_t)t * 8, heap_flag);
+    } else if (lane == 0) {
+      ids[(size_t)t * 8] = -1;
+    }
   } else if (lane < 8) {
     const float wv = my_val / tot;
     ids[(size_t)t * 8 + lane] = my_id;
@@ -603,13 +612,21 @@ int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dt
   return moe_check_launch("router_logits");
 }
 
+// up to this many tokens the exact replays run inside the top-k launch
+constexpr int kFusedReplayMaxT = 512;
+
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
                           float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st,
                           bool exact_order) {
   if (E == 256 && K == 8 && T >= 16) {
     const dim3 grid((T + 3) / 4);
-    hipLaunchKernelGGL(k_route_topk8, grid, dim3(256), 0, st, logits, T, probs, ids, w_f32, w_bf16,
-                       exact_order ? 1 : 0);
+    if (T <= kFusedReplayMaxT) {
+      hipLaunchKernelGGL(k_route_topk8<true>, grid, dim3(256), 0, st, logits, T, probs, ids, w_f32, w_bf16,
+                         heap_flag, exact_order ? 1 : 0);
+      return moe_check_launch("route_topk");
+    }
+    hipLaunchKernelGGL(k_route_topk8<false>, grid, dim3(256), 0, st, logits, T, probs, ids, w_f32, w_bf16,
+                       heap_flag, exact_order ? 1 : 0);
     hipLaunchKernelGGL(k_route_replay8, grid, dim3(256), 0, st, logits, T, ids, w_f32, w_bf16, heap_flag);
     return moe_check_launch("route_topk");
   }

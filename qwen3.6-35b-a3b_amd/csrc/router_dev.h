@@ -105,7 +105,7 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-struct TopkLds {
+struct __attribute__((aligned(16))) TopkLds {
   float v[256];
   int i[256];
   int pa[256];
@@ -192,7 +192,9 @@ __device__ void q_heap_select(TopkLds& s, int lo, int mid, int hi) {
 // ---- torch CPU topk(values, k) for k*64 > n: nth_element(k-1) then sort of the first k-1 ----
 // (libstdc++ introselect: median-of-three pivot to the front, unguarded Hoare partition, until at
 // most 3 elements remain or the depth limit 2 floor(log2 n) sends it to heap-select; then the
-// insertion sorts). The partition rounds run on registers: lane l holds positions l + 64 j.
+// insertion sorts). The partition rounds run on registers: lane l holds positions l + 64 j, as
+// the f32 bits of the probabilities, which are >= +0, so their unsigned order is the float order
+// and every comparison is an integer one (scalar where the operands are wave-uniform).
 // value (or id bits) at position p: register p >> 6 (wave-uniform) of lane p & 63
 __device__ __forceinline__ uint32_t reg_at(const uint32_t (&r)[4], int p) {
   // four reads and scalar selects: no branches
@@ -204,38 +206,33 @@ __device__ __forceinline__ uint32_t reg_at(const uint32_t (&r)[4], int p) {
   const uint32_t lo = (j & 1) ? x1 : x0, hi = (j & 1) ? x3 : x2;
   return (j & 2) ? hi : lo;
 }
+// number of set bits of m below this lane
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
 
 // One unguarded Hoare partition of [a, b) around pv (the pivot, at a - 1), by rank pairing: the
 // i-th stop of the left scan (an A position, !(v > pv)) trades places with the i-th stop of the
 // right scan (a B position, !(pv > v)) while it lies to the left of it, which is the sequence of
-// swaps the sequential scans make. Partners meet through LDS slots indexed by the rank, with no
-// position lookup. Returns the cut, min(A[M], B[M-1], b) for M swaps.
-__device__ int reg_partition(TopkLds& s, uint32_t (&v)[4], uint32_t (&id)[4], int a, int b, float pv,
-                             int lane) {
-  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  const uint64_t gt = (lane == 63) ? 0ull : ((~0ull) << (lane + 1));
-  // registers holding positions of [a, b) (wave-uniform): the others are skipped
-  const int j0 = a >> 6, j1 = (b - 1) >> 6;
+// swaps the sequential scans make. Partners meet through LDS slots indexed by the rank (value and
+// id as one 64-bit word; a swapping A element writes slot r of X and reads slot r of Y, a
+// swapping B element the reverse), with no position lookup. Every register is processed under
+// its in-range mask, without branches. Returns the cut, min(A[M], B[M-1], b) for M swaps.
+__device__ int reg_partition(TopkLds& s, uint32_t (&v)[4], uint32_t (&id)[4], int a, int b,
+                             uint32_t pv, int lane) {
   bool isA[4], isB[4];
   uint64_t mA[4], mB[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    isA[j] = isB[j] = false;
-    mA[j] = mB[j] = 0ull;
-    if (j < j0 || j > j1) continue;
-    const int pos = 64 * j + lane;
-    const bool in = pos >= a && pos < b;
-    const float x = __uint_as_float(v[j]);
-    isA[j] = in && !(x > pv);
-    isB[j] = in && !(pv > x);
-    mA[j] = __ballot(isA[j]);
-    mB[j] = __ballot(isB[j]);
-  }
   int cA[5], cB[5];
   cA[0] = 0;
   cB[0] = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    const int pos = 64 * j + lane;
+    const bool in = pos >= a && pos < b;
+    isA[j] = in && v[j] <= pv;
+    isB[j] = in && v[j] >= pv;
+    mA[j] = __ballot(isA[j]);
+    mB[j] = __ballot(isB[j]);
     cA[j + 1] = cA[j] + __popcll(mA[j]);
     cB[j + 1] = cB[j] + __popcll(mB[j]);
   }
@@ -245,54 +242,40 @@ __device__ int reg_partition(TopkLds& s, uint32_t (&v)[4], uint32_t (&id)[4], in
   int M = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    rankA[j] = cA[j] + __popcll(mA[j] & lt);                 // # A positions < pos
-    rankB[j] = (totB - cB[j + 1]) + __popcll(mB[j] & gt);    // # B positions > pos
+    rankA[j] = cA[j] + lanes_below(mA[j]);                              // # A positions < pos
+    rankB[j] = totB - cB[j] - lanes_below(mB[j]) - (isB[j] ? 1 : 0);   // # B positions > pos
     swA[j] = isA[j] && rankB[j] > rankA[j];
     swB[j] = isB[j] && rankA[j] > rankB[j];
-    if (j >= j0 && j <= j1) M += __popcll(__ballot(swA[j]));
+    M += __popcll(__ballot(swA[j]));
   }
   // A[M] and B[M-1]: the positions holding those ranks (none: past the range)
   int cut = b;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if (j < j0 || j > j1) continue;
     const uint64_t fa = __ballot(isA[j] && rankA[j] == M);
     const uint64_t fb = __ballot(isB[j] && rankB[j] == M - 1);
-    if (fa) cut = min(cut, 64 * j + (int)__builtin_ctzll(fa));
-    if (fb) cut = min(cut, 64 * j + (int)__builtin_ctzll(fb));
+    const int pa = fa ? 64 * j + (int)__builtin_ctzll(fa) : b;
+    const int pb = fb ? 64 * j + (int)__builtin_ctzll(fb) : b;
+    cut = min(cut, min(pa, pb));
   }
   if (M > 0) {
-    // the rank slots: swapping A of rank r -> v[r] / i[r], swapping B of rank r -> pa[r] / pb[r]
-    // (r < M <= 128). Every lane of a register in range stores and loads: the others use slot
-    // 128 + lane, which no rank reaches.
-    const int dummy = 128 + lane;
+    // X and Y: 192 slots each over s.v .. s.pb (ranks < M <= 128; lanes that do not swap use
+    // slot 128 + lane, which no rank reaches)
+    uint2* X = reinterpret_cast<uint2*>(&s.v[0]);
+    uint2* Y = X + 192;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j < j0 || j > j1) continue;
-      const int ia = swA[j] ? rankA[j] : dummy;
-      const int ib = swB[j] ? rankB[j] : dummy;
-      s.v[ia] = __uint_as_float(v[j]);
-      s.i[ia] = (int)id[j];
-      s.pa[ib] = (int)v[j];
-      s.pb[ib] = (int)id[j];
+      const int slot = swA[j] ? rankA[j] : (swB[j] ? rankB[j] : 128 + lane);
+      (swB[j] ? Y : X)[slot] = make_uint2(v[j], id[j]);
     }
     wave_sync();
-    uint32_t na[4], nia[4], nb[4], nib[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j < j0 || j > j1) continue;
-      const int ra = swA[j] ? rankA[j] : dummy;
-      const int rb = swB[j] ? rankB[j] : dummy;
-      na[j] = (uint32_t)s.pa[ra];
-      nia[j] = (uint32_t)s.pb[ra];
-      nb[j] = __float_as_uint(s.v[rb]);
-      nib[j] = (uint32_t)s.i[rb];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < j0 || j > j1) continue;
-      v[j] = swA[j] ? na[j] : (swB[j] ? nb[j] : v[j]);
-      id[j] = swA[j] ? nia[j] : (swB[j] ? nib[j] : id[j]);
+      const int slot = swA[j] ? rankA[j] : (swB[j] ? rankB[j] : 128 + lane);
+      const uint2 got = (swA[j] ? Y : X)[slot];
+      const bool sw = swA[j] || swB[j];
+      v[j] = sw ? got.x : v[j];
+      id[j] = sw ? got.y : id[j];
     }
     wave_sync();
   }
@@ -317,10 +300,9 @@ __device__ int wave_torch_topk_reg(TopkLds& s, const float* p, int n, int k, int
     if (depth == 0) { deep = true; break; }
     --depth;
     const int mid = lo + (hi - lo) / 2;
-    // move_median_to_first(lo, lo+1, mid, hi-1)
+    // move_median_to_first(lo, lo+1, mid, hi-1) with comp = greater
     const int a = lo + 1, b = mid, c = hi - 1;
-    const float va = __uint_as_float(reg_at(v, a)), vb = __uint_as_float(reg_at(v, b));
-    const float vc = __uint_as_float(reg_at(v, c));
+    const uint32_t va = reg_at(v, a), vb = reg_at(v, b), vc = reg_at(v, c);
     int pick;
     if (va > vb) {
       if (vb > vc) pick = b;
@@ -338,7 +320,7 @@ __device__ int wave_torch_topk_reg(TopkLds& s, const float* p, int n, int k, int
       v[j] = at_lo ? vpk : (at_pk ? vlo : v[j]);
       id[j] = at_lo ? ipk : (at_pk ? ilo : id[j]);
     }
-    const int cut = reg_partition(s, v, id, lo + 1, hi, __uint_as_float(vpk), lane);
+    const int cut = reg_partition(s, v, id, lo + 1, hi, vpk, lane);
     if (cut <= nth) lo = cut;
     else hi = cut;
   }

@@ -60,8 +60,12 @@ def test_routed_experts_q5k_down(pkg, layer_q5k, dev):
         assert_close(raw, want, f"expert_raw q5k T={T} path={path}", max_abs=BOUND[path])
 
 
+# path 2 up to 256 tokens runs the narrow-slab kernels (one or two 32-row groups in the last
+# 64-row tile: 7, 33, 100), above it the 128 x 256 items (257)
 @pytest.mark.parametrize("T,path,dtype", [(1, 1, torch.float32), (16, 1, torch.float32),
-                                          (64, 2, torch.float32), (257, 2, torch.bfloat16),
+                                          (7, 2, torch.float32), (33, 2, torch.bfloat16),
+                                          (64, 2, torch.float32), (100, 2, torch.float32),
+                                          (256, 2, torch.bfloat16), (257, 2, torch.bfloat16),
                                           (64, 3, torch.bfloat16)])
 def test_shared_expert_vs_oracle(pkg, layer_c0, dev, T, path, dtype):
     lw, ow = layer_c0
