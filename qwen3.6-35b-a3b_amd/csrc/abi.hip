@@ -113,7 +113,7 @@ static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
   c.xn = r256((size_t)T * H * 4);
   c.x16 = r256((size_t)T * H * 2);
   c.flag = 256;
-  c.rscr = moe_router_i8_scratch_bytes(T, H, E);
+  c.rscr = moe_router_scratch_bytes(T, H, E);
   return c;
 }
 
@@ -132,7 +132,7 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int K, int I_s) {
 
 size_t moe_router_workspace_bytes(int T, int H, int E) {
   if (T < 1 || H < 1 || E < 1) return 0;
-  return kSyncBytes + r256((size_t)T * E * 2) + moe_router_i8_scratch_bytes(T, H, E);
+  return kSyncBytes + r256((size_t)T * E * 2) + moe_router_scratch_bytes(T, H, E);
 }
 
 int moe_dequant(const void* blocks, int fmt, int64_t n_elts, void* out, int out_dtype,
@@ -165,9 +165,14 @@ int moe_router_topk(const void* x, int x_dtype, const void* w_router, int w_dtyp
     logits = reinterpret_cast<uint16_t*>(w.take((size_t)T * E * 2));
     if (!logits) return moe_set_error(MOE_E_WORKSPACE, "moe_router_topk: workspace too small for the logits");
   }
-  // room for the int8 matrix-core R1 (large T), else the f64 one; the bits are the same
-  const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);
+  // room for the int8 matrix-core R1 (large T) or the single-launch R1-R5 (small T), else the
+  // f64 one; the bits are the same
+  const size_t rsb = moe_router_scratch_bytes(T, H, E);
   void* rscr = w.take(rsb);
+  if (rscr && moe_router_chain_supported(T, H, E, K))
+    return moe_launch_router_chain(x, x_dtype, w_router, w_dtype, logit_bias, T, H, E, logits, probs,
+                                   topk_ids, w_f32, reinterpret_cast<uint16_t*>(w_bf16), nullptr, true,
+                                   rscr, reinterpret_cast<int*>(ws), st);
   MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, w_dtype, logit_bias, T, H, E, logits, rscr, rsb, st));
   return moe_launch_route_topk(logits, T, E, K, probs, topk_ids, w_f32,
                                reinterpret_cast<uint16_t*>(w_bf16), nullptr, st);
@@ -364,8 +369,13 @@ int moe_experts(const void* x, int x_dtype, const void* gate_up_q, const void* u
 // The small-T shared-expert kernels (narrow slabs, K split over the waves) up to this many tokens;
 // above it the 128 x 256 items keep every CU busy and reuse each weight tile over 128 rows.
 constexpr int kSharedSkinnyMaxT = 256;
+// the shared expert's own path: AUTO takes the GEMV kernels up to 16 tokens, MFMA above
+static int shared_path(int path, int T) {
+  return path == MOE_PATH_AUTO ? (T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA) : path;
+}
 static bool shared_skinny(int path, int sfmt, int T, int H, int Is) {
-  return path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && T <= kSharedSkinnyMaxT && moe_gemm5s_supports(H, Is);
+  return shared_path(path, T) == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && T <= kSharedSkinnyMaxT &&
+         moe_gemm5s_supports(H, Is);
 }
 
 // x16: the f16 rows of x when the caller already has them (else NULL); x16_make: where to write
@@ -374,7 +384,7 @@ static int shared_body(const void* x, int x_dtype, const uint16_t* x16, const vo
                        const void* wu, const void* wd, int sfmt, const void* wsg, int gate_dtype, int T, int H,
                        int Is, int path, float* shared_raw, float* gate_prob, MoeWs& w, hipStream_t st,
                        uint16_t* x16_make, bool& made) {
-  if (path == MOE_PATH_AUTO) path = T <= 16 ? MOE_PATH_GEMV : MOE_PATH_MFMA;
+  path = shared_path(path, T);
   if (path == MOE_PATH_GEMV || path == MOE_PATH_GEMV_MULTI) {
     float* s = reinterpret_cast<float*>(w.take((size_t)T * Is * 4));
     if (!s) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
@@ -622,10 +632,15 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
                        x16_late ? x16 : nullptr);
   // the router's scratch is dead before the experts take theirs (same stream)
   MoeWs wr = w;
-  const size_t rsb = moe_router_i8_scratch_bytes(T, H, E);
+  const size_t rsb = moe_router_scratch_bytes(T, H, E);
   void* rscr = wr.take(rsb);
-  if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, rscr, rsb, st);
-  if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order);
+  if (rc == MOE_OK && rscr && moe_router_chain_supported(T, H, E, K)) {
+    rc = moe_launch_router_chain(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits,
+                                 nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st);
+  } else {
+    if (rc == MOE_OK) rc = moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, rscr, rsb, st);
+    if (rc == MOE_OK) rc = moe_launch_route_topk(logits, T, E, K, nullptr, ids, wf, wb, nullptr, st, exact_order);
+  }
   if (rc == MOE_OK) rc = moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm);
   // joined before the routed GEMMs: their persistent grids take every CU and each block owns a
   // fixed share of the items, so a block kept waiting by a still-running shared-expert kernel

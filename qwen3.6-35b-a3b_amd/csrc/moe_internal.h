@@ -25,6 +25,17 @@ bool moe_router_i8_supported(int T, int H, int E);
 int moe_launch_router_logits_i8(const void* x, int x_dtype, const void* w, int w_dtype,
                                 const float* bias, int T, int H, int E, uint16_t* logits,
                                 void* scratch, hipStream_t st);
+// R1-R5 in one launch (8 <= T <= 256, E = 256, K = 8, H % 2048 == 0): scratch of
+// moe_router_chain_scratch_bytes(T, E) bytes, sync = the workspace's sync words (arrival counters
+// at kRouterCntWord, zero between launches). Same bits as router_logits + route_topk.
+bool moe_router_chain_supported(int T, int H, int E, int K);
+size_t moe_router_chain_scratch_bytes(int T, int E);
+int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
+                            int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
+                            float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
+                            void* scratch, int* sync, hipStream_t st);
+// bytes of router scratch that let every R1 form run (the int8 one, the single-launch chain)
+size_t moe_router_scratch_bytes(int T, int H, int E);
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,
                           float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, hipStream_t st,
                           bool exact_order = true);
@@ -169,6 +180,9 @@ int moe_launch_take_status(int* word, int32_t* out, hipStream_t st);
 // buffers). They must be zero before the first call (moe_workspace_init); calls keep them
 // consistent.
 constexpr size_t kSyncBytes = 524288;
+// first sync word of the single-launch router's arrival counters (272 words; the decode layer's
+// words end before it)
+constexpr int kRouterCntWord = 120000;
 // single-launch decode layer (decode_layer.hip): 256 co-resident workgroups, model geometry only
 bool moe_layer_kernel_supported(int H, int I, int E, int K, int Is, int gu_fmt, int dn_fmt);
 size_t moe_layer_exchange_bytes();

@@ -178,26 +178,19 @@ __global__ __launch_bounds__(256) void k_router_logits_gemv(
   }
 }
 
-// ------------------------------------------------- R1, 8 <= T <= 256: f64 MFMA, K split by wave --
-// Block = 8 waves on one tile of 16 tokens x 16 experts; wave w sums k in [w H/8, (w+1) H/8) with
-// v_mfma_f64_16x16x4f64 (A: lane l holds x[t0 + l%16][k], B: W[e0 + l%16][k], k = k0 + 4(l/16) + i
-// for the step's MFMA i; D: lane l, register j holds D[4j + l/16][l%16]). The 8 partial tiles are
-// added through LDS in wave order, so the f64 sum has a fixed order; any order stays inside the
-// certificate's bound 4(H+3) 2^-53 (|x||W_e| + |b|). Logits the bound does not settle are
-// recomputed in double-double by one wave. grid = (ceil(T/16), ceil(E/16)), block = 512.
+// One wave's share of a 16 x 16 f64 tile: x[t0 + .][k] . W[e0 + .][k] over k in [kb, kb + kw)
+// (kw % 64 == 0) on v_mfma_f64_16x16x4f64 (A: lane l holds x[t0 + l%16][k], B: W[e0 + l%16][k],
+// k = k0 + 4(l/16) + i for the step's MFMA i; D: lane l, register j holds D[4j + l/16][l%16]),
+// written to s_d[wave] with the rows' partial squared norms (s_xsq / s_wsq[wave]).
 template <int XDT, int WDT>
-__global__ __launch_bounds__(512) void k_router_logits_small(
-    const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias,
-    int T, int H, int E, uint16_t* __restrict__ logits) {
+__device__ __forceinline__ void tile_f64_partial(const void* __restrict__ xv, const void* __restrict__ w,
+                                                 int T, int H, int E, int t0, int e0, int kb, int kw,
+                                                 double (*s_d)[256], double (*s_xsq)[16],
+                                                 double (*s_wsq)[16]) {
   using d4 = double __attribute__((ext_vector_type(4)));
-  __shared__ double s_d[8][256];
-  __shared__ double s_xsq[8][16], s_wsq[8][16];
-  __shared__ int s_fail[256];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
   const int tr = min(t0 + r, T - 1), er = min(e0 + r, E - 1);   // clamped rows: never stored
-  const int kw = H / 8, kb = wv * kw;
   d4 acc = {0, 0, 0, 0}, acc2 = acc;                  // two chains of dependent MFMAs
   double xsq = 0.0, wsq = 0.0;
 #pragma unroll 4
@@ -234,6 +227,26 @@ __global__ __launch_bounds__(512) void k_router_logits_small(
   if (g == 0) { s_xsq[wv][r] = xsq; s_wsq[wv][r] = wsq; }
 #pragma unroll
   for (int j = 0; j < 4; ++j) s_d[wv][16 * (4 * j + g) + r] = acc[j] + acc2[j];
+}
+
+// ------------------------------------------------- R1, 8 <= T <= 256: f64 MFMA, K split by wave --
+// Block = 8 waves on one tile of 16 tokens x 16 experts; wave w sums k in [w H/8, (w+1) H/8) with
+// v_mfma_f64_16x16x4f64 (A: lane l holds x[t0 + l%16][k], B: W[e0 + l%16][k], k = k0 + 4(l/16) + i
+// for the step's MFMA i; D: lane l, register j holds D[4j + l/16][l%16]). The 8 partial tiles are
+// added through LDS in wave order, so the f64 sum has a fixed order; any order stays inside the
+// certificate's bound 4(H+3) 2^-53 (|x||W_e| + |b|). Logits the bound does not settle are
+// recomputed in double-double by one wave. grid = (ceil(T/16), ceil(E/16)), block = 512.
+template <int XDT, int WDT>
+__global__ __launch_bounds__(512) void k_router_logits_small(
+    const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias,
+    int T, int H, int E, uint16_t* __restrict__ logits) {
+  __shared__ double s_d[8][256];
+  __shared__ double s_xsq[8][16], s_wsq[8][16];
+  __shared__ int s_fail[256];
+  const int tid = threadIdx.x, wv = tid >> 6;
+  const int lane = tid & 63;
+  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+  tile_f64_partial<XDT, WDT>(xv, w, T, H, E, t0, e0, wv * (H / 8), H / 8, s_d, s_xsq, s_wsq);
   __syncthreads();
   if (tid < 256) {
     const int tt = tid >> 4, ee = tid & 15;            // D[tt][ee]: token t0 + tt, expert e0 + ee
@@ -574,6 +587,159 @@ __global__ __launch_bounds__(256) void k_route_replay8(const uint16_t* __restric
                          w_bf16 + (size_t)t * 8, heap_flag);
 }
 
+constexpr int kChainKS = 4;       // blocks per tile (K splits)
+constexpr int kChainPart = 288;   // doubles per partial: 256 tile sums, 16 + 16 row norms
+constexpr int kChainTiles = 256;  // tile counters (T <= 256, E = 256); 16 group counters follow
+static_assert((kRouterCntWord + kChainTiles + 16) * 4 <= (int)kSyncBytes, "router counters in the sync words");
+
+// ------------------------------------------- R1-R5 in one launch, 8 <= T <= 256, E = 256, K = 8 --
+// The small-T R1 above runs one 16 x 16 tile per block, so at T = 64 it keeps 64 CUs busy for the
+// whole K; here each tile's K is split over kChainKS blocks (grid = tiles x kChainKS: 256 blocks at
+// T = 64), and the launches of R2-R5 are folded in:
+//   1. every block: the f64 partial tile of its K range (wave partials added in wave order), written
+//      with its partial row norms to scratch; then an arrival count per tile;
+//   2. the tile's last block to arrive: the kChainKS partials added in split order (a fixed order;
+//      any order stays inside the certificate's bound), the certified bf16 rounding (double-double
+//      recompute where it does not settle), the logits stored; then an arrival count per 16-token
+//      group;
+//   3. the group's last tile to arrive: R2-R5 for the group's 16 tokens, two per wave, as
+//      k_route_topk8 with the exact replay inline.
+// What one block hands to another (partials, logits) goes through agent-scope stores and loads,
+// which meet past the XCDs' L2s, and every thread waits for its stores before the block's arrival
+// is counted. (Fences would write back and invalidate whole L2s, 256 times per launch, under the
+// shared expert's concurrent GEMMs.) Each last arriver resets its counter, so the words are zero
+// again for the next launch (also under graph replay). Counters: cnt[tile] for tiles <
+// kChainTiles, cnt[kChainTiles + group].
+// agent-scope (cross-XCD) stores and loads of the single-launch router's hand-offs
+__device__ __forceinline__ void st_agent(double* p, double v) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), (unsigned long long)__double_as_longlong(v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_agent(const double* p) {
+  return __longlong_as_double((long long)__hip_atomic_load(reinterpret_cast<const unsigned long long*>(p),
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void st16_agent(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// this thread's stores complete (acknowledged) before what follows; the signal fence keeps the
+// compiler from moving them past the wait
+__device__ __forceinline__ void stores_done() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int XDT, int WDT>
+__global__ __launch_bounds__(512) void k_router_chain(
+    const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias, int T,
+    int H, int E, uint16_t* __restrict__ logits, float* __restrict__ probs, int32_t* __restrict__ ids,
+    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ heap_flag,
+    int exact_order, double* __restrict__ part, int* __restrict__ cnt) {
+  __shared__ double s_d[8][256];
+  __shared__ double s_xsq[8][16], s_wsq[8][16];
+  __shared__ double s_xt[16], s_wt[16];
+  __shared__ int s_fail[256];
+  __shared__ int s_last;
+  __shared__ TopkLds s_tk[8];
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int nE = E / 16;
+  const int ks = blockIdx.x % kChainKS, tile = blockIdx.x / kChainKS;
+  const int et = tile % nE, tg = tile / nE;
+  const int t0 = tg * 16, e0 = et * 16;
+  const int kw = H / (8 * kChainKS);
+  tile_f64_partial<XDT, WDT>(xv, w, T, H, E, t0, e0, ks * (H / kChainKS) + wv * kw, kw, s_d, s_xsq, s_wsq);
+  __syncthreads();
+  double* my = part + ((size_t)tile * kChainKS + ks) * kChainPart;
+  if (tid < 256) {
+    double sum = 0.0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sum += s_d[q][tid];
+    st_agent(&my[tid], sum);
+  } else if (tid < 288) {
+    const int i = tid - 256;
+    double n = 0.0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) n += i < 16 ? s_xsq[q][i] : s_wsq[q][i - 16];
+    st_agent(&my[tid], n);
+  }
+  stores_done();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(&cnt[tile], 1) == kChainKS - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) __hip_atomic_store(&cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const double* tp = part + (size_t)tile * kChainKS * kChainPart;
+  if (tid < 32) {
+    double n = 0.0;
+#pragma unroll
+    for (int q = 0; q < kChainKS; ++q) n += ld_agent(&tp[q * kChainPart + 256 + tid]);
+    if (tid < 16) s_xt[tid] = n;
+    else s_wt[tid - 16] = n;
+  }
+  __syncthreads();
+  if (tid < 256) {
+    const int tt = tid >> 4, ee = tid & 15;            // D[tt][ee]: token t0 + tt, expert e0 + ee
+    const int t = t0 + tt, e = e0 + ee;
+    int fail = 0;
+    if (t < T) {
+      double sum = 0.0;
+#pragma unroll
+      for (int q = 0; q < kChainKS; ++q) sum += ld_agent(&tp[q * kChainPart + tid]);
+      const double bval = bias ? (double)bias[e] : 0.0;
+      const double sv = sum + bval;
+      const double bound = 4.0 * (double)(H + 3) * 0x1p-53 * (sqrt(s_xt[tt]) * sqrt(s_wt[ee]) + fabs(bval));
+      uint32_t bits;
+      if (round_bf16_certified(sv, bound, &bits)) st16_agent(&logits[(size_t)t * E + e], (uint16_t)bits);
+      else fail = 1;
+    }
+    s_fail[tid] = fail;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    for (int base = 0; base < 256; base += 64) {
+      uint64_t m = __ballot(s_fail[base + lane] != 0);
+      while (m) {
+        const int idx = base + __builtin_ctzll(m);
+        m &= m - 1;
+        const int t = t0 + (idx >> 4), e = e0 + (idx & 15);
+        const double bval = bias ? (double)bias[e] : 0.0;
+        const uint32_t bits = gemv_dd_logit<XDT, WDT>(xv, w, t, e, H, lane, bval, s_xt[idx >> 4], s_wt[idx & 15]);
+        if (lane == 0) st16_agent(&logits[(size_t)t * E + e], (uint16_t)bits);
+      }
+    }
+  }
+  stores_done();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(&cnt[kChainTiles + tg], 1) == nE - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) __hip_atomic_store(&cnt[kChainTiles + tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll 1
+  for (int j = 0; j < 2; ++j) {
+    const int t = t0 + 2 * wv + j;
+    if (t >= T) break;
+    float p[4];
+    route_softmax<true>(logits + (size_t)t * 256, 256, lane, p);
+    if (probs) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) probs[(size_t)t * 256 + 64 * q + lane] = p[q];
+    }
+    int my_id;
+    float my_val, tot;
+    const int code = wave_topk32<8>(p, lane, my_id, my_val, tot);
+    if (code == 2 || (code == 1 && exact_order)) {
+      route_replay_and_write(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
+                             w_bf16 + (size_t)t * 8, heap_flag);
+    } else if (lane < 8) {
+      const float wv8 = my_val / tot;
+      ids[(size_t)t * 8 + lane] = my_id;
+      w_f32[(size_t)t * 8 + lane] = wv8;
+      w_bf16[(size_t)t * 8 + lane] = (uint16_t)f32_to_bf16(wv8);
+    }
+  }
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -594,6 +760,40 @@ static void launch_router_logits(const void* x, const void* w, const float* bias
     hipLaunchKernelGGL((k_router_logits_gemm<XDT, WDT>), dim3((E + 63) / 64, (T + 63) / 64), dim3(256), 0, st,
                        x, w, bias, T, H, E, logits);
   }
+}
+
+bool moe_router_chain_supported(int T, int H, int E, int K) {
+  return T >= 8 && T <= 256 && E == 256 && K == 8 && H % (64 * 8 * kChainKS) == 0;
+}
+
+size_t moe_router_chain_scratch_bytes(int T, int E) {
+  return (size_t)((T + 15) / 16) * (size_t)((E + 15) / 16) * kChainKS * kChainPart * sizeof(double);
+}
+
+size_t moe_router_scratch_bytes(int T, int H, int E) {
+  const size_t a = moe_router_i8_scratch_bytes(T, H, E), b = moe_router_chain_scratch_bytes(T, E);
+  return a > b ? a : b;
+}
+
+int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
+                            int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
+                            float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
+                            void* scratch, int* sync, hipStream_t st) {
+  if (!moe_router_chain_supported(T, H, E, 8) || !scratch || !sync)
+    return moe_set_error(MOE_E_UNSUPPORTED, "router_chain: needs 8 <= T <= 256, E = 256, K = 8, H %% 2048 == 0");
+  const dim3 grid(((T + 15) / 16) * (E / 16) * kChainKS);
+  double* part = reinterpret_cast<double*>(scratch);
+  int* cnt = sync + kRouterCntWord;
+  const int eo = exact_order ? 1 : 0;
+#define MOE_CHAIN(XD, WD)                                                                          \
+  hipLaunchKernelGGL((k_router_chain<XD, WD>), grid, dim3(512), 0, st, x, w, bias, T, H, E, logits, \
+                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt)
+  if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_F32);
+  else if (x_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_BF16);
+  else if (w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_BF16, MOE_DT_F32);
+  else MOE_CHAIN(MOE_DT_BF16, MOE_DT_BF16);
+#undef MOE_CHAIN
+  return moe_check_launch("router_chain");
 }
 
 int moe_launch_router_logits(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,

@@ -418,12 +418,18 @@ __device__ __forceinline__ int wave_topk_fast(const float* p, int E, int K, int 
 }
 
 // R2: softmax over E bf16 logits in f32 (max-subtracted, sum, multiply by the reciprocal — the
-// same form as torch's CPU kernel); lane holds positions lane + 64j.
+// same form as torch's CPU kernel); lane holds positions lane + 64j. AGENT: the logits were
+// written by other workgroups of this launch through agent-scope stores, and are read likewise.
+template <bool AGENT = false>
 __device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lane, float* p) {
   // clamped loads, all four in flight at once (guarded loads would each wait for the last)
   uint32_t raw[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) raw[j] = lg[min(64 * j + lane, E - 1)];
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t* a = lg + min(64 * j + lane, E - 1);
+    if constexpr (AGENT) raw[j] = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else raw[j] = *a;
+  }
   float lv[4];
   float m = -INFINITY;
 #pragma unroll

@@ -248,14 +248,17 @@ __global__ __launch_bounds__(256) void k_sort_scan_scatter(const int32_t* __rest
 }
 
 // 64 < P <= kChunk: the three phases in one block (histogram, scan, the one chunk's scatter), so
-// a small batch pays one launch instead of three; same positions as the three-kernel form.
+// a small batch pays one launch instead of three; same positions as the three-kernel form. With
+// tiles != NULL the block also writes the MFMA tile list (build_tiles_block).
 __global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ ids, int P, int E,
                                                   int32_t* __restrict__ offsets,
                                                   int32_t* __restrict__ sorted_pairs,
                                                   int32_t* __restrict__ pair_pos,
-                                                  int32_t* __restrict__ hit_list) {
+                                                  int32_t* __restrict__ hit_list,
+                                                  int32_t* __restrict__ tiles, int bm) {
   __shared__ int h[256], start[256], tmp[256], run[256];
   __shared__ int wcnt[4][256];
+  __shared__ uint64_t tmp64[4];
   const int e = threadIdx.x;
   h[e] = 0;
   run[e] = 0;
@@ -275,6 +278,7 @@ __global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ id
   const int hidx = block_exclusive_scan((e < E && tot > 0) ? 1 : 0, tmp, &hsum);
   if (e < E && tot > 0) hit_list[1 + hidx] = e;
   if (e == 0) hit_list[0] = hsum;
+  if (tiles) build_tiles_block(tot, base, e, bm, tiles, tmp64);
   __syncthreads();
   scatter_chunk(ids, P, E, 0, start, sorted_pairs, pair_pos, run, wcnt);
 }
@@ -336,14 +340,14 @@ size_t moe_sort_ws_bytes(int P, int E) {
 int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t* sorted_pairs,
                     int32_t* pair_pos, int32_t* hit_list, void* ws, hipStream_t st,
                     int32_t* tiles, int bm) {
-  const bool fuse_tiles = tiles && P > kChunk && E <= 256 && bm <= 160 &&
+  const bool fuse_tiles = tiles && P > 64 && E <= 256 && bm <= 160 &&
                           moe_max_mtiles(P, E, bm) <= kTilesPacked;
   if (P <= 64) {
     hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(64), 0, st, ids, P, E, offsets, sorted_pairs,
                        pair_pos, hit_list);
   } else if (P <= kChunk) {
     hipLaunchKernelGGL(k_sort_one, dim3(1), dim3(256), 0, st, ids, P, E, offsets, sorted_pairs,
-                       pair_pos, hit_list);
+                       pair_pos, hit_list, fuse_tiles ? tiles : nullptr, bm);
   } else {
     const int nchunks = (P + kChunk - 1) / kChunk, hs = hist_stride(nchunks);
     int32_t* hist = reinterpret_cast<int32_t*>(ws);

@@ -42,7 +42,9 @@ def test_router_decode_c0(pkg, layer_c0, dev):
     _check_route(pkg, x, lw.router, None)
 
 
+# 8..256 tokens: R1-R5 in one launch (K split over blocks, last arrivals reduce and route)
 @pytest.mark.parametrize("T,dtype", [(8, torch.float32), (9, torch.float32), (64, torch.float32),
+                                     (200, torch.bfloat16), (256, torch.float32),
                                      (300, torch.bfloat16), (4096, torch.bfloat16)])
 def test_router_batched(pkg, layer_c0, dev, T, dtype):
     lw, _ = layer_c0
@@ -142,6 +144,25 @@ def test_router_int8_and_f64_matrix_cores_same_bits(pkg, dev, xdt, wdt):
     assert torch.equal(r["router_logits"].view(torch.int16), lg.view(torch.int16)), \
         f"{(r['router_logits'] != lg).sum().item()} logits differ"
     assert torch.equal(r["topk_ids"], ids)
+
+
+@pytest.mark.parametrize("xdt,wdt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.bfloat16), (torch.float32, torch.float32)])
+def test_router_single_launch_and_per_tile_kernels_same_bits(pkg, dev, xdt, wdt):
+    """T = 100 (a partial 16-token group): R1-R5 in one launch (K split over four blocks per tile,
+    the partials and the routing done by the last arrivals) against the one-block-per-tile R1 and
+    the separate top-k launch: the same logits, ids and weights bit for bit, twice in a row (the
+    arrival counters are back at zero after each launch)."""
+    g = torch.Generator().manual_seed(100)
+    x = torch.randn(100, 2048, generator=g).to(xdt).to(dev)
+    w = (torch.randn(256, 2048, generator=g) * 0.02).to(wdt).to(dev)
+    bias = (torch.randn(256, generator=g) * 0.1).to(dev)
+    lg, ids = _router_f64_path(pkg, x, w, bias)
+    for _ in range(2):
+        r = pkg.abi.router_topk(x, w, 8, bias)
+        torch.cuda.synchronize()
+        assert torch.equal(r["router_logits"].view(torch.int16), lg.view(torch.int16))
+        assert torch.equal(r["topk_ids"], ids)
 
 
 @pytest.mark.parametrize("T,E,xdt,wdt", [(333, 200, torch.bfloat16, torch.float32),
