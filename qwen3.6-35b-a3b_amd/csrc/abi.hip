@@ -104,7 +104,7 @@ static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
   c.pos = r256(P * 4);
   c.hits = r256((size_t)(E + 1) * 4);
   c.sort_ws = moe_sort_ws_bytes((int)P, E);
-  c.tiles = r256((size_t)(1 + 2 * moe_max_mtiles((int)P, E, MOE_GEMM_BM)) * 4);
+  c.tiles = r256((size_t)(1 + 2 * moe_max_mtiles((int)P, E, MOE_GEMM6_BM)) * 4);
   c.S = r256(P * I * 4);
   c.y = r256(P * H * 4);
   c.sS = r256((size_t)T * Is * 4);
@@ -213,10 +213,19 @@ static bool mfma_gu4_mixed(int path, int H, int I, int gu_fmt, int dn_fmt) {
          !mfma_v2(path, H, I, gu_fmt, dn_fmt);
 }
 
+// Q4_K experts with few rows each (up to kSmallRowsMaxT tokens): the 32-row kernels (gemm6.hip),
+// which keep three K steps of activations and nibbles in flight per item
+constexpr int kSmallRowsMaxT = 256;
+static bool mfma_small(int path, int T, int H, int I, int gu_fmt, int dn_fmt) {
+  return mfma_v2(path, H, I, gu_fmt, dn_fmt) && gu_fmt == MOE_FMT_Q4_K && dn_fmt == MOE_FMT_Q4_K &&
+         T <= kSmallRowsMaxT && H >= 512 && I >= 512;
+}
+
 // rows per MFMA tile of the first grouped GEMM experts_impl runs (0: a GEMV path)
 static int mfma_tile_rows(int path, int T, int H, int I, int gu_fmt, int dn_fmt) {
   path = pick_path(path, T, gu_fmt, dn_fmt);
   if (path == MOE_PATH_GEMV) return 0;
+  if (mfma_small(path, T, H, I, gu_fmt, dn_fmt)) return MOE_GEMM6_BM;
   return (mfma_v2(path, H, I, gu_fmt, dn_fmt) || mfma_gu4_mixed(path, H, I, gu_fmt, dn_fmt)) ? MOE_GEMM3_BM
                                                                                            : MOE_GEMM_BM;
 }
@@ -228,8 +237,8 @@ static bool y16_rows(int path, int T, int H, int I, int K, int gu_fmt, int dn_fm
   return path != MOE_PATH_GEMV && mfma_v2(path, H, I, gu_fmt, dn_fmt) && K == 8 && H % 4 == 0;
 }
 
-// ints of a tile-list buffer that holds the list of either tile height
-static size_t tile_list_ints(int P, int E) { return 1 + 2 * (size_t)moe_max_mtiles(P, E, MOE_GEMM_BM); }
+// ints of a tile-list buffer that holds the list of any tile height (the shortest tiles: most)
+static size_t tile_list_ints(int P, int E) { return 1 + 2 * (size_t)moe_max_mtiles(P, E, MOE_GEMM6_BM); }
 
 // tiles_pre: the tile list of mfma_tile_rows(...) rows, already built in a buffer of
 // tile_list_ints(P, E) ints (NULL: built here)
@@ -257,7 +266,8 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
     return moe_set_error(MOE_E_FORMAT, "moe_experts: Q5_K down runs on the GEMV and MFMA (f16) paths");
   const bool v2 = mfma_v2(path, H, I, gu_fmt, dn_fmt);
   const bool gu4 = mfma_gu4_mixed(path, H, I, gu_fmt, dn_fmt);
-  const int bm = (v2 || gu4) ? MOE_GEMM3_BM : MOE_GEMM_BM;
+  const bool small = mfma_small(path, T, H, I, gu_fmt, dn_fmt);
+  const int bm = small ? MOE_GEMM6_BM : (v2 || gu4) ? MOE_GEMM3_BM : MOE_GEMM_BM;
   const int max_tiles = moe_max_mtiles(P, E, bm);
   int32_t* tiles = tiles_pre;
   if (!tiles) {
@@ -287,6 +297,11 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
       if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
       MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
       x16 = c;
+    }
+    if (small) {
+      MOE_TRY(moe_launch_gemm6_gateup(x16, gate, up, estride, tiles, max_tiles, offsets, sorted_pairs,
+                                      K, H, I, S, st));
+      return moe_launch_gemm6_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st);
     }
     // gemm4's persistent item stream needs two super-blocks per item (H, I >= 512)
     if (gu_fmt == MOE_FMT_Q4_K && H >= 512)

@@ -51,6 +51,7 @@ int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t*
 // MOE_GEMM3_BM for gemm3.hip)
 #define MOE_GEMM_BM 64
 #define MOE_GEMM3_BM 160
+#define MOE_GEMM6_BM 32
 int moe_max_mtiles(int P, int E, int bm = MOE_GEMM_BM);
 int moe_launch_build_tiles(const int32_t* offsets, const int32_t* hit_list, int E, int P,
                            int32_t* tiles, hipStream_t st, int bm = MOE_GEMM_BM);
@@ -98,6 +99,16 @@ int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void*
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
                             int I, uint16_t* S, hipStream_t st);
 int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_stride,
+                          const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
+                          void* y, int y16, hipStream_t st);
+
+// gemm6.hip: the same GEMMs for few rows per expert: 32-row tiles (MOE_GEMM6_BM), one block per
+// (tile, 256-row slab), activations and nibbles both requested three K steps ahead
+int moe_launch_gemm6_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
+                            size_t expert_stride, const int32_t* tiles, int max_tiles,
+                            const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
+                            int I, uint16_t* S, hipStream_t st);
+int moe_launch_gemm6_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
                           void* y, int y16, hipStream_t st);
 

@@ -36,6 +36,24 @@ def test_routed_experts_vs_oracle(pkg, layer_c0, dev, T, path):
     assert_close(raw, want, f"expert_raw T={T} path={path}", max_abs=BOUND[path])
 
 
+def test_small_and_large_tile_kernels_same_bits(pkg, layer_zipf, dev):
+    """Q4_K experts at up to 256 tokens run on 32-row tiles (one block per tile and slab), above
+    on the 160-row persistent kernels. Both take the same K steps in the same order, so a
+    (token, slot) row comes out with the same bits whichever tile it sits in: the rows of a
+    256-token call equal those of the same tokens inside a 257-token call (Zipf routing: a few
+    experts with many rows, many with one)."""
+    lw, _ = layer_zipf
+    x = pkg.synth.make_input(257, seed=257, device=dev)
+    rows = []
+    for T in (256, 257):
+        r, gr = _route_and_group(pkg, lw, x[:T].contiguous())
+        y = pkg.abi.experts(x[:T].contiguous(), lw.gate_up_q, lw.gate_up_fmt, lw.down_q, lw.down_fmt, gr, 8, 2)
+        torch.cuda.synchronize()
+        rows.append(y.cpu()[gr["pair_pos"].cpu().long()][: 256 * 8])
+    assert torch.isfinite(rows[0]).all()
+    assert torch.equal(rows[0], rows[1])
+
+
 def test_routed_experts_q6k_down(pkg, layer_q6k, dev):
     lw, ow = layer_q6k
     for T, path in ((2, 1), (96, 2)):
