@@ -603,7 +603,8 @@ static_assert((kRouterCntWord + kChainTiles + 16) * 4 <= (int)kSyncBytes, "route
 //      recompute where it does not settle), the logits stored; then an arrival count per 16-token
 //      group;
 //   3. the group's last tile to arrive: R2-R5 for the group's 16 tokens, two per wave, as
-//      k_route_topk8 with the exact replay inline.
+//      k_route_topk8; then the exact replays of the tokens the fast path could not settle, one
+//      per wave.
 // What one block hands to another (partials, logits) goes through agent-scope stores and loads,
 // which meet past the XCDs' L2s, and every thread waits for its stores before the block's arrival
 // is counted. (Fences would write back and invalidate whole L2s, 256 times per launch, under the
@@ -640,7 +641,8 @@ __global__ __launch_bounds__(512) void k_router_chain(
   __shared__ double s_xsq[8][16], s_wsq[8][16];
   __shared__ double s_xt[16], s_wt[16];
   __shared__ int s_fail[256];
-  __shared__ int s_last;
+  __shared__ int s_last, s_nrep;
+  __shared__ int s_rep[16];
   __shared__ TopkLds s_tk[8];
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   const int nE = E / 16;
@@ -714,7 +716,13 @@ __global__ __launch_bounds__(512) void k_router_chain(
   if (tid == 0) s_last = atomicAdd(&cnt[kChainTiles + tg], 1) == nE - 1;
   __syncthreads();
   if (!s_last) return;
-  if (tid == 0) __hip_atomic_store(&cnt[kChainTiles + tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    __hip_atomic_store(&cnt[kChainTiles + tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_nrep = 0;
+  }
+  __syncthreads();
+  // the fast path for the group's 16 tokens, two per wave; the tokens it cannot settle are listed
+  // and replayed afterwards, one per wave, so that no wave runs two replays while others idle
 #pragma unroll 1
   for (int j = 0; j < 2; ++j) {
     const int t = t0 + 2 * wv + j;
@@ -729,14 +737,22 @@ __global__ __launch_bounds__(512) void k_router_chain(
     float my_val, tot;
     const int code = wave_topk32<8>(p, lane, my_id, my_val, tot);
     if (code == 2 || (code == 1 && exact_order)) {
-      route_replay_and_write(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
-                             w_bf16 + (size_t)t * 8, heap_flag);
+      if (lane == 0) s_rep[atomicAdd(&s_nrep, 1)] = t;
     } else if (lane < 8) {
       const float wv8 = my_val / tot;
       ids[(size_t)t * 8 + lane] = my_id;
       w_f32[(size_t)t * 8 + lane] = wv8;
       w_bf16[(size_t)t * 8 + lane] = (uint16_t)f32_to_bf16(wv8);
     }
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int i = wv; i < s_nrep; i += 8) {
+    const int t = s_rep[i];
+    float p[4];
+    route_softmax<true>(logits + (size_t)t * 256, 256, lane, p);
+    route_replay_and_write(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
+                           w_bf16 + (size_t)t * 8, heap_flag);
   }
 }
 

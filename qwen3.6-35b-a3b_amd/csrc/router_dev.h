@@ -259,24 +259,62 @@ __device__ int reg_partition(TopkLds& s, uint32_t (&v)[4], uint32_t (&id)[4], in
     cut = min(cut, min(pa, pb));
   }
   if (M > 0) {
-    // X and Y: 192 slots each over s.v .. s.pb (ranks < M <= 128; lanes that do not swap use
-    // slot 128 + lane, which no rank reaches)
-    uint2* X = reinterpret_cast<uint2*>(&s.v[0]);
-    uint2* Y = X + 192;
+    // X = slots 0..191 and Y = slots 192..383 over s.v .. s.pb (ranks < M <= 128; lanes that do not
+    // swap use slot 128 + lane of X, which no rank reaches); indices, not pointers, are selected,
+    // so the exchange has no branches
+    uint2* XY = reinterpret_cast<uint2*>(&s.v[0]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int slot = swA[j] ? rankA[j] : (swB[j] ? rankB[j] : 128 + lane);
-      (swB[j] ? Y : X)[slot] = make_uint2(v[j], id[j]);
+      const int slot = swA[j] ? rankA[j] : (swB[j] ? 192 + rankB[j] : 128 + lane);
+      XY[slot] = make_uint2(v[j], id[j]);
     }
     wave_sync();
+    // all four reads issued by every lane before any result is used (the empty asm keeps the
+    // compiler from turning them into reads under each lane's swap condition, one at a time)
+    uint2 got[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int slot = swA[j] ? rankA[j] : (swB[j] ? rankB[j] : 128 + lane);
-      const uint2 got = (swA[j] ? Y : X)[slot];
-      const bool sw = swA[j] || swB[j];
-      v[j] = sw ? got.x : v[j];
-      id[j] = sw ? got.y : id[j];
+      const int slot = swA[j] ? 192 + rankA[j] : (swB[j] ? rankB[j] : 128 + lane);
+      got[j] = XY[slot];
     }
+    asm volatile("" ::"v"(got[0].x), "v"(got[0].y), "v"(got[1].x), "v"(got[1].y), "v"(got[2].x),
+                 "v"(got[2].y), "v"(got[3].x), "v"(got[3].y));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool sw = swA[j] || swB[j];
+      v[j] = sw ? got[j].x : v[j];
+      id[j] = sw ? got[j].y : id[j];
+    }
+    wave_sync();
+  }
+  return cut;
+}
+
+// The same partition when [a - 1, b) lies in one register: x / xi hold positions base + lane.
+__device__ int reg_partition1(TopkLds& s, uint32_t& x, uint32_t& xi, int a, int b, uint32_t pv,
+                              int lane, int base) {
+  const int pos = base + lane;
+  const bool in = pos >= a && pos < b;
+  const bool isA = in && x <= pv, isB = in && x >= pv;
+  const uint64_t mA = __ballot(isA), mB = __ballot(isB);
+  const int rankA = lanes_below(mA);
+  const int rankB = __popcll(mB) - lanes_below(mB) - (isB ? 1 : 0);
+  const bool swA = isA && rankB > rankA, swB = isB && rankA > rankB;
+  const int M = __popcll(__ballot(swA));
+  const uint64_t fa = __ballot(isA && rankA == M);
+  const uint64_t fb = __ballot(isB && rankB == M - 1);
+  int cut = b;
+  if (fa) cut = min(cut, base + (int)__builtin_ctzll(fa));
+  if (fb) cut = min(cut, base + (int)__builtin_ctzll(fb));
+  if (M > 0) {
+    uint2* XY = reinterpret_cast<uint2*>(&s.v[0]);
+    XY[swA ? rankA : (swB ? 192 + rankB : 128 + lane)] = make_uint2(x, xi);
+    wave_sync();
+    const uint2 got = XY[swA ? 192 + rankA : (swB ? rankB : 128 + lane)];
+    asm volatile("" ::"v"(got.x), "v"(got.y));
+    const bool sw = swA || swB;
+    x = sw ? got.x : x;
+    xi = sw ? got.y : xi;
     wave_sync();
   }
   return cut;
@@ -298,6 +336,8 @@ __device__ int wave_torch_topk_reg(TopkLds& s, const float* p, int n, int k, int
   bool deep = false;
   while (hi - lo > 3) {
     if (depth == 0) { deep = true; break; }
+    // once the range sits in one register it stays there: the rounds below work on that register
+    if ((lo >> 6) == ((hi - 1) >> 6)) break;
     --depth;
     const int mid = lo + (hi - lo) / 2;
     // move_median_to_first(lo, lo+1, mid, hi-1) with comp = greater
@@ -323,6 +363,43 @@ __device__ int wave_torch_topk_reg(TopkLds& s, const float* p, int n, int k, int
     const int cut = reg_partition(s, v, id, lo + 1, hi, vpk, lane);
     if (cut <= nth) lo = cut;
     else hi = cut;
+  }
+  if (!deep && hi - lo > 3) {
+    const int j0 = lo >> 6, base = 64 * j0;
+    uint32_t x = j0 == 0 ? v[0] : (j0 == 1 ? v[1] : (j0 == 2 ? v[2] : v[3]));
+    uint32_t xi = j0 == 0 ? id[0] : (j0 == 1 ? id[1] : (j0 == 2 ? id[2] : id[3]));
+    while (hi - lo > 3) {
+      if (depth == 0) { deep = true; break; }
+      --depth;
+      const int mid = lo + (hi - lo) / 2;
+      const int a = lo + 1, b = mid, c = hi - 1;
+      const uint32_t va = (uint32_t)__builtin_amdgcn_readlane((int)x, a - base);
+      const uint32_t vb = (uint32_t)__builtin_amdgcn_readlane((int)x, b - base);
+      const uint32_t vc = (uint32_t)__builtin_amdgcn_readlane((int)x, c - base);
+      int pick;
+      if (va > vb) {
+        if (vb > vc) pick = b;
+        else if (va > vc) pick = c;
+        else pick = a;
+      } else if (va > vc) pick = a;
+      else if (vb > vc) pick = c;
+      else pick = b;
+      const uint32_t vlo = (uint32_t)__builtin_amdgcn_readlane((int)x, lo - base);
+      const uint32_t ilo = (uint32_t)__builtin_amdgcn_readlane((int)xi, lo - base);
+      const uint32_t vpk = (uint32_t)__builtin_amdgcn_readlane((int)x, pick - base);
+      const uint32_t ipk = (uint32_t)__builtin_amdgcn_readlane((int)xi, pick - base);
+      const bool at_lo = base + lane == lo, at_pk = base + lane == pick;
+      x = at_lo ? vpk : (at_pk ? vlo : x);
+      xi = at_lo ? ipk : (at_pk ? ilo : xi);
+      const int cut = reg_partition1(s, x, xi, lo + 1, hi, vpk, lane, base);
+      if (cut <= nth) lo = cut;
+      else hi = cut;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = j == j0 ? x : v[j];
+      id[j] = j == j0 ? xi : id[j];
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
