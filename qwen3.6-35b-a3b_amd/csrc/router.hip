@@ -723,12 +723,17 @@ __global__ __launch_bounds__(512) void k_router_chain(
   __syncthreads();
   // the fast path for the group's 16 tokens, two per wave; the tokens it cannot settle are listed
   // and replayed afterwards, one per wave, so that no wave runs two replays while others idle
-#pragma unroll 1
+  // both tokens' logits requested before either is used
+  uint32_t raw[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    route_logits_load<true>(logits + (size_t)min(t0 + 2 * wv + j, T - 1) * 256, 256, lane, raw[j]);
+#pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int t = t0 + 2 * wv + j;
     if (t >= T) break;
     float p[4];
-    route_softmax<true>(logits + (size_t)t * 256, 256, lane, p);
+    route_softmax_raw(raw[j], 256, lane, p);
     if (probs) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) probs[(size_t)t * 256 + 64 * q + lane] = p[q];

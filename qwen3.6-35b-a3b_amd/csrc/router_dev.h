@@ -497,16 +497,19 @@ __device__ __forceinline__ int wave_topk_fast(const float* p, int E, int K, int 
 // R2: softmax over E bf16 logits in f32 (max-subtracted, sum, multiply by the reciprocal — the
 // same form as torch's CPU kernel); lane holds positions lane + 64j. AGENT: the logits were
 // written by other workgroups of this launch through agent-scope stores, and are read likewise.
+// (route_logits_load and route_softmax_raw: the same in two halves, so that a wave can have
+// several tokens' loads in flight)
 template <bool AGENT = false>
-__device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lane, float* p) {
+__device__ __forceinline__ void route_logits_load(const uint16_t* lg, int E, int lane, uint32_t* raw) {
   // clamped loads, all four in flight at once (guarded loads would each wait for the last)
-  uint32_t raw[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint16_t* a = lg + min(64 * j + lane, E - 1);
     if constexpr (AGENT) raw[j] = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else raw[j] = *a;
   }
+}
+__device__ __forceinline__ void route_softmax_raw(const uint32_t* raw, int E, int lane, float* p) {
   float lv[4];
   float m = -INFINITY;
 #pragma unroll
@@ -525,6 +528,12 @@ __device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lan
   const float rs = 1.0f / sum;
 #pragma unroll
   for (int j = 0; j < 4; ++j) p[j] *= rs;
+}
+template <bool AGENT = false>
+__device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lane, float* p) {
+  uint32_t raw[4];
+  route_logits_load<AGENT>(lg, E, lane, raw);
+  route_softmax_raw(raw, E, lane, p);
 }
 
 // R3-R5 by the exact replay of torch's CPU topk (for ties that the fast paths cannot settle),

@@ -6,13 +6,22 @@
 // phases below. Otherwise two launches: per-chunk histograms, then per chunk one block that sums
 // the histograms itself (totals, scan, its own chunk's start positions) and scatters its chunk
 // stably, where ranks inside a 256-pair round come from wave-level id matching (8 ballots on the
-// id bits) and a per-wave count table, so no atomics decide any position.
+// id bits) and a per-wave count table, so no atomics decide any position. Chunks are 1024 pairs
+// (four rounds per block; measured faster at 32K pairs than 256-pair chunks, whose blocks each read
+// four times the counts) up to 128 chunks, longer above, so each block reads at most 128 counts
+// per expert.
 #include "common.h"
 #include "moe_internal.h"
 
 namespace moe {
 
-constexpr int kChunk = 1024;   // pairs per scatter block
+constexpr int kOneMax = 1024;   // pairs the one-block sort takes
+constexpr int kMaxChunks = 128;
+// pairs per chunk: a multiple of 256, at most kMaxChunks chunks
+__host__ __device__ inline int sort_chunk(int P) {
+  const int per = (P + kMaxChunks - 1) / kMaxChunks;
+  return per <= 1024 ? 1024 : (per + 255) / 256 * 256;
+}
 
 __global__ __launch_bounds__(64) void k_sort_small(const int32_t* __restrict__ ids, int P, int E,
                                                    int32_t* __restrict__ offsets,
@@ -65,12 +74,12 @@ __host__ __device__ inline int hist_stride(int nchunks) { return (nchunks + 3) &
 
 // phase 1: histogram of each chunk -> hist[e][chunk] (an expert's counts contiguous)
 __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ ids, int P, int E,
-                                                   int32_t* __restrict__ hist, int hs) {
+                                                   int32_t* __restrict__ hist, int hs, int chunk) {
   __shared__ int h[256];
   for (int i = threadIdx.x; i < E; i += 256) h[i] = 0;
   __syncthreads();
-  const int base = blockIdx.x * kChunk;
-  for (int i = threadIdx.x; i < kChunk; i += 256) {
+  const int base = blockIdx.x * chunk;
+  for (int i = threadIdx.x; i < chunk; i += 256) {
     const int p = base + i;
     if (p < P) {
       const int e = ids[p];
@@ -85,32 +94,38 @@ __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ i
       for (int c = gridDim.x; c < hs; ++c) hist[(size_t)i * hs + c] = 0;
 }
 
-// block-wide exclusive scan of one int per thread (256 threads)
+// block-wide exclusive scan of one int per thread (256 threads): wave scans by lane shuffles, then
+// the four wave totals through LDS (two barriers); tmp holds at least 4 ints
 __device__ int block_exclusive_scan(int v, int* tmp, int* total) {
-  const int tid = threadIdx.x;
-  tmp[tid] = v;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    int add = tid >= o ? tmp[tid - o] : 0;
-    __syncthreads();
-    tmp[tid] += add;
-    __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += n;
   }
-  const int incl = tmp[tid];
-  *total = tmp[255];
+  if (lane == 63) tmp[wave] = incl;
   __syncthreads();
-  return incl - v;
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    base += w < wave ? tmp[w] : 0;
+    tot += tmp[w];
+  }
+  *total = tot;
+  __syncthreads();
+  return base + incl - v;
 }
 
-// Stable scatter of the pairs [base, base + kChunk) given the start position of the chunk's pairs
+// Stable scatter of the pairs [base, base + len) given the start position of the chunk's pairs
 // of every expert (start_row[e]): ranks inside a 256-pair round come from wave-level id matching
 // and per-wave counts, run[e] carries them across rounds. run (LDS, 256 ints) must be zero.
-__device__ void scatter_chunk(const int32_t* __restrict__ ids, int P, int E, int base,
+__device__ void scatter_chunk(const int32_t* __restrict__ ids, int P, int E, int base, int len,
                               const int32_t* start_row, int32_t* __restrict__ sorted_pairs,
                               int32_t* __restrict__ pair_pos, int* run, int (*wcnt)[256]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  for (int r = 0; r < kChunk; r += 256) {
+  for (int r = 0; r < len; r += 256) {
     for (int i = tid; i < 4 * 256; i += 256) (&wcnt[0][0])[i] = 0;
     __syncthreads();
     const int p = base + r + tid;
@@ -212,7 +227,7 @@ __global__ __launch_bounds__(256) void k_sort_scan_scatter(const int32_t* __rest
                                                            int32_t* __restrict__ sorted_pairs,
                                                            int32_t* __restrict__ pair_pos,
                                                            int32_t* __restrict__ hit_list,
-                                                           int32_t* __restrict__ tiles, int bm) {
+                                                           int32_t* __restrict__ tiles, int bm, int chunk) {
   __shared__ int start[256], tmp[256], run[256];
   __shared__ int wcnt[4][256];
   __shared__ uint64_t tmp64[4];
@@ -244,10 +259,10 @@ __global__ __launch_bounds__(256) void k_sort_scan_scatter(const int32_t* __rest
     if (tiles) build_tiles_block(e < E ? tot : 0, base, e, bm, tiles, tmp64);
   }
   __syncthreads();
-  scatter_chunk(ids, P, E, c0 * kChunk, start, sorted_pairs, pair_pos, run, wcnt);
+  scatter_chunk(ids, P, E, c0 * chunk, chunk, start, sorted_pairs, pair_pos, run, wcnt);
 }
 
-// 64 < P <= kChunk: the three phases in one block (histogram, scan, the one chunk's scatter), so
+// 64 < P <= kOneMax: the three phases in one block (histogram, scan, the one chunk's scatter), so
 // a small batch pays one launch instead of three; same positions as the three-kernel form. With
 // tiles != NULL the block also writes the MFMA tile list (build_tiles_block).
 __global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ ids, int P, int E,
@@ -280,7 +295,7 @@ __global__ __launch_bounds__(256) void k_sort_one(const int32_t* __restrict__ id
   if (e == 0) hit_list[0] = hsum;
   if (tiles) build_tiles_block(tot, base, e, bm, tiles, tmp64);
   __syncthreads();
-  scatter_chunk(ids, P, E, 0, start, sorted_pairs, pair_pos, run, wcnt);
+  scatter_chunk(ids, P, E, 0, P, start, sorted_pairs, pair_pos, run, wcnt);
 }
 
 // the tile list of build_tiles_block from the expert offsets (E <= 256), one scan
@@ -333,7 +348,7 @@ __global__ __launch_bounds__(256) void k_build_tiles(const int32_t* __restrict__
 using namespace moe;
 
 size_t moe_sort_ws_bytes(int P, int E) {
-  const size_t nchunks = (size_t)(P + kChunk - 1) / kChunk;
+  const size_t nchunks = (size_t)(P + sort_chunk(P) - 1) / sort_chunk(P);
   return ((size_t)hist_stride((int)nchunks) * E * sizeof(int32_t) + 255) & ~size_t(255);
 }
 
@@ -345,15 +360,16 @@ int moe_launch_sort(const int32_t* ids, int P, int E, int32_t* offsets, int32_t*
   if (P <= 64) {
     hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(64), 0, st, ids, P, E, offsets, sorted_pairs,
                        pair_pos, hit_list);
-  } else if (P <= kChunk) {
+  } else if (P <= kOneMax) {
     hipLaunchKernelGGL(k_sort_one, dim3(1), dim3(256), 0, st, ids, P, E, offsets, sorted_pairs,
                        pair_pos, hit_list, fuse_tiles ? tiles : nullptr, bm);
   } else {
-    const int nchunks = (P + kChunk - 1) / kChunk, hs = hist_stride(nchunks);
+    const int chunk = sort_chunk(P);
+    const int nchunks = (P + chunk - 1) / chunk, hs = hist_stride(nchunks);
     int32_t* hist = reinterpret_cast<int32_t*>(ws);
-    hipLaunchKernelGGL(k_sort_hist, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, hs);
+    hipLaunchKernelGGL(k_sort_hist, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, hs, chunk);
     hipLaunchKernelGGL(k_sort_scan_scatter, dim3(nchunks), dim3(256), 0, st, ids, P, E, hist, hs,
-                       offsets, sorted_pairs, pair_pos, hit_list, fuse_tiles ? tiles : nullptr, bm);
+                       offsets, sorted_pairs, pair_pos, hit_list, fuse_tiles ? tiles : nullptr, bm, chunk);
   }
   if (tiles && !fuse_tiles) return moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, bm);
   return moe_check_launch("sort");

@@ -14,8 +14,11 @@ def _ids(T, K, E, seed, zipf):
     return torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32)
 
 
+# chunks of 1024 pairs up to 128 chunks (129, 300, 4096, 4097, 16384 tokens: partial last chunks
+# at 129, 300, 4097), longer above (20000 tokens: 1280-pair chunks)
 @pytest.mark.parametrize("T,zipf", [(1, False), (8, False), (9, True), (64, True), (128, True),
-                                    (129, False), (300, False), (4096, False), (16384, True)])
+                                    (129, False), (300, False), (4096, False), (4097, True),
+                                    (16384, True), (20000, False)])
 def test_sort_permute_matches_stable_argsort(pkg, dev, T, zipf):
     K, E = 8, 256
     ids = _ids(T, K, E, seed=T, zipf=zipf)
