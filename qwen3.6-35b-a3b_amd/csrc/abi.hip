@@ -247,7 +247,8 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                         const void* dn, int dn_fmt, const int32_t* offsets,
                         const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
                         int E, int K, int path, void* y, MoeWs& w, hipStream_t st,
-                        int32_t* tiles_pre = nullptr, int y16 = 0) {
+                        int32_t* tiles_pre = nullptr, int y16 = 0, const MoeShJob* shg = nullptr,
+                        const MoeShJob* shd = nullptr) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
   if (y16 && !y16_rows(path, T, H, I, K, gu_fmt, dn_fmt))
@@ -300,8 +301,8 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
     }
     if (small) {
       MOE_TRY(moe_launch_gemm6_gateup(x16, gate, up, estride, tiles, max_tiles, offsets, sorted_pairs,
-                                      K, H, I, S, st));
-      return moe_launch_gemm6_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st);
+                                      K, H, I, S, st, shg));
+      return moe_launch_gemm6_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st, shd);
     }
     // gemm4's persistent item stream needs two super-blocks per item (H, I >= 512)
     if (gu_fmt == MOE_FMT_Q4_K && H >= 512)
@@ -612,15 +613,43 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   // with bf16 rows and the shared expert forked, the shared GEMMs read the rows as they are and
   // the conversion runs on the shared expert's stream after them (off the router's path)
   const bool fork = T >= kForkMinT && allow_fork;
+  // Few rows per expert (the 32-row routed kernels) with the narrow-slab shared expert: no second
+  // stream. The single-launch router also writes the f16 copy of x, and the shared expert's blocks
+  // run inside the routed gate/up and down launches, whose grids leave CUs idle at this size; the
+  // fork and join cost more than the shared expert's time left after that overlap.
+  const bool fuse = rpath == MOE_PATH_MFMA && Wt.shared_fmt == MOE_FMT_BF16 && H % 2048 == 0 &&
+                    I_s % 256 == 0 && mfma_small(rpath, T, H, I, gate_up_fmt, down_fmt) &&
+                    shared_skinny(path, Wt.shared_fmt, T, H, I_s) && moe_router_chain_supported(T, H, E, K);
   uint16_t* x16 = nullptr;
   bool x16_late = false;
   if (rpath == MOE_PATH_MFMA) {
     x16 = reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
     if (!x16) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
     // made on the shared expert's stream: beside (or after) its GEMMs, off the router's path
-    x16_late = fork && Wt.shared_fmt == MOE_FMT_BF16 &&
+    x16_late = !fuse && fork && Wt.shared_fmt == MOE_FMT_BF16 &&
                (x_dtype == MOE_DT_BF16 || shared_skinny(path, Wt.shared_fmt, T, H, I_s));
-    if (!x16_late) MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
+    if (!x16_late && !fuse) MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, x16, st));
+  }
+  if (fuse) {
+    uint16_t* ssh = reinterpret_cast<uint16_t*>(w.take((size_t)T * I_s * 2));
+    MoeWs wr = w;   // the router's scratch is dead before the experts take theirs (same stream)
+    const size_t rsb = moe_router_scratch_bytes(T, H, E);
+    void* rscr = wr.take(rsb);
+    if (!ssh || !rscr) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
+    MOE_TRY(moe_launch_router_chain(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits,
+                                    nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st, x16));
+    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
+    MoeShJob g, d;
+    g.n = moe_shjob_gateup_blocks(T, I_s);
+    g.a16 = x16; g.x = x; g.x_dtype = x_dtype; g.wsg = ws_scalar_gate; g.gdt = Wt.scalar_gate_dtype;
+    g.gate_prob = gp; g.w0 = reinterpret_cast<const uint16_t*>(ws_gate);
+    g.w1 = reinterpret_cast<const uint16_t*>(ws_up); g.S = ssh; g.T = T; g.H = H; g.Is = I_s;
+    d.n = moe_shjob_down_blocks(T, H);
+    d.w0 = reinterpret_cast<const uint16_t*>(ws_down); d.S = ssh; d.y = sraw; d.T = T; d.H = H; d.Is = I_s;
+    MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
+                         sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16, &g, &d));
+    return moe_launch_combine(y, y16, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
+                              shared_out, expert_raw, st);
   }
   if (!fork) {
     MOE_TRY(moe_launch_router_logits(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits, nullptr, 0, st));

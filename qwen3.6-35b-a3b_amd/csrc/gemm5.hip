@@ -22,7 +22,7 @@
 #include "common.h"
 #include "moe_internal.h"
 #include "lds_dma.h"
-#include "gemv_dev.h"
+#include "shared_small.h"
 
 namespace moe {
 
@@ -53,26 +53,8 @@ static_assert(sizeof(Smem) <= 160 * 1024, "one block per CU");
 
 __device__ __forceinline__ int swz(int m) { return (m ^ (m >> 1)) & 7; }
 
-template <bool BF>
-__device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
-  if constexpr (BF)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
-// 8 bf16 (16 bytes, element order kept) -> 8 f16, round to nearest even
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t d) {
-  const _Float16 lo = (_Float16)__uint_as_float(d << 16);
-  const _Float16 hi = (_Float16)__uint_as_float(d & 0xFFFF0000u);
-  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-}
-__device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w) {
-  return make_uint4(bf16x2_to_f16x2(w.x), bf16x2_to_f16x2(w.y), bf16x2_to_f16x2(w.z),
-                    bf16x2_to_f16x2(w.w));
-}
+using shs::bf16x8_to_f16;
+using shs::mfma;
 
 // One item: rows [m0, m0 + rows) of A (row length K elements, 2 bytes each) against the 256
 // weight rows n (n < 128: base g, else base u, each + (n & 127) * K * 2). Lane l of wave w: token
@@ -246,127 +228,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 // ------------------------------------------------------------ small-T shared expert --
 // Below a few hundred tokens the 128 x 256 items above leave most CUs idle (T = 64: 4 blocks of
-// gate/up, each streaming 1 MB of weights on its own). These kernels cut the weights into narrow
-// slabs instead: one block per (64-row token tile, slab), gate/up slab = 16 gate + the matching 16
-// up rows (one 32-column MFMA group), down slab = 32 rows of w_down, and the 8 waves of a block
-// split K in eighths (contiguous ranges), each wave holding the tile's two 32-row groups for its
-// range in registers (no LDS staging: every operand is used once per block). The eight f32
-// partial tiles meet in LDS and are summed in wave order, then the epilogue runs as in the
-// kernels above (gate/up: SiLU(gate) * up to f16; down: f32 rows).
-// The gate/up launch also computes the scalar gate (one wave per token, k_shared_gate's
-// arithmetic) and, when asked, the routed GEMMs' f16 copy of x (k_to_f16's conversion), so the
-// small-T shared expert is two launches.
-namespace g5s {
-
-constexpr int kWaves = 8;
-constexpr int kBM = 64;                 // token rows per tile
-constexpr int kCK = 64;                 // K per register chunk (4 MFMA substeps)
-constexpr int kF16 = 2;                 // activation type of f16 rows (beside MOE_DT_F32 / _BF16)
-
-__device__ __forceinline__ uint32_t f16x2_sat(float u, float v) {
-  u = fminf(fmaxf(u, -65504.0f), 65504.0f);
-  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
-  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)u) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v) << 16);
-}
-
-// 8 activations of one row: f32 (32 bytes, converted to f16 at use), bf16 or f16 (16 bytes)
-template <int AT>
-struct ARaw {
-  uint4 v[AT == MOE_DT_F32 ? 2 : 1];
-};
-template <int AT>
-__device__ __forceinline__ void ld_a(ARaw<AT>& r, const uint8_t* p) {
-  r.v[0] = *reinterpret_cast<const uint4*>(p);
-  if constexpr (AT == MOE_DT_F32) r.v[1] = *reinterpret_cast<const uint4*>(p + 16);
-}
-template <int AT>
-__device__ __forceinline__ uint4 a_frag(const ARaw<AT>& r) {
-  if constexpr (AT == MOE_DT_F32)
-    return make_uint4(f16x2_sat(__uint_as_float(r.v[0].x), __uint_as_float(r.v[0].y)),
-                      f16x2_sat(__uint_as_float(r.v[0].z), __uint_as_float(r.v[0].w)),
-                      f16x2_sat(__uint_as_float(r.v[1].x), __uint_as_float(r.v[1].y)),
-                      f16x2_sat(__uint_as_float(r.v[1].z), __uint_as_float(r.v[1].w)));
-  else
-    return r.v[0];
-}
-
-// This wave's K range [k0, k0 + kw) of the tile: rows ar0 (group 0) and ar1 (group 1, TWO) at
-// element k0 + 8 h, weight row br at the same element; AT's element size es. BF16 activations run
-// the bf16 MFMA on the weights as they are, the others the f16 MFMA on converted weights.
-template <int AT, bool TWO>
-__device__ __forceinline__ void wave_k(const uint8_t* ar0, const uint8_t* ar1, const uint8_t* br,
-                                       int nch, f32x16_t& acc0, f32x16_t& acc1) {
-  constexpr int es = AT == MOE_DT_F32 ? 4 : 2;
-  constexpr bool BF = AT == MOE_DT_BF16;
-  ARaw<AT> a0[4], a1[4];
-  uint4 b[4];
-  auto load = [&](int c, ARaw<AT>(&x0)[4], ARaw<AT>(&x1)[4], uint4(&y)[4]) {
-#pragma unroll
-    for (int ss = 0; ss < 4; ++ss) {
-      const size_t k = (size_t)(c * kCK + 16 * ss);
-      y[ss] = *reinterpret_cast<const uint4*>(br + k * 2);
-      ld_a<AT>(x0[ss], ar0 + k * es);
-      if constexpr (TWO) ld_a<AT>(x1[ss], ar1 + k * es);
-    }
-  };
-  load(0, a0, a1, b);
-  for (int c = 0; c < nch; ++c) {
-    ARaw<AT> n0[4], n1[4];
-    uint4 nb[4];
-    if (c + 1 < nch) load(c + 1, n0, n1, nb);
-#pragma unroll
-    for (int ss = 0; ss < 4; ++ss) {
-      const uint4 w = BF ? b[ss] : g5::bf16x8_to_f16(b[ss]);
-      acc0 = g5::mfma<BF>(a_frag<AT>(a0[ss]), w, acc0);
-      if constexpr (TWO) acc1 = g5::mfma<BF>(a_frag<AT>(a1[ss]), w, acc1);
-    }
-    if (c + 1 < nch) {
-#pragma unroll
-      for (int ss = 0; ss < 4; ++ss) {
-        a0[ss] = n0[ss];
-        if constexpr (TWO) a1[ss] = n1[ss];
-        b[ss] = nb[ss];
-      }
-    }
-  }
-}
-
-// The block's partial tiles: wave w's element i of group mg at red[((2 w + mg) 16 + i) 64 + lane]
-// (element i of lane l: row 8 (i / 4) + 4 (l / 32) + i % 4 of the group, column l % 32).
-template <int AT>
-__device__ __forceinline__ void tile_k(const void* a, int T, int K, int m0, const uint16_t* brow,
-                                       float* red) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = lane >> 5, r = lane & 31;
-  constexpr int es = AT == MOE_DT_F32 ? 4 : 2;
-  const int kw = K / kWaves, k0 = wave * kw + 8 * h;
-  const uint8_t* ab = reinterpret_cast<const uint8_t*>(a);
-  const uint8_t* ar0 = ab + ((size_t)min(m0 + r, T - 1) * K + k0) * es;
-  const uint8_t* ar1 = ab + ((size_t)min(m0 + 32 + r, T - 1) * K + k0) * es;
-  const uint8_t* br = reinterpret_cast<const uint8_t*>(brow + k0);
-  f32x16_t acc0 = {}, acc1 = {};
-  if (T - m0 > 32) wave_k<AT, true>(ar0, ar1, br, kw / kCK, acc0, acc1);
-  else wave_k<AT, false>(ar0, ar1, br, kw / kCK, acc0, acc1);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    red[((2 * wave) * 16 + i) * 64 + lane] = acc0[i];
-    red[((2 * wave + 1) * 16 + i) * 64 + lane] = acc1[i];
-  }
-  __syncthreads();
-}
-// sum over the waves (in wave order) of tile element (row rr, column c)
-__device__ __forceinline__ float red_sum(const float* red, int rr, int c) {
-  const int mg = rr >> 5, q = rr & 31;
-  const int idx = (mg * 16 + 4 * (q >> 3) + (q & 3)) * 64 + 32 * ((q >> 2) & 1) + c;
-  float s = red[idx];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) s += red[idx + w * 2 * 16 * 64];
-  return s;
-}
-
-}  // namespace g5s
+// gate/up, each streaming 1 MB of weights on its own). These launches run shared_small.h's narrow
+// slab blocks with 8 waves each. The gate/up launch also computes the scalar gate (one wave per
+// token, k_shared_gate's arithmetic) and, when asked, the routed GEMMs' f16 copy of x (k_to_f16's
+// conversion), so the small-T shared expert is two launches.
 
 // grid (Is / 16, ceil(T / 64)): S [T, Is] f16 = SiLU(x wg^T) * (x wu^T) from x (f32 or bf16);
 // gate_prob [T] = sigmoid(x . wsg) (NULL: skipped); x16 [T, H] = f16(x) (NULL: skipped)
@@ -375,8 +240,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const void* __restrict__ x, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
     const void* __restrict__ wsg, int gdt, int T, int H, int Is, uint16_t* __restrict__ S,
     float* __restrict__ gate_prob, uint16_t* __restrict__ x16) {
-  using namespace g5s;
-  __shared__ float red[kWaves * 2 * 16 * 64];
+  __shared__ float red[shs::red_floats<8>()];
   const int nblk = gridDim.x * gridDim.y;
   const int bid = blockIdx.y * gridDim.x + blockIdx.x;
   if (x16) {
@@ -386,69 +250,29 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       uint4 o;
       if constexpr (XDT == MOE_DT_BF16) {
         const uint4 v = reinterpret_cast<const uint4*>(x)[i];
-        o = make_uint4(f16x2_sat(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16)),
-                       f16x2_sat(bf16_to_f32(v.y & 0xFFFFu), bf16_to_f32(v.y >> 16)),
-                       f16x2_sat(bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16)),
-                       f16x2_sat(bf16_to_f32(v.w & 0xFFFFu), bf16_to_f32(v.w >> 16)));
+        o = make_uint4(shs::f16x2_sat(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16)),
+                       shs::f16x2_sat(bf16_to_f32(v.y & 0xFFFFu), bf16_to_f32(v.y >> 16)),
+                       shs::f16x2_sat(bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16)),
+                       shs::f16x2_sat(bf16_to_f32(v.w & 0xFFFFu), bf16_to_f32(v.w >> 16)));
       } else {
         const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
         const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
-        o = make_uint4(f16x2_sat(a.x, a.y), f16x2_sat(a.z, a.w), f16x2_sat(b.x, b.y), f16x2_sat(b.z, b.w));
+        o = make_uint4(shs::f16x2_sat(a.x, a.y), shs::f16x2_sat(a.z, a.w), shs::f16x2_sat(b.x, b.y),
+                       shs::f16x2_sat(b.z, b.w));
       }
       reinterpret_cast<uint4*>(x16)[i] = o;
     }
   }
-  const int slab = blockIdx.x, m0 = blockIdx.y * kBM;
-  const int r = threadIdx.x & 31;
-  const uint16_t* brow = (r < 16 ? wg : wu) + (size_t)(16 * slab + (r & 15)) * H;
-  tile_k<XDT>(x, T, H, m0, brow, red);
-  {
-    // thread t: tile row t / 8, S columns 16 slab + 2 (t % 8) + 0..1 (gate at tile column c, up
-    // at c + 16)
-    const int rr = threadIdx.x >> 3, c = 2 * (threadIdx.x & 7);
-    if (m0 + rr < T) {
-      float v[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const float gv = red_sum(red, rr, c + j), uv = red_sum(red, rr, c + j + 16);
-        v[j] = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv;
-      }
-      *reinterpret_cast<uint32_t*>(S + (size_t)(m0 + rr) * Is + 16 * slab + c) = f16x2_sat(v[0], v[1]);
-    }
-  }
-  if (gate_prob) {
-    const int lane = threadIdx.x & 63;
-    for (int t = bid * kWaves + (int)(threadIdx.x >> 6); t < T; t += nblk * kWaves) {
-      float a = 0.0f;
-      for (int c = 0; c < H / 512; ++c) {
-        float xv[8];
-        load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
-        a += dot8_w(wsg, (size_t)512 * c + 8 * lane, gdt, xv);
-      }
-      a = wave_sum_f32(a);
-      if (lane == 0) gate_prob[t] = 1.0f / (1.0f + expf(-a));
-    }
-  }
+  shs::gateup_tile<XDT, 8>(x, wg, wu, T, H, Is, blockIdx.x, blockIdx.y * shs::kBM, S, red);
+  if (gate_prob) shs::gate_rows<XDT>(x, wsg, gdt, T, H, gate_prob, bid * 8 + (int)(threadIdx.x >> 6), nblk * 8);
 }
 
 // grid (H / 32, ceil(T / 64)): y [T, H] f32 = S [T, Is] f16 . w_down^T (w_down [H, Is] bf16)
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm5s_down(
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ wd, int T, int H, int Is,
     float* __restrict__ y) {
-  using namespace g5s;
-  __shared__ float red[kWaves * 2 * 16 * 64];
-  const int slab = blockIdx.x, m0 = blockIdx.y * kBM;
-  tile_k<kF16>(S, T, Is, m0, wd + (size_t)(32 * slab + (threadIdx.x & 31)) * Is, red);
-  // thread t: tile row t / 8, columns 32 slab + 4 (t % 8) + 0..3
-  const int rr = threadIdx.x >> 3, c = 4 * (threadIdx.x & 7);
-  if (m0 + rr < T) {
-    float4 o;
-    o.x = red_sum(red, rr, c);
-    o.y = red_sum(red, rr, c + 1);
-    o.z = red_sum(red, rr, c + 2);
-    o.w = red_sum(red, rr, c + 3);
-    *reinterpret_cast<float4*>(y + (size_t)(m0 + rr) * H + 32 * slab + c) = o;
-  }
+  __shared__ float red[shs::red_floats<8>()];
+  shs::down_tile<8>(S, wd, T, H, Is, blockIdx.x, blockIdx.y * shs::kBM, y, red);
 }
 
 }  // namespace moe
@@ -465,7 +289,7 @@ int moe_launch_gemm5s_gateup(const void* x, int x_dtype, const void* w_gate, con
                              float* gate_prob, uint16_t* x16, hipStream_t st) {
   if (!moe_gemm5s_supports(H, Is))
     return moe_set_error(MOE_E_UNSUPPORTED, "small-T shared gate_up needs H %% 512 == 0, I_s %% 512 == 0");
-  const dim3 grid(Is / 16, (T + g5s::kBM - 1) / g5s::kBM);
+  const dim3 grid(Is / 16, (T + shs::kBM - 1) / shs::kBM);
   const uint16_t* g = reinterpret_cast<const uint16_t*>(w_gate);
   const uint16_t* u = reinterpret_cast<const uint16_t*>(w_up);
   if (x_dtype == MOE_DT_BF16)
@@ -481,7 +305,7 @@ int moe_launch_gemm5s_down(const uint16_t* S, const void* w_down, int T, int H, 
                            hipStream_t st) {
   if (!moe_gemm5s_supports(H, Is))
     return moe_set_error(MOE_E_UNSUPPORTED, "small-T shared down needs H %% 512 == 0, I_s %% 512 == 0");
-  const dim3 grid(H / 32, (T + g5s::kBM - 1) / g5s::kBM);
+  const dim3 grid(H / 32, (T + shs::kBM - 1) / shs::kBM);
   hipLaunchKernelGGL(k_gemm5s_down, grid, dim3(512), 0, st, S, reinterpret_cast<const uint16_t*>(w_down), T,
                      H, Is, y);
   return moe_check_launch("gemm5s_down");

@@ -23,6 +23,7 @@
 #include "moe_internal.h"
 #include "lds_dma.h"
 #include "q4k_mfma.h"
+#include "shared_small.h"
 
 namespace moe {
 namespace g6 {
@@ -160,13 +161,26 @@ __device__ __forceinline__ void geo_lds(Geo& g, Smem& sm, int wave) {
 
 }  // namespace g6
 
-// S [P, I] f16 (sorted order) = SiLU(x16[token] . gate^T) * (x16[token] . up^T) per tile row
+// S [P, I] f16 (sorted order) = SiLU(x16[token] . gate^T) * (x16[token] . up^T) per tile row; the
+// last sh.n blocks run the small-T shared expert's gate/up (and scalar gate, x of dtype GX)
+template <int GX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm6_gateup(
     const uint16_t* __restrict__ x16, const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
     size_t estride, const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ sorted_pairs, int K, int H, int I, uint16_t* __restrict__ S) {
+    const int32_t* __restrict__ sorted_pairs, int K, int H, int I, uint16_t* __restrict__ S,
+    MoeShJob sh) {
   using namespace g6;
   __shared__ __attribute__((aligned(16))) Smem sm;
+  const int nr = (int)gridDim.x - sh.n;
+  if ((int)blockIdx.x >= nr) {
+    const int b = (int)blockIdx.x - nr, nslab = sh.Is / 16;
+    float* red = reinterpret_cast<float*>(&sm);
+    shs::gateup_tile<shs::kF16, 4, 32>(sh.a16, sh.w0, sh.w1, sh.T, sh.H, sh.Is, b % nslab,
+                                       (b / nslab) * 32, sh.S, red);
+    shs::gate_rows<GX>(sh.x, sh.wsg, sh.gdt, sh.T, sh.H, sh.gate_prob, b * 4 + (int)(threadIdx.x >> 6),
+                       sh.n * 4);
+    return;
+  }
   Item it;
   if (!get_item(tiles, offsets, I / 128, it)) return;
   const int t = threadIdx.x, lane = t & 63;
@@ -216,9 +230,17 @@ template <bool Y16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm6_down(
     const uint16_t* __restrict__ S, const uint8_t* __restrict__ wd, size_t estride,
     const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets, int H, int I,
-    void* __restrict__ y) {
+    void* __restrict__ y, MoeShJob sh) {
   using namespace g6;
   __shared__ __attribute__((aligned(16))) Smem sm;
+  const int nr = (int)gridDim.x - sh.n;
+  if ((int)blockIdx.x >= nr) {
+    // the small-T shared expert's down: y = shared_raw
+    const int b = (int)blockIdx.x - nr, nslab = sh.H / 32;
+    shs::down_tile<4, 32>(sh.S, sh.w0, sh.T, sh.H, sh.Is, b % nslab, (b / nslab) * 32, sh.y,
+                          reinterpret_cast<float*>(&sm));
+    return;
+  }
   Item it;
   if (!get_item(tiles, offsets, H / kBN, it)) return;
   const int t = threadIdx.x, lane = t & 63;
@@ -278,27 +300,50 @@ static dim3 g6_grid(int max_tiles, int ncol) {
   return dim3((unsigned)((max_tiles + g6::kXcd - 1) / g6::kXcd * ncol * g6::kXcd));
 }
 
+// the shared-expert blocks need H % 2048 == 0 (K split over 4 waves in 64-wide chunks, the
+// scalar gate's 512-wide passes) and I_s % 256 == 0
+static int check_shjob(const MoeShJob* sh, bool down) {
+  if (!sh || sh->n == 0) return MOE_OK;
+  if (sh->H % 2048 || sh->Is % 256 || !sh->S || (down ? (!sh->w0 || !sh->y) : (!sh->a16 || !sh->w0 || !sh->w1 || !sh->x || !sh->wsg || !sh->gate_prob)))
+    return moe_set_error(MOE_E_UNSUPPORTED, "gemm6: shared-expert blocks need H %% 2048 == 0, I_s %% 256 == 0 and every pointer");
+  const int want = down ? moe_shjob_down_blocks(sh->T, sh->H) : moe_shjob_gateup_blocks(sh->T, sh->Is);
+  if (sh->n != want) return moe_set_error(MOE_E_ARG, "gemm6: %d shared-expert blocks given, %d needed", sh->n, want);
+  return MOE_OK;
+}
+
 int moe_launch_gemm6_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
                             size_t expert_stride, const int32_t* tiles, int max_tiles,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
-                            int I, uint16_t* S, hipStream_t st) {
+                            int I, uint16_t* S, hipStream_t st, const MoeShJob* sh) {
   if (H % 256 || I % 128)
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm6 gate_up needs H %% 256 == 0, I %% 128 == 0");
-  hipLaunchKernelGGL(k_gemm6_gateup, g6_grid(max_tiles, I / 128), dim3(256), 0, st, x16,
-                     reinterpret_cast<const uint8_t*>(w_gate), reinterpret_cast<const uint8_t*>(w_up),
-                     expert_stride, tiles, offsets, sorted_pairs, K, H, I, S);
+  { const int rc_ = check_shjob(sh, false); if (rc_ != MOE_OK) return rc_; }
+  const MoeShJob job = sh ? *sh : MoeShJob{};
+  dim3 grid = g6_grid(max_tiles, I / 128);
+  grid.x += (unsigned)job.n;
+  const uint8_t* g = reinterpret_cast<const uint8_t*>(w_gate);
+  const uint8_t* u = reinterpret_cast<const uint8_t*>(w_up);
+  if (job.n && job.x_dtype == MOE_DT_BF16)
+    hipLaunchKernelGGL(k_gemm6_gateup<MOE_DT_BF16>, grid, dim3(256), 0, st, x16, g, u, expert_stride, tiles,
+                       offsets, sorted_pairs, K, H, I, S, job);
+  else
+    hipLaunchKernelGGL(k_gemm6_gateup<MOE_DT_F32>, grid, dim3(256), 0, st, x16, g, u, expert_stride, tiles,
+                       offsets, sorted_pairs, K, H, I, S, job);
   return moe_check_launch("gemm6_gateup");
 }
 
 int moe_launch_gemm6_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
-                          void* y, int y16, hipStream_t st) {
+                          void* y, int y16, hipStream_t st, const MoeShJob* sh) {
   if (I % 256 || H % 256) return moe_set_error(MOE_E_UNSUPPORTED, "gemm6 down needs H %% 256 == 0, I %% 256 == 0");
-  const dim3 grid = g6_grid(max_tiles, H / 256);
+  { const int rc_ = check_shjob(sh, true); if (rc_ != MOE_OK) return rc_; }
+  const MoeShJob job = sh ? *sh : MoeShJob{};
+  dim3 grid = g6_grid(max_tiles, H / 256);
+  grid.x += (unsigned)job.n;
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_down);
   if (y16)
-    hipLaunchKernelGGL(k_gemm6_down<true>, grid, dim3(256), 0, st, S, w, expert_stride, tiles, offsets, H, I, y);
+    hipLaunchKernelGGL(k_gemm6_down<true>, grid, dim3(256), 0, st, S, w, expert_stride, tiles, offsets, H, I, y, job);
   else
-    hipLaunchKernelGGL(k_gemm6_down<false>, grid, dim3(256), 0, st, S, w, expert_stride, tiles, offsets, H, I, y);
+    hipLaunchKernelGGL(k_gemm6_down<false>, grid, dim3(256), 0, st, S, w, expert_stride, tiles, offsets, H, I, y, job);
   return moe_check_launch("gemm6_down");
 }

@@ -20,6 +20,7 @@
 #include "common.h"
 #include "moe_internal.h"
 #include "router_dev.h"
+#include "shared_small.h"
 
 namespace moe {
 
@@ -636,7 +637,7 @@ __global__ __launch_bounds__(512) void k_router_chain(
     const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias, int T,
     int H, int E, uint16_t* __restrict__ logits, float* __restrict__ probs, int32_t* __restrict__ ids,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ heap_flag,
-    int exact_order, double* __restrict__ part, int* __restrict__ cnt) {
+    int exact_order, double* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ x16) {
   __shared__ double s_d[8][256];
   __shared__ double s_xsq[8][16], s_wsq[8][16];
   __shared__ double s_xt[16], s_wt[16];
@@ -650,6 +651,29 @@ __global__ __launch_bounds__(512) void k_router_chain(
   const int et = tile % nE, tg = tile / nE;
   const int t0 = tg * 16, e0 = et * 16;
   const int kw = H / (8 * kChainKS);
+  if (x16 && et == 0) {
+    // the f16 copy of x (k_to_f16's conversion): rows t0 .. t0 + 15, this block's K quarter
+    const int kq = H / kChainKS, upr = kq / 8;
+    for (int u = tid; u < 16 * upr; u += 512) {
+      const int t = t0 + u / upr;
+      if (t >= T) break;
+      const size_t i = (size_t)t * H + (size_t)ks * kq + (size_t)(u % upr) * 8;
+      uint4 o;
+      if constexpr (XDT == MOE_DT_BF16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xv) + i);
+        o = make_uint4(shs::f16x2_sat(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16)),
+                       shs::f16x2_sat(bf16_to_f32(v.y & 0xFFFFu), bf16_to_f32(v.y >> 16)),
+                       shs::f16x2_sat(bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16)),
+                       shs::f16x2_sat(bf16_to_f32(v.w & 0xFFFFu), bf16_to_f32(v.w >> 16)));
+      } else {
+        const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(xv) + i);
+        const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(xv) + i + 4);
+        o = make_uint4(shs::f16x2_sat(a.x, a.y), shs::f16x2_sat(a.z, a.w), shs::f16x2_sat(b.x, b.y),
+                       shs::f16x2_sat(b.z, b.w));
+      }
+      *reinterpret_cast<uint4*>(x16 + i) = o;
+    }
+  }
   tile_f64_partial<XDT, WDT>(xv, w, T, H, E, t0, e0, ks * (H / kChainKS) + wv * kw, kw, s_d, s_xsq, s_wsq);
   __syncthreads();
   double* my = part + ((size_t)tile * kChainKS + ks) * kChainPart;
@@ -799,7 +823,7 @@ size_t moe_router_scratch_bytes(int T, int H, int E) {
 int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
                             int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
                             float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
-                            void* scratch, int* sync, hipStream_t st) {
+                            void* scratch, int* sync, hipStream_t st, uint16_t* x16) {
   if (!moe_router_chain_supported(T, H, E, 8) || !scratch || !sync)
     return moe_set_error(MOE_E_UNSUPPORTED, "router_chain: needs 8 <= T <= 256, E = 256, K = 8, H %% 2048 == 0");
   const dim3 grid(((T + 15) / 16) * (E / 16) * kChainKS);
@@ -808,7 +832,7 @@ int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dty
   const int eo = exact_order ? 1 : 0;
 #define MOE_CHAIN(XD, WD)                                                                          \
   hipLaunchKernelGGL((k_router_chain<XD, WD>), grid, dim3(512), 0, st, x, w, bias, T, H, E, logits, \
-                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt)
+                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, x16)
   if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_F32);
   else if (x_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_BF16);
   else if (w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_BF16, MOE_DT_F32);
