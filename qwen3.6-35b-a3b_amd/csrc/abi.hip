@@ -413,9 +413,13 @@ static int shared_body(const void* x, int x_dtype, const uint16_t* x16, const vo
     made = x16_make != nullptr;
     return moe_launch_gemm5s_down(s, wd, T, H, Is, shared_raw, st);
   }
-  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
-  // bf16 shared weights on the MFMA path: the dense 128-row kernels, on bf16 rows as they are
-  if (path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && moe_gemm5_supports(H, Is)) {
+  // bf16 shared weights on the MFMA path: the dense 128-row kernels, on bf16 rows as they are;
+  // the gate kernel, which reads every row first, writes the f16 rows the caller asked for
+  const bool dense = path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && moe_gemm5_supports(H, Is);
+  const bool gate_x16 = dense && x_dtype == MOE_DT_BF16 && x16_make;
+  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st, gate_x16 ? x16_make : nullptr));
+  if (gate_x16) made = true;
+  if (dense) {
     if (x_dtype == MOE_DT_BF16) {
       MOE_TRY(moe_launch_gemm5_gateup(x, 1, wg, wu, T, H, Is, s, st));
     } else {

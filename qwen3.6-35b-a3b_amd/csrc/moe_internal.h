@@ -159,8 +159,9 @@ int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const voi
                            const void* wd, int shared_fmt, const void* wsg, int gate_dtype, int T,
                            int H, int Is, float* s_tmp, float* shared_raw, float* gate_prob,
                            hipStream_t st);
+// x16 (optional): also the f16 rows of x, as moe_launch_to_f16 writes them
 int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int gate_dtype, int T, int H,
-                           float* gate_prob, hipStream_t st);
+                           float* gate_prob, hipStream_t st, uint16_t* x16 = nullptr);
 
 // combine
 // y: the per-slot expert rows, f32 or (y16) f16

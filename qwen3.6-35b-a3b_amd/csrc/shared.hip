@@ -71,16 +71,30 @@ __global__ __launch_bounds__(256) void k_shared_down(const float* __restrict__ s
   }
 }
 
-// scalar gate only (used beside the MFMA path): one wave per token
+// f16 RNE of two values saturated to +-65504, packed (k_to_f16's conversion)
+__device__ __forceinline__ uint32_t f16x2_sat_pk(float u, float v) {
+  u = fminf(fmaxf(u, -65504.0f), 65504.0f);
+  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)u) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v) << 16);
+}
+
+// scalar gate only (used beside the MFMA path): one wave per token. With x16 given, the wave also
+// writes its token's f16 row (same bits as k_to_f16), since it reads the whole row anyway.
 template <int XDT>
 __global__ __launch_bounds__(64) void k_shared_gate(const void* __restrict__ x,
                                                      const void* __restrict__ wsg, int gdt, int T,
-                                                     int H, float* __restrict__ gate_prob) {
+                                                     int H, float* __restrict__ gate_prob,
+                                                     uint16_t* __restrict__ x16) {
   const int t = blockIdx.x, lane = threadIdx.x;
   float a = 0.0f;
   for (int c = 0; c < H / 512; ++c) {
     float xv[8];
-    load_x8<XDT>(x, (size_t)t * H + 512 * c + 8 * lane, xv);
+    const size_t o = (size_t)t * H + 512 * c + 8 * lane;
+    load_x8<XDT>(x, o, xv);
+    if (x16)
+      *reinterpret_cast<uint4*>(x16 + o) = make_uint4(f16x2_sat_pk(xv[0], xv[1]), f16x2_sat_pk(xv[2], xv[3]),
+                                                      f16x2_sat_pk(xv[4], xv[5]), f16x2_sat_pk(xv[6], xv[7]));
     a += dot8_w(wsg, (size_t)512 * c + 8 * lane, gdt, xv);
   }
   a = wave_sum_f32(a);
@@ -116,10 +130,10 @@ int moe_launch_shared_gemv(const void* x, int x_dtype, const void* wg, const voi
 }
 
 int moe_launch_shared_gate(const void* x, int x_dtype, const void* wsg, int gate_dtype, int T, int H,
-                           float* gate_prob, hipStream_t st) {
+                           float* gate_prob, hipStream_t st, uint16_t* x16) {
   if (x_dtype == MOE_DT_F32)
-    hipLaunchKernelGGL(k_shared_gate<MOE_DT_F32>, dim3(T), dim3(64), 0, st, x, wsg, gate_dtype, T, H, gate_prob);
+    hipLaunchKernelGGL(k_shared_gate<MOE_DT_F32>, dim3(T), dim3(64), 0, st, x, wsg, gate_dtype, T, H, gate_prob, x16);
   else
-    hipLaunchKernelGGL(k_shared_gate<MOE_DT_BF16>, dim3(T), dim3(64), 0, st, x, wsg, gate_dtype, T, H, gate_prob);
+    hipLaunchKernelGGL(k_shared_gate<MOE_DT_BF16>, dim3(T), dim3(64), 0, st, x, wsg, gate_dtype, T, H, gate_prob, x16);
   return moe_check_launch("shared_gate");
 }
