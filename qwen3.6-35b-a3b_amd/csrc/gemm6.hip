@@ -161,6 +161,9 @@ __device__ __forceinline__ void geo_lds(Geo& g, Smem& sm, int wave) {
 
 }  // namespace g6
 
+// the shared-expert blocks reduce their four waves' partial tiles in the routed blocks' LDS
+static_assert(sizeof(g6::Smem) >= shs::red_floats<4>() * sizeof(float), "shared-expert partial tiles fit in LDS");
+
 // S [P, I] f16 (sorted order) = SiLU(x16[token] . gate^T) * (x16[token] . up^T) per tile row; the
 // last sh.n blocks run the small-T shared expert's gate/up (and scalar gate, x of dtype GX)
 template <int GX>
