@@ -80,6 +80,29 @@ def test_reference_surfaces_agree(pkg, layer_c0, dev):
     assert int(info["used"]) == len(torch.unique(whole["topk_ids"]))
 
 
+@pytest.mark.parametrize("T,bf16", [(64, False), (200, True)])
+def test_small_t_folded_block_vs_stage_calls(pkg, layer_c3, dev, T, bf16):
+    """Up to 256 tokens the block runs the shared expert inside the routed small-T launches, on
+    the caller's stream alone. The separate stage calls (engine/block_forward.py:614-667: their
+    own router, shared-expert and routed-expert launches) give the same routing, and shared and
+    block outputs within the oracle tolerance; the oracle checks sampled rows of the block."""
+    lw, ow = layer_c3
+    cfg = pkg.load_geometry()
+    x = pkg.synth.make_input(T, seed=33, device=dev, dtype=torch.bfloat16 if bf16 else torch.float32)
+    r = pkg.block.moe_router(x, lw, cfg)
+    s = pkg.block.moe_shared(x, lw, cfg)
+    ro = pkg.block.moe_routed(x, lw, cfg, r)
+    whole = pkg.block.moe_block(x, lw, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(r["topk_ids"], whole["topk_ids"])
+    assert_close(whole["shared_out"].cpu(), s["shared_out"].cpu(), f"T={T} shared_out vs stage call")
+    assert_close(whole["combined_out"].cpu(), (ro["routed_sum"] + s["shared_out"]).cpu(),
+                 f"T={T} combined_out vs stage calls")
+    rows = torch.randperm(T, generator=torch.Generator().manual_seed(T))[:24]
+    ref = O.moe_block(x.cpu()[rows], ow)
+    _compare(whole, ref, rows=rows, tag=f"folded T={T}")
+
+
 def test_deterministic_repeat(pkg, layer_c0, dev):
     lw, _ = layer_c0
     x = pkg.synth.make_input(64, seed=4, device=dev)
