@@ -80,7 +80,7 @@ def test_reference_surfaces_agree(pkg, layer_c0, dev):
     assert int(info["used"]) == len(torch.unique(whole["topk_ids"]))
 
 
-@pytest.mark.parametrize("T,bf16", [(64, False), (200, True)])
+@pytest.mark.parametrize("T,bf16", [(7, False), (64, False), (200, True), (256, True)])
 def test_small_t_folded_block_vs_stage_calls(pkg, layer_c3, dev, T, bf16):
     """Up to 256 tokens the block runs the shared expert inside the routed small-T launches, on
     the caller's stream alone. The separate stage calls (engine/block_forward.py:614-667: their
@@ -98,7 +98,7 @@ def test_small_t_folded_block_vs_stage_calls(pkg, layer_c3, dev, T, bf16):
     assert_close(whole["shared_out"].cpu(), s["shared_out"].cpu(), f"T={T} shared_out vs stage call")
     assert_close(whole["combined_out"].cpu(), (ro["routed_sum"] + s["shared_out"]).cpu(),
                  f"T={T} combined_out vs stage calls")
-    rows = torch.randperm(T, generator=torch.Generator().manual_seed(T))[:24]
+    rows = torch.randperm(T, generator=torch.Generator().manual_seed(T))[:min(T, 24)]
     ref = O.moe_block(x.cpu()[rows], ow)
     _compare(whole, ref, rows=rows, tag=f"folded T={T}")
 
