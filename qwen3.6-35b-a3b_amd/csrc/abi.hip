@@ -413,25 +413,26 @@ static int shared_body(const void* x, int x_dtype, const uint16_t* x16, const vo
     made = x16_make != nullptr;
     return moe_launch_gemm5s_down(s, wd, T, H, Is, shared_raw, st);
   }
-  // bf16 shared weights on the MFMA path: the dense 128-row kernels, on bf16 rows as they are;
-  // the gate kernel, which reads every row first, writes the f16 rows the caller asked for
+  // bf16 shared weights on the MFMA path: the dense 128-row kernels, on bf16 rows as they are.
+  // With bf16 rows the GEMMs go first and the gate kernel last; it reads every row anyway and
+  // writes the f16 rows the caller asked for.
   const bool dense = path == MOE_PATH_MFMA && sfmt == MOE_FMT_BF16 && moe_gemm5_supports(H, Is);
-  const bool gate_x16 = dense && x_dtype == MOE_DT_BF16 && x16_make;
-  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st, gate_x16 ? x16_make : nullptr));
-  if (gate_x16) made = true;
+  if (dense && x_dtype == MOE_DT_BF16) {
+    MOE_TRY(moe_launch_gemm5_gateup(x, 1, wg, wu, T, H, Is, s, st));
+    MOE_TRY(moe_launch_gemm5_down(s, wd, T, H, Is, shared_raw, st));
+    made = x16_make != nullptr;
+    return moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st, x16_make);
+  }
+  MOE_TRY(moe_launch_shared_gate(x, x_dtype, wsg, gate_dtype, T, H, gate_prob, st));
   if (dense) {
-    if (x_dtype == MOE_DT_BF16) {
-      MOE_TRY(moe_launch_gemm5_gateup(x, 1, wg, wu, T, H, Is, s, st));
-    } else {
-      if (!x16) {
-        uint16_t* c = x16_make ? x16_make : reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
-        if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
-        MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
-        made = c == x16_make;
-        x16 = c;
-      }
-      MOE_TRY(moe_launch_gemm5_gateup(x16, 0, wg, wu, T, H, Is, s, st));
+    if (!x16) {
+      uint16_t* c = x16_make ? x16_make : reinterpret_cast<uint16_t*>(w.take((size_t)T * H * 2));
+      if (!c) return moe_set_error(MOE_E_WORKSPACE, "moe_shared_expert: workspace too small");
+      MOE_TRY(moe_launch_to_f16(x, x_dtype, (size_t)T * H, c, st));
+      made = c == x16_make;
+      x16 = c;
     }
+    MOE_TRY(moe_launch_gemm5_gateup(x16, 0, wg, wu, T, H, Is, s, st));
     return moe_launch_gemm5_down(s, wd, T, H, Is, shared_raw, st);
   }
   // Q8_0 shared weights take the 160-row f16 kernels on either MFMA path
