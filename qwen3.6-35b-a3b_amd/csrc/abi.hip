@@ -619,9 +619,10 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
   // the conversion runs on the shared expert's stream after them (off the router's path)
   const bool fork = T >= kForkMinT && allow_fork;
   // Few rows per expert (the 32-row routed kernels) with the narrow-slab shared expert: no second
-  // stream. The single-launch router also writes the f16 copy of x, and the shared expert's blocks
-  // run inside the routed gate/up and down launches, whose grids leave CUs idle at this size; the
-  // fork and join cost more than the shared expert's time left after that overlap.
+  // stream. The single-launch router also writes the f16 copy of x and runs the shared gate/up
+  // blocks, and the shared down blocks run inside the routed down launch: both grids leave CUs
+  // idle at this size, and the fork and join cost more than the shared expert's time left after
+  // that overlap.
   const bool fuse = rpath == MOE_PATH_MFMA && Wt.shared_fmt == MOE_FMT_BF16 && H % 2048 == 0 &&
                     I_s % 256 == 0 && mfma_small(rpath, T, H, I, gate_up_fmt, down_fmt) &&
                     shared_skinny(path, Wt.shared_fmt, T, H, I_s) && moe_router_chain_supported(T, H, E, K);
@@ -641,18 +642,20 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     const size_t rsb = moe_router_scratch_bytes(T, H, E);
     void* rscr = wr.take(rsb);
     if (!ssh || !rscr) return moe_set_error(MOE_E_WORKSPACE, "moe_block_forward: workspace too small");
-    MOE_TRY(moe_launch_router_chain(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits,
-                                    nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st, x16));
-    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
+    // the shared gate/up (and scalar gate) as extra blocks of the router launch, which leaves CUs
+    // idle once its partial tiles are in; the shared down as extra blocks of the routed down
     MoeShJob g, d;
     g.n = moe_shjob_gateup_blocks(T, I_s);
-    g.a16 = x16; g.x = x; g.x_dtype = x_dtype; g.wsg = ws_scalar_gate; g.gdt = Wt.scalar_gate_dtype;
+    g.x = x; g.x_dtype = x_dtype; g.wsg = ws_scalar_gate; g.gdt = Wt.scalar_gate_dtype;
     g.gate_prob = gp; g.w0 = reinterpret_cast<const uint16_t*>(ws_gate);
     g.w1 = reinterpret_cast<const uint16_t*>(ws_up); g.S = ssh; g.T = T; g.H = H; g.Is = I_s;
     d.n = moe_shjob_down_blocks(T, H);
     d.w0 = reinterpret_cast<const uint16_t*>(ws_down); d.S = ssh; d.y = sraw; d.T = T; d.H = H; d.Is = I_s;
+    MOE_TRY(moe_launch_router_chain(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits,
+                                    nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st, x16, &g));
+    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
     MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
-                         sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16, &g, &d));
+                         sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16, nullptr, &d));
     return moe_launch_combine(y, y16, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                               shared_out, expert_raw, st);
   }

@@ -31,10 +31,14 @@ int moe_launch_router_logits_i8(const void* x, int x_dtype, const void* w, int w
 bool moe_router_chain_supported(int T, int H, int E, int K);
 size_t moe_router_chain_scratch_bytes(int T, int E);
 // x16 (NULL: skipped): also the f16 copy of x (k_to_f16's conversion)
+struct MoeShJob;
+// sh (optional): the small-T shared expert's gate/up and scalar gate as extra blocks of the
+// launch, reading x in its own dtype (a16 unused)
 int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
                             int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
                             float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
-                            void* scratch, int* sync, hipStream_t st, uint16_t* x16 = nullptr);
+                            void* scratch, int* sync, hipStream_t st, uint16_t* x16 = nullptr,
+                            const MoeShJob* sh = nullptr);
 // bytes of router scratch that let every R1 form run (the int8 one, the single-launch chain)
 size_t moe_router_scratch_bytes(int T, int H, int E);
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,

@@ -637,15 +637,42 @@ __global__ __launch_bounds__(512) void k_router_chain(
     const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias, int T,
     int H, int E, uint16_t* __restrict__ logits, float* __restrict__ probs, int32_t* __restrict__ ids,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ heap_flag,
-    int exact_order, double* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ x16) {
-  __shared__ double s_d[8][256];
-  __shared__ double s_xsq[8][16], s_wsq[8][16];
-  __shared__ double s_xt[16], s_wt[16];
-  __shared__ int s_fail[256];
-  __shared__ int s_last, s_nrep;
-  __shared__ int s_rep[16];
-  __shared__ TopkLds s_tk[8];
+    int exact_order, double* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ x16,
+    MoeShJob sh) {
+  // the router blocks' arrays, or the shared-expert blocks' partial tiles, in one LDS region
+  struct Chain {
+    double d[8][256];
+    double xsq[8][16], wsq[8][16];
+    double xt[16], wt[16];
+    int fail[256];
+    int last, nrep;
+    int rep[16];
+    TopkLds tk[8];
+  };
+  __shared__ __attribute__((aligned(16))) union {
+    Chain c;
+    float red[shs::red_floats<8>()];
+  } sm;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int nr = (int)gridDim.x - sh.n;
+  if ((int)blockIdx.x >= nr) {
+    // the small-T shared expert's gate/up tile (32 token rows x 16 columns), x read as it is,
+    // then the scalar gate of this block's share of the tokens
+    const int b = (int)blockIdx.x - nr, nslab = sh.Is / 16;
+    shs::gateup_tile<XDT, 8, 32>(xv, sh.w0, sh.w1, T, H, sh.Is, b % nslab, (b / nslab) * 32, sh.S, sm.red);
+    shs::gate_rows<XDT>(xv, sh.wsg, sh.gdt, T, H, sh.gate_prob, b * 8 + wv, sh.n * 8);
+    return;
+  }
+  auto& s_d = sm.c.d;
+  auto& s_xsq = sm.c.xsq;
+  auto& s_wsq = sm.c.wsq;
+  auto& s_xt = sm.c.xt;
+  auto& s_wt = sm.c.wt;
+  auto& s_fail = sm.c.fail;
+  auto& s_last = sm.c.last;
+  auto& s_nrep = sm.c.nrep;
+  auto& s_rep = sm.c.rep;
+  auto& s_tk = sm.c.tk;
   const int nE = E / 16;
   const int ks = blockIdx.x % kChainKS, tile = blockIdx.x / kChainKS;
   const int et = tile % nE, tg = tile / nE;
@@ -823,16 +850,26 @@ size_t moe_router_scratch_bytes(int T, int H, int E) {
 int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
                             int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
                             float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
-                            void* scratch, int* sync, hipStream_t st, uint16_t* x16) {
+                            void* scratch, int* sync, hipStream_t st, uint16_t* x16,
+                            const MoeShJob* sh) {
   if (!moe_router_chain_supported(T, H, E, 8) || !scratch || !sync)
     return moe_set_error(MOE_E_UNSUPPORTED, "router_chain: needs 8 <= T <= 256, E = 256, K = 8, H %% 2048 == 0");
-  const dim3 grid(((T + 15) / 16) * (E / 16) * kChainKS);
+  const MoeShJob job = sh ? *sh : MoeShJob{};
+  if (job.n) {
+    if (job.T != T || job.H != H || job.Is % 256 || !job.w0 || !job.w1 || !job.S || !job.wsg || !job.gate_prob)
+      return moe_set_error(MOE_E_UNSUPPORTED, "router_chain: shared-expert blocks need I_s %% 256 == 0 and every pointer");
+    if (job.n != moe_shjob_gateup_blocks(T, job.Is))
+      return moe_set_error(MOE_E_ARG, "router_chain: %d shared-expert blocks given, %d needed", job.n,
+                           moe_shjob_gateup_blocks(T, job.Is));
+  }
+  dim3 grid(((T + 15) / 16) * (E / 16) * kChainKS);
+  grid.x += (unsigned)job.n;
   double* part = reinterpret_cast<double*>(scratch);
   int* cnt = sync + kRouterCntWord;
   const int eo = exact_order ? 1 : 0;
 #define MOE_CHAIN(XD, WD)                                                                          \
   hipLaunchKernelGGL((k_router_chain<XD, WD>), grid, dim3(512), 0, st, x, w, bias, T, H, E, logits, \
-                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, x16)
+                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, x16, job)
   if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_F32);
   else if (x_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_BF16);
   else if (w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_BF16, MOE_DT_F32);

@@ -82,8 +82,8 @@ def test_reference_surfaces_agree(pkg, layer_c0, dev):
 
 @pytest.mark.parametrize("T,bf16", [(7, False), (64, False), (200, True), (256, True)])
 def test_small_t_folded_block_vs_stage_calls(pkg, layer_c3, dev, T, bf16):
-    """Up to 256 tokens the block runs the shared expert inside the routed small-T launches, on
-    the caller's stream alone. The separate stage calls (engine/block_forward.py:614-667: their
+    """Up to 256 tokens the block runs the shared expert inside the router and routed down
+    launches, on the caller's stream alone. The separate stage calls (engine/block_forward.py:614-667: their
     own router, shared-expert and routed-expert launches) give the same routing, and shared and
     block outputs within the oracle tolerance; the oracle checks sampled rows of the block."""
     lw, ow = layer_c3
