@@ -247,8 +247,7 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                         const void* dn, int dn_fmt, const int32_t* offsets,
                         const int32_t* sorted_pairs, const int32_t* hit_list, int T, int H, int I,
                         int E, int K, int path, void* y, MoeWs& w, hipStream_t st,
-                        int32_t* tiles_pre = nullptr, int y16 = 0, const MoeShJob* shg = nullptr,
-                        const MoeShJob* shd = nullptr) {
+                        int32_t* tiles_pre = nullptr, int y16 = 0, const MoeShJob* shd = nullptr) {
   const int P = T * K;
   const int max_hits = P < E ? P : E;
   if (y16 && !y16_rows(path, T, H, I, K, gu_fmt, dn_fmt))
@@ -301,7 +300,7 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
     }
     if (small) {
       MOE_TRY(moe_launch_gemm6_gateup(x16, gate, up, estride, tiles, max_tiles, offsets, sorted_pairs,
-                                      K, H, I, S, st, shg));
+                                      K, H, I, S, st));
       return moe_launch_gemm6_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st, shd);
     }
     // gemm4's persistent item stream needs two super-blocks per item (H, I >= 512)
@@ -655,7 +654,7 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
                                     nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st, x16, &g));
     MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
     MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
-                         sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16, nullptr, &d));
+                         sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16, &d));
     return moe_launch_combine(y, y16, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,
                               shared_out, expert_raw, st);
   }

@@ -164,26 +164,13 @@ __device__ __forceinline__ void geo_lds(Geo& g, Smem& sm, int wave) {
 // the shared-expert blocks reduce their four waves' partial tiles in the routed blocks' LDS
 static_assert(sizeof(g6::Smem) >= shs::red_floats<4>() * sizeof(float), "shared-expert partial tiles fit in LDS");
 
-// S [P, I] f16 (sorted order) = SiLU(x16[token] . gate^T) * (x16[token] . up^T) per tile row; the
-// last sh.n blocks run the small-T shared expert's gate/up (and scalar gate, x of dtype GX)
-template <int GX>
+// S [P, I] f16 (sorted order) = SiLU(x16[token] . gate^T) * (x16[token] . up^T) per tile row
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm6_gateup(
     const uint16_t* __restrict__ x16, const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
     size_t estride, const int32_t* __restrict__ tiles, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ sorted_pairs, int K, int H, int I, uint16_t* __restrict__ S,
-    MoeShJob sh) {
+    const int32_t* __restrict__ sorted_pairs, int K, int H, int I, uint16_t* __restrict__ S) {
   using namespace g6;
   __shared__ __attribute__((aligned(16))) Smem sm;
-  const int nr = (int)gridDim.x - sh.n;
-  if ((int)blockIdx.x >= nr) {
-    const int b = (int)blockIdx.x - nr, nslab = sh.Is / 16;
-    float* red = reinterpret_cast<float*>(&sm);
-    shs::gateup_tile<shs::kF16, 4, 32>(sh.a16, sh.w0, sh.w1, sh.T, sh.H, sh.Is, b % nslab,
-                                       (b / nslab) * 32, sh.S, red);
-    shs::gate_rows<GX>(sh.x, sh.wsg, sh.gdt, sh.T, sh.H, sh.gate_prob, b * 4 + (int)(threadIdx.x >> 6),
-                       sh.n * 4);
-    return;
-  }
   Item it;
   if (!get_item(tiles, offsets, I / 128, it)) return;
   const int t = threadIdx.x, lane = t & 63;
@@ -303,13 +290,13 @@ static dim3 g6_grid(int max_tiles, int ncol) {
   return dim3((unsigned)((max_tiles + g6::kXcd - 1) / g6::kXcd * ncol * g6::kXcd));
 }
 
-// the shared-expert blocks need H % 2048 == 0 (K split over 4 waves in 64-wide chunks, the
-// scalar gate's 512-wide passes) and I_s % 256 == 0
-static int check_shjob(const MoeShJob* sh, bool down) {
+// the shared-expert down blocks need H % 32 == 0 (32-column slabs) and I_s % 256 == 0 (K split
+// over 4 waves in 64-wide chunks)
+static int check_shjob(const MoeShJob* sh) {
   if (!sh || sh->n == 0) return MOE_OK;
-  if (sh->H % 2048 || sh->Is % 256 || !sh->S || (down ? (!sh->w0 || !sh->y) : (!sh->a16 || !sh->w0 || !sh->w1 || !sh->x || !sh->wsg || !sh->gate_prob)))
-    return moe_set_error(MOE_E_UNSUPPORTED, "gemm6: shared-expert blocks need H %% 2048 == 0, I_s %% 256 == 0 and every pointer");
-  const int want = down ? moe_shjob_down_blocks(sh->T, sh->H) : moe_shjob_gateup_blocks(sh->T, sh->Is);
+  if (sh->H % 32 || sh->Is % 256 || !sh->S || !sh->w0 || !sh->y)
+    return moe_set_error(MOE_E_UNSUPPORTED, "gemm6: shared-expert blocks need H %% 32 == 0, I_s %% 256 == 0 and every pointer");
+  const int want = moe_shjob_down_blocks(sh->T, sh->H);
   if (sh->n != want) return moe_set_error(MOE_E_ARG, "gemm6: %d shared-expert blocks given, %d needed", sh->n, want);
   return MOE_OK;
 }
@@ -317,21 +304,12 @@ static int check_shjob(const MoeShJob* sh, bool down) {
 int moe_launch_gemm6_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
                             size_t expert_stride, const int32_t* tiles, int max_tiles,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
-                            int I, uint16_t* S, hipStream_t st, const MoeShJob* sh) {
+                            int I, uint16_t* S, hipStream_t st) {
   if (H % 256 || I % 128)
     return moe_set_error(MOE_E_UNSUPPORTED, "gemm6 gate_up needs H %% 256 == 0, I %% 128 == 0");
-  { const int rc_ = check_shjob(sh, false); if (rc_ != MOE_OK) return rc_; }
-  const MoeShJob job = sh ? *sh : MoeShJob{};
-  dim3 grid = g6_grid(max_tiles, I / 128);
-  grid.x += (unsigned)job.n;
-  const uint8_t* g = reinterpret_cast<const uint8_t*>(w_gate);
-  const uint8_t* u = reinterpret_cast<const uint8_t*>(w_up);
-  if (job.n && job.x_dtype == MOE_DT_BF16)
-    hipLaunchKernelGGL(k_gemm6_gateup<MOE_DT_BF16>, grid, dim3(256), 0, st, x16, g, u, expert_stride, tiles,
-                       offsets, sorted_pairs, K, H, I, S, job);
-  else
-    hipLaunchKernelGGL(k_gemm6_gateup<MOE_DT_F32>, grid, dim3(256), 0, st, x16, g, u, expert_stride, tiles,
-                       offsets, sorted_pairs, K, H, I, S, job);
+  hipLaunchKernelGGL(k_gemm6_gateup, g6_grid(max_tiles, I / 128), dim3(256), 0, st, x16,
+                     reinterpret_cast<const uint8_t*>(w_gate), reinterpret_cast<const uint8_t*>(w_up),
+                     expert_stride, tiles, offsets, sorted_pairs, K, H, I, S);
   return moe_check_launch("gemm6_gateup");
 }
 
@@ -339,7 +317,7 @@ int moe_launch_gemm6_down(const uint16_t* S, const void* w_down, size_t expert_s
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
                           void* y, int y16, hipStream_t st, const MoeShJob* sh) {
   if (I % 256 || H % 256) return moe_set_error(MOE_E_UNSUPPORTED, "gemm6 down needs H %% 256 == 0, I %% 256 == 0");
-  { const int rc_ = check_shjob(sh, true); if (rc_ != MOE_OK) return rc_; }
+  { const int rc_ = check_shjob(sh); if (rc_ != MOE_OK) return rc_; }
   const MoeShJob job = sh ? *sh : MoeShJob{};
   dim3 grid = g6_grid(max_tiles, H / 256);
   grid.x += (unsigned)job.n;

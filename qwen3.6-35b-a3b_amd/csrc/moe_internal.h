@@ -33,7 +33,7 @@ size_t moe_router_chain_scratch_bytes(int T, int E);
 // x16 (NULL: skipped): also the f16 copy of x (k_to_f16's conversion)
 struct MoeShJob;
 // sh (optional): the small-T shared expert's gate/up and scalar gate as extra blocks of the
-// launch, reading x in its own dtype (a16 unused)
+// launch, reading x in its own dtype
 int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
                             int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
                             float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
@@ -107,15 +107,11 @@ int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_s
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
                           void* y, int y16, hipStream_t st);
 
-// gemm6.hip: the same GEMMs for few rows per expert: 32-row tiles (MOE_GEMM6_BM), one block per
-// (tile, 256-row slab), activations and nibbles both requested three K steps ahead. sh (NULL or
-// n == 0: none): the small-T shared expert's blocks (shared_small.h, 4 waves), run after the
-// routed ones in the same launch: gate/up (with the scalar gate) in the gate_up launch, down in
-// the down launch.
+// The small-T shared expert's blocks (shared_small.h), appended to another launch's grid: gate/up
+// (with the scalar gate) in the single-launch router's, down in the gemm6 down launch's.
 struct MoeShJob {
   int n = 0;                       // shared-expert blocks appended to the launch
-  const uint16_t* a16 = nullptr;   // gate/up: the f16 rows of x [T, H]
-  const void* x = nullptr;         // gate/up: x itself, for the scalar gate
+  const void* x = nullptr;         // gate/up: x [T, H], read as it is
   int x_dtype = 0;
   const void* wsg = nullptr;       // the scalar gate's row and its dtype
   int gdt = 0;
@@ -126,14 +122,17 @@ struct MoeShJob {
   float* y = nullptr;              // down: shared_raw (f32 [T, H])
   int T = 0, H = 0, Is = 0;
 };
+// gemm6.hip: the same GEMMs for few rows per expert: 32-row tiles (MOE_GEMM6_BM), one block per
+// (tile, 256-row slab), activations and nibbles both requested three K steps ahead. sh (NULL or
+// n == 0: none): the small-T shared expert's down blocks (4 waves), run after the routed ones.
 int moe_launch_gemm6_gateup(const uint16_t* x16, const void* w_gate, const void* w_up,
                             size_t expert_stride, const int32_t* tiles, int max_tiles,
                             const int32_t* offsets, const int32_t* sorted_pairs, int K, int H,
-                            int I, uint16_t* S, hipStream_t st, const MoeShJob* sh = nullptr);
+                            int I, uint16_t* S, hipStream_t st);
 int moe_launch_gemm6_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
                           void* y, int y16, hipStream_t st, const MoeShJob* sh = nullptr);
-// shared-expert blocks of the gate/up and down launches for T tokens (32-row token tiles x
+// shared-expert blocks of the router (gate/up) and down launches for T tokens (32-row token tiles x
 // 16-column / 32-column slabs)
 inline int moe_shjob_gateup_blocks(int T, int Is) { return (T + 31) / 32 * (Is / 16); }
 inline int moe_shjob_down_blocks(int T, int H) { return (T + 31) / 32 * (H / 32); }
