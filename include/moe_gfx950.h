@@ -4,9 +4,11 @@
  * data_ptr()); `stream` is a hipStream_t passed as void*. Every call is asynchronous on `stream`,
  * allocates no device memory, frees nothing and never synchronises the host; scratch memory
  * comes in through (ws, ws_bytes). One exception to "creates nothing": the first
- * moe_block_forward* call of 7 or more tokens on a device creates that device's second stream (default
- * priority, non-blocking) and two events, kept until the process ends, on which the shared expert
- * runs beside the routed path (moe_block_forward_w_noalloc never does). Routing values never
+ * moe_block_forward* call on a device that runs the shared expert beside the routed path creates
+ * that device's second stream (default priority, non-blocking) and two events, kept until the
+ * process ends. That is a call of 7 or more tokens, except where the step folds the shared expert
+ * into its own launches (up to 256 tokens with Q4_K routed weights, bf16 shared weights,
+ * H % 2048 == 0 and I_s % 256 == 0: one stream). moe_block_forward_w_noalloc never forks. Routing values never
  * travel to the host (specification/11-moe-block.md §11.7: the block is computable with zero
  * host-visible routing values).
  *
