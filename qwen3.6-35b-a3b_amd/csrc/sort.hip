@@ -20,7 +20,7 @@ constexpr int kMaxChunks = 128;
 // pairs per chunk: a multiple of 256, at most kMaxChunks chunks
 __host__ __device__ inline int sort_chunk(int P) {
   const int per = (P + kMaxChunks - 1) / kMaxChunks;
-  return per <= 1024 ? 1024 : (per + 255) / 256 * 256;
+  return per <= 512 ? 512 : (per + 255) / 256 * 256;
 }
 
 __global__ __launch_bounds__(64) void k_sort_small(const int32_t* __restrict__ ids, int P, int E,
