@@ -297,7 +297,7 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
   const float m = bf16_to_f32(bf16_unkey(top[0] >> 8));
   float sum = 0.0f;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) { p[q] = expf(bf16_to_f32(lb[q]) - m); sum += p[q]; }
+  for (int q = 0; q < 4; ++q) { p[q] = r2_exp(bf16_to_f32(lb[q]) - m); sum += p[q]; }
 #pragma unroll
   for (int r = 1; r <= K; ++r) {
     top[r] = wave_max_u32(k0);
@@ -310,7 +310,7 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
   uint32_t mine = top[0];
 #pragma unroll
   for (int r = 1; r <= K; ++r) mine = lane == r ? top[r] : mine;
-  const float ps = expf(bf16_to_f32(bf16_unkey(mine >> 8)) - m) * rs;
+  const float ps = r2_exp(bf16_to_f32(bf16_unkey(mine >> 8)) - m) * rs;
   const float nxt = __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(ps), 0x101, 0xF, 0xF, false));
   const uint64_t ties = __ballot(lane < K && ps == nxt);       // p_r == p_{r+1}, r < K
   if (((ties >> (K - 1)) & 1ull) || (ties && exact_order)) return false;

@@ -494,6 +494,13 @@ __device__ __forceinline__ int wave_topk_fast(const float* p, int E, int K, int 
   return boundary_tie ? 2 : (inner_tie ? 1 : 0);
 }
 
+// R2's exp, correctly rounded to f32 (the f64 exp's error is far below an f32 half-ulp, so one
+// rounding of it lands on the nearest f32 except for arguments within ~2^-29 relative of an f32
+// midpoint, none of which an exact f32 argument other than 0 reaches in practice). torch's CPU
+// softmax evaluates its exps within one ulp of this; hipcc's expf is further off near zero, where
+// distinct logits' probabilities sit within an ulp of each other and the last bit decides ties.
+__device__ __forceinline__ float r2_exp(float a) { return (float)exp((double)a); }
+
 // R2: softmax over E bf16 logits in f32 (max-subtracted, sum, multiply by the reciprocal — the
 // same form as torch's CPU kernel); lane holds positions lane + 64j. AGENT: the logits were
 // written by other workgroups of this launch through agent-scope stores, and are read likewise.
@@ -521,7 +528,7 @@ __device__ __forceinline__ void route_softmax_raw(const uint32_t* raw, int E, in
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    p[j] = (64 * j + lane) < E ? expf(lv[j] - m) : 0.0f;
+    p[j] = (64 * j + lane) < E ? r2_exp(lv[j] - m) : 0.0f;
     sum += p[j];
   }
   sum = wave_sum_f32(sum);

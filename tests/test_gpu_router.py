@@ -198,3 +198,33 @@ def test_router_int8_midpoints_round_to_even(pkg, dev, xdt):
     lg = r["router_logits"].cpu().float()
     assert (lg[0::2] == 1.0).all()
     assert (lg[1::2] == 1.0 + 2.0 ** -7).all()
+
+
+@pytest.mark.parametrize("T", [1, 64, 256, 2048])
+def test_router_r2_near_equal_probabilities(pkg, dev, T):
+    """R2 fixture (tests/r2_fixture.py): rows whose distinct near-zero logits give probabilities
+    within a few f32 ulps. x[t] = e_t and router column t = row t's logits, so R1 returns them
+    exactly. The ids must equal the box host's torch.topk(torch.softmax) on every row outside the
+    fragile class (distinct logits within 2 ulps in the top 9). Inside it they depend on the last
+    bit of each exp and of the reciprocal of the sum: the device's exps are correctly rounded and
+    torch's CPU softmax exps are within one ulp of that, so the ids may differ on a small share of
+    these rows (measured: 1 of 2,360 fragile rows; hipcc's expf instead gave 546). The bound below
+    is 2 % of the fragile rows; the count is printed."""
+    import r2_fixture as F
+    rows = F.logit_rows(T, seed=100 + T)
+    H = 2048
+    w = torch.zeros(256, H, dtype=torch.bfloat16)
+    w[:, :T] = rows.t()
+    x = torch.zeros(T, H)
+    x[torch.arange(T), torch.arange(T)] = 1.0
+    r = pkg.abi.router_topk(x.to(dev), w.to(dev), 8)
+    torch.cuda.synchronize()
+    assert torch.equal(r["router_logits"].cpu().view(torch.int16), rows.view(torch.int16))
+    _, ids = torch.topk(torch.softmax(rows.float(), dim=-1), 8, dim=-1)
+    differ = (r["topk_ids"].cpu().long() != ids).any(-1)
+    frag = F.fragile_rows(rows)
+    print(f"\nR2 fixture T={T}: fragile rows {int(frag.sum())}, ids differ on "
+          f"{int((differ & frag).sum())} of them; robust rows {int((~frag).sum())}, "
+          f"differ {int((differ & ~frag).sum())}", flush=True)
+    assert not (differ & ~frag).any()
+    assert int((differ & frag).sum()) <= max(1, int(0.02 * int(frag.sum())))

@@ -177,3 +177,127 @@ def test_metrics_fields_and_refusals():
         O.metrics(torch.tensor([float("nan"), 0.0, 0.0, 1.0]), ref)
     with pytest.raises(AssertionError, match="all zero"):
         O.metrics(got, torch.zeros(4))
+
+
+# ------------------------------------------------------------------------------------------------
+# Pins for the reference's own must-catch injections (speccheck/selftest_moe.py:65-73, cases
+# :93-107) and the combine's addend order (speccheck/moe_ref.py:464-475). Each test fixes a fact a
+# plausible one-line slip in the oracle would break; the closed forms are evaluated from the
+# definitions (one-hot columns, hand-built addends, an own bf16 RNE on bit patterns), not by
+# calling the oracle's formula a second time.
+
+def _bf16_rne_f32(v: torch.Tensor) -> torch.Tensor:
+    """f32 -> bf16 round-to-nearest-even on the bit pattern (moe_router_kernels.h:189-205),
+    returned as f32 values: (b + 0x7FFF + ((b >> 16) & 1)) >> 16, then << 16."""
+    b = v.contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    r = torch.where(r >= 2 ** 31, r - 2 ** 32, r)
+    return r.to(torch.int32).view(torch.float32)
+
+
+def test_gather_applies_each_slots_own_expert():
+    """expert_raw[t, k] is expert ids[t, k] applied to x[t] (`wrong_expert_index`,
+    speccheck/selftest_moe.py:66). With x[t] = e_j the closed form is
+    W_down[e] @ (silu(W_gu[e][j-th column of the gate rows]) * (j-th column of the up rows)), which
+    a gather that used a neighbouring expert's weights cannot meet (experts are distinct draws)."""
+    lw = _layer(11)
+    cols = [3, 77, 130, 255, 1, 200]
+    x = torch.zeros(len(cols), H)
+    for t, j in enumerate(cols):
+        x[t, j] = 1.0
+    out = O.moe_block(x, lw, K)
+    ids = out["topk_ids"]
+    assert ids.shape == (len(cols), K)
+    closed = {}
+
+    def closed_form(e, j):
+        if (e, j) not in closed:
+            gu, dn = lw.expert_f32(e)
+            closed[e, j] = dn.double() @ (_silu64(gu[:I, j].double()) * gu[I:, j].double())
+        return closed[e, j]
+
+    for t, j in enumerate(cols):
+        for k in range(K):
+            e = int(ids[t, k])
+            want = closed_form(e, j)
+            got = out["expert_raw"][t, k].double()
+            assert torch.allclose(got, want, rtol=1e-5, atol=1e-7), (t, k, e)
+            # negative control: the neighbouring expert's closed form is far away
+            assert (closed_form((e + 1) % E, j) - want).abs().max() > 1e-4
+
+
+def test_r5_weights_are_cast_to_bf16_before_the_multiply():
+    """R5 (`cast_after_multiply`, speccheck/selftest_moe.py:70; moe_ref.py:345-355): the routing
+    weights handed to the combine are bf16_rne(vals / sum vals). With unit expert rows (slot k writes
+    column k only) routed_sum[t, k] is exactly f32(w_bf16[t, k]); a combine fed the f32 weights
+    would carry bits below bf16 precision."""
+    lw = _layer(12)
+    g = torch.Generator().manual_seed(12)
+    T = 24
+    x = torch.randn(T, H, generator=g)
+    r = O.route(x, lw.router, K)
+    assert r["topk_weights"].dtype == torch.bfloat16
+    wpre = r["topk_weights_f32"]
+    assert wpre.dtype == torch.float32
+    # the pre-cast weights are not bf16 values, so the cast is observable
+    assert ((wpre.view(torch.int32) & 0xFFFF) != 0).float().mean() > 0.9
+    want = _bf16_rne_f32(wpre)
+    assert torch.equal(r["topk_weights"].float(), want)
+    raw = torch.zeros(T, K, H)
+    for k in range(K):
+        raw[:, k, k] = 1.0
+    e = O.routed_combine(raw, r["topk_ids"], r["topk_weights"])
+    assert torch.equal(e[:, :K], want)
+    assert torch.count_nonzero(e[:, K:]) == 0
+    # and through the block's own gather/combine
+    blk = O.experts_and_combine(x[:2], r["topk_ids"][:2], r["topk_weights"][:2], lw)
+    assert blk["routed_sum"].dtype == torch.float32
+
+
+def test_combine_adds_in_ascending_expert_id():
+    """The combine's addends go in ascending expert id with the weight reached by rank
+    (speccheck/moe_ref.py:464-475). Addends 2^24, 1, -2^24 make the order visible in f32:
+    ascending id gives (2^24 + 1) - 2^24 = 2^24 - 2^24 = 0 (2^24 + 1 rounds to even), rank order
+    gives (-2^24 + 2^24) + 1 = 1."""
+    ids = torch.tensor([[7, 1, 3, 0, 2, 4, 5, 6],      # rank 0 holds expert 7, rank 1 expert 1 ...
+                        [2, 6, 0, 1, 3, 4, 5, 7]])
+    w = torch.ones(2, K, dtype=torch.bfloat16)
+    raw = torch.zeros(2, K, 4)
+    big = float(2 ** 24)
+    # token 0, column 0: rank 0 (expert 7) -big, rank 1 (expert 1) +big, rank 2 (expert 3) +1
+    raw[0, 0, 0], raw[0, 1, 0], raw[0, 2, 0] = -big, big, 1.0
+    # token 1, column 1: expert 0 (rank 2) +big, expert 2 (rank 0) +1, expert 6 (rank 1) -big
+    raw[1, 2, 1], raw[1, 0, 1], raw[1, 1, 1] = big, 1.0, -big
+    # column 2: weights by rank, not by id: distinct power-of-two weights, one unit addend each
+    wd = torch.tensor([[2.0 ** -k for k in range(K)]] * 2).to(torch.bfloat16)
+    raw[:, :, 2] = 1.0
+    out = O.routed_combine(raw, ids, w)
+    assert out[0, 0].item() == 0.0
+    assert out[1, 1].item() == 0.0           # ids 0 (+big), 2 (+1 -> rounds away), 6 (-big)
+    rank_order = (torch.tensor(-big) + torch.tensor(big)) + torch.tensor(1.0)
+    assert rank_order.item() == 1.0          # the order the test excludes
+    outw = O.routed_combine(raw, ids, wd)
+    assert torch.equal(outw[:, 2], wd.float().sum(-1))
+    # token 0 with column 3 = rank index: the sum is the same in every order, so weights by rank
+    raw[:, :, 3] = torch.arange(K, dtype=torch.float32)
+    outw = O.routed_combine(raw, ids, wd)
+    want = sum(float(wd[0, k]) * k for k in range(K))
+    assert outw[0, 3].item() == want
+
+
+def test_from_device_stacks_gate_before_up_for_split_records():
+    """Separate `ffn_gate_exps` / `ffn_up_exps` records become the fused record's row order: gate
+    rows 0..I-1, up rows I..2I-1 (spec §11.4: chunk(2) on the output axis, gate first)."""
+    from types import SimpleNamespace
+    e_, h_, i_ = 2, 256, 3
+    rb = Q.row_bytes(Q.FMT_Q4_K, h_)
+    gate = torch.full((e_, i_, rb), 11, dtype=torch.uint8)
+    up = torch.full((e_, i_, rb), 22, dtype=torch.uint8)
+    bf = lambda *s: torch.zeros(*s, dtype=torch.bfloat16)
+    dev = SimpleNamespace(router=bf(e_, h_), gate_up_q=gate, up_q=up, gate_up_fmt=Q.FMT_Q4_K,
+                          down_q=torch.zeros(e_, h_, Q.row_bytes(Q.FMT_Q4_K, 256), dtype=torch.uint8),
+                          down_fmt=Q.FMT_Q4_K, shared_gate=bf(4, h_), shared_up=bf(4, h_),
+                          shared_down=bf(h_, 4), shared_scalar_gate=bf(1, h_), router_bias=None)
+    lw = O.from_device(dev)
+    assert lw.gate_up_q.shape == (e_, 2 * i_, rb)
+    assert (lw.gate_up_q[:, :i_] == 11).all() and (lw.gate_up_q[:, i_:] == 22).all()

@@ -40,6 +40,27 @@ def test_scale_is_the_correctly_rounded_exact_value():
             assert np.array_equal(xn[t].numpy().view(np.uint32), want.view(np.uint32)), (eps, t)
 
 
+def test_association_is_x_times_r_then_times_w():
+    """Form A is (x * r) * w (engine/m3_forward.py:303-307), two f32 roundings in that order. With
+    r from the exact decimal scale and w not a power of two, the bits are fixed, and the other
+    association x * (r * w) differs on a share of the elements (negative control)."""
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(4, H, generator=g) * 1.7
+    w = (1.0 + 0.3 * torch.randn(H, generator=g)).float()
+    eps = 1e-6
+    xn = O.rmsnorm_a(x, w, eps)
+    wn = w.numpy().astype(np.float32)
+    n_other = 0
+    for t in range(x.shape[0]):
+        r = np.float32(_exact_scale(x[t], eps))
+        xr = (x[t].numpy().astype(np.float32) * r).astype(np.float32)
+        want = (xr * wn).astype(np.float32)
+        assert np.array_equal(xn[t].numpy().view(np.uint32), want.view(np.uint32)), t
+        other = (x[t].numpy().astype(np.float32) * (r * wn).astype(np.float32)).astype(np.float32)
+        n_other += int((other.view(np.uint32) != want.view(np.uint32)).sum())
+    assert n_other > 0.05 * x.numel()
+
+
 def test_constant_rows_closed_form():
     w = torch.linspace(0.5, 1.5, H)
     # x = 2^k: r = 2^-k exactly, so the output is exactly sign(x) * w
