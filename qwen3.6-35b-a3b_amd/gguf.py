@@ -33,11 +33,14 @@ BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (25
 TYPE_NAMES = {GGML_F32: "F32", GGML_F16: "F16", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K",
               GGML_Q5_K: "Q5_K", GGML_Q6_K: "Q6_K", GGML_BF16: "BF16"}
 
-# metadata value types: id -> (struct format, size); 8 = string, 9 = array (handled apart).
-# BOOL is one byte.
-_SCALAR = {0: ("<B", 1), 1: ("<b", 1), 2: ("<H", 2), 3: ("<h", 2), 4: ("<I", 4), 5: ("<i", 4),
-           6: ("<f", 4), 7: ("<B", 1), 10: ("<Q", 8), 11: ("<q", 8), 12: ("<d", 8)}
+# Metadata value types of the container: type id -> numpy dtype of one element (little endian).
+# 8 (a length-prefixed string) and 9 (a typed, counted array) carry their own lengths.
+_META_DTYPE = {0: np.dtype("<u1"), 1: np.dtype("<i1"), 2: np.dtype("<u2"), 3: np.dtype("<i2"),
+               4: np.dtype("<u4"), 5: np.dtype("<i4"), 6: np.dtype("<f4"), 7: np.dtype("?"),
+               10: np.dtype("<u8"), 11: np.dtype("<i8"), 12: np.dtype("<f8")}
 GGUF_STRING, GGUF_ARRAY = 8, 9
+_U32, _U64 = np.dtype("<u4"), np.dtype("<u8")
+LIST_MAX = 4096            # numeric arrays up to this length become lists, longer ones stay arrays
 
 
 def _refused(tag: str, msg: str):
@@ -55,6 +58,10 @@ def record_bytes(type_id: int, n_elts: int) -> int:
     return n_elts // qk * bb
 
 
+def _round_up(n: int, a: int) -> int:
+    return (n + a - 1) // a * a
+
+
 @dataclass(frozen=True)
 class GgufTensor:
     index: int
@@ -66,103 +73,127 @@ class GgufTensor:
 
     @property
     def shape_hf(self) -> tuple:
-        """Row-major (slowest first) shape: the reverse of the GGUF order."""
-        return tuple(reversed(self.dims))
+        """The record's shape with the slowest axis first (HF / torch order)."""
+        return self.dims[::-1]
 
     @property
     def type_name(self) -> str:
         return TYPE_NAMES.get(self.type_id, f"type_{self.type_id}")
 
 
+class _HeaderCursor:
+    """A forward-only position in the mapped file. Every field is decoded in place from the
+    memoryview (numpy views of the bytes, no reads through a file object); a field that would run
+    past the end of the file is refused with its name and position."""
+
+    __slots__ = ("buf", "pos", "path")
+
+    def __init__(self, buf: memoryview, path: str):
+        self.buf, self.pos, self.path = buf, 0, path
+
+    def claim(self, n: int, what: str) -> int:
+        """Start of the next n bytes, which now belong to `what`."""
+        at = self.pos
+        if n < 0 or at + n > len(self.buf):
+            raise _refused("truncated-header", f"{self.path}: the {what} at byte {at} needs {n} bytes; "
+                                               f"the file ends at byte {len(self.buf)}")
+        self.pos = at + n
+        return at
+
+    def array(self, dt: np.dtype, count: int, what: str) -> np.ndarray:
+        at = self.claim(dt.itemsize * count, what)
+        return np.frombuffer(self.buf, dtype=dt, count=count, offset=at)
+
+    def u32(self, what: str) -> int:
+        return int(self.array(_U32, 1, what)[0])
+
+    def u64(self, what: str) -> int:
+        return int(self.array(_U64, 1, what)[0])
+
+    def text(self, what: str) -> str:
+        n = self.u64(f"length of the {what}")
+        at = self.claim(n, what)
+        return bytes(self.buf[at:at + n]).decode("utf-8", "replace")
+
+    def meta_value(self, vt: int, key: str):
+        if vt == GGUF_STRING:
+            return self.text(f"string value of {key!r}")
+        if vt == GGUF_ARRAY:
+            et = self.u32(f"element type of {key!r}")
+            n = self.u64(f"element count of {key!r}")
+            dt = _META_DTYPE.get(et)
+            if dt is not None:
+                vals = self.array(dt, n, f"array value of {key!r}")
+                return vals.tolist() if n <= LIST_MAX else vals
+            return [self.meta_value(et, key) for _ in range(n)]
+        dt = _META_DTYPE.get(vt)
+        if dt is None:
+            raise _refused("bad-header", f"{self.path}: metadata {key!r} has value type {vt}, "
+                                         "which the container does not define")
+        return self.array(dt, 1, f"value of {key!r}")[0].item()
+
+
 class GgufFile:
-    """A GGUF file's header, parsed by reading exactly the bytes each field asks for (nothing of the
-    data section), plus read-only memory-mapped windows onto the data section."""
+    """A GGUF file mapped read-only once: the header is decoded in place from the map (nothing of
+    the data section is touched), and record bytes are views of the same map."""
 
     def __init__(self, path: str):
         self.path = str(path)
         self.size = os.path.getsize(self.path)
+        if self.size < 4:
+            raise _refused("not-gguf", f"{self.path}: {self.size} bytes, shorter than the magic")
         with open(self.path, "rb") as fh:
-            self._parse(fh)
-        self._fh = None
-        self._mm = None
+            self._mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+        self._buf = memoryview(self._mm)
+        self._read_header(_HeaderCursor(self._buf, self.path))
 
     # ------------------------------------------------------------------------------ header --
-    def _parse(self, fh) -> None:
-        def take(k: int) -> bytes:
-            v = fh.read(k)
-            if len(v) != k:
-                raise _refused("truncated-header", f"{self.path}: asked for {k} bytes at offset "
-                                                   f"{fh.tell()}, got {len(v)}")
-            return v
-
-        def u32() -> int:
-            return struct.unpack("<I", take(4))[0]
-
-        def u64() -> int:
-            return struct.unpack("<Q", take(8))[0]
-
-        def string() -> str:
-            n = u64()
-            if n > self.size:
-                raise _refused("bad-header", f"{self.path}: string length {n} exceeds the file")
-            return take(n).decode("utf-8", "replace")
-
-        def value(vt: int):
-            if vt == GGUF_STRING:
-                return string()
-            if vt in _SCALAR:
-                f, k = _SCALAR[vt]
-                v = struct.unpack(f, take(k))[0]
-                return bool(v) if vt == 7 else v
-            raise _refused("bad-header", f"{self.path}: unknown metadata value type {vt} at byte {fh.tell()}")
-
-        if take(4) != b"GGUF":
-            raise _refused("not-gguf", f"{self.path}: bad magic")
-        self.version = u32()
+    def _read_header(self, cur: _HeaderCursor) -> None:
+        if bytes(self._buf[:4]) != b"GGUF":
+            raise _refused("not-gguf", f"{self.path}: the first bytes are {bytes(self._buf[:4])!r}, not b'GGUF'")
+        cur.claim(4, "magic")
+        self.version = cur.u32("version")
         if self.version not in (2, 3):
-            raise _refused("gguf-version", f"{self.path}: version {self.version} (this reader takes 2 and 3)")
-        n_tensors, n_kv = u64(), u64()
+            raise _refused("gguf-version", f"{self.path}: container version {self.version}; "
+                                           "versions 2 and 3 are read")
+        n_tensors = cur.u64("tensor count")
+        n_kv = cur.u64("metadata count")
         self.meta: dict = {}
         for _ in range(n_kv):
-            key = string()
-            vt = u32()
-            if vt == GGUF_ARRAY:
-                et, cnt = u32(), u64()
-                if et in _SCALAR:
-                    f, k = _SCALAR[et]
-                    raw = take(k * cnt)
-                    self.meta[key] = list(struct.unpack("<" + f[1] * cnt, raw)) if cnt <= 4096 else raw
-                else:
-                    self.meta[key] = [value(et) for _ in range(cnt)]
-            else:
-                self.meta[key] = value(vt)
+            key = cur.text("metadata key")
+            self.meta[key] = cur.meta_value(cur.u32(f"value type of {key!r}"), key)
         self.tensors: list[GgufTensor] = []
+        self.by_name: dict[str, GgufTensor] = {}
         for i in range(n_tensors):
-            name = string()
-            nd = u32()
-            if not 1 <= nd <= 4:
-                raise _refused("bad-header", f"{name}: {nd} dimensions")
-            dims = tuple(u64() for _ in range(nd))
-            tid = u32()
-            off = u64()
-            n = 1
+            name = cur.text(f"name of tensor {i}")
+            nd = cur.u32(f"rank of {name!r}")
+            if nd < 1 or nd > 4:
+                raise _refused("bad-header", f"{self.path}: {name!r} claims {nd} axes (1 to 4 exist)")
+            dims = tuple(int(d) for d in cur.array(_U64, nd, f"axes of {name!r}"))
+            tid = cur.u32(f"ggml type of {name!r}")
+            off = cur.u64(f"data offset of {name!r}")
+            n_elts = 1
             for d in dims:
-                n *= int(d)
-            nbytes = record_bytes(tid, n) if tid in BLOCK else -1
-            self.tensors.append(GgufTensor(i, name, dims, tid, off, nbytes))
-        self.header_end = fh.tell()
-        self.alignment = int(self.meta.get("general.alignment", 32)) or 32
-        self.data_start = -(-self.header_end // self.alignment) * self.alignment
-        self.by_name = {t.name: t for t in self.tensors}
-        if len(self.by_name) != len(self.tensors):
-            raise _refused("duplicate-tensor", f"{self.path}: duplicate tensor names in the header")
+                n_elts *= d
+            rec = GgufTensor(i, name, dims, tid, off, record_bytes(tid, n_elts) if tid in BLOCK else -1)
+            if name in self.by_name:
+                raise _refused("duplicate-tensor", f"{self.path}: tensor {name!r} is listed twice "
+                                                   f"(entries {self.by_name[name].index} and {i})")
+            self.by_name[name] = rec
+            self.tensors.append(rec)
+        self.header_end = cur.pos
+        align = self.meta.get("general.alignment", 32)
+        if not isinstance(align, int) or align <= 0:
+            raise _refused("bad-header", f"{self.path}: general.alignment = {align!r}")
+        self.alignment = align
+        self.data_start = _round_up(self.header_end, align)
         for t in self.tensors:
-            if t.offset % self.alignment:
-                raise _refused("misaligned-tensor", f"{t.name}: offset {t.offset} is not a multiple "
-                                                    f"of the alignment {self.alignment}")
+            if t.offset % align:
+                raise _refused("misaligned-tensor", f"{t.name}: data offset {t.offset} is off the "
+                                                    f"{align}-byte grid")
             if t.nbytes >= 0 and self.data_start + t.offset + t.nbytes > self.size:
-                raise _refused("truncated-data", f"{t.name}: [{t.offset}, +{t.nbytes}) runs past the "
-                                                 f"end of {self.path}")
+                raise _refused("truncated-data", f"{t.name}: its {t.nbytes} bytes at data offset "
+                                                 f"{t.offset} end past byte {self.size} of {self.path}")
 
     # --------------------------------------------------------------------------- records --
     def tensor(self, name: str) -> GgufTensor:
@@ -173,16 +204,10 @@ class GgufFile:
             raise _refused("unsupported-type", f"{name} stores ggml type {t.type_id}")
         return t
 
-    def _data(self) -> mmap.mmap:
-        if self._mm is None:
-            self._fh = open(self.path, "rb")
-            self._mm = mmap.mmap(self._fh.fileno(), 0, access=mmap.ACCESS_READ)
-        return self._mm
-
     def view(self, name: str) -> np.ndarray:
         """The record's bytes, a read-only uint8 view of the mapped file (no copy)."""
         t = self.tensor(name)
-        return np.frombuffer(self._data(), dtype=np.uint8, count=t.nbytes,
+        return np.frombuffer(self._buf, dtype=np.uint8, count=t.nbytes,
                              offset=self.data_start + t.offset)
 
     def expert_range(self, name: str, idx: int) -> dict:
@@ -210,10 +235,16 @@ class GgufFile:
                     length=length, elts=inner, type_name=t.type_name)
 
     def close(self) -> None:
-        for h in (self._mm, self._fh):
-            if h is not None:
-                h.close()
-        self._mm = self._fh = None
+        """Release the map. Views returned by `view` keep it alive until they are collected."""
+        if self._buf is not None:
+            self._buf.release()
+            self._buf = None
+        if self._mm is not None:
+            try:
+                self._mm.close()
+            except BufferError:
+                pass
+            self._mm = None
 
 
 # ------------------------------------------------------------------------- one MoE block --
