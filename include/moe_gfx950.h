@@ -55,9 +55,12 @@ enum { MOE_FMT_Q8_0 = 8, MOE_FMT_Q4_K = 12, MOE_FMT_Q5_K = 13, MOE_FMT_Q6_K = 14
 
 /* expert contraction path: GEMV = fused decode + f32 GEMV; MFMA = tiles decoded to f16 in LDS on
  * MFMA (f32 accumulation); MFMA_BF16 = the same with bf16 operands (8 significant bits instead of
- * 11; same MFMA rate; block outputs ~3e-3 from the f32 oracle instead of ~4e-4). A single-token
- * moe_block_forward on the GEMV path runs one persistent launch on devices with >= 256 CUs;
- * GEMV_MULTI forces the three-launch form of the same arithmetic (any CU count). */
+ * 11; same MFMA rate). MFMA_BF16 is OUTSIDE the block-output bar that AUTO, GEMV, MFMA and
+ * GEMV_MULTI meet (max-abs 2e-3 / rel 1e-2 against the f32 oracle): its outputs land ~3e-3 from the
+ * oracle (~4e-4 for MFMA), and its test holds it to 8e-3. AUTO never picks it; it is there only for
+ * a caller that asks for bf16 operands by name. A single-token moe_block_forward on the GEMV path
+ * runs one persistent launch on devices with >= 256 CUs; GEMV_MULTI forces the three-launch form
+ * of the same arithmetic (any CU count). */
 enum { MOE_PATH_AUTO = 0, MOE_PATH_GEMV = 1, MOE_PATH_MFMA = 2, MOE_PATH_MFMA_BF16 = 3,
        MOE_PATH_GEMV_MULTI = 4 };
 
@@ -269,11 +272,16 @@ int moe_lm_head(const void *h, int h_dtype, int B, int H, const void *w, int w_f
  * the bits recorded since the last call, and the word is cleared. Bit MOE_STATUS_SPIN_TIMEOUT: a
  * bounded wait of the single-launch decode layer gave up (its workgroups were not all co-resident,
  * or not placed on the XCDs round robin as it assumes); the output rows of every workgroup that
- * gave up are NaN and the rest of that call's outputs are unspecified. No host synchronisation:
+ * gave up are NaN and the rest of that call's outputs are unspecified. Bit MOE_STATUS_SYNC_STATE:
+ * a block-arrival counter of the single-launch router (8 to 256 tokens) held a count its launch
+ * cannot produce (a workspace that skipped moe_workspace_init, or two calls overlapping on one
+ * workspace); that call's logits, ids and weights are unspecified, and moe_workspace_init restores
+ * the counters. No host synchronisation:
  * read *status after the stream reaches it. No counterpart in the reference (its device work ran
  * in fresh processes and reported through their exit status, engine/device_arm.py:417-463). */
 #define MOE_STATUS_WORD 3              /* int32 index of the status word in the workspace */
 #define MOE_STATUS_SPIN_TIMEOUT 1
+#define MOE_STATUS_SYNC_STATE 2
 /* Test hook: while the workspace's int32 word MOE_TEST_HOOK_WORD is non-zero, every bounded wait
  * of the single-launch decode layer completes as usual and then reports a timeout, so a caller's
  * handling of the status and the NaN rows can be exercised without a real timeout. Zero in normal

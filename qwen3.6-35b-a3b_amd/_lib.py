@@ -37,10 +37,13 @@ SYNC_BYTES = 512 * 1024
 # moe_block_forward_w_noalloc's static scratch (include/moe_gfx950.h)
 NOALLOC_SCRATCH_BYTES = 16 << 20
 NOALLOC_MAX_T = 120
-# the workspace's status word and test-hook word (int32 indices), and the status bit
+# the workspace's status word and test-hook word (int32 indices), the status bits, and the first
+# of the single-launch router's block-arrival counters (int32 index)
 STATUS_WORD = 3
 TEST_HOOK_WORD = 4
 STATUS_SPIN_TIMEOUT = 1
+STATUS_SYNC_STATE = 2
+ROUTER_CNT_WORD = 120000
 
 
 

@@ -611,7 +611,10 @@ static_assert((kRouterCntWord + kChainTiles + 16) * 4 <= (int)kSyncBytes, "route
 // is counted. (Fences would write back and invalidate whole L2s, 256 times per launch, under the
 // shared expert's concurrent GEMMs.) Each last arriver resets its counter, so the words are zero
 // again for the next launch (also under graph replay). Counters: cnt[tile] for tiles <
-// kChainTiles, cnt[kChainTiles + group].
+// kChainTiles, cnt[kChainTiles + group]. An arrival that reads a count its launch cannot produce
+// (at least the number of arrivals: a workspace never initialised, or two launches overlapping on
+// one workspace) sets MOE_STATUS_SYNC_STATE in the status word; that launch's routing outputs are
+// then unspecified, and moe_workspace_init restores the counters.
 // agent-scope (cross-XCD) stores and loads of the single-launch router's hand-offs
 __device__ __forceinline__ void st_agent(double* p, double v) {
   __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), (unsigned long long)__double_as_longlong(v),
@@ -637,8 +640,8 @@ __global__ __launch_bounds__(512) void k_router_chain(
     const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias, int T,
     int H, int E, uint16_t* __restrict__ logits, float* __restrict__ probs, int32_t* __restrict__ ids,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ heap_flag,
-    int exact_order, double* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ x16,
-    MoeShJob sh) {
+    int exact_order, double* __restrict__ part, int* __restrict__ cnt, int* __restrict__ status,
+    uint16_t* __restrict__ x16, MoeShJob sh) {
   // the router blocks' arrays, or the shared-expert blocks' partial tiles, in one LDS region
   struct Chain {
     double d[8][256];
@@ -718,7 +721,11 @@ __global__ __launch_bounds__(512) void k_router_chain(
   }
   stores_done();
   __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&cnt[tile], 1) == kChainKS - 1;
+  if (tid == 0) {
+    const int c = atomicAdd(&cnt[tile], 1);
+    if (c >= kChainKS) atomicOr(status, MOE_STATUS_SYNC_STATE);   // a start this launch cannot produce
+    s_last = c == kChainKS - 1;
+  }
   __syncthreads();
   if (!s_last) return;
   if (tid == 0) __hip_atomic_store(&cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -764,7 +771,11 @@ __global__ __launch_bounds__(512) void k_router_chain(
   }
   stores_done();
   __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&cnt[kChainTiles + tg], 1) == nE - 1;
+  if (tid == 0) {
+    const int c = atomicAdd(&cnt[kChainTiles + tg], 1);
+    if (c >= nE) atomicOr(status, MOE_STATUS_SYNC_STATE);
+    s_last = c == nE - 1;
+  }
   __syncthreads();
   if (!s_last) return;
   if (tid == 0) {
@@ -869,7 +880,7 @@ int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dty
   const int eo = exact_order ? 1 : 0;
 #define MOE_CHAIN(XD, WD)                                                                          \
   hipLaunchKernelGGL((k_router_chain<XD, WD>), grid, dim3(512), 0, st, x, w, bias, T, H, E, logits, \
-                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, x16, job)
+                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, sync + MOE_STATUS_WORD, x16, job)
   if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_F32);
   else if (x_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_BF16);
   else if (w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_BF16, MOE_DT_F32);

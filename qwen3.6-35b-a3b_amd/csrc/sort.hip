@@ -6,10 +6,11 @@
 // phases below. Otherwise two launches: per-chunk histograms, then per chunk one block that sums
 // the histograms itself (totals, scan, its own chunk's start positions) and scatters its chunk
 // stably, where ranks inside a 256-pair round come from wave-level id matching (8 ballots on the
-// id bits) and a per-wave count table, so no atomics decide any position. Chunks are 1024 pairs
-// (four rounds per block; measured faster at 32K pairs than 256-pair chunks, whose blocks each read
-// four times the counts) up to 128 chunks, longer above, so each block reads at most 128 counts
-// per expert.
+// id bits) and a per-wave count table, so no atomics decide any position. sort_chunk() sets the
+// chunk length: 512 pairs (two rounds per block) up to 128 chunks, above that the smallest multiple
+// of 256 that keeps 128 chunks, so each block reads at most 128 counts per expert. (At 32K pairs
+// 512-pair chunks measured 3-4 us faster per config-3 step than 1024-pair ones; 256-pair chunks
+// were slower, each block reading four times the counts of the 1024-pair form.)
 #include "common.h"
 #include "moe_internal.h"
 

@@ -61,6 +61,21 @@ def test_abi_version_and_enums_match_header(pkg):
         assert m and int(m.group(1)) == getattr(pkg._lib, name), name
 
 
+def test_status_words_match_header_and_library(pkg):
+    """The status word, test-hook word and status bits of the header, and the router's counter
+    index of the library's internal header, as the Python layer uses them."""
+    L = pkg._lib
+    text = HEADER.read_text()
+    for name, attr in (("MOE_STATUS_WORD", "STATUS_WORD"), ("MOE_TEST_HOOK_WORD", "TEST_HOOK_WORD"),
+                       ("MOE_STATUS_SPIN_TIMEOUT", "STATUS_SPIN_TIMEOUT"),
+                       ("MOE_STATUS_SYNC_STATE", "STATUS_SYNC_STATE")):
+        m = re.search(r"#define " + name + r" (\d+)", text)
+        assert m and int(m.group(1)) == getattr(L, attr), name
+    internal = (ROOT / "qwen3.6-35b-a3b_amd" / "csrc" / "moe_internal.h").read_text()
+    assert int(re.search(r"kRouterCntWord = (\d+)", internal).group(1)) == L.ROUTER_CNT_WORD
+    assert 4 * (L.ROUTER_CNT_WORD + 256 + 16) <= L.SYNC_BYTES
+
+
 def test_workspace_bytes_is_monotone(pkg):
     f = pkg._lib.lib.moe_workspace_bytes
     a = f(1, 2048, 512, 256, 8, 512)

@@ -228,3 +228,29 @@ def test_router_r2_near_equal_probabilities(pkg, dev, T):
           f"differ {int((differ & ~frag).sum())}", flush=True)
     assert not (differ & ~frag).any()
     assert int((differ & frag).sum()) <= max(1, int(0.02 * int(frag.sum())))
+
+
+def test_router_chain_reports_a_count_it_cannot_produce(pkg, dev):
+    """The single-launch router (8-256 tokens) counts block arrivals in the workspace's sync words
+    and each last arriver resets its counter. A counter left at a value no launch produces (set
+    here from the host, as after a workspace that skipped moe_workspace_init) makes the arrivals
+    set MOE_STATUS_SYNC_STATE in the status word; the launch has no waits, so it still ends. After
+    moe_workspace_init the same call gives the first call's bits again and reports nothing."""
+    import ctypes
+    L, abi, synth = pkg._lib, pkg.abi, pkg.synth
+    lw = synth.make_layer(seed=1, device=dev, zipf=True)
+    x = synth.make_input(64, seed=1, device=dev)
+    good = abi.router_topk(x, lw.router, 8, lw.router_bias)
+    torch.cuda.synchronize()
+    assert abi.workspace_status(dev) == 0
+    buf = abi.workspace(dev, 0)
+    buf[:L.SYNC_BYTES].view(torch.int32)[L.ROUTER_CNT_WORD + 3] = 1000
+    abi.router_topk(x, lw.router, 8, lw.router_bias)
+    assert abi.workspace_status(dev) & L.STATUS_SYNC_STATE
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    assert L.lib.moe_workspace_init(ctypes.c_void_p(buf.data_ptr()), buf.numel(), stream) == L.MOE_OK
+    again = abi.router_topk(x, lw.router, 8, lw.router_bias)
+    torch.cuda.synchronize()
+    assert abi.workspace_status(dev) == 0
+    for k in ("router_logits", "topk_ids", "topk_weights", "topk_weights_f32"):
+        assert torch.equal(again[k].cpu(), good[k].cpu()), k

@@ -69,15 +69,26 @@ def _same_bits(a, b, what):
 
 @pytest.mark.gpu
 def test_noalloc_matches_workspace_entry_on_shrinking_calls(pkg, dev):
-    """Three calls in a row on one device: T = 64 (Zipf routing, the grouped MFMA path, where the
-    workspace entry forks the shared expert onto a second stream), T = 4 (GEMV path), T = 1 (the
-    single-launch decode layer, norm and residual fused). Each against moe_block_forward_w."""
-    synth, abi = pkg.synth, pkg.abi
+    """Calls in a row on one device, each against moe_block_forward_w:
+    - T = 120 and then 64 with Q6_K down (config 4's weights) and T = 64 with the artifact's widths
+      (Q5_K down, Q8_0 shared expert, f32 router and scalar gate, split gate/up, the norm in
+      front): here the workspace entry forks the shared expert onto its second stream and the
+      no-alloc entry runs it on the caller's stream, so these compare the forked and the one-stream
+      orders;
+    - T = 64 with Q4_K routed and bf16 shared weights (Zipf routing): both entries fold the shared
+      expert into the router and routed launches (one stream);
+    - T = 4 (GEMV path) and T = 1 (the single-launch decode layer, norm and residual fused)."""
+    synth, abi, Q = pkg.synth, pkg.abi, pkg.quant
     lz = synth.make_layer(seed=1, device=dev, zipf=True)
     l0 = synth.make_layer(seed=0, device=dev)
+    l6 = synth.make_layer(seed=3, device=dev, down_fmt=Q.FMT_Q6_K, zipf=True)
+    la = synth.make_layer(seed=7, device=dev, down_fmt=Q.FMT_Q5_K, zipf=True,
+                          router_dtype=torch.float32, scalar_gate_dtype=torch.float32,
+                          split_gate_up=True, shared_fmt=Q.FMT_Q8_0)
     nw = synth.make_norm_weight(seed=5000, device=dev)
-    ws = abi.workspace(dev, abi.workspace_bytes(64, 2048, 512, 256, 8, 512))
-    for T, lw, norm in ((64, lz, None), (4, l0, nw), (1, l0, nw), (1, lz, nw)):
+    ws = abi.workspace(dev, abi.workspace_bytes(120, 2048, 512, 256, 8, 512))
+    for T, lw, norm in ((120, l6, None), (64, l6, None), (64, la, nw), (64, lz, None), (4, l0, nw),
+                        (1, l0, nw), (1, lz, nw)):
         x = synth.make_input(T, seed=100 + T, device=dev)
         res = synth.make_input(T, seed=200 + T, device=dev) if norm is not None else None
         print(f"noalloc T={T} norm={norm is not None}", flush=True)
