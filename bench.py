@@ -78,6 +78,8 @@ def parse():
     ap.add_argument("--lm-head-only", action="store_true",
                     help="only the untied lm_head GEMV timing (what the lm_head profile covers)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--peaks-only", action="store_true",
+                    help="only the measured HBM read and f16 MFMA peaks")
     ap.add_argument("--pmc", action="store_true")
     ap.add_argument("--no-hint", action="store_true",
                     help="call moe_block_forward (no next-layer L2 warm-up) in the decode runs")
@@ -428,6 +430,54 @@ def prefill_c3(torch, synth, abi, lwp, dev, steps: int) -> dict:
             "prefill_tflops": tflops, "prefill_mfma_util": tflops / BF16_PEAK_TFLOPS}
 
 
+PROBE_LIB = ROOT / "qwen3.6-35b-a3b_amd" / "libmoe_peak_probe.so"
+
+
+def measured_peaks(torch, dev, read_gib: int = 4) -> dict:
+    """Peaks measured on this GPU with the probes of csrc/probe/peak_probe.hip (the method of the
+    reference's tools/bw_probe_hip.cpp and tools/gemm_peak.cpp): the best HBM read rate over a
+    sweep of grid sizes (a read_gib GiB buffer, 16 times the MALL, so every byte comes from HBM),
+    and the best f16 MFMA rate (v_mfma_f32_32x32x16_f16, operands in registers) over a sweep of
+    waves per CU. HIP events on the stream the probes are launched on."""
+    import ctypes
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    lib.probe_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    lib.probe_mfma_f16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    st = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(st.cuda_stream)
+    sink = torch.zeros(16, dtype=torch.float32, device=dev)
+    nbytes = read_gib << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    best_bw, bw_sweep = 0.0, {}
+    for blocks in (2048, 4096, 8192, 16384, 32768, 65536):
+        run = lambda: lib.probe_hbm_read(ctypes.c_void_p(buf.data_ptr()), nbytes, blocks,
+                                         ctypes.c_void_p(sink.data_ptr()), sp)
+        if run() != 0:
+            raise RuntimeError("probe_hbm_read failed")
+        ms = time_stream(run, 5, torch, st)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        bw_sweep[blocks] = round(gbs, 1)
+        best_bw = max(best_bw, gbs)
+    del buf
+    torch.cuda.empty_cache()
+    best_tf, tf_sweep = 0.0, {}
+    iters = 2048
+    for blocks in (256, 512, 1024, 2048):
+        run = lambda: lib.probe_mfma_f16(blocks, iters, ctypes.c_void_p(sink.data_ptr()), sp)
+        if run() != 0:
+            raise RuntimeError("probe_mfma_f16 failed")
+        ms = time_stream(run, 5, torch, st)
+        flop = blocks * 4 * 4 * iters * 32768.0
+        tf = flop / (ms * 1e-3) / 1e12
+        tf_sweep[blocks] = round(tf, 1)
+        best_tf = max(best_tf, tf)
+    log(f"measured peaks: HBM read {best_bw:.0f} GB/s (by grid {bw_sweep}); f16 MFMA "
+        f"{best_tf:.0f} TFLOP/s (by grid {tf_sweep})")
+    return {"hbm_read_gbps": round(best_bw, 1), "hbm_read_sweep": bw_sweep,
+            "mfma_f16_tflops": round(best_tf, 1), "mfma_f16_sweep": tf_sweep}
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -438,24 +488,33 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def usable_cores() -> int:
+    """Cores this process may run on (its affinity mask), not os.cpu_count()."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_baselines(torch, synth, lw_dec, x0, lw_pf, dev, seconds: float):
     """The reference's CPU path timed on this host (oracle port, BASELINE.md's plan): config-1
-    decode tokens through one layer with every host thread and with one thread (each layer-token
-    dequantizes its 8 selected experts), and config 3's 4096-token prefill block (every used
-    expert dequantized once, grouped F.linear). Bounded samples; the decode figures are best-of
-    per-token times' mean over the sample, the prefill one a single timed block after a warm-up
-    call on 64 tokens."""
+    decode tokens through one layer (each layer-token dequantizes its 8 selected experts), and
+    config 3's 4096-token prefill block (every used expert dequantized once, grouped F.linear).
+    Decode: a short probe at 1, 2, 4, 8 and all usable cores (the affinity mask), then the
+    bounded sample at the fastest of them, plus a 1-thread line; the sample's mean per-token time
+    is reported with the thread count that gave it. Prefill: one timed block at the usable core
+    count after a warm-up call on 64 tokens."""
     from oracle import moe_oracle as O
-    ncpu = os.cpu_count() or 1
+    ncpu = usable_cores()
     model = cpu_model()
     ow = O.from_device(lw_dec)
 
-    def decode(threads: int, budget: float):
+    def decode(threads: int, budget: float, min_tokens: int = 3):
         torch.set_num_threads(threads)
         xc = x0.cpu()
         n, t_cpu, per = 0, 0.0, []
         t_start = time.time()
-        while time.time() - t_start < budget:
+        while time.time() - t_start < budget or n < min_tokens:
             t1 = time.perf_counter()
             res = O.moe_block(xc, ow)
             dt = time.perf_counter() - t1
@@ -464,16 +523,32 @@ def cpu_baselines(torch, synth, lw_dec, x0, lw_pf, dev, seconds: float):
             xc = synth.rms_normalize(xc + res["combined_out"])
             n += 1
         per.sort()
-        return {"value": round(t_cpu / n * 1e6, 1), "unit": "us/token/layer",
-                "cores": torch.get_num_threads(), "kind": "port",
+        return t_cpu / n, n, per
+
+    probe = {}
+    for th in sorted({1, 2, 4, 8, ncpu}):
+        if th > ncpu:
+            continue
+        mean, _, _ = decode(th, 1.5)
+        probe[th] = round(mean * 1e6, 1)
+    best = min(probe, key=probe.get)
+    log(f"cpu baseline probe (us/token/layer by threads, {ncpu} usable cores): {probe}; best {best}")
+
+    def line(threads, mean, n, per, what):
+        return {"value": round(mean * 1e6, 1), "unit": "us/token/layer", "cores": threads,
+                "kind": "port",
                 "sample": f"{n} sequential decode tokens through one config-1 layer: oracle "
                           "dequant of the 8 selected Q4_K experts + f32 F.linear + shared expert "
-                          f"(os.cpu_count()={ncpu}, {model}; per-token min "
-                          f"{per[0] * 1e6:.0f} us, median {per[len(per) // 2] * 1e6:.0f} us)"}
+                          f"at {threads} torch threads ({what}; {ncpu} usable cores by the affinity "
+                          f"mask, os.cpu_count()={os.cpu_count()}, {model}; per-token min "
+                          f"{per[0] * 1e6:.0f} us, median {per[len(per) // 2] * 1e6:.0f} us; probe "
+                          f"by threads {probe})"}
 
-    cpu = decode(ncpu, seconds)
-    log(f"cpu baseline: {cpu['value']:.0f} us/token/layer, {cpu['cores']} threads")
-    cpu1 = decode(1, max(4.0, seconds / 2))
+    mean, n, per = decode(best, seconds)
+    cpu = line(best, mean, n, per, "the fastest thread count of the probe")
+    log(f"cpu baseline: {cpu['value']:.0f} us/token/layer, {best} threads")
+    mean1, n1, per1 = decode(1, max(4.0, seconds / 2))
+    cpu1 = line(1, mean1, n1, per1, "one thread")
     log(f"cpu baseline, 1 thread: {cpu1['value']:.0f} us/token/layer")
     cpu_pf = None
     if lw_pf is not None:
@@ -488,7 +563,7 @@ def cpu_baselines(torch, synth, lw_dec, x0, lw_pf, dev, seconds: float):
                   "kind": "port",
                   "sample": f"config 3's 4096-token block once: oracle R1-R5, every used Q4_K expert "
                             f"dequantized once, grouped f32 F.linear, shared expert ({dt:.2f} s; "
-                            f"os.cpu_count()={ncpu}, {model})"}
+                            f"{ncpu} usable cores, {model})"}
         log(f"cpu baseline, prefill: {cpu_pf['value']:.0f} tok/s ({dt:.2f} s for 4096 tokens)")
     torch.set_num_threads(ncpu)
     return cpu, cpu1, cpu_pf
@@ -574,6 +649,10 @@ def main():
         pmc_workload(pkg, torch, dev, L, not args.no_hint)
         return
 
+    if args.peaks_only:
+        print(json.dumps(measured_peaks(torch, dev)), flush=True)
+        return
+
     if args.c2_only:
         print(json.dumps(c2_step(torch, synth, abi, dev, 50)), flush=True)
         return
@@ -598,6 +677,9 @@ def main():
         r = prefill_c3(torch, synth, abi, lwp, dev, args.prefill_steps)
         print(json.dumps({k: round(v, 4) for k, v in r.items()}), flush=True)
         return
+
+    # ---------------------------------------------------------------- measured peaks
+    peaks = measured_peaks(torch, dev) if not args.kernel_only else None
 
     # ---------------------------------------------------------------- decode, config 1
     t0 = time.time()
@@ -721,7 +803,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "kernel": DECODE_KERNEL,
-                     "bytes_per_launch": active, "avg_us": round(ms_k * 1000, 3)},
+                     "bytes_per_launch": active, "avg_us": round(ms_k * 1000, 3),
+                     "peak_measured": peaks["hbm_read_gbps"],
+                     "frac_of_measured": round(kern_gbps / peaks["hbm_read_gbps"], 4)},
+        "peaks_measured": peaks,
         "cpu_baseline": cpu,
         "cpu_baseline_1thread": cpu1,
         "cpu_baseline_prefill": cpu_pf,
@@ -732,6 +817,8 @@ def main():
     result.update({k: round(v, 3) for k, v in lmh.items()})
     result.update({k: round(v, 4) for k, v in c4.items()})
     result.update({k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()})
+    if prefill:
+        result["prefill_mfma_util_of_measured"] = round(prefill["prefill_tflops"] / peaks["mfma_f16_tflops"], 4)
     print(json.dumps(result), flush=True)
 
 

@@ -55,7 +55,24 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
     os.replace(tmp, OUT)
     build_hostcheck()
+    build_probe()
     return OUT
+
+
+PROBE = PKG / "libmoe_peak_probe.so"
+
+
+def build_probe() -> Path:
+    """libmoe_peak_probe.so: the HBM read and f16 MFMA peak probes bench.py reports beside the
+    published peaks (csrc/probe/). Measurement infrastructure; the MoE library does not link it."""
+    src = CSRC / "probe" / "peak_probe.hip"
+    tmp = PROBE.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, "-shared", "-o", str(tmp), str(src)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("peak probe build failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, PROBE)
+    return PROBE
 
 
 HOSTCHECK = PKG / "libmoe_hostcheck.so"
