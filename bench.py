@@ -73,6 +73,8 @@ def parse():
                     help="only the dominant-kernel timing (what the kernel-trace profile covers)")
     ap.add_argument("--no-lm-head", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 prefill timing")
+    ap.add_argument("--c4-only", action="store_true",
+                    help="only the config-4 prefill timing (what the c4 profile covers)")
     ap.add_argument("--no-artifact", action="store_true",
                     help="skip the decode chain over the shipped artifact's weight widths")
     ap.add_argument("--lm-head-only", action="store_true",
@@ -670,6 +672,11 @@ def main():
             abi.block_forward(xp, lwp, out=outp)
         torch.cuda.synchronize()
         log("pmc prefill workload done: 3 config-3 blocks")
+        return
+
+    if args.c4_only:
+        r = prefill_c4(torch, pkg, dev, args.prefill_steps)
+        print(json.dumps({k: round(v, 4) for k, v in r.items()}), flush=True)
         return
 
     if args.prefill_only:

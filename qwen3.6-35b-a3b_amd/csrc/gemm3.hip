@@ -199,22 +199,7 @@ struct WRaw<MOE_FMT_BF16> {
 // K step is g = 2 gp, 2 gp + 1 of one half: its element s takes nibble gp of ql byte 64 hf + s,
 // qh byte 32 hf + s % 32 (bits 4 gp + 2 (s / 32)) and scale 8 hf + 4 gp + s / 16. Super-blocks
 // start on even bytes only, so each piece is read as the aligned dwords that cover it (never past
-// its last byte) and shifted into place by 0 or 2 bytes (alignbyte) at decode. Mantissa trick as
-// Q5_K's with two high bits: under 0x6400 they go to mantissa bits 4-5 (1024 + q), under 0x5400
-// (high nibble) to bits 8-9 (64 + q); one packed subtract leaves q - 32 exactly and one packed
-// multiply by f16(d * sc) rounds once.
-template <bool HIGH>
-__device__ __forceinline__ uint32_t q6_pair(uint32_t w, uint32_t h, uint32_t sel, uint32_t hs,
-                                            f16x2_t ds) {
-  const uint32_t p = __builtin_amdgcn_perm(0u, w, sel);
-  const uint32_t hp = __builtin_amdgcn_perm(0u, h, sel) >> hs;
-  const uint32_t magic = HIGH ? and_or_s(p, 0x00F000F0u, 0x54005400u) | ((hp << 8) & 0x03000300u)
-                              : and_or_s(p, 0x000F000Fu, 0x64006400u) | ((hp << 4) & 0x00300030u);
-  const _Float16 off = HIGH ? (_Float16)96.0f : (_Float16)1056.0f;
-  const f16x2_t q = __builtin_bit_cast(f16x2_t, magic) - (f16x2_t){off, off};
-  return __builtin_bit_cast(uint32_t, q * ds);
-}
-
+// its last byte) and shifted into place by 0 or 2 bytes (alignbyte) at decode.
 template <>
 struct WRaw<MOE_FMT_Q6_K> {
   uint32_t ql[17], qh[9], sc[2], d, sh;
@@ -234,32 +219,34 @@ struct WRaw<MOE_FMT_Q6_K> {
     sc[1] = a[48 + 2 * hf + gp + x];
     d = *reinterpret_cast<const uint16_t*>(b + 208);
   }
-  // 64 f16 in k order into dst (LDS row, 128 B)
+  // 64 f16 in k order into dst (LDS row, 128 B). Four elements at a time: the dword of ql bytes
+  // 4i..4i+3 (nibble gp) and the dword of their qh bytes (two bits at 4 gp + 2 (i / 8)) give the
+  // four 6-bit q in the bytes of one register (one shift of each, one mask, one and-or); one perm
+  // per pair puts two of them under the f16 magic 0x6400 (1024 + q, exact for q <= 63), one packed
+  // subtract of 1056 leaves q - 32 exactly and one packed multiply by f16(d * sc) rounds once.
   __device__ __forceinline__ void decode(int k0, uint16_t* dst) const {
     const int gp = (k0 >> 6) & 1;
-    uint32_t w[16], h[8];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = __builtin_amdgcn_alignbyte(ql[i + 1], ql[i], sh);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = __builtin_amdgcn_alignbyte(qh[i + 1], qh[i], sh);
     const uint32_t scw = __builtin_amdgcn_alignbyte(sc[1], sc[0], sh);
     const float df = f16_to_f32(d);
+    const f16x2_t off = {(_Float16)1056.0f, (_Float16)1056.0f};
     uint32_t o[32];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {                  // 16 elements of scale j
       const _Float16 dsj = (_Float16)(df * (float)(int8_t)(scw >> (8 * j)));
       const f16x2_t ds = {dsj, dsj};
-      const uint32_t hs = 4u * (uint32_t)gp + 2u * (uint32_t)(j >> 1);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {                // dword m of the group: elements 16 j + 4 m ..
-        const uint32_t wv = w[4 * j + m], hv = h[(4 * j + m) & 7];
-        if (gp) {
-          o[8 * j + 2 * m] = q6_pair<true>(wv, hv, 0x0C010C00u, hs, ds);
-          o[8 * j + 2 * m + 1] = q6_pair<true>(wv, hv, 0x0C030C02u, hs, ds);
-        } else {
-          o[8 * j + 2 * m] = q6_pair<false>(wv, hv, 0x0C010C00u, hs, ds);
-          o[8 * j + 2 * m + 1] = q6_pair<false>(wv, hv, 0x0C030C02u, hs, ds);
-        }
+      for (int m = 0; m < 4; ++m) {                // dword i = 4 j + m: elements 4 i .. 4 i + 3
+        const int i = 4 * j + m;
+        const uint32_t wv = __builtin_amdgcn_alignbyte(ql[i + 1], ql[i], sh);
+        const uint32_t hv = __builtin_amdgcn_alignbyte(qh[(i & 7) + 1], qh[i & 7], sh);
+        const uint32_t hs = 4u * (uint32_t)gp + 2u * (uint32_t)(i >> 3);
+        // the two high bits of each byte to bits 4-5, then the nibble below them
+        const uint32_t h30 = (hs >= 4u ? (hv >> (hs - 4u)) : (hv << (4u - hs))) & 0x30303030u;
+        const uint32_t q6 = and_or_s(gp ? (wv >> 4) : wv, 0x0F0F0F0Fu, h30);
+        const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, q6, 0x04010400u)) - off;
+        const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, q6, 0x04030402u)) - off;
+        o[2 * i] = __builtin_bit_cast(uint32_t, a * ds);
+        o[2 * i + 1] = __builtin_bit_cast(uint32_t, b * ds);
       }
     }
     uint4* dd = reinterpret_cast<uint4*>(dst);
