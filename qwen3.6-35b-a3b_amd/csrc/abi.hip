@@ -312,6 +312,8 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
                                       sorted_pairs, K, H, I, S, st));
     if (dn_fmt == MOE_FMT_Q4_K && I >= 512)
       return moe_launch_gemm4_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st);
+    if (dn_fmt == MOE_FMT_Q6_K && moe_gemm7_down_supports(dn, (size_t)H * dn_row, H, I))
+      return moe_launch_gemm7_down(S, dn, (size_t)H * dn_row, tiles, max_tiles, offsets, H, I, y, y16, st);
     return moe_launch_gemm3_down(S, dn, dn_fmt, (size_t)H * dn_row, tiles, max_tiles, T, offsets, H, I, y, y16, st);
   }
   const int opb = path == MOE_PATH_MFMA_BF16;

@@ -106,6 +106,14 @@ int moe_launch_gemm4_gateup(const uint16_t* x16, const void* w_gate, const void*
 int moe_launch_gemm4_down(const uint16_t* S, const void* w_down, size_t expert_stride,
                           const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
                           void* y, int y16, hipStream_t st);
+// gemm7.hip: the Q6_K down GEMM in gemm4's form (decode in the MFMA waves, raw super-block bytes
+// in LDS half a super-block at a time); same tiles, arguments and results as gemm3's Q6_K down,
+// within f32 rounding (another k order). Supported when H % 256 == 0, I % 256 == 0 and the tensor
+// and its expert stride are 16-byte aligned (moe_gemm7_down_supports).
+bool moe_gemm7_down_supports(const void* w_down, size_t expert_stride, int H, int I);
+int moe_launch_gemm7_down(const uint16_t* S, const void* w_down, size_t expert_stride,
+                          const int32_t* tiles, int max_tiles, const int32_t* offsets, int H, int I,
+                          void* y, int y16, hipStream_t st);
 
 // The small-T shared expert's blocks (shared_small.h), appended to another launch's grid: gate/up
 // (with the scalar gate) in the single-launch router's, down in the gemm6 down launch's.

@@ -55,8 +55,11 @@ def test_small_and_large_tile_kernels_same_bits(pkg, layer_zipf, dev):
 
 
 def test_routed_experts_q6k_down(pkg, layer_q6k, dev):
+    """GEMV (path 1) and the 160-row MFMA kernels (path 2: Q6_K down decoded in the MFMA waves
+    from raw super-block bytes in LDS); at 600 Zipf-routed tokens the hot experts span several
+    tiles and end on a partial one."""
     lw, ow = layer_q6k
-    for T, path in ((2, 1), (96, 2)):
+    for T, path in ((2, 1), (96, 2), (600, 2)):
         x = pkg.synth.make_input(T, seed=7 + T, device=dev)
         r, gr = _route_and_group(pkg, lw, x)
         y = pkg.abi.experts(x, lw.gate_up_q, lw.gate_up_fmt, lw.down_q, lw.down_fmt, gr, 8, path)
