@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "moe_internal.h"
@@ -105,7 +106,9 @@ static Carve carve_sizes(int T, int H, int I, int E, int K, int Is) {
   c.hits = r256((size_t)(E + 1) * 4);
   c.sort_ws = moe_sort_ws_bytes((int)P, E);
   c.tiles = r256((size_t)(1 + 2 * moe_max_mtiles((int)P, E, MOE_GEMM6_BM)) * 4);
-  c.S = r256(P * I * 4);
+  // f32 rows (GEMV path) or f16 rows plus MOE_GEMM3_BM padding rows (the 160-row down kernels
+  // read whole tiles past the last row)
+  c.S = r256(std::max(P * I * 4, (P + MOE_GEMM3_BM) * I * 2));
   c.y = r256(P * H * 4);
   c.sS = r256((size_t)T * Is * 4);
   c.sraw = r256((size_t)T * H * 4);
@@ -275,7 +278,7 @@ static int experts_impl(const void* x, int x_dtype, const uint16_t* x16, const v
     if (!tiles) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
     MOE_TRY(moe_launch_build_tiles(offsets, hit_list, E, P, tiles, st, bm));
   }
-  uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)P * I * 2));
+  uint16_t* S = reinterpret_cast<uint16_t*>(w.take((size_t)(P + MOE_GEMM3_BM) * I * 2));
   if (!S) return moe_set_error(MOE_E_WORKSPACE, "moe_experts: workspace too small");
   if (gu4) {
     if (!x16) {

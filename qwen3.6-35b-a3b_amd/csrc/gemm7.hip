@@ -20,15 +20,16 @@
 //         chunk c ^ a_swz(m) (as gemm4.hip);
 //   R:    one half of the slab's 256 rows, 10 units per row: units 0-4 cover the 64 ql bytes, 5-7
 //         the 32 qh bytes, 8-9 the super-block's 16 scales and d. Unit i of row n sits at
-//         R + 4096 i + 16 slot(n); slot(n) transposes n's low five bits (8 x 4 -> 4 x 8), so 32
-//         lanes that read one dword each from rows n0 .. n0 + 31 (at offsets that follow n % 4)
-//         hit 32 different banks.
+//         R + 4096 i + 16 slot(n); slot(n) transposes n's low five bits (8 x 4 -> 4 x 8), so the
+//         32 lanes that read one dword each from rows n0, n0 + 2, .., n0 + 62 (at offsets that
+//         follow n % 4) hit 16 different banks (two lanes per bank).
 // A half starts when R and the step's A have landed: every lane copies its pieces out of R into
-// registers (lane (r, h) of wave w: rows n0 + r and n1 + r, n0 = 64 w, n1 = n0 + 32; ql bytes
-// 16 h .. 16 h + 15 and 32 + 16 h .. 32 + 16 h + 15, qh bytes 16 h .. 16 h + 15, the half's 8
-// scales and d), the waves meet at a barrier and request the next half into R, which then has two
-// K steps to land. A is requested one step ahead. k order inside a K step as gemm4.hip: substep ss
-// covers the 16-byte chunks 4 (ss >> 1) + (ss & 1) (lane half 0) and that + 2 (half 1).
+// registers (lane (r, h) of wave w: weight rows 64 w + 2 r and 64 w + 2 r + 1, so that it ends
+// with two adjacent output columns; ql bytes 16 h .. 16 h + 15 and 32 + 16 h .. 32 + 16 h + 15,
+// qh bytes 16 h .. 16 h + 15, the half's 8 scales and d), the waves meet at a barrier and request
+// the next half into R, which then has two K steps to land. A is requested one step ahead. k order
+// inside a K step as gemm4.hip: substep ss covers the 16-byte chunks 4 (ss >> 1) + (ss & 1) (lane
+// half 0) and that + 2 (half 1).
 // Decode (exact): per register of four elements, the two qh bits go to bits 4-5 of each byte and
 // the nibble below them; one perm per pair puts two 6-bit q under the f16 magic 0x6400 (1024 + q),
 // one packed subtract of 1056 leaves q - 32 and one packed multiply by f16(d * sc) (d * sc exact
@@ -47,6 +48,8 @@ using dma::wait_vm;
 using q4m::a_swz;
 using q4m::and_or_s;
 using q4m::mfma;
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = MOE_GEMM3_BM;            // 160 activation rows per tile
 constexpr int kMG = kBM / 32;                // MFMA row groups
@@ -103,34 +106,30 @@ __device__ __forceinline__ bool get_item(const int32_t* __restrict__ tiles,
 struct Addr {
   const uint8_t* wb;                    // the slab's first byte
   const uint8_t* ab;                    // the tile's first activation row
-  int last;                             // the tile's last row (rows past it repeat it)
 };
 
 __device__ __forceinline__ void item_addr(Addr& ad, const Item& it, const uint16_t* S,
                                           const uint8_t* wd, size_t estride, size_t rowb, int I) {
   ad.wb = wd + (size_t)it.e * estride + (size_t)it.col * kBN * rowb;
   ad.ab = reinterpret_cast<const uint8_t*>(S + (size_t)it.m0 * I);
-  ad.last = it.mend - it.m0 - 1;
 }
 
-// this wave's LDS addresses (slot 0 of A, unit 0 of R) and the weight row its R loads cover
+// this wave's LDS addresses (slot 0 of A, unit 0 of R), the weight row its R loads cover and its
+// A load offset: load j of thread t covers tile row t / 8 + 32 j, 16-byte chunk t % 8 of the
+// step's 128 bytes, stored at chunk position (t % 8) ^ a_swz(row) (a_swz(row + 32 j) = a_swz(row),
+// so load j adds 32 j rows to the uniform base). Rows past the tile are read as they are (the next
+// expert's rows, or the padding rows past S's last): they only reach output rows past the tile,
+// which the epilogue's stores drop.
 struct Ld {
-  uint32_t la, lr;
+  uint32_t la, lr, aoff;
   int nrow;
 };
 
-// A load j of thread t: tile row (t + 256 j) / 8 (clamped to the tile), 16-byte chunk
-// (t + 256 j) % 8 of the step's 128 bytes at chunk position chunk ^ a_swz(row); the offsets are
-// recomputed at each load rather than held across the item
 __device__ __forceinline__ void ld_a(const Ld& ld, const Addr& ad, int I, int slot, int ks) {
   const uint8_t* b = ad.ab + (size_t)ks * 128;
-  const int t = tid_fresh();
 #pragma unroll
-  for (int j = 0; j < kAI; ++j) {
-    const int u = t + 256 * j, m = u >> 3;
-    const uint32_t off = (uint32_t)min(m, ad.last) * (uint32_t)I * 2u + 16u * (uint32_t)((u & 7) ^ a_swz(m));
-    dma::load16(off, b, ld.la + slot * (kBM * 128) + j * 4096);
-  }
+  for (int j = 0; j < kAI; ++j)
+    dma::load16(ld.aoff + (uint32_t)(j * 64 * I), b, ld.la + slot * (kBM * 128) + j * 4096);
 }
 
 // half hf of super-block sb: unit i of this lane's row into R unit i
@@ -145,19 +144,18 @@ __device__ __forceinline__ void ld_r(const Ld& ld, const Addr& ad, int nsb, int 
 // one weight row's half, in registers: p0 / p1 = ql bytes 16 h .. + 15 / 32 + 16 h .. + 15,
 // hh = qh bytes 16 h .. + 15, sc = the half's 8 scales, d
 struct Row6 {
-  uint32_t p0[4], p1[4], hh[4], sc[2];
-  float d;
+  uint32_t p0[4], p1[4], hh[4];
+  f16x2_t ds[2];                        // part gp: {f16(d sc[4 gp + h]), f16(d sc[4 gp + 2 + h])}
 };
 
-// rows n (= n0 + r) and n + 32 of half hf of super-block sb out of R (byte offset o = 2 g mod 16
-// of super-block g = n nsb + sb within its first unit, the same for both rows)
+// rows n (= 64 w + 2 r) and n + 1 of half hf of super-block sb out of R (byte offset
+// o = 2 g mod 16 of super-block g = n nsb + sb within its first unit)
 template <int HF>
-__device__ __forceinline__ void stash(const uint8_t* R, int n, int nsb, int sb, int h, Row6& w0,
-                                      Row6& w1) {
+__device__ __forceinline__ void stash_row(const uint8_t* R, int n, int nsb, int sb, int h, Row6& w) {
   const int o = (2 * (n * nsb + sb)) & 15, q = o >> 2;
   const uint32_t sh = (uint32_t)(o & 3);
   const int base = 16 * slot_of(n);
-  // window dword q + t (t < 5) of a row: unit (q + t) / 4, dword (q + t) % 4 of that unit
+  // window dword q + t (t < 5) of the row: unit (q + t) / 4, dword (q + t) % 4 of that unit
   int a[5];
 #pragma unroll
   for (int t = 0; t < 5; ++t) a[t] = base + 4096 * ((q + t) >> 2) + 4 * ((q + t) & 3);
@@ -169,30 +167,20 @@ __device__ __forceinline__ void stash(const uint8_t* R, int n, int nsb, int sb, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) dst[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
   };
-  auto tail = [&](int off, Row6& w) {               // scales 8 hf .. 8 hf + 7 and d
-    uint32_t v[3];
+  piece(0, w.p0);
+  piece(2 * 4096, w.p1);
+  piece(5 * 4096, w.hh);
+  // scales 8 hf .. 8 hf + 7 (window dwords q + 2 hf ..) and d (window bytes 16, 17)
+  uint32_t v[3];
 #pragma unroll
-    for (int t = 0; t < 3; ++t) v[t] = rd(a[t + 2 * HF] + off);
-    w.sc[0] = __builtin_amdgcn_alignbyte(v[1], v[0], sh);
-    w.sc[1] = __builtin_amdgcn_alignbyte(v[2], v[1], sh);
-    w.d = f16_to_f32((rd(a[4] + off) >> (8 * sh)) & 0xFFFFu);
-  };
-  piece(0, w0.p0);
-  piece(2 * 4096, w0.p1);
-  piece(5 * 4096, w0.hh);
-  tail(8 * 4096, w0);
-  piece(512, w1.p0);
-  piece(512 + 2 * 4096, w1.p1);
-  piece(512 + 5 * 4096, w1.hh);
-  tail(512 + 8 * 4096, w1);
-}
-
-// f16(d * sc) of scale 4 gp + 2 j + h of the half, as a pair
-template <int GP>
-__device__ __forceinline__ f16x2_t q6_scale(const Row6& w, int j, int h) {
-  const int sc = (int)(int8_t)(w.sc[GP] >> (16 * j + 8 * h));
-  const _Float16 v = (_Float16)(w.d * (float)sc);
-  return (f16x2_t){v, v};
+  for (int t = 0; t < 3; ++t) v[t] = rd(a[t + 2 * HF] + 8 * 4096);
+  const uint32_t sc[2] = {__builtin_amdgcn_alignbyte(v[1], v[0], sh), __builtin_amdgcn_alignbyte(v[2], v[1], sh)};
+  const float d = f16_to_f32((rd(a[4] + 8 * 4096) >> (8 * sh)) & 0xFFFFu);
+  // f16(d * sc) of scales 4 gp + 2 j + h (d * sc exact in f32, rounded to f16 once)
+#pragma unroll
+  for (int gp = 0; gp < 2; ++gp)
+    w.ds[gp] = (f16x2_t){(_Float16)(d * (float)(int)(int8_t)(sc[gp] >> (8 * h))),
+                         (_Float16)(d * (float)(int)(int8_t)(sc[gp] >> (16 + 8 * h)))};
 }
 
 // the 8 f16 of substep ss's B fragment (chunk 4 (ss >> 1) + 2 h + (ss & 1) of part gp)
@@ -218,9 +206,11 @@ __device__ __forceinline__ uint4 q6_frag(const Row6& w, f16x2_t ds) {
 // the MFMAs of one K step (part gp of the stashed half) over NG row groups
 template <int NG, int GP>
 __device__ __forceinline__ void mma_step(const uint8_t* As, const int (&aoff)[4], const Row6& w0,
-                                         const Row6& w1, int h, f32x16_t (&acc)[kMG][2]) {
-  const f16x2_t d00 = q6_scale<GP>(w0, 0, h), d01 = q6_scale<GP>(w0, 1, h);
-  const f16x2_t d10 = q6_scale<GP>(w1, 0, h), d11 = q6_scale<GP>(w1, 1, h);
+                                         const Row6& w1, f32x16_t (&acc)[kMG][2]) {
+  const f16x2_t d00 = __builtin_shufflevector(w0.ds[GP], w0.ds[GP], 0, 0);
+  const f16x2_t d01 = __builtin_shufflevector(w0.ds[GP], w0.ds[GP], 1, 1);
+  const f16x2_t d10 = __builtin_shufflevector(w1.ds[GP], w1.ds[GP], 0, 0);
+  const f16x2_t d11 = __builtin_shufflevector(w1.ds[GP], w1.ds[GP], 1, 1);
   auto afrag = [&](int ss, uint4 (&a)[NG]) {
 #pragma unroll
     for (int mg = 0; mg < NG; ++mg) a[mg] = *reinterpret_cast<const uint4*>(As + aoff[ss] + 4096 * mg);
@@ -243,36 +233,31 @@ __device__ __forceinline__ void mma_step(const uint8_t* As, const int (&aoff)[4]
 }
 
 // ------------------------------------------------------------------------------- epilogue --
-// Y16: rows out as f16 (saturated to +-65504) instead of f32. Raw buffer stores whose descriptor
-// ends at the tile's last row drop the rows past it (the whole offset is in the VGPR operand).
-template <bool Y16>
+// Lane r of wave w holds output columns 64 w + 2 r (acc[.][0]) and 64 w + 2 r + 1 (acc[.][1]) of
+// rows 32 mg + 8 (i / 4) + 4 h + i % 4: one 4-byte store per row (Y16: the pair as f16, saturated
+// to +-65504) or one 8-byte store (f32). Raw buffer stores whose descriptor ends at the tile's
+// last row drop the rows past it (the whole offset is in the VGPR operand).
+template <bool Y16, int NG>
 __device__ __forceinline__ void epilogue(void* y, int H, const Item& it, int wave, int lane,
                                          const f32x16_t (&acc)[kMG][2]) {
   constexpr int kB = Y16 ? 2 : 4;
   char* yb = reinterpret_cast<char*>(y) + (size_t)it.m0 * H * kB;
   const __amdgpu_buffer_rsrc_t rs = dma::rsrc(yb, (it.mend - it.m0) * H * kB);
   const int rsb = opaque(H * kB);
-  const int lane_off = (4 * (lane >> 5) * H + it.col * kBN + 64 * wave + (lane & 31)) * kB;
+  const int lane_off = (4 * (lane >> 5) * H + it.col * kBN + 64 * wave + 2 * (lane & 31)) * kB;
 #pragma unroll
-  for (int mg = 0; mg < kMG; ++mg) {
+  for (int mg = 0; mg < NG; ++mg) {
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int vo = lane_off + (32 * mg + 8 * rq) * rsb;
-#pragma unroll
-      for (int r3 = 0; r3 < 4; ++r3) {
-        const int r = 4 * rq + r3;
-        float v0 = acc[mg][0][r], v1 = acc[mg][1][r];
-        if constexpr (Y16) {
-          v0 = fminf(fmaxf(v0, -65504.0f), 65504.0f);
-          v1 = fminf(fmaxf(v1, -65504.0f), 65504.0f);
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v0), rs,
-                                                vo + r3 * rsb, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v1), rs,
-                                                vo + r3 * rsb + 64, 0, 0);
-        } else {
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v0), rs, vo + r3 * rsb, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v1), rs, vo + r3 * rsb + 128, 0, 0);
-        }
+    for (int i = 0; i < 16; ++i) {
+      const int vo = lane_off + (32 * mg + 8 * (i >> 2) + (i & 3)) * rsb;
+      const float v0 = acc[mg][0][i], v1 = acc[mg][1][i];
+      if constexpr (Y16) {
+        const f16x2_t p = {(_Float16)__builtin_amdgcn_fmed3f(v0, -65504.0f, 65504.0f),
+                           (_Float16)__builtin_amdgcn_fmed3f(v1, -65504.0f, 65504.0f)};
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, p), rs, vo, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, (float2_t){v0, v1}), rs,
+                                              vo, 0, 0);
       }
     }
   }
@@ -287,18 +272,21 @@ __device__ __forceinline__ void epilogue(void* y, int H, const Item& it, int wav
 // item's A(0), or a repeat). Every step thus issues the same loads and the vmcnt counts are
 // constants; before an item's first step the previous item's epilogue stores are the newest
 // operations.
-template <int NG>
+template <int NG, bool Y16>
 __device__ __forceinline__ void run_item(const Ld& ld, const Addr& ca, const Addr& na, bool has_next,
-                                         bool first, int nsb, int I, int wave, Smem& sm,
-                                         f32x16_t (&acc)[kMG][2]) {
+                                         bool first, int nsb, int I, int H, void* y, const Item& it,
+                                         int wave, Smem& sm) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, r = lane & 31;
-  const int n = 64 * wave + r;
+  const int n = 64 * wave + 2 * r;
   int aoff[4];
 #pragma unroll
   for (int ss = 0; ss < 4; ++ss)
     aoff[ss] = 16 * (8 * r + ((4 * (ss >> 1) + 2 * h + (ss & 1)) ^ a_swz(r)));
   const uint8_t* R = sm.R[0];
+  f32x16_t acc[kMG][2];
+#pragma unroll
+  for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
   Row6 w0, w1;
   for (int sb = 0; sb < nsb; ++sb) {
     const bool last_sb = sb == nsb - 1;
@@ -307,43 +295,47 @@ __device__ __forceinline__ void run_item(const Ld& ld, const Addr& ca, const Add
     if (sb == 0 && !first) wait_vm<kStoreWait>(); else wait_vm<0>();
     __syncthreads();
     ld_a(ld, ca, I, 1, ks + 1);
-    stash<0>(R, n, nsb, sb, h, w0, w1);
+    stash_row<0>(R, n, nsb, sb, h, w0);
+    stash_row<0>(R, n + 1, nsb, sb, h, w1);
     __syncthreads();
     ld_r<1>(ld, ca, nsb, sb);
-    mma_step<NG, 0>(sm.A[0], aoff, w0, w1, h, acc);
+    mma_step<NG, 0>(sm.A[0], aoff, w0, w1, acc);
     // ---- half 0, part 1
     wait_vm<kRU>();
     __syncthreads();
     ld_a(ld, ca, I, 0, ks + 2);
-    mma_step<NG, 1>(sm.A[1], aoff, w0, w1, h, acc);
+    mma_step<NG, 1>(sm.A[1], aoff, w0, w1, acc);
     // ---- half 1, part 0
     wait_vm<0>();
     __syncthreads();
     ld_a(ld, ca, I, 1, ks + 3);
-    stash<1>(R, n, nsb, sb, h, w0, w1);
+    stash_row<1>(R, n, nsb, sb, h, w0);
+    stash_row<1>(R, n + 1, nsb, sb, h, w1);
     __syncthreads();
     if (!last_sb) ld_r<0>(ld, ca, nsb, sb + 1);
     else if (has_next) ld_r<0>(ld, na, nsb, 0);
     else ld_r<0>(ld, ca, nsb, sb);
-    mma_step<NG, 0>(sm.A[0], aoff, w0, w1, h, acc);
+    mma_step<NG, 0>(sm.A[0], aoff, w0, w1, acc);
     // ---- half 1, part 1
     wait_vm<kRU>();
     __syncthreads();
     if (!last_sb) ld_a(ld, ca, I, 0, ks + 4);
     else if (has_next) ld_a(ld, na, I, 0, 0);
     else ld_a(ld, ca, I, 0, ks + 3);
-    mma_step<NG, 1>(sm.A[1], aoff, w0, w1, h, acc);
+    mma_step<NG, 1>(sm.A[1], aoff, w0, w1, acc);
   }
+  epilogue<Y16, NG>(y, H, it, wave, lane, acc);
 }
 
+template <bool Y16>
 __device__ __forceinline__ void run_n(int ng, const Ld& ld, const Addr& ca, const Addr& na,
-                                      bool has_next, bool first, int nsb, int I, int wave, Smem& sm,
-                                      f32x16_t (&acc)[kMG][2]) {
-  if (ng >= 5) run_item<5>(ld, ca, na, has_next, first, nsb, I, wave, sm, acc);
-  else if (ng == 4) run_item<4>(ld, ca, na, has_next, first, nsb, I, wave, sm, acc);
-  else if (ng == 3) run_item<3>(ld, ca, na, has_next, first, nsb, I, wave, sm, acc);
-  else if (ng == 2) run_item<2>(ld, ca, na, has_next, first, nsb, I, wave, sm, acc);
-  else run_item<1>(ld, ca, na, has_next, first, nsb, I, wave, sm, acc);
+                                      bool has_next, bool first, int nsb, int I, int H, void* y,
+                                      const Item& it, int wave, Smem& sm) {
+  if (ng >= 5) run_item<5, Y16>(ld, ca, na, has_next, first, nsb, I, H, y, it, wave, sm);
+  else if (ng == 4) run_item<4, Y16>(ld, ca, na, has_next, first, nsb, I, H, y, it, wave, sm);
+  else if (ng == 3) run_item<3, Y16>(ld, ca, na, has_next, first, nsb, I, H, y, it, wave, sm);
+  else if (ng == 2) run_item<2, Y16>(ld, ca, na, has_next, first, nsb, I, H, y, it, wave, sm);
+  else run_item<1, Y16>(ld, ca, na, has_next, first, nsb, I, H, y, it, wave, sm);
 }
 
 }  // namespace g7
@@ -368,6 +360,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   ld.la = dma::lds_addr(sm.A[0]) + 1024 * wave;
   ld.lr = dma::lds_addr(sm.R[0]) + 1024 * wave;
   ld.nrow = row_of(64 * wave + lane);
+  {
+    const int t = tid_fresh(), m = t >> 3;
+    ld.aoff = (uint32_t)m * (uint32_t)I * 2u + 16u * (uint32_t)((t & 7) ^ a_swz(m));
+  }
   Addr ca;
   item_addr(ca, cur, S, wd, estride, rowb, I);
   ld_r<0>(ld, ca, nsb, 0);
@@ -379,12 +375,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!has_next) nx = cur;
     Addr na;
     item_addr(na, nx, S, wd, estride, rowb, I);
-    f32x16_t acc[kMG][2];
-#pragma unroll
-    for (int mg = 0; mg < kMG; ++mg) { acc[mg][0] = (f32x16_t){}; acc[mg][1] = (f32x16_t){}; }
     const int ng = __builtin_amdgcn_readfirstlane((cur.mend - cur.m0 + 31) >> 5);
-    run_n(ng, ld, ca, na, has_next, first, nsb, I, wave, sm, acc);
-    epilogue<Y16>(y, H, cur, wave, lane, acc);
+    run_n<Y16>(ng, ld, ca, na, has_next, first, nsb, I, H, y, cur, wave, sm);
     if (!has_next) break;
     cur = nx;
     ca = na;
