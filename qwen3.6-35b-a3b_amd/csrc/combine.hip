@@ -134,6 +134,89 @@ __global__ __launch_bounds__(256) void k_combine4(const void* __restrict__ y,
                   comb_out(rs.z, acc.z, gp, sr.z), comb_out(rs.w, acc.w, gp, sr.w));
 }
 
+
+// The block forward's f16 rows, eight columns per thread (H % 8 == 0): one 16-byte non-temporal
+// load per expert row (each row is read once), the same sums in the same order as k_combine4.
+// grid = (T, ceil(H / 2048)), block = 256.
+template <int KK>
+__global__ __launch_bounds__(256) void k_combine8(const void* __restrict__ y,
+                                                  const int32_t* __restrict__ pair_pos,
+                                                  const int32_t* __restrict__ ids,
+                                                  const uint16_t* __restrict__ w_bf16,
+                                                  const float* __restrict__ shared_raw,
+                                                  const float* __restrict__ gate_prob,
+                                                  const float* __restrict__ residual, int T,
+                                                  int H, float* __restrict__ out,
+                                                  float* __restrict__ routed_sum,
+                                                  float* __restrict__ shared_out,
+                                                  float* __restrict__ expert_raw) {
+  __shared__ int s_pos[KK], s_slot[KK];
+  __shared__ float s_w[KK];
+  const int t = blockIdx.x;
+  if (threadIdx.x < KK) {
+    const int k = threadIdx.x;
+    const int32_t* tid = ids + (size_t)t * KK;
+    const int id = tid[k];
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < KK; ++j) {
+      const int o = tid[j];
+      rank += (o < id) || (o == id && j < k);
+    }
+    s_pos[rank] = pair_pos[(size_t)t * KK + k];
+    s_slot[rank] = k;
+    s_w[rank] = bf16_to_f32(w_bf16[(size_t)t * KK + k]);
+  }
+  __syncthreads();
+  const int h = (blockIdx.y * 256 + threadIdx.x) * 8;
+  if (h >= H) return;
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  u32x4v q[KK];
+#pragma unroll
+  for (int j = 0; j < KK; ++j) {
+    const int pos = s_pos[j];
+    q[j] = pos < 0 ? (u32x4v){0u, 0u, 0u, 0u}
+                   : __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(reinterpret_cast<const uint16_t*>(y) + (size_t)pos * H + h));
+  }
+  const size_t o = (size_t)t * H + h;
+  const float4 sr0 = *reinterpret_cast<const float4*>(shared_raw + o);
+  const float4 sr1 = *reinterpret_cast<const float4*>(shared_raw + o + 4);
+  const float4 rs0 = residual ? *reinterpret_cast<const float4*>(residual + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 rs1 = residual ? *reinterpret_cast<const float4*>(residual + o + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float gp = gate_prob[t];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < KK; ++j) {
+    const float w = s_w[j];
+    const uint32_t u[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = f16_to_f32(u[i] & 0xFFFFu); v[2 * i + 1] = f16_to_f32(u[i] >> 16); }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = comb_madd(acc[i], w, v[i]);
+    if (expert_raw) {
+      float* er = expert_raw + ((size_t)t * KK + s_slot[j]) * H + h;
+      *reinterpret_cast<float4*>(er) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(er + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  }
+  const float sr[8] = {sr0.x, sr0.y, sr0.z, sr0.w, sr1.x, sr1.y, sr1.z, sr1.w};
+  const float rs[8] = {rs0.x, rs0.y, rs0.z, rs0.w, rs1.x, rs1.y, rs1.z, rs1.w};
+  if (routed_sum) {
+    *reinterpret_cast<float4*>(routed_sum + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(routed_sum + o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+  if (shared_out) {
+    *reinterpret_cast<float4*>(shared_out + o) = make_float4(gp * sr[0], gp * sr[1], gp * sr[2], gp * sr[3]);
+    *reinterpret_cast<float4*>(shared_out + o + 4) = make_float4(gp * sr[4], gp * sr[5], gp * sr[6], gp * sr[7]);
+  }
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = comb_out(rs[i], acc[i], gp, sr[i]);
+  *reinterpret_cast<float4*>(out + o) = make_float4(r[0], r[1], r[2], r[3]);
+  *reinterpret_cast<float4*>(out + o + 4) = make_float4(r[4], r[5], r[6], r[7]);
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -148,6 +231,12 @@ int moe_launch_combine(const void* y, int y16, const int32_t* pair_pos, const in
     if (K != 8 || H % 4 || !a16(y) || !a16(shared_raw) || !a16(residual) || !a16(out) ||
         !a16(routed_sum) || !a16(shared_out) || !a16(expert_raw))
       return moe_set_error(MOE_E_UNSUPPORTED, "combine: f16 expert rows need K == 8, H %% 4 == 0 and 16-byte aligned rows");
+    if (H % 8 == 0) {
+      dim3 grid(T, (H + 2047) / 2048);
+      hipLaunchKernelGGL((k_combine8<8>), grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16,
+                         shared_raw, gate_prob, residual, T, H, out, routed_sum, shared_out, expert_raw);
+      return moe_check_launch("combine");
+    }
     dim3 grid(T, (H + 1023) / 1024);
     hipLaunchKernelGGL((k_combine4<8, true>), grid, dim3(256), 0, st, y, pair_pos, ids, w_bf16,
                        shared_raw, gate_prob, residual, T, H, out, routed_sum, shared_out, expert_raw);
