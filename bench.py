@@ -708,7 +708,7 @@ def main():
 
     def one_token():
         # the residual stream through L layers: h <- h + MoE(rmsnorm(h)), in place; each call
-        # names the next layer so its routing-independent weights are warmed into L2
+        # names the next layer so its router rows and norm weight are warmed into L2
         for l, (lw, nw) in enumerate(zip(layers, norms)):
             abi.block_forward(xbuf, lw, out=xbuf, residual=xbuf, norm_w=nw,
                               next_layer=None if args.no_hint else layers[(l + 1) % L],

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 2
+#define MOE_ABI_VERSION 3
 
 enum {
   MOE_OK = 0,
@@ -192,8 +192,8 @@ typedef struct moe_layer_weights {
  * optional next-layer hint (next: as moe_block_forward_prefetch, the router rows and norm weight of
  * a bf16-router next layer). Same outputs, limits and errors as moe_block_forward. The
  * single-launch decode layer takes a bf16 or f32 router and scalar gate, Q4_K gate/up (fused or
- * split), Q4_K, Q5_K or Q6_K down, and a bf16 or Q8_0 shared expert. The next
- * layer's router rows (bf16 or f32) and norm weight are the L2 warm-up hint.
+ * split), Q4_K, Q5_K or Q6_K down, and a bf16 or Q8_0 shared expert. Of `next` only the router
+ * rows (w_router, router_dtype: bf16 or f32) and norm_w are read, as the L2 warm-up hint.
  * Replaces engine/m3_forward.py:430-476 and engine/block_forward.py:670-681 on the policy-A
  * weights (engine/block_forward.py:211-231). */
 int moe_block_forward_w(const void *x, int x_dtype, int T, int H, int I, int E, int K, int I_s,
@@ -203,23 +203,20 @@ int moe_block_forward_w(const void *x, int x_dtype, int T, int H, int I, int E, 
                         float *expert_raw, void *ws, size_t ws_bytes, void *stream,
                         const moe_layer_weights *next);
 
-/* The routing-independent weights of the layer that the same stream runs next (its router, its
- * shared expert and the shared expert's scalar gate, its post-attention norm weight; shapes as in
- * moe_block_forward). */
+/* The weights of the layer that the same stream runs next that its routing waits on: its router
+ * rows and its post-attention norm weight (shapes as in moe_block_forward). The next layer's
+ * shared expert is not named: its rows have slack in that layer (requested at its first barrier,
+ * off the routing chain), and warming them here measured slower (the extra 6.3 MB of misses
+ * delay this layer's last exchange more than they save). */
 typedef struct moe_next_layer {
   const void *w_router;         /* [E,H] bf16 */
-  const void *ws_gate, *ws_up;  /* [I_s,H] bf16 */
-  const void *ws_down;          /* [H,I_s] bf16 */
-  const void *ws_scalar_gate;   /* [H] bf16 */
   const float *norm_w;          /* [H] f32, or NULL when the next call passes no norm weight */
 } moe_next_layer;
 
-/* moe_block_forward with a hint: `next` (may be NULL) names the next layer's routing-independent
- * weights. The single-launch decode layer then reads, at the end of its run, the parts of them
- * that the next layer's routing waits on (each workgroup's router rows and the norm weight), so
- * that they come from the L2 of the same XCD instead of HBM; the shared-expert fields are
- * accepted and not read at present (they have slack in the next layer). Other paths ignore the
- * hint. Results are identical with or without it.
+/* moe_block_forward with a hint: `next` (may be NULL) names the next layer's router rows and norm
+ * weight. The single-launch decode layer then reads them at the end of its run (each workgroup its
+ * own router rows), so that they come from the L2 of the same XCD instead of HBM. Other paths
+ * ignore the hint. Results are identical with or without it.
  * Same arguments, limits and errors as moe_block_forward otherwise. Replaces, like
  * moe_block_forward, engine/m3_forward.py:430-476 in its layer loop (engine/m3_forward.py:714-737),
  * where the next layer's weights are known ahead of its input. */

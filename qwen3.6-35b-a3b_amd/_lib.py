@@ -60,10 +60,8 @@ class LayerWeightsC(ctypes.Structure):
 
 
 class NextLayer(ctypes.Structure):
-    """moe_next_layer: the routing-independent weights of the layer the stream runs next."""
-    _fields_ = [("w_router", ctypes.c_void_p), ("ws_gate", ctypes.c_void_p),
-                ("ws_up", ctypes.c_void_p), ("ws_down", ctypes.c_void_p),
-                ("ws_scalar_gate", ctypes.c_void_p), ("norm_w", ctypes.c_void_p)]
+    """moe_next_layer: the router rows and norm weight of the layer the stream runs next."""
+    _fields_ = [("w_router", ctypes.c_void_p), ("norm_w", ctypes.c_void_p)]
 
 
 # every symbol include/moe_gfx950.h declares, with its ctypes signature

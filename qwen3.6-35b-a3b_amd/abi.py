@@ -278,7 +278,7 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
     input = x, or the post-attention RMSNorm of x when `norm_w` (f32 [H], the artifact's 1+w) is
     given: engine/m3_forward.py:732-737 is then block_forward(x1, lw, norm_w=w, residual=x1).
     `next_layer` (a LayerWeights, optional) is the layer this stream runs next and `next_norm_w`
-    its norm weight: their routing-independent weights are warmed into L2 by the single-launch
+    its norm weight: its router rows and that norm weight are warmed into L2 by the single-launch
     decode layer (moe_block_forward_prefetch); results do not depend on them. Weights in other
     widths than the bf16 router / fused gate_up / bf16 scalar gate (the artifact's F32 router and
     scalar gate, separate gate and up tensors) go through moe_block_forward_w."""
@@ -330,15 +330,10 @@ def block_forward(x: torch.Tensor, lw, path: int = L.MOE_PATH_AUTO, stages=False
         _check(L.lib.moe_block_forward(*args), "block_forward")
     else:
         nl = next_layer
-        for name, t in (("next router", nl.router), ("next shared_gate", nl.shared_gate),
-                        ("next shared_up", nl.shared_up), ("next shared_down", nl.shared_down),
-                        ("next shared_scalar_gate", nl.shared_scalar_gate)):
-            _need(t, name, device=dev)
+        _need(nl.router, "next router", device=dev)
         if next_norm_w is not None:
             _need(next_norm_w, "next_norm_w", torch.float32, (H,), dev)
-        hint = L.NextLayer(nl.router.data_ptr(), nl.shared_gate.data_ptr(), nl.shared_up.data_ptr(),
-                           nl.shared_down.data_ptr(), nl.shared_scalar_gate.data_ptr(),
-                           None if next_norm_w is None else next_norm_w.data_ptr())
+        hint = L.NextLayer(nl.router.data_ptr(), None if next_norm_w is None else next_norm_w.data_ptr())
         _check(L.lib.moe_block_forward_prefetch(*args, ctypes.byref(hint)), "block_forward")
     st["combined_out"] = out
     return st

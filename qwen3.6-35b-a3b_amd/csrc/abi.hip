@@ -756,7 +756,7 @@ int moe_block_forward_prefetch(const void* x, int x_dtype, int T, int H, int I, 
   moe_layer_weights N{};
   if (next)
     N = bf16_layer(next->norm_w, next->w_router, nullptr, nullptr, MOE_FMT_Q4_K, nullptr, MOE_FMT_Q4_K,
-                   next->ws_gate, next->ws_up, next->ws_down, next->ws_scalar_gate);
+                   nullptr, nullptr, nullptr, nullptr);
   return block_forward_impl(x, x_dtype, T, H, I, E, K, I_s, W, norm_eps, path, residual, out, logits_bf16,
                             topk_ids, topk_w_bf16, topk_w_f32, routed_sum, shared_out, gate_prob,
                             expert_raw, ws, ws_bytes, stream, next ? &N : nullptr);

@@ -272,7 +272,7 @@ def test_batched_with_post_attention_norm(pkg, layer_zipf, dev, path):
 
 
 def test_decode_next_layer_hint_same_bits(pkg, layer_c0, layer_zipf, dev):
-    """moe_block_forward_prefetch (the next layer's routing-independent weights warmed into the
+    """moe_block_forward_prefetch (the next layer's router rows and norm weight warmed into the
     L2 of the XCD that reads them first) gives the same bits as moe_block_forward, through a
     two-layer chain h <- h + MoE(rmsnorm(h)) run for several tokens."""
     lw0, _ = layer_c0
