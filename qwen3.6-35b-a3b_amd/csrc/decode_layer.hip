@@ -21,8 +21,8 @@
 //   phase 2  wait for the XCD's 256 logits; R2-R5 (same answer everywhere); routed gate/up rows of
 //            slot x, i in [16r, 16r+16), its down rows requested ahead of use;
 //            shared-down partial over the XCD's 64 i-values for rows h in [64r, 64r+64)
-//   phase 3  wait for slot x's 512 activations (XCD-local); down rows h in [64r, 64r+64) (Q4_K rows
-//            on the activations' int8 digit planes)
+//   phase 3  wait for slot x's 512 activations (XCD-local); down rows h in [64r, 64r+64) (Q4_K, Q5_K
+//            rows on the activations' int8 digit planes)
 //   phase 4  wg (x, r) combines rows [8j, 8j+8), j = 32x + r: the 8 slots' outputs in ascending
 //            expert id, the 8 shared-down partials in ascending x, gate, residual
 //   (hint)   with the next layer's weights named, waves 4-7 read the router rows and the norm
@@ -156,17 +156,18 @@ __device__ __forceinline__ uint4 xload4(__amdgpu_buffer_rsrc_t r, int off) {
 }
 __device__ __forceinline__ bool xfull(uint4 v) { return v.x && v.y && v.z && v.w; }
 
-// ------------------------------------------------------------ activation digit planes (Q4_K) --
-// The Q4_K down rows' dot products (phase 3, right after the slot activations arrive) run on
-// v_dot4_i32_i8: 1.1 VALU operations per weight instead of 2.25 (a byte convert and an f32 FMA per
-// nibble), which took 0.4 us off the launch. The activations of each 16-element group become
-// three balanced base-256 digit planes: with e the group's exponent (every |v| < 2^e; 0 for
+// ----------------------------------------------------- activation digit planes (down rows) --
+// The Q4_K and Q5_K down rows' dot products (phase 3, right after the slot activations arrive)
+// run on v_dot4_i32_i8: 1.1 VALU operations per weight instead of 2.25 (a byte convert and an f32
+// FMA per nibble), which took 0.4 us off the launch. The activations of each 16-element group
+// become three balanced base-256 digit planes: with e the group's exponent (every |v| < 2^e; 0 for
 // an all-zero group), N = rint(v 2^(22-e)) is an integer with |N| <= 2^22, and
-// N = 65536 D0 + 256 D1 + D2 with D1, D2 in [-128, 127] and |D0| <= 64. For the 16 nibbles q of a
+// N = 65536 D0 + 256 D1 + D2 with D1, D2 in [-128, 127] and |D0| <= 64. For the 16 quants q of a
 // sub-block, sum q v = 2^(e-22) (65536 S0 + 256 S1 + S2) + err, where S_p = sum q D_p is exact in
-// int32 (the combination stays below 2^31) and |err| <= 60 2^(e-22): half a unit of N per element
-// times q <= 15, the order of an f32 multiply-add chain over the group. The min term uses the
-// group's float sum, so a NaN or infinite activation still reaches the output.
+// int32 (the combination stays below 2^31) and |err| <= 8 qmax 2^(e-22) (half a unit of N per
+// element; qmax = 15 for Q4_K, 31 for Q5_K), the order of an f32 multiply-add chain over the
+// group. The min term uses the group's float sum, so a NaN or infinite activation still reaches
+// the output.
 // digits of 4 consecutive values: byte i of dword p holds D_p of value i
 __device__ __forceinline__ void digits4(const float (&v)[4], int e, uint32_t (&w)[3]) {
   w[0] = w[1] = w[2] = 0u;
@@ -188,12 +189,16 @@ __device__ __forceinline__ int group_exp(float m) {
   (void)frexpf(m, &e);
   return e;
 }
-// q4k_chunk_dot (gemv_dev.h) on digit planes: the lane's 16-byte chunk (sub-blocks 2g, low nibbles, and 2g+1,
-// high nibbles) against its two activation groups (planes zl / zh, exponents el / eh, float sums
-// sl / sh for the min terms); the 6-bit scales as in q4k_chunk_dot
-__device__ __forceinline__ float q4k_chunk_dot_dig(uint4 hdr, uint4 qs, int g, const uint4 (&zl)[3],
-                                                   const uint4 (&zh)[3], int el, int eh, float sl,
-                                                   float sh) {
+// The K-quant chunk dot on digit planes: the lane's 16-byte chunk covers sub-blocks 2g (its low
+// nibbles) and 2g+1 (high nibbles); lo[i] / hi[i] hold the q values of elements 4i .. 4i+3 of the
+// two sub-blocks as bytes (Q4_K: the nibbles; Q5_K: with the 5th bit at bit 4, q <= 31, so the
+// combination 65536 S0 + 256 S1 + S2 stays below 2^31). zl / zh are the planes of the two
+// activation groups (exponents el / eh, float sums sl / sh for the min terms); the 6-bit scales
+// as in q4k_chunk_dot (gemv_dev.h).
+__device__ __forceinline__ float kquant_chunk_dot_dig(uint4 hdr, const uint32_t (&lo)[4],
+                                                      const uint32_t (&hi)[4], int g,
+                                                      const uint4 (&zl)[3], const uint4 (&zh)[3],
+                                                      int el, int eh, float sl, float sh) {
   const float d = f16_to_f32(hdr.x & 0xFFFFu), dmin = f16_to_f32(hdr.x >> 16);
   const uint32_t sh0 = 16u * (uint32_t)(g & 1), sh1 = sh0 + 8u;
   const uint32_t low = 0u - (uint32_t)(g < 2);
@@ -203,22 +208,41 @@ __device__ __forceinline__ float q4k_chunk_dot_dig(uint4 hdr, uint4 qs, int g, c
   const uint32_t m0 = ((z0 & 63u) & low) | ((((w0 >> 4) & 15u) | ((z0 >> 2) & 48u)) & ~low);
   const uint32_t sc1 = ((y1 & 63u) & low) | (((w1 & 15u) | ((y1 >> 2) & 48u)) & ~low);
   const uint32_t m1 = ((z1 & 63u) & low) | ((((w1 >> 4) & 15u) | ((z1 >> 2) & 48u)) & ~low);
-  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
   int s[2][3] = {{0, 0, 0}, {0, 0, 0}};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = and_opaque(w[i], 0x0F0F0F0Fu), hi = and_opaque(w[i] >> 4, 0x0F0F0F0Fu);
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
       const uint32_t al[4] = {zl[p].x, zl[p].y, zl[p].z, zl[p].w};
       const uint32_t ah[4] = {zh[p].x, zh[p].y, zh[p].z, zh[p].w};
-      s[0][p] = __builtin_amdgcn_sdot4((int)lo, (int)al[i], s[0][p], false);
-      s[1][p] = __builtin_amdgcn_sdot4((int)hi, (int)ah[i], s[1][p], false);
+      s[0][p] = __builtin_amdgcn_sdot4((int)lo[i], (int)al[i], s[0][p], false);
+      s[1][p] = __builtin_amdgcn_sdot4((int)hi[i], (int)ah[i], s[1][p], false);
     }
   }
   const float fl = ldexpf((float)(s[0][0] * 65536 + s[0][1] * 256 + s[0][2]), el - 22);
   const float fh = ldexpf((float)(s[1][0] * 65536 + s[1][1] * 256 + s[1][2]), eh - 22);
   return d * ((float)sc0 * fl + (float)sc1 * fh) - dmin * ((float)m0 * sl + (float)m1 * sh);
+}
+// the q bytes of a Q4_K chunk (qs) and of a Q5_K chunk (qs and the qh bytes of its element
+// positions, the 5th bits placed as in q5k_chunk_dot)
+__device__ __forceinline__ void q4k_bytes(uint4 qs, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo[i] = and_opaque(w[i], 0x0F0F0F0Fu);
+    hi[i] = and_opaque(w[i] >> 4, 0x0F0F0F0Fu);
+  }
+}
+__device__ __forceinline__ void q5k_bytes(uint4 qs, uint4 qh, int g, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+  const uint32_t h[4] = {qh.x, qh.y, qh.z, qh.w};
+  const uint32_t hs = 2u * (uint32_t)g;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t hb = h[i] >> hs;
+    lo[i] = and_opaque(w[i], 0x0F0F0F0Fu) | ((hb << 4) & 0x10101010u);
+    hi[i] = and_opaque(w[i] >> 4, 0x0F0F0F0Fu) | ((hb << 3) & 0x10101010u);
+  }
 }
 
 // one 16-byte group at byte offset `off` of the buffer, same protocol
@@ -460,7 +484,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ float s_x[H];
   __shared__ TopkLds tk;                 // the exact replay's scratch (ties only)
   __shared__ float s_k[I];               // routed activations of this XCD's slot
-  // digit planes, exponents and float sums of the 16-element groups of s_k (Q4_K down dots)
+  // digit planes, exponents and float sums of the 16-element groups of s_k (Q4_K and Q5_K down dots)
   __shared__ uint4 s_kd[3][I / 16];
   __shared__ int s_ke[I / 16];
   __shared__ float s_ks[I / 16];
@@ -871,7 +895,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     const uint4 v = lwait4(xr, 4 * (XW_SR + I * x) + 16 * t, sp);
     const float f[4] = {xdec(v.x), xdec(v.y), xdec(v.z), xdec(v.w)};
     reinterpret_cast<float4*>(s_k)[t] = make_float4(f[0], f[1], f[2], f[3]);
-    if constexpr (DFMT == MOE_FMT_Q4_K) {
+    if constexpr (DFMT == MOE_FMT_Q4_K || DFMT == MOE_FMT_Q5_K) {
       // the digit planes of the slot's activations: group t / 4 is the quad of lanes 4g .. 4g+3
       // (waves 0-1 whole, so the quad moves see every lane); its float sum in element order
       float m = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
@@ -909,32 +933,21 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     // both rows before either store: a load wait placed after an agent-scope store would also
     // wait for that store's write-through (vmcnt counts both)
     float v[2];
-    if constexpr (DFMT == MOE_FMT_Q4_K) {
-      const int glo = 16 * b + 4 * gq + (l0 >> 4), ghi = glo + 2;
-      uint4 zl[3], zh[3];
+    const int glo = 16 * b + 4 * gq + (l0 >> 4), ghi = glo + 2;
+    uint4 zl[3], zh[3];
 #pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        zl[p] = s_kd[p][glo];
-        zh[p] = s_kd[p][ghi];
-      }
-      const int el = s_ke[glo], eh = s_ke[ghi];
-      const float sl = s_ks[glo], sh = s_ks[ghi];
+    for (int p = 0; p < 3; ++p) {
+      zl[p] = s_kd[p][glo];
+      zh[p] = s_kd[p][ghi];
+    }
+    const int el = s_ke[glo], eh = s_ke[ghi];
+    const float sl = s_ks[glo], sh = s_ks[ghi];
 #pragma unroll
-      for (int pass = 0; pass < 2; ++pass)
-        v[pass] = row16_sum_f32(q4k_chunk_dot_dig(dh[pass], dq[pass], gq, zl, zh, el, eh, sl, sh));
-    } else {
-      const float* sp = s_k + 256 * b + 64 * gq + l0;
-      float xl[16], xh[16], sxl = 0.0f, sxh = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        xl[i] = sp[i];
-        xh[i] = sp[32 + i];
-        sxl += xl[i];
-        sxh += xh[i];
-      }
-#pragma unroll
-      for (int pass = 0; pass < 2; ++pass)
-        v[pass] = row16_sum_f32(q5k_chunk_dot(dh[pass], dq[pass], dqh[pass], gq, xl, xh, sxl, sxh));
+    for (int pass = 0; pass < 2; ++pass) {
+      uint32_t lo[4], hi[4];
+      if (DFMT == MOE_FMT_Q5_K) q5k_bytes(dq[pass], dqh[pass], gq, lo, hi);
+      else q4k_bytes(dq[pass], lo, hi);
+      v[pass] = row16_sum_f32(kquant_chunk_dot_dig(dh[pass], lo, hi, gq, zl, zh, el, eh, sl, sh));
     }
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
