@@ -18,8 +18,10 @@
 //   phase 1  wg (x, r): router logits e in [8r, 8r+8) (one wave each; f64, certified bf16), so
 //            each XCD computes all 256 logits itself | shared gate/up rows i = 64x + 2r (+1) |
 //            the scalar shared gate p (every workgroup, for its own combine rows)
-//   phase 2  wait for the XCD's 256 logits; R2-R5 (same answer everywhere); routed gate/up rows of
-//            slot x, i in [16r, 16r+16), its down rows requested ahead of use;
+//   phase 2  wait for the XCD's 256 logits; the top-8 set from the logits alone (same answer
+//            everywhere; slots in ascending expert id), with the exact selection where the 8th and
+//            9th logits are (nearly) equal; routed gate/up rows of slot x, i in [16r, 16r+16), its
+//            down rows requested ahead of use; R2-R5 weights by wave 3 while its rows are in flight;
 //            shared-down partial over the XCD's 64 i-values for rows h in [64r, 64r+64)
 //   phase 3  wait for slot x's 512 activations (XCD-local); down rows h in [64r, 64r+64) (Q4_K, Q5_K
 //            rows on the activations' int8 digit planes)
@@ -416,6 +418,130 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
   return true;
 }
 
+// Maximum over the wave, in every lane, without a scalar round trip (a VALU -> SGPR -> SALU hop
+// costs ~60 cycles): DPP maxima inside each 16-lane row, then gfx950's lane swaps, whose two
+// results hold lanes i and i ^ 16 (i ^ 32) of the value in either order.
+__device__ __forceinline__ uint32_t wave_max_u32_v(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(b[0], b[1]);
+}
+
+// The top-K set of one token's 256 logits (bf16 bits lb[q] of expert lane + 64q; no NaNs), for
+// the expert loads, without the probabilities: K + 1 rounds pop the wave maximum of distinct
+// 24-bit keys (value key << 8 | 255 - id, wave_route_keys' order). The first K are the set when
+// a8 - a9 >= 2^-20, a = f32(l - max) being the softmax's argument (l8, l9 the K-th and (K+1)-th
+// logits), and a9 >= -64: then r2_exp(a8) / r2_exp(a9) > 1 + 2^-21 (each is exp rounded once to
+// f32, both normal), so after the multiply by 1/sum the K-th probability is strictly above the
+// (K+1)-th and the probability-based selection (wave_route_keys, torch's topk) takes the same set.
+// Writes s_ids[0..K) in ascending id and returns true; false (equal or nearly equal logits at the
+// K-th place) leaves the decision to the exact path.
+template <int K>
+__device__ __forceinline__ bool wave_topk_set(const uint32_t* lb, int lane, int* s_ids) {
+  uint32_t k0 = (bf16_key(lb[0]) << 8) | (uint32_t)(255 - lane);
+  uint32_t k1 = (bf16_key(lb[1]) << 8) | (uint32_t)(191 - lane);
+  uint32_t k2 = (bf16_key(lb[2]) << 8) | (uint32_t)(127 - lane);
+  uint32_t k3 = (bf16_key(lb[3]) << 8) | (uint32_t)(63 - lane);
+  {
+    const uint32_t a = max(k0, k1), b = min(k0, k1), c = max(k2, k3), d = min(k2, k3);
+    k0 = max(a, c); const uint32_t t1 = min(a, c);
+    k3 = min(b, d); const uint32_t t2 = max(b, d);
+    k1 = max(t1, t2); k2 = min(t1, t2);
+  }
+  uint32_t top[K + 1];
+#pragma unroll
+  for (int r = 0; r <= K; ++r) {
+    top[r] = wave_max_u32_v(k0);
+    if (k0 == top[r]) { k0 = k1; k1 = k2; k2 = k3; k3 = 0u; }
+  }
+  const float m = bf16_to_f32(bf16_unkey(top[0] >> 8));
+  const float a8 = bf16_to_f32(bf16_unkey(top[K - 1] >> 8)) - m;
+  const float a9 = bf16_to_f32(bf16_unkey(top[K] >> 8)) - m;
+  if (!(a8 - a9 >= 0x1p-20f) || !(a9 >= -64.0f)) return false;
+  uint32_t mine = top[0];
+#pragma unroll
+  for (int r = 1; r < K; ++r) mine = lane == r ? top[r] : mine;
+  const uint32_t id = 255u - (mine & 255u);
+  int pos = 0;
+#pragma unroll
+  for (int r = 0; r < K; ++r) pos += (255u - (top[r] & 255u)) < id ? 1 : 0;
+  if (lane < K) s_ids[pos] = (int)id;
+  return true;
+}
+
+// Stage outputs of a token's routing (the workgroup that writes them), in torch's slot order.
+struct RouteOut {
+  int32_t* ids;
+  float* w_f32;
+  uint16_t* w_bf16;
+};
+
+// The weights of the set wave_topk_set chose (s_ids ascending, s_lb the 256 logits' bits), with
+// wave_route_keys' arithmetic: the same softmax, rank order = descending (logit, -id) key, and
+// w = p / (sum of the K in rank order) cast to bf16. Writes s_w[slot] (the bf16 weight as f32) and
+// s_tslot[slot] (the slot's rank) and, given o.ids, the stage outputs by rank. With exact_order and
+// equal probabilities inside the set, the slot order is torch's, from the exact replay (same set).
+template <int K>
+__device__ __forceinline__ void wave_route_weights(const uint32_t* s_lb, const int* s_ids, int lane,
+                                                   bool exact_order, TopkLds& tk, int* s_rid,
+                                                   float* s_wf, uint16_t* s_wb, float* s_w,
+                                                   int* s_tslot, uint32_t* s_key, RouteOut o) {
+  uint32_t lb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) lb[q] = s_lb[lane + 64 * q];
+  const int sid = s_ids[lane < K ? lane : 0];
+  const uint32_t sb = s_lb[sid];
+  const uint32_t key = lane < K ? (bf16_key(sb) << 8) | (uint32_t)(255 - sid) : 0u;
+  if (lane < K) s_key[lane] = key;
+  const float m = bf16_to_f32(bf16_unkey(wave_max_u32_v(key) >> 8));
+  float p[4], sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) { p[q] = r2_exp(bf16_to_f32(lb[q]) - m); sum += p[q]; }
+  sum = wave_sum_f32(sum);
+  const float rs = 1.0f / sum;
+  const float ps = r2_exp(bf16_to_f32(sb) - m) * rs;
+  int rank = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) rank += s_key[k] > key ? 1 : 0;
+  if (lane < K) s_wf[rank] = ps;
+  wave_sync();
+  const uint64_t ties = __ballot(lane < K - 1 && s_wf[lane] == s_wf[lane + 1]);
+  if (ties && exact_order) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[q] *= rs;
+    route_replay_and_write(tk, p, 256, K, lane, s_rid, s_wf, s_wb, nullptr);
+    if (lane < K) {
+      const int id = s_rid[lane];
+      int pos = 0;
+#pragma unroll
+      for (int q = 0; q < K; ++q) pos += s_ids[q] < id ? 1 : 0;
+      s_w[pos] = bf16_to_f32(s_wb[lane]);
+      s_tslot[pos] = lane;
+      if (o.ids) o.ids[lane] = id;
+      if (o.w_f32) o.w_f32[lane] = s_wf[lane];
+      if (o.w_bf16) o.w_bf16[lane] = s_wb[lane];
+    }
+    return;
+  }
+  float tot = 0.0f;
+#pragma unroll
+  for (int r = 0; r < K; ++r) tot += s_wf[r];
+  if (lane < K) {
+    const float wv = ps / tot;
+    const uint16_t wb = (uint16_t)f32_to_bf16(wv);
+    s_w[lane] = bf16_to_f32(wb);
+    s_tslot[lane] = rank;
+    if (o.ids) o.ids[rank] = sid;
+    if (o.w_f32) o.w_f32[rank] = wv;
+    if (o.w_bf16) o.w_bf16[rank] = wb;
+  }
+}
+
 // 32-bit word at a 2-byte-aligned byte offset of an LDS region (4-byte-aligned base): the two
 // dwords around it, realigned
 __device__ __forceinline__ uint32_t lds_u32_at(const uint32_t* base, int off) {
@@ -489,11 +615,17 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   __shared__ int s_ke[I / 16];
   __shared__ float s_ks[I / 16];
   __shared__ float s_sh[ISX];            // shared activations of this XCD's slice
+  // the routed slots in ascending expert id: XCD x runs slot x (s_ids[x]); s_w its bf16 weight,
+  // s_tslot its position in torch's slot order (stage outputs)
   __shared__ int s_ids[K];
   __shared__ float s_w[K];
+  __shared__ int s_tslot[K];
+  __shared__ int s_rid[K];               // ids in torch's slot order (the exact paths)
   __shared__ float s_wf[K];
   __shared__ uint16_t s_wb[K];
-  __shared__ int s_order[K];
+  __shared__ uint32_t s_lb[256];         // the logits' bf16 bits, for the weights wave
+  __shared__ int s_wdone;                // the weights are in s_w already (an exact path ran)
+  __shared__ uint32_t s_key[K];          // the set's keys (rank order of the weights wave)
   __shared__ float s_comb[2][K][8];      // [y | shared partial][slot | xcd][row]
   __shared__ float s_gate;
   __shared__ double s_red[2][kThreads / 64];
@@ -754,22 +886,33 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) a.logits_out[64 * q + lane] = (uint16_t)lb[q];
     }
-    float p[4];
-    if (!wave_route_keys<K>(lb, lane, a.exact_order != 0, p, s_ids, s_wf, s_wb))
-      route_replay_and_write(tk, p, E, K, lane, s_ids, s_wf, s_wb, nullptr);
-    wave_sync();
-    if (lane < K) {
-      const int id = s_ids[lane];
-      int rank = 0;
+    // the set decides the expert loads; its weights are formed by wave 3 while those loads are in
+    // flight. Otherwise (a tie or near tie at the K-th place) the probability-based selection and,
+    // where it cannot settle, the exact replay run here, weights included.
+    if (wave_topk_set<K>(lb, lane, s_ids)) {
 #pragma unroll
-      for (int q = 0; q < K; ++q) rank += (s_ids[q] < id) ? 1 : 0;
-      s_order[rank] = lane;              // ascending expert id (ids are distinct)
-      s_w[lane] = bf16_to_f32(s_wb[lane]);
-      if (j == 0) {
-        if (a.ids_out) a.ids_out[lane] = id;
-        if (a.w_f32_out) a.w_f32_out[lane] = s_wf[lane];
-        if (a.w_bf16_out) a.w_bf16_out[lane] = s_wb[lane];
+      for (int q = 0; q < 4; ++q) s_lb[lane + 64 * q] = lb[q];
+      if (lane == 0) s_wdone = 0;
+    } else {
+      float p[4];
+      if (!wave_route_keys<K>(lb, lane, a.exact_order != 0, p, s_rid, s_wf, s_wb))
+        route_replay_and_write(tk, p, E, K, lane, s_rid, s_wf, s_wb, nullptr);
+      wave_sync();
+      if (lane < K) {
+        const int id = s_rid[lane];
+        int pos = 0;
+#pragma unroll
+        for (int q = 0; q < K; ++q) pos += (s_rid[q] < id) ? 1 : 0;
+        s_ids[pos] = id;                 // ascending expert id (ids are distinct)
+        s_w[pos] = bf16_to_f32(s_wb[lane]);
+        s_tslot[pos] = lane;
+        if (j == 0) {
+          if (a.ids_out) a.ids_out[lane] = id;
+          if (a.w_f32_out) a.w_f32_out[lane] = s_wf[lane];
+          if (a.w_bf16_out) a.w_bf16_out[lane] = s_wb[lane];
+        }
       }
+      if (lane == 0) s_wdone = 1;
     }
   }
   __syncthreads();
@@ -817,6 +960,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
         if (DFMT == MOE_FMT_Q5_K) dqh[pass] = *reinterpret_cast<const uint4*>(p + 16 + 16 * (dc & 1));
       }
     }
+    // wave 3, its rows requested: the routing weights of the set wave 0 chose
+    if (wave == 3 && !s_wdone)
+      wave_route_weights<K>(s_lb, s_ids, lane, a.exact_order != 0, tk, s_rid, s_wf, s_wb, s_w, s_tslot, s_key,
+                            j == 0 ? RouteOut{a.ids_out, a.w_f32_out, a.w_bf16_out} : RouteOut{nullptr, nullptr, nullptr});
     float xl[16], xh[16];
     {
       const float* xp = s_x + 256 * b + 64 * gq + l0;
@@ -915,6 +1062,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     }
   }
   __syncthreads();
+  const int xslot = s_tslot[x];          // this XCD's slot in torch's order (expert_raw)
   if (DFMT == MOE_FMT_Q6_K) {
     // down row 64r + (t >> 3): 8 lanes per row, 64 elements each, from the staged rows
     const int rho = t >> 3, s8 = t & 7, b = s8 >> 2, g = (s8 >> 1) & 1, m = s8 & 1;
@@ -926,7 +1074,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     if (s8 == 0) {
       const int h = 64 * r + rho;
       xstore(xb + XW_Y + H * x + h, xenc(v));
-      if (a.expert_raw) a.expert_raw[(size_t)x * H + h] = v;
+      if (a.expert_raw) a.expert_raw[(size_t)xslot * H + h] = v;
     }
   } else {
     const int b = l16 >> 3, c = l16 & 7, gq = c >> 1, l0 = 16 * (c & 1);
@@ -954,7 +1102,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       if (l16 == 0) {
         const int h = 64 * r + 2 * (t >> 4) + pass;
         xstore(xb + XW_Y + H * x + h, xenc(v[pass]));
-        if (a.expert_raw) a.expert_raw[(size_t)x * H + h] = v[pass];
+        if (a.expert_raw) a.expert_raw[(size_t)xslot * H + h] = v[pass];
       }
     }
   }
@@ -998,10 +1146,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       const int h = 8 * j + t;
       float acc = 0.0f;
 #pragma unroll
-      for (int q = 0; q < K; ++q) {
-        const int k = s_order[q];
-        acc = comb_madd(acc, s_w[k], s_comb[0][k][t]);
-      }
+      for (int k = 0; k < K; ++k) acc = comb_madd(acc, s_w[k], s_comb[0][k][t]);   // ascending id
       float shr = 0.0f;
 #pragma unroll
       for (int q = 0; q < kXcd; ++q) shr += s_comb[1][q][t];
