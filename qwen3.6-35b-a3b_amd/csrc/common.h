@@ -88,6 +88,53 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return __longlong_as_double((long long)(lo | (hi << 32)));
 }
 
+// The same sums without the scalar hop (a readlane and its SALU consumers cost ~60 cycles): after
+// the row sums, gfx950's lane swaps add rows i ^ 16, then halves i ^ 32. Every lane ends with
+// (r0 + r1) + (r2 + r3) up to the order of the operands of each addition, the value wave_sum_*
+// reads from lane 63 ((r3 + r2) + (r1 + r0)): the same bits.
+__device__ __forceinline__ float wave_sum_f32_v(float v) {
+  v = row16_sum_f32(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ double swap_add_f64_16(double v) {
+  const uint64_t u = __double_as_longlong(v);
+  const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)u, (uint32_t)u, false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+  return __longlong_as_double((long long)((uint64_t)lo[0] | ((uint64_t)hi[0] << 32))) +
+         __longlong_as_double((long long)((uint64_t)lo[1] | ((uint64_t)hi[1] << 32)));
+}
+__device__ __forceinline__ double swap_add_f64_32(double v) {
+  const uint64_t u = __double_as_longlong(v);
+  const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)u, (uint32_t)u, false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+  return __longlong_as_double((long long)((uint64_t)lo[0] | ((uint64_t)hi[0] << 32))) +
+         __longlong_as_double((long long)((uint64_t)lo[1] | ((uint64_t)hi[1] << 32)));
+}
+__device__ __forceinline__ double wave_sum_f64_v(double v) {
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x141>(v);
+  v += dpp_f64<0x140>(v);
+  return swap_add_f64_32(swap_add_f64_16(v));
+}
+
+// Maximum over the wave, in every lane, without a scalar round trip (a VALU -> SGPR -> SALU hop
+// costs ~60 cycles): DPP maxima inside each 16-lane row, then gfx950's lane swaps, whose two
+// results hold lanes i and i ^ 16 (i ^ 32) of the value in either order.
+__device__ __forceinline__ uint32_t wave_max_u32_v(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(b[0], b[1]);
+}
+
 __device__ __forceinline__ float silu_f32(float z) { return z / (1.0f + __expf(-z)); }
 
 // ------------------------------------------------------------------- the combine's roundings --

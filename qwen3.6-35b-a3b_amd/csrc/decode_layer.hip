@@ -292,13 +292,8 @@ __device__ __forceinline__ uint32_t router_row_bits(const uint4* w, const float 
       wm = max(wm, __float_as_uint(wv) & 0x7FFFFFFFu);
     }
   }
-  acc = wave_sum_f64(acc);
-  wm = max(wm, dpp_u32<0xB1>(wm));
-  wm = max(wm, dpp_u32<0x4E>(wm));
-  wm = max(wm, dpp_u32<0x141>(wm));
-  wm = max(wm, dpp_u32<0x140>(wm));
-  wm = max(max((uint32_t)__builtin_amdgcn_readlane((int)wm, 15), (uint32_t)__builtin_amdgcn_readlane((int)wm, 31)),
-           max((uint32_t)__builtin_amdgcn_readlane((int)wm, 47), (uint32_t)__builtin_amdgcn_readlane((int)wm, 63)));
+  acc = wave_sum_f64_v(acc);
+  wm = wave_max_u32_v(wm);
   const double nrm = xl1 * (double)__uint_as_float(wm) + fabs(bval);
   uint32_t bits;
   if (!round_bf16_certified(acc + bval, 4.0 * (double)(H + 3) * 0x1p-53 * nrm, &bits)) {
@@ -416,20 +411,6 @@ __device__ __forceinline__ bool wave_route_keys(const uint32_t* lb, int lane, bo
     wb[lane] = (uint16_t)f32_to_bf16(wv);
   }
   return true;
-}
-
-// Maximum over the wave, in every lane, without a scalar round trip (a VALU -> SGPR -> SALU hop
-// costs ~60 cycles): DPP maxima inside each 16-lane row, then gfx950's lane swaps, whose two
-// results hold lanes i and i ^ 16 (i ^ 32) of the value in either order.
-__device__ __forceinline__ uint32_t wave_max_u32_v(uint32_t v) {
-  v = max(v, dpp_u32<0xB1>(v));
-  v = max(v, dpp_u32<0x4E>(v));
-  v = max(v, dpp_u32<0x141>(v));
-  v = max(v, dpp_u32<0x140>(v));
-  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = max(a[0], a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return max(b[0], b[1]);
 }
 
 // The top-K set of one token's 256 logits (bf16 bits lb[q] of expert lane + 64q; no NaNs), for
@@ -696,8 +677,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     double ss = (double)xin.x * xin.x + (double)xin.y * xin.y + (double)xin.z * xin.z + (double)xin.w * xin.w;
     double sa = fabs((double)xin.x * nw.x) + fabs((double)xin.y * nw.y) + fabs((double)xin.z * nw.z) +
                 fabs((double)xin.w * nw.w);
-    ss = wave_sum_f64(ss);
-    sa = wave_sum_f64(sa);
+    ss = wave_sum_f64_v(ss);
+    sa = wave_sum_f64_v(sa);
     if (lane == 0) { s_red[0][wave] = ss; s_red[1][wave] = sa; }
   }
   if (t == 0) {
@@ -817,8 +798,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
         xq[4 * k] = u.x; xq[4 * k + 1] = u.y; xq[4 * k + 2] = u.z; xq[4 * k + 3] = u.w;
       }
       float ag = q8_0_block_dot(bg, lane & 1, xq), au = q8_0_block_dot(bu, lane & 1, xq);
-      ag = wave_sum_f32(ag);
-      au = wave_sum_f32(au);
+      ag = wave_sum_f32_v(ag);
+      au = wave_sum_f32_v(au);
       if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + (wave - 5)), xenc(silu_f32(ag) * au));
     } else if (wave == 5 || wave == 6) {
       float ag = 0.0f, au = 0.0f;
@@ -827,8 +808,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
         ag += shared_dot(wx[c], xv[c]);
         au += shared_dot(wx[4 + c], xv[c]);
       }
-      ag = wave_sum_f32(ag);
-      au = wave_sum_f32(au);
+      ag = wave_sum_f32_v(ag);
+      au = wave_sum_f32_v(au);
       if (lane == 0) lstore(xr, 4 * (XW_SSH + ISX * x + 2 * r + (wave - 5)), xenc(silu_f32(ag) * au));
     } else if (wave == 7) {
       float gs = 0.0f;
@@ -847,7 +828,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) gs += dot8_bf16(wx[c], xv[c]);
       }
-      gs = wave_sum_f32(gs);
+      gs = wave_sum_f32_v(gs);
       const float p = 1.0f / (1.0f + expf(-gs));
       if (lane == 0) {
         s_gate = p;
@@ -980,7 +961,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
     for (int i = 0; i < 16; ++i) { sxl += xl[i]; sxh += xh[i]; }
     float acc[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = wave_sum_f32(q4k_chunk_dot(hdr[q], qs[q], gq, xl, xh, sxl, sxh));
+    for (int q = 0; q < 4; ++q) acc[q] = wave_sum_f32_v(q4k_chunk_dot(hdr[q], qs[q], gq, xl, xh, sxl, sxh));
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       if (lane == q) lstore(xr, 4 * (XW_SR + I * x + i0 + q), xenc(silu_f32(acc[2 * q]) * acc[2 * q + 1]));
