@@ -71,8 +71,13 @@ __device__ __forceinline__ uint4 a_frag(const ARaw<AT>& r) {
     return r.v[0];
 }
 
-// This wave's K range [k0, k0 + kw) of the tile: rows ar0 (group 0) and ar1 (group 1, TWO) at
-// element k0 + 8 h, weight row br at the same element; AT's element size es. BF16 activations run
+// This wave's K range of the tile: rows ar0 (group 0) and ar1 (group 1, TWO) and weight row br at
+// the lane's first element; AT's element size es. The K order is permuted inside each 64-wide
+// chunk, the same way for both operands: lane half h takes the chunk's elements [32 h, 32 h + 32),
+// substep ss the 8 at 32 h + 8 ss. A lane's four substep slices are then one contiguous run, so a
+// cache line is consumed by consecutive loads of one wave (in MFMA order, lanes 0-31 and 32-63 of
+// a substep taking elements 8 apart, each line was revisited by four loads issued far apart, and
+// eight waves' working sets overflowed L1). BF16 activations run
 // the bf16 MFMA on the weights as they are, the others the f16 MFMA on converted weights.
 template <int AT, bool TWO>
 __device__ __forceinline__ void wave_k(const uint8_t* ar0, const uint8_t* ar1, const uint8_t* br,
@@ -84,7 +89,7 @@ __device__ __forceinline__ void wave_k(const uint8_t* ar0, const uint8_t* ar1, c
   auto load = [&](int c, ARaw<AT>(&x0)[4], ARaw<AT>(&x1)[4], uint4(&y)[4]) {
 #pragma unroll
     for (int ss = 0; ss < 4; ++ss) {
-      const size_t k = (size_t)(c * kCK + 16 * ss);
+      const size_t k = (size_t)(c * kCK + 8 * ss);
       y[ss] = *reinterpret_cast<const uint4*>(br + k * 2);
       ld_a<AT>(x0[ss], ar0 + k * es);
       if constexpr (TWO) ld_a<AT>(x1[ss], ar1 + k * es);
@@ -121,7 +126,7 @@ __device__ __forceinline__ void tile_k(const void* a, int T, int K, int m0, cons
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, r = lane & 31;
   constexpr int es = AT == MOE_DT_F32 ? 4 : 2;
-  const int kw = K / NW, k0 = wave * kw + 8 * h;
+  const int kw = K / NW, k0 = wave * kw + 32 * h;
   const uint8_t* ab = reinterpret_cast<const uint8_t*>(a);
   const uint8_t* ar0 = ab + ((size_t)min(m0 + r, T - 1) * K + k0) * es;
   const uint8_t* ar1 = ab + ((size_t)min(m0 + 32 + r, T - 1) * K + k0) * es;
