@@ -259,11 +259,14 @@ __device__ __forceinline__ uint4 xwait4(__amdgpu_buffer_rsrc_t r, int off, const
   return v;
 }
 
-// R1 for one router row held by a wave: w[c] = W[e, 512c + 8 lane .. +8), xv[c] = the matching x.
-// The correctly rounded bf16 of sum + bias: f64 sum (every product x_j w_j is exact in f64) with
-// the certified error bound 4(H+3) 2^-53 (|x|_1 max|w| + |b|), which bounds sum |x_j w_j| + |b|
-// times the summation's error factor; a double-double recompute settles what that does not.
-// xl1 >= |x|_1 is the workgroup's bound on the input's 1-norm.
+// R1 for one router row held by a wave: w[c] = W[e, 512c + 8 lane .. +8), xd[c] = the matching x
+// in f64. The correctly rounded bf16 of sum + bias: f64 sum (every product x_j w_j is exact in
+// f64) with the certified error bound 4(H+3) 2^-53 (|x|_2 |w|_2 + |b|), which by Cauchy-Schwarz
+// bounds sum |x_j w_j| + |b| times the summation's error factor; a double-double recompute
+// settles what that does not. xl2 >= |x|_2 is the workgroup's bound on the input's 2-norm; |w|_2
+// comes from an f32 sum of squares (one FMA per weight, where a running maximum of |w| took two
+// operations; its rounding stays below 40 * 2^-24 of the sum) raised by 2^-15 before an f32 square
+// root, whose result is raised by 2^-20 (more than its error) and taken to f64.
 // Weight i (0..7) of chunk c of the row a lane holds: bf16 rows take one uint4 per chunk, f32
 // rows two (w[2c], w[2c + 1]); either way x_j w_j is exact in f64.
 template <int RDT>
@@ -278,30 +281,30 @@ __device__ __forceinline__ float router_w(const uint4* w, int c, int i) {
 }
 
 template <int RDT>
-__device__ __forceinline__ uint32_t router_row_bits(const uint4* w, const float (*xv)[8],
-                                                   double bval, double xl1) {
+__device__ __forceinline__ uint32_t router_row_bits(const uint4* w, const double (*xd)[8],
+                                                   double bval, double xl2) {
   constexpr int H = 2048;
   double acc = 0.0;
-  uint32_t wm = 0;                       // max |w| as f32 bits (ordered like the magnitudes)
+  float wsq = 0.0f;                      // sum of w^2 (f32)
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float wv = router_w<RDT>(w, c, i);
-      acc = fma((double)xv[c][i], (double)wv, acc);
-      wm = max(wm, __float_as_uint(wv) & 0x7FFFFFFFu);
+      acc = fma(xd[c][i], (double)wv, acc);
+      wsq = fmaf(wv, wv, wsq);
     }
   }
   acc = wave_sum_f64_v(acc);
-  wm = wave_max_u32_v(wm);
-  const double nrm = xl1 * (double)__uint_as_float(wm) + fabs(bval);
+  wsq = wave_sum_f32_v(wsq);
+  const double nrm = xl2 * (double)__builtin_sqrtf(wsq * (1.0f + 0x1p-15f)) * (1.0 + 0x1p-20) + fabs(bval);
   uint32_t bits;
   if (!round_bf16_certified(acc + bval, 4.0 * (double)(H + 3) * 0x1p-53 * nrm, &bits)) {
     DD d = {0.0, 0.0};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d = dd_add(d, DD{(double)xv[c][i] * (double)router_w<RDT>(w, c, i), 0.0});
+      for (int i = 0; i < 8; ++i) d = dd_add(d, DD{xd[c][i] * (double)router_w<RDT>(w, c, i), 0.0});
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -672,11 +675,17 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   const float bias_e = *(gfloat*)(a.bias ? a.bias + 8 * r + wave : &kZeroBias);
   const float resid = (t < 8 && a.residual) ? a.residual[8 * j + t] : 0.0f;
   // norm: r = f32(1 / sqrt(mean(x^2) + eps)) in f64 (every square exact, one final rounding);
-  // xl1 >= |input|_1 for the router's error bound, from sum |x_j nw_j| (exact products)
+  // and sum (x_j nw_j)^2 (exact products, their squares rounded in f64) for the router's bound on
+  // the normalized input's 2-norm: each element of x_n = (x r) nw is within two f32 roundings of
+  // x_j r nw_j
   {
     double ss = (double)xin.x * xin.x + (double)xin.y * xin.y + (double)xin.z * xin.z + (double)xin.w * xin.w;
-    double sa = fabs((double)xin.x * nw.x) + fabs((double)xin.y * nw.y) + fabs((double)xin.z * nw.z) +
-                fabs((double)xin.w * nw.w);
+    double sa = 0.0;
+    {
+      const double p0 = (double)xin.x * nw.x, p1 = (double)xin.y * nw.y;
+      const double p2 = (double)xin.z * nw.z, p3 = (double)xin.w * nw.w;
+      sa = p0 * p0 + p1 * p1 + p2 * p2 + p3 * p3;
+    }
     ss = wave_sum_f64_v(ss);
     sa = wave_sum_f64_v(sa);
     if (lane == 0) { s_red[0][wave] = ss; s_red[1][wave] = sa; }
@@ -750,21 +759,21 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(xb, 0, XW_BUF * 4, 0x00020000);
   {
-    double tot = 0.0, tabs = 0.0;
+    double tot = 0.0, tsq = 0.0;
 #pragma unroll
-    for (int q = 0; q < kThreads / 64; ++q) { tot += s_red[0][q]; tabs += s_red[1][q]; }
+    for (int q = 0; q < kThreads / 64; ++q) { tot += s_red[0][q]; tsq += s_red[1][q]; }
     float4 v = xin;
-    double xl1 = tabs * (1.0 + 0x1p-20);
+    double xl2 = sqrt(tsq) * (1.0 + 0x1p-20);
     if (a.norm_w) {
       const float rs = (float)(1.0 / sqrt(tot / (double)H + (double)a.norm_eps));
       v = make_float4((v.x * rs) * nw.x, (v.y * rs) * nw.y, (v.z * rs) * nw.z, (v.w * rs) * nw.w);
-      xl1 *= (double)rs;
+      xl2 *= (double)rs;
     }
     reinterpret_cast<float4*>(s_x)[t] = v;
     __syncthreads();
 
     // ---------------------------------------------------------------------------- phase 1 --
-    // x at cols 512c + 8 lane (c = 0..3)
+    // x at cols 512c + 8 lane (c = 0..3): f64 for the router dot, f32 for waves 5-7's dots
     float xv[4][8];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -773,8 +782,13 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
       xv[c][0] = u0.x; xv[c][1] = u0.y; xv[c][2] = u0.z; xv[c][3] = u0.w;
       xv[c][4] = u1.x; xv[c][5] = u1.y; xv[c][6] = u1.z; xv[c][7] = u1.w;
     }
+    double xd[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xd[c][i] = (double)xv[c][i];
     const int e = 8 * r + wave;
-    const uint32_t bits = router_row_bits<RDT>(wr4, xv, (double)bias_e, xl1);
+    const uint32_t bits = router_row_bits<RDT>(wr4, xd, (double)bias_e, xl2);
     if (lane == 0) lstore(xr, 4 * (XW_LOG + 256 * x + e), ~bits);
     if ((wave == 5 || wave == 6) && SFMT == MOE_FMT_Q8_0) {
       uint32_t* st = s_q8 + 1088 * (wave - 5);
