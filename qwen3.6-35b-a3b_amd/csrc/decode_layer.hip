@@ -763,14 +763,17 @@ __global__ __launch_bounds__(kThreads) void k_dec_layer(LayerArgs a) {
 #pragma unroll
     for (int q = 0; q < kThreads / 64; ++q) { tot += s_red[0][q]; tsq += s_red[1][q]; }
     float4 v = xin;
-    double xl2 = sqrt(tsq) * (1.0 + 0x1p-20);
+    float rs = 1.0f;
     if (a.norm_w) {
-      const float rs = (float)(1.0 / sqrt(tot / (double)H + (double)a.norm_eps));
+      rs = (float)(1.0 / sqrt(tot / (double)H + (double)a.norm_eps));
       v = make_float4((v.x * rs) * nw.x, (v.y * rs) * nw.y, (v.z * rs) * nw.z, (v.w * rs) * nw.w);
-      xl2 *= (double)rs;
     }
     reinterpret_cast<float4*>(s_x)[t] = v;
     __syncthreads();
+    // the router's bound on |x_n|_2, after the barrier (nothing before it waits for this): the
+    // f32 root of the f64 sum raised by 2^-15 (its rounding to f32), the root raised by 2^-20
+    // (its error and the two f32 roundings of each normalized element)
+    const double xl2 = (double)__builtin_sqrtf((float)tsq * (1.0f + 0x1p-15f)) * (1.0 + 0x1p-20) * (double)rs;
 
     // ---------------------------------------------------------------------------- phase 1 --
     // x at cols 512c + 8 lane (c = 0..3): f64 for the router dot, f32 for waves 5-7's dots
