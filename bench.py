@@ -334,13 +334,35 @@ def pmc_prefill_summary(dir_pmc: str, dir_trace: str) -> str:
 PREFILL_PMC_SUMMARY = ROOT / "profiles" / "prefill_c3_pmc.md"
 
 
+PREFILL_STATS_SUMMARY = ROOT / "profiles" / "prefill_c3_kernel_stats.md"
+
+
 def committed_prefill_pmc():
-    """The GEMMs' counter figures from the committed summary (or None)."""
+    """The GEMMs' counter figures from the committed summary (or None). Their "us" is the counter
+    pass's own kernel trace (3 blocks of the --pmc-prefill workload); "us_kernel_stats" and
+    "frac_kernel_stats" put the same algorithmic FLOPs over the average duration of the committed
+    22-block kernel statistics of the timed workload, which is the figure the block time
+    contains."""
     try:
         m = re.search(r"prefill_gemm_summary:\s*(\{.*\})", PREFILL_PMC_SUMMARY.read_text())
-        return json.loads(m.group(1)) if m else None
+        out = json.loads(m.group(1)) if m else None
     except (OSError, ValueError):
         return None
+    if out is None:
+        return None
+    try:
+        stats = PREFILL_STATS_SUMMARY.read_text()
+    except OSError:
+        stats = ""
+    for name, v in out.items():
+        v["us_source"] = "profiles/prefill_c3_pmc.md (counter pass, 3 blocks)"
+        row = re.search(r"\|\s*`[^`]*" + re.escape(name) + r"[^`]*`\s*\|\s*\d+\s*\|\s*([0-9.]+)\s*\|", stats)
+        if row and v.get("us") and v.get("tflops"):
+            us = float(row.group(1))
+            flop = v["tflops"] * 1e12 * v["us"] * 1e-6
+            v["us_kernel_stats"] = us
+            v["frac_kernel_stats"] = round(flop / (us * 1e-6) / (BF16_PEAK_TFLOPS * 1e12), 4)
+    return out
 
 
 def committed_traffic():
