@@ -655,9 +655,15 @@ static int block_forward_impl(const void* x, int x_dtype, int T, int H, int I, i
     g.w1 = reinterpret_cast<const uint16_t*>(ws_up); g.S = ssh; g.T = T; g.H = H; g.Is = I_s;
     d.n = moe_shjob_down_blocks(T, H);
     d.w0 = reinterpret_cast<const uint16_t*>(ws_down); d.S = ssh; d.y = sraw; d.T = T; d.H = H; d.Is = I_s;
+    // the sort and the tile list inside the router launch, by its last group to finish routing
+    MoeSortJob sj;
+    if (tiles && bm >= 32 && bm <= 160) {
+      sj.P = P; sj.offsets = offsets; sj.sorted = sorted; sj.pos = pos; sj.hits = hits;
+      sj.tiles = tiles; sj.bm = bm;
+    }
     MOE_TRY(moe_launch_router_chain(x, x_dtype, w_router, Wt.router_dtype, logit_bias, T, H, E, logits,
-                                    nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st, x16, &g));
-    MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
+                                    nullptr, ids, wf, wb, nullptr, exact_order, rscr, sync, st, x16, &g, &sj));
+    if (!sj.P) MOE_TRY(moe_launch_sort(ids, P, E, offsets, sorted, pos, hits, sort_ws, st, tiles, bm));
     MOE_TRY(experts_impl(x, x_dtype, x16, gate, up, gu_estride, gate_up_fmt, down_q, down_fmt, offsets,
                          sorted, hits, T, H, I, E, K, path, y, w, st, tiles, y16, &d));
     return moe_launch_combine(y, y16, pos, ids, wb, sraw, gp, residual, T, K, H, out, routed_sum,

@@ -32,13 +32,25 @@ bool moe_router_chain_supported(int T, int H, int E, int K);
 size_t moe_router_chain_scratch_bytes(int T, int E);
 // x16 (NULL: skipped): also the f16 copy of x (k_to_f16's conversion)
 struct MoeShJob;
+// moe_launch_sort's outputs (P = T * K pairs, E = 256) and the MFMA tile list of bm-row tiles
+// (bm <= 160), produced inside the single-launch router by the last 16-token group to finish its
+// routing; P = 0: none (the caller sorts)
+struct MoeSortJob {
+  int P = 0;
+  int32_t* offsets = nullptr;      // [E + 1]
+  int32_t* sorted = nullptr;       // [P]
+  int32_t* pos = nullptr;          // [P]
+  int32_t* hits = nullptr;         // [E + 1]
+  int32_t* tiles = nullptr;        // the packed tile list (moe_launch_build_tiles' layout)
+  int bm = 0;
+};
 // sh (optional): the small-T shared expert's gate/up and scalar gate as extra blocks of the
-// launch, reading x in its own dtype
+// launch, reading x in its own dtype; srt (optional): the sort, as above
 int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dtype, const float* bias,
                             int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
                             float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
                             void* scratch, int* sync, hipStream_t st, uint16_t* x16 = nullptr,
-                            const MoeShJob* sh = nullptr);
+                            const MoeShJob* sh = nullptr, const MoeSortJob* srt = nullptr);
 // bytes of router scratch that let every R1 form run (the int8 one, the single-launch chain)
 size_t moe_router_scratch_bytes(int T, int H, int E);
 int moe_launch_route_topk(const uint16_t* logits, int T, int E, int K, float* probs, int32_t* ids,

@@ -591,7 +591,8 @@ __global__ __launch_bounds__(256) void k_route_replay8(const uint16_t* __restric
 constexpr int kChainKS = 4;       // blocks per tile (K splits)
 constexpr int kChainPart = 288;   // doubles per partial: 256 tile sums, 16 + 16 row norms
 constexpr int kChainTiles = 256;  // tile counters (T <= 256, E = 256); 16 group counters follow
-static_assert((kRouterCntWord + kChainTiles + 16) * 4 <= (int)kSyncBytes, "router counters in the sync words");
+constexpr int kChainSortCnt = kChainTiles + 16;   // then the count of groups routed (the fused sort)
+static_assert((kRouterCntWord + kChainSortCnt + 1) * 4 <= (int)kSyncBytes, "router counters in the sync words");
 
 // ------------------------------------------- R1-R5 in one launch, 8 <= T <= 256, E = 256, K = 8 --
 // The small-T R1 above runs one 16 x 16 tile per block, so at T = 64 it keeps 64 CUs busy for the
@@ -627,6 +628,9 @@ __device__ __forceinline__ double ld_agent(const double* p) {
 __device__ __forceinline__ void st16_agent(uint16_t* p, uint16_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ int ld32_agent(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // this thread's stores complete (acknowledged) before what follows; the signal fence keeps the
 // compiler from moving them past the wait
 __device__ __forceinline__ void stores_done() {
@@ -635,13 +639,149 @@ __device__ __forceinline__ void stores_done() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// The stable grouping of the P = T * 8 pairs by expert (E = 256) by one 512-thread block: the
+// positions of moe_launch_sort (pairs p = t * 8 + k ordered by expert, equal experts in ascending
+// p; a stable counting sort, so any correct one gives the same positions), the offsets, the hit
+// list, and the bm-row tile list in build_tiles_block's order (by decreasing 32-row group count,
+// then ascending expert; an expert's full tiles before its partial one). The ids come from other
+// blocks of the launch, so they are read by agent-scope loads. P <= 2048, bm <= 160.
+struct ChainSortLds {
+  int h[256], start[256], run[256];
+  int wcnt[8][256];
+  int tmp[8];
+  uint64_t tmp64[4];
+};
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(v, o, 64);
+    if (lane >= o) v += n;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_incl_scan64(uint64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t n = __shfl_up(v, o, 64);
+    if (lane >= o) v += n;
+  }
+  return v;
+}
+__device__ void chain_sort(const int32_t* __restrict__ ids, const MoeSortJob& j, ChainSortLds& s) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int P = j.P;
+  if (tid < 256) {
+    s.h[tid] = 0;
+    s.run[tid] = 0;
+  }
+  __syncthreads();
+  // pair tid + 512 q (q < 4), read once
+  int idv[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int p = tid + 512 * q;
+    idv[q] = p < P ? ld32_agent(ids + p) : -1;
+    if ((unsigned)idv[q] < 256u) atomicAdd(&s.h[idv[q]], 1);
+  }
+  __syncthreads();
+  // thread e < 256: expert e's count; exclusive prefixes of the counts, of the hit flags and of
+  // the packed per-group-count tile counts (12 bits each) over the 256 experts
+  const int e = tid;
+  const int tot = e < 256 ? s.h[e] : 0, hit = tot > 0 ? 1 : 0;
+  const int ngmax = (j.bm + 31) / 32;
+  const int nfull = tot / j.bm, rem = tot - nfull * j.bm;
+  const int grem = rem > 0 ? (rem + 31) / 32 : 0;
+  const uint64_t packed = ((uint64_t)nfull << (12 * (ngmax - 1))) + (grem ? (1ull << (12 * (grem - 1))) : 0ull);
+  const int it = wave_incl_scan(tot, lane), ih = wave_incl_scan(hit, lane);
+  const uint64_t ip = wave_incl_scan64(packed, lane);
+  if (lane == 63 && wave < 4) {
+    s.tmp[wave] = it;
+    s.tmp[4 + wave] = ih;
+    s.tmp64[wave] = ip;
+  }
+  __syncthreads();
+  if (tid < 256) {
+    int bt = 0, bh = 0, tt = 0, th = 0;
+    uint64_t bp = 0, tp = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      bt += w < wave ? s.tmp[w] : 0;
+      bh += w < wave ? s.tmp[4 + w] : 0;
+      bp += w < wave ? s.tmp64[w] : 0ull;
+      tt += s.tmp[w];
+      th += s.tmp[4 + w];
+      tp += s.tmp64[w];
+    }
+    const int base = bt + it - tot, hidx = bh + ih - hit;
+    const uint64_t pre = bp + ip - packed;
+    s.start[e] = base;
+    j.offsets[e] = base;
+    if (hit) j.hits[1 + hidx] = e;
+    if (e == 0) {
+      j.offsets[256] = tt;
+      j.hits[0] = th;
+    }
+    auto field = [](uint64_t v, int g) { return (int)((v >> (12 * (g - 1))) & 4095u); };
+    int gstart[6] = {0, 0, 0, 0, 0, 0};
+    int acc = 0;
+    for (int g = ngmax; g >= 1; --g) {
+      gstart[g] = acc;
+      acc += field(tp, g);
+    }
+    const int p_full = gstart[ngmax] + field(pre, ngmax);
+    for (int i = 0; i < nfull; ++i) {
+      j.tiles[1 + 2 * (p_full + i)] = e;
+      j.tiles[2 + 2 * (p_full + i)] = base + i * j.bm;
+    }
+    if (grem) {
+      const int pt = gstart[grem] + field(pre, grem) + (grem == ngmax ? nfull : 0);
+      j.tiles[1 + 2 * pt] = e;
+      j.tiles[2 + 2 * pt] = base + nfull * j.bm;
+    }
+    if (e == 0) j.tiles[0] = acc;
+  }
+  // the scatter, 512 pairs a round: ranks inside a wave from id matching (8 ballots on the id
+  // bits), across waves from per-wave counts, across rounds from run[]
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull) >> (64 - lane);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (512 * q >= P) break;
+    for (int i = tid; i < 8 * 256; i += 512) (&s.wcnt[0][0])[i] = 0;
+    __syncthreads();
+    const int p = tid + 512 * q;
+    const bool valid = (unsigned)idv[q] < 256u;
+    const int id = valid ? idv[q] : 0;
+    if (p < P && !valid) j.pos[p] = -1;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (id >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank_w = __popcll(peers & lt);
+    const bool leader = valid && rank_w == 0;
+    if (leader) s.wcnt[wave][id] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int before = 0;
+      for (int w2 = 0; w2 < wave; ++w2) before += s.wcnt[w2][id];
+      const int dest = s.start[id] + s.run[id] + before + rank_w;
+      j.sorted[dest] = p;
+      j.pos[p] = dest;
+    }
+    __syncthreads();
+    if (leader) atomicAdd(&s.run[id], __popcll(peers));
+  }
+}
+
 template <int XDT, int WDT>
 __global__ __launch_bounds__(512) void k_router_chain(
     const void* __restrict__ xv, const void* __restrict__ w, const float* __restrict__ bias, int T,
     int H, int E, uint16_t* __restrict__ logits, float* __restrict__ probs, int32_t* __restrict__ ids,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ heap_flag,
     int exact_order, double* __restrict__ part, int* __restrict__ cnt, int* __restrict__ status,
-    uint16_t* __restrict__ x16, MoeShJob sh) {
+    uint16_t* __restrict__ x16, MoeShJob sh, MoeSortJob srt) {
   // the router blocks' arrays, or the shared-expert blocks' partial tiles, in one LDS region
   struct Chain {
     double d[8][256];
@@ -655,6 +795,7 @@ __global__ __launch_bounds__(512) void k_router_chain(
   __shared__ __attribute__((aligned(16))) union {
     Chain c;
     float red[shs::red_floats<8>()];
+    ChainSortLds srt;
   } sm;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   const int nr = (int)gridDim.x - sh.n;
@@ -807,7 +948,9 @@ __global__ __launch_bounds__(512) void k_router_chain(
       if (lane == 0) s_rep[atomicAdd(&s_nrep, 1)] = t;
     } else if (lane < 8) {
       const float wv8 = my_val / tot;
-      ids[(size_t)t * 8 + lane] = my_id;
+      // read by the fused sort's block (another XCD) in this launch
+      if (srt.P) __hip_atomic_store(&ids[(size_t)t * 8 + lane], my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else ids[(size_t)t * 8 + lane] = my_id;
       w_f32[(size_t)t * 8 + lane] = wv8;
       w_bf16[(size_t)t * 8 + lane] = (uint16_t)f32_to_bf16(wv8);
     }
@@ -818,9 +961,28 @@ __global__ __launch_bounds__(512) void k_router_chain(
     const int t = s_rep[i];
     float p[4];
     route_softmax<true>(logits + (size_t)t * 256, 256, lane, p);
-    route_replay_and_write(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
-                           w_bf16 + (size_t)t * 8, heap_flag);
+    if (srt.P)
+      route_replay_and_write<true>(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
+                                   w_bf16 + (size_t)t * 8, heap_flag);
+    else
+      route_replay_and_write(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
+                             w_bf16 + (size_t)t * 8, heap_flag);
   }
+  if (!srt.P) return;
+  // 4. the last group to finish its routing: the sort (every group's ids stored and acknowledged
+  // before its arrival is counted)
+  stores_done();
+  __syncthreads();
+  if (tid == 0) {
+    const int ng = (T + 15) / 16;
+    const int c = atomicAdd(&cnt[kChainSortCnt], 1);
+    if (c >= ng) atomicOr(status, MOE_STATUS_SYNC_STATE);
+    s_last = c == ng - 1;
+    if (s_last) __hip_atomic_store(&cnt[kChainSortCnt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  chain_sort(ids, srt, sm.srt);
 }
 
 }  // namespace moe
@@ -862,7 +1024,7 @@ int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dty
                             int T, int H, int E, uint16_t* logits, float* probs, int32_t* ids,
                             float* w_f32, uint16_t* w_bf16, int32_t* heap_flag, bool exact_order,
                             void* scratch, int* sync, hipStream_t st, uint16_t* x16,
-                            const MoeShJob* sh) {
+                            const MoeShJob* sh, const MoeSortJob* srt) {
   if (!moe_router_chain_supported(T, H, E, 8) || !scratch || !sync)
     return moe_set_error(MOE_E_UNSUPPORTED, "router_chain: needs 8 <= T <= 256, E = 256, K = 8, H %% 2048 == 0");
   const MoeShJob job = sh ? *sh : MoeShJob{};
@@ -873,6 +1035,11 @@ int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dty
       return moe_set_error(MOE_E_ARG, "router_chain: %d shared-expert blocks given, %d needed", job.n,
                            moe_shjob_gateup_blocks(T, job.Is));
   }
+  const MoeSortJob sj = srt ? *srt : MoeSortJob{};
+  if (sj.P) {
+    if (sj.P != T * 8 || !sj.offsets || !sj.sorted || !sj.pos || !sj.hits || !sj.tiles || sj.bm < 32 || sj.bm > 160)
+      return moe_set_error(MOE_E_ARG, "router_chain: the fused sort needs P = 8 T, 32 <= bm <= 160 and every output");
+  }
   dim3 grid(((T + 15) / 16) * (E / 16) * kChainKS);
   grid.x += (unsigned)job.n;
   double* part = reinterpret_cast<double*>(scratch);
@@ -880,7 +1047,7 @@ int moe_launch_router_chain(const void* x, int x_dtype, const void* w, int w_dty
   const int eo = exact_order ? 1 : 0;
 #define MOE_CHAIN(XD, WD)                                                                          \
   hipLaunchKernelGGL((k_router_chain<XD, WD>), grid, dim3(512), 0, st, x, w, bias, T, H, E, logits, \
-                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, sync + MOE_STATUS_WORD, x16, job)
+                     probs, ids, w_f32, w_bf16, heap_flag, eo, part, cnt, sync + MOE_STATUS_WORD, x16, job, sj)
   if (x_dtype == MOE_DT_F32 && w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_F32);
   else if (x_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_F32, MOE_DT_BF16);
   else if (w_dtype == MOE_DT_F32) MOE_CHAIN(MOE_DT_BF16, MOE_DT_F32);

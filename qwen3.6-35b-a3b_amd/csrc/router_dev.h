@@ -545,7 +545,9 @@ __device__ __forceinline__ void route_softmax(const uint16_t* lg, int E, int lan
 
 // R3-R5 by the exact replay of torch's CPU topk (for ties that the fast paths cannot settle),
 // then w = p_k / sum_k p_k (rank order) and its bf16 cast. Writes ids/w_f32/w_bf16[0..K) from
-// lane 0. p: lane's probabilities at positions lane + 64j.
+// lane 0. p: lane's probabilities at positions lane + 64j. AGENT_IDS: the ids by agent-scope
+// stores, for a reader in another XCD during the same launch.
+template <bool AGENT_IDS = false>
 __device__ __forceinline__ void route_replay_and_write(TopkLds& s, const float* p, int E, int K,
                                                        int lane, int32_t* ids, float* w_f32,
                                                        uint16_t* w_bf16, int32_t* heap_flag) {
@@ -555,7 +557,8 @@ __device__ __forceinline__ void route_replay_and_write(TopkLds& s, const float* 
     for (int k = 0; k < K; ++k) tot += s.v[k];
     for (int k = 0; k < K; ++k) {
       const float wv = s.v[k] / tot;
-      ids[k] = s.i[k];
+      if (AGENT_IDS) __hip_atomic_store(&ids[k], (int32_t)s.i[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else ids[k] = s.i[k];
       w_f32[k] = wv;
       w_bf16[k] = (uint16_t)f32_to_bf16(wv);
     }
