@@ -648,23 +648,18 @@ __device__ __forceinline__ void stores_done() {
 struct ChainSortLds {
   int h[256], start[256], run[256];
   int wcnt[8][256];
-  int tmp[8];
-  uint64_t tmp64[4];
+  uint32_t tmp[4][4];
 };
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int n = __shfl_up(v, o, 64);
-    if (lane >= o) v += n;
-  }
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_incl_scan64(uint64_t v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint64_t n = __shfl_up(v, o, 64);
-    if (lane >= o) v += n;
-  }
+// inclusive prefix sum over the wave on DPP moves: row shifts by 1, 2, 4, 8 inside each 16-lane
+// row (lanes shifted in from outside the row read 0), then the row totals carried by the row
+// broadcasts of lanes 15 and 31 (the wave_sum_f32 pattern)
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp_u32<0x111>(v);
+  v += dpp_u32<0x112>(v);
+  v += dpp_u32<0x114>(v);
+  v += dpp_u32<0x118>(v);
+  v += dpp_u32<0x142, 0xA>(v);
+  v += dpp_u32<0x143, 0xC>(v);
   return v;
 }
 __device__ void chain_sort(const int32_t* __restrict__ ids, const MoeSortJob& j, ChainSortLds& s) {
@@ -685,56 +680,60 @@ __device__ void chain_sort(const int32_t* __restrict__ ids, const MoeSortJob& j,
   }
   __syncthreads();
   // thread e < 256: expert e's count; exclusive prefixes of the counts, of the hit flags and of
-  // the packed per-group-count tile counts (12 bits each) over the 256 experts
+  // the tile counts per 32-row group count g (10-bit fields, at most 2048 / 32 + 256 = 320 tiles:
+  // g = 1..3 in one word, g = 4..5 in another) over the 256 experts
   const int e = tid;
   const int tot = e < 256 ? s.h[e] : 0, hit = tot > 0 ? 1 : 0;
   const int ngmax = (j.bm + 31) / 32;
   const int nfull = tot / j.bm, rem = tot - nfull * j.bm;
   const int grem = rem > 0 ? (rem + 31) / 32 : 0;
-  const uint64_t packed = ((uint64_t)nfull << (12 * (ngmax - 1))) + (grem ? (1ull << (12 * (grem - 1))) : 0ull);
-  const int it = wave_incl_scan(tot, lane), ih = wave_incl_scan(hit, lane);
-  const uint64_t ip = wave_incl_scan64(packed, lane);
+  auto fbit = [](int g) { return 10 * ((g - 1) % 3); };
+  const uint32_t pk0 = (ngmax <= 3 ? (uint32_t)nfull << fbit(ngmax) : 0u) + (grem && grem <= 3 ? 1u << fbit(grem) : 0u);
+  const uint32_t pk1 = (ngmax > 3 ? (uint32_t)nfull << fbit(ngmax) : 0u) + (grem > 3 ? 1u << fbit(grem) : 0u);
+  const uint32_t it = wave_incl_scan((uint32_t)tot), ih = wave_incl_scan((uint32_t)hit);
+  const uint32_t ip0 = wave_incl_scan(pk0), ip1 = wave_incl_scan(pk1);
   if (lane == 63 && wave < 4) {
-    s.tmp[wave] = it;
-    s.tmp[4 + wave] = ih;
-    s.tmp64[wave] = ip;
+    s.tmp[0][wave] = it;
+    s.tmp[1][wave] = ih;
+    s.tmp[2][wave] = ip0;
+    s.tmp[3][wave] = ip1;
   }
   __syncthreads();
   if (tid < 256) {
-    int bt = 0, bh = 0, tt = 0, th = 0;
-    uint64_t bp = 0, tp = 0;
+    uint32_t b[4] = {0u, 0u, 0u, 0u}, tt[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      bt += w < wave ? s.tmp[w] : 0;
-      bh += w < wave ? s.tmp[4 + w] : 0;
-      bp += w < wave ? s.tmp64[w] : 0ull;
-      tt += s.tmp[w];
-      th += s.tmp[4 + w];
-      tp += s.tmp64[w];
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t v = s.tmp[q][w];
+        b[q] += w < wave ? v : 0u;
+        tt[q] += v;
+      }
     }
-    const int base = bt + it - tot, hidx = bh + ih - hit;
-    const uint64_t pre = bp + ip - packed;
+    const int base = (int)(b[0] + it) - tot, hidx = (int)(b[1] + ih) - hit;
+    const uint32_t pre0 = b[2] + ip0 - pk0, pre1 = b[3] + ip1 - pk1;
     s.start[e] = base;
     j.offsets[e] = base;
     if (hit) j.hits[1 + hidx] = e;
     if (e == 0) {
-      j.offsets[256] = tt;
-      j.hits[0] = th;
+      j.offsets[256] = (int)tt[0];
+      j.hits[0] = (int)tt[1];
     }
-    auto field = [](uint64_t v, int g) { return (int)((v >> (12 * (g - 1))) & 4095u); };
+    auto field = [&](uint32_t w0, uint32_t w1, int g) { return (int)(((g <= 3 ? w0 : w1) >> fbit(g)) & 1023u); };
+    const uint32_t tp0 = tt[2], tp1 = tt[3];
     int gstart[6] = {0, 0, 0, 0, 0, 0};
     int acc = 0;
     for (int g = ngmax; g >= 1; --g) {
       gstart[g] = acc;
-      acc += field(tp, g);
+      acc += field(tp0, tp1, g);
     }
-    const int p_full = gstart[ngmax] + field(pre, ngmax);
+    const int p_full = gstart[ngmax] + field(pre0, pre1, ngmax);
     for (int i = 0; i < nfull; ++i) {
       j.tiles[1 + 2 * (p_full + i)] = e;
       j.tiles[2 + 2 * (p_full + i)] = base + i * j.bm;
     }
     if (grem) {
-      const int pt = gstart[grem] + field(pre, grem) + (grem == ngmax ? nfull : 0);
+      const int pt = gstart[grem] + field(pre0, pre1, grem) + (grem == ngmax ? nfull : 0);
       j.tiles[1 + 2 * pt] = e;
       j.tiles[2 + 2 * pt] = base + nfull * j.bm;
     }
@@ -765,7 +764,8 @@ __device__ void chain_sort(const int32_t* __restrict__ ids, const MoeSortJob& j,
     __syncthreads();
     if (valid) {
       int before = 0;
-      for (int w2 = 0; w2 < wave; ++w2) before += s.wcnt[w2][id];
+#pragma unroll
+      for (int w2 = 0; w2 < 8; ++w2) before += w2 < wave ? s.wcnt[w2][id] : 0;
       const int dest = s.start[id] + s.run[id] + before + rank_w;
       j.sorted[dest] = p;
       j.pos[p] = dest;
