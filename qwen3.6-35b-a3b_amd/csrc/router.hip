@@ -791,6 +791,7 @@ __global__ __launch_bounds__(512) void k_router_chain(
     int last, nrep;
     int rep[16];
     TopkLds tk[8];
+    float prep[16][256];   // the probabilities of the group's tokens that the replays take
   };
   __shared__ __attribute__((aligned(16))) union {
     Chain c;
@@ -945,6 +946,8 @@ __global__ __launch_bounds__(512) void k_router_chain(
     float my_val, tot;
     const int code = wave_topk32<8>(p, lane, my_id, my_val, tot);
     if (code == 2 || (code == 1 && exact_order)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sm.c.prep[t - t0][64 * q + lane] = p[q];
       if (lane == 0) s_rep[atomicAdd(&s_nrep, 1)] = t;
     } else if (lane < 8) {
       const float wv8 = my_val / tot;
@@ -959,8 +962,10 @@ __global__ __launch_bounds__(512) void k_router_chain(
 #pragma unroll 1
   for (int i = wv; i < s_nrep; i += 8) {
     const int t = s_rep[i];
+    // the fast path's probabilities (route_softmax's values: the same logits, the same arithmetic)
     float p[4];
-    route_softmax<true>(logits + (size_t)t * 256, 256, lane, p);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[q] = sm.c.prep[t - t0][64 * q + lane];
     if (srt.P)
       route_replay_and_write<true>(s_tk[wv], p, 256, 8, lane, ids + (size_t)t * 8, w_f32 + (size_t)t * 8,
                                    w_bf16 + (size_t)t * 8, heap_flag);
