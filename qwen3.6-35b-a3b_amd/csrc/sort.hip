@@ -3,7 +3,8 @@
 // torch.argsort(ids.flatten(), stable=True) returns. Integer work only, so bit-exact by design.
 //
 // P <= 64 (decode): one wave ranks every pair directly. P <= 1024: one block runs the three
-// phases below. Otherwise two launches: per-chunk histograms, then per chunk one block that sums
+// phases below. (The block forward at 8 <= T <= 256 with the single-launch router sorts inside
+// that launch instead: chain_sort in router.hip, the same positions and tile list.) Otherwise two launches: per-chunk histograms, then per chunk one block that sums
 // the histograms itself (totals, scan, its own chunk's start positions) and scatters its chunk
 // stably, where ranks inside a 256-pair round come from wave-level id matching (8 ballots on the
 // id bits) and a per-wave count table, so no atomics decide any position. sort_chunk() sets the
