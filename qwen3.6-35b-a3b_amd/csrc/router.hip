@@ -612,10 +612,13 @@ static_assert((kRouterCntWord + kChainSortCnt + 1) * 4 <= (int)kSyncBytes, "rout
 // is counted. (Fences would write back and invalidate whole L2s, 256 times per launch, under the
 // shared expert's concurrent GEMMs.) Each last arriver resets its counter, so the words are zero
 // again for the next launch (also under graph replay). Counters: cnt[tile] for tiles <
-// kChainTiles, cnt[kChainTiles + group]. An arrival that reads a count its launch cannot produce
-// (at least the number of arrivals: a workspace never initialised, or two launches overlapping on
-// one workspace) sets MOE_STATUS_SYNC_STATE in the status word; that launch's routing outputs are
-// then unspecified, and moe_workspace_init restores the counters.
+// kChainTiles, cnt[kChainTiles + group], then the groups routed (kChainSortCnt, with the fused
+// sort). An arrival that reads a count its launch cannot produce (at least the number of
+// arrivals: a workspace never initialised, or two launches overlapping on one workspace) sets
+// MOE_STATUS_SYNC_STATE in the status word; that launch's routing outputs are then unspecified,
+// and moe_workspace_init restores the counters. The last arrival is recognised modulo the number
+// of arrivals, so whatever a counter held, each stage still runs once per launch: the sort always
+// writes a tile list consistent with its own positions, which the grouped GEMMs then read.
 // agent-scope (cross-XCD) stores and loads of the single-launch router's hand-offs
 __device__ __forceinline__ void st_agent(double* p, double v) {
   __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), (unsigned long long)__double_as_longlong(v),
@@ -866,7 +869,7 @@ __global__ __launch_bounds__(512) void k_router_chain(
   if (tid == 0) {
     const int c = atomicAdd(&cnt[tile], 1);
     if (c >= kChainKS) atomicOr(status, MOE_STATUS_SYNC_STATE);   // a start this launch cannot produce
-    s_last = c == kChainKS - 1;
+    s_last = (unsigned)c % kChainKS == kChainKS - 1;
   }
   __syncthreads();
   if (!s_last) return;
@@ -916,7 +919,7 @@ __global__ __launch_bounds__(512) void k_router_chain(
   if (tid == 0) {
     const int c = atomicAdd(&cnt[kChainTiles + tg], 1);
     if (c >= nE) atomicOr(status, MOE_STATUS_SYNC_STATE);
-    s_last = c == nE - 1;
+    s_last = (unsigned)c % (unsigned)nE == (unsigned)nE - 1;
   }
   __syncthreads();
   if (!s_last) return;
@@ -982,7 +985,7 @@ __global__ __launch_bounds__(512) void k_router_chain(
     const int ng = (T + 15) / 16;
     const int c = atomicAdd(&cnt[kChainSortCnt], 1);
     if (c >= ng) atomicOr(status, MOE_STATUS_SYNC_STATE);
-    s_last = c == ng - 1;
+    s_last = (unsigned)c % (unsigned)ng == (unsigned)ng - 1;
     if (s_last) __hip_atomic_store(&cnt[kChainSortCnt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();

@@ -103,6 +103,43 @@ def test_small_t_folded_block_vs_stage_calls(pkg, layer_c3, dev, T, bf16):
     _compare(whole, ref, rows=rows, tag=f"folded T={T}")
 
 
+@pytest.mark.parametrize("T", [24, 64, 136, 256])
+def test_small_t_sort_in_router_launch(pkg, layer_zipf, dev, T):
+    """From 17 to 256 tokens (Q4_K experts, bf16 shared expert; at 16 tokens and below the shared
+    expert takes its GEMV form and the block its separate launches) the block sorts its (token, slot)
+    pairs inside the router launch: the last 16-token group to finish routing counts its arrival
+    in a sync word, resets it, and sorts. Two calls in a row give the same bits and report nothing
+    in the status word. A count no launch produces, planted in that word from the host, makes the
+    arrivals report MOE_STATUS_SYNC_STATE (the last arrival is taken modulo the number of groups,
+    so the sort still runs once and the grouped GEMMs read a consistent tile list); after
+    moe_workspace_init the call gives the first bits again. The word sits after the router's 256
+    tile counters and 16 group counters."""
+    import ctypes
+    L, abi, synth = pkg._lib, pkg.abi, pkg.synth
+    lw, _ = layer_zipf
+    x = synth.make_input(T, seed=T, device=dev)
+    outs = []
+    for _ in range(2):
+        o = torch.empty(T, 2048, dtype=torch.float32, device=dev)
+        abi.block_forward(x, lw, out=o)
+        torch.cuda.synchronize()
+        assert abi.workspace_status(dev) == 0
+        outs.append(o.cpu())
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    buf = abi.workspace(dev, 0)
+    buf[:L.SYNC_BYTES].view(torch.int32)[L.ROUTER_CNT_WORD + 256 + 16] = 1000
+    o = torch.empty(T, 2048, dtype=torch.float32, device=dev)
+    abi.block_forward(x, lw, out=o)
+    torch.cuda.synchronize()
+    assert abi.workspace_status(dev) & L.STATUS_SYNC_STATE
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    assert L.lib.moe_workspace_init(ctypes.c_void_p(buf.data_ptr()), buf.numel(), stream) == L.MOE_OK
+    abi.block_forward(x, lw, out=o)
+    torch.cuda.synchronize()
+    assert abi.workspace_status(dev) == 0
+    assert torch.equal(o.cpu().view(torch.int32), outs[0].view(torch.int32))
+
+
 def test_deterministic_repeat(pkg, layer_c0, dev):
     lw, _ = layer_c0
     x = pkg.synth.make_input(64, seed=4, device=dev)
