@@ -272,8 +272,9 @@ int moe_lm_head(const void *h, int h_dtype, int B, int H, const void *w, int w_f
  * gave up are NaN and the rest of that call's outputs are unspecified. Bit MOE_STATUS_SYNC_STATE:
  * a block-arrival counter of the single-launch router (8 to 256 tokens) held a count its launch
  * cannot produce (a workspace that skipped moe_workspace_init, or two calls overlapping on one
- * workspace); that call's logits, ids and weights are unspecified, and moe_workspace_init restores
- * the counters. No host synchronisation:
+ * workspace); that call's logits, ids, weights and block outputs are unspecified (every stage of
+ * the launch still runs once, so the grouped GEMMs after it stay in bounds), and
+ * moe_workspace_init restores the counters. No host synchronisation:
  * read *status after the stream reaches it. No counterpart in the reference (its device work ran
  * in fresh processes and reported through their exit status, engine/device_arm.py:417-463). */
 #define MOE_STATUS_WORD 3              /* int32 index of the status word in the workspace */
